@@ -1,0 +1,163 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized kernel layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline: INT8 grouped GEMV throughput (GB/s and fraction of the 8 TB/s HBM
+peak) on the Gemma-3-270m MLP up-projection shape M=1, K=640, N=2048, group
+32, with FP16 activations quantized in-kernel.  One step is one launch of the
+strided-batched GEMV over R distinct weight sets (R x 1.4 MB > 1 GiB, so the
+256 MB Infinity Cache cannot hold them): every launch streams its weights
+from HBM.  Inputs are resident in HBM before the timed region starts.
+
+The same JSON line carries the CPU baseline: the CPU restatement of the
+reference kernel (oracle/, x86 build) timed on this host on a bounded sample
+of the same workload, with the reference's M=1 thread policy
+(min(pool, 4) threads, kernel_utils.h:446-453).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "tests"))
+
+HBM_PEAK_GBS = 8000.0
+
+# Gemma-3-270m MLP up-projection GEMV
+M, K, N, GS = 1, 640, 2048, 32
+SET_BYTES = N * K + 2 * N * (K // GS) + 2 * K + 2 * N   # 1,398,016 algorithmic bytes
+
+
+def gemv_sets(R: int, seed: int = 1):
+    """Device buffers for R distinct GEMV problems (weights at distinct addresses)."""
+    import cactus_amd as cm
+    from _data import f16
+    rng = np.random.default_rng(seed)
+    # 64 MiB of random codes, tiled over the R weight sets at distinct addresses
+    pool = rng.integers(-127, 128, size=(48, N, K), dtype=np.int8)
+    B = cm.DeviceBuffer(R * N * K)
+    chunk = pool.reshape(-1)
+    per = pool.shape[0]
+    for r0 in range(0, R, per):
+        n = min(per, R - r0)
+        cm.call("cactus_hip_memcpy_h2d", B.ptr + r0 * N * K, chunk.ctypes.data, n * N * K, None)
+    Bs = cm.DeviceBuffer.from_numpy(
+        f16(np.abs(rng.normal(0, 0.02, size=(R, N, K // GS))) / 127.0))
+    A = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, size=(R, M, K))))
+    C = cm.DeviceBuffer(R * M * N * 2)
+    return A, B, Bs, C
+
+
+def bench_gemv(steps: int, warmup: int, R: int = 768):
+    import cactus_amd as cm
+    A, B, Bs, C = gemv_sets(R)
+    stream = cm.Stream()
+
+    def launch():
+        cm.call("cactus_hip_matmul_int8_f16act_batched", A.ptr, B.ptr, Bs.ptr, C.ptr, M, K, N, GS, R,
+                M * K, N * K, N * (K // GS), M * N, stream.handle)
+
+    for _ in range(warmup):
+        launch()
+    stream.sync()
+    e0, e1 = cm.Event(), cm.Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    stream.sync()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    per_launch_s = ms / 1e3 / steps
+    gbs = R * SET_BYTES / per_launch_s / 1e9
+    return {"gbs": gbs, "ms_per_step": ms / steps, "wall_s": wall, "R": R}
+
+
+def cpu_baseline(seconds: float = 10.0):
+    """Reference-restated CPU GEMV (oracle build) on this host."""
+    import oracle
+    from _data import activations, grouped_int8_weights
+    L = oracle.lib()
+    threads = min(4, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(11)
+    x = activations(rng, M, K)
+    B, Bs = grouped_int8_weights(rng, N, K, GS)
+    q = np.empty((M, K), np.int8)
+    s = np.empty(M, np.float32)
+    C = np.empty((M, N), np.uint16)
+    P = oracle.ptr
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        L.orc_quantize_activations(P(x), P(q), P(s), M, K)
+        L.orc_matmul_int8_mt(P(q), P(s), P(B), P(Bs), P(C), M, K, N, GS, threads)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n * SET_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} GEMVs M=1 K=640 N=2048 g=32 (one weight set, cache-warm) in {dt:.1f} s, "
+                      f"x86 build of the CPU restatement, {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(this build has no multi-GPU path)", file=sys.stderr)
+        sys.exit(2)
+
+    import cactus_amd as cm
+    cm.call("cactus_hip_init", 0)
+    g = bench_gemv(args.steps, args.warmup)
+    cpu = cpu_baseline(args.cpu_seconds)
+    out = {
+        "metric": "INT8 GEMV GB/s (% HBM peak) + Qwen3-0.6B-shape decode tok/s, 1 MI355X",
+        "value": round(g["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded INT8 codes, |N(0,0.02)|/127 fp16 group scales, N(0,1) fp16 activations)",
+        "config": {
+            "workload": f"int8 grouped GEMV M=1 K=640 N=2048 group=32, fp16 activations quantized "
+                        f"in-kernel; one step = one launch over {g['R']} distinct weight sets",
+            "sets_per_launch": g["R"],
+            "bytes_per_set": SET_BYTES,
+        },
+        "hbm_fraction": round(g["gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(g["gbs"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

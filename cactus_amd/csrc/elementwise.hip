@@ -1,0 +1,374 @@
+// elementwise.hip -- RMSNorm (a8), RoPE (a9), softmax (a10), SiLU (a11),
+// fp16 add/multiply (a12), embedding gather (a13) and the greedy sampler (a14).
+#include "hip_common.h"
+
+#include <cmath>
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+namespace cactus_hip {
+
+// ---------------------------------------------------------------- RMSNorm
+// One wave per row.  The row is staged in LDS; lanes 0..15 each run one of
+// the reference's 16 fp32 FMA chains (element i -> chain i mod 16, i.e.
+// accumulator (i%16)/4, lane i%4, kernel_attention.cpp:500-523), which are
+// combined as ((v0+v1)+v2)+v3 per lane and then (l0+l1)+(l2+l3) (:525-530).
+// Output: y = fp16(fp16(x * fp16(1/rms)) * w) on the 8-aligned prefix.
+constexpr int RMS_MAX_DIMS = 8192;
+
+__global__ void __launch_bounds__(256) rms_norm_kernel(const uint16_t* __restrict__ X,
+                                                       const uint16_t* __restrict__ W,
+                                                       uint16_t* __restrict__ Y, size_t rows,
+                                                       int dims, float eps) {
+    extern __shared__ __align__(16) uint16_t srow[];
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * 4 + wid;
+    uint16_t* xs = srow + wid * dims;
+    const bool active = row < rows;
+    const uint16_t* x = X + row * dims;
+    if (active)
+        for (int i = lane; i < dims; i += 64) xs[i] = x[i];
+    __syncthreads();
+    float ss = 0.0f;
+    float chain = 0.0f;
+    const int n16 = dims / 16;
+    const int end8 = (dims / 8) * 8;
+    if (active && lane < 16) {
+        for (int i = 0; i < n16; i++) {
+            const float a = h2f(xs[i * 16 + lane]);
+            chain = __builtin_fmaf(a, a, chain);
+        }
+        if (lane < 8 && n16 * 16 + 8 <= dims) {
+            const float a = h2f(xs[n16 * 16 + lane]);
+            chain = __builtin_fmaf(a, a, chain);
+        }
+    }
+    const float c4 = __shfl(chain, (lane + 4) & 63, 64);
+    const float c8 = __shfl(chain, (lane + 8) & 63, 64);
+    const float c12 = __shfl(chain, (lane + 12) & 63, 64);
+    const float t = ((chain + c4) + c8) + c12;
+    const float t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    const float t0 = __shfl(t, 0, 64);
+    ss = (t0 + t1) + (t2 + t3);
+    for (int k = end8; k < dims; k++) {
+        const float a = h2f(xs[k]);
+        ss = __builtin_fmaf(a, a, ss);
+    }
+    const float rms = __builtin_sqrtf(ss / (float)dims + eps);
+    const float inv = 1.0f / rms;
+    const uint16_t hinv = f2h(inv);
+    if (active) {
+        uint16_t* y = Y + row * dims;
+        for (int i = lane; i < dims; i += 64) {
+            if (i < end8) y[i] = hmul(hmul(xs[i], hinv), W[i]);
+            else y[i] = f2h((h2f(xs[i]) * inv) * h2f(W[i]));
+        }
+    }
+}
+
+// ---------------------------------------------------------------- RoPE
+struct RopeTable {
+    uint16_t* cos_d = nullptr;
+    uint16_t* sin_d = nullptr;
+    size_t npos = 0;
+};
+static std::mutex g_rope_mu;
+static std::map<std::tuple<int, size_t, uint32_t>, RopeTable> g_rope;
+
+// Table of precompute_rope_tables_f16 (kernel_attention.cpp:588-612), built
+// on the host with the host libm and uploaded.  Tables only grow; a replaced
+// table stays allocated because queued kernels may still read it.
+static int rope_table(size_t npos, size_t d, float theta, const RopeTable** out) {
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    uint32_t tb;
+    memcpy(&tb, &theta, 4);
+    std::lock_guard<std::mutex> lk(g_rope_mu);
+    RopeTable& t = g_rope[std::make_tuple(dev, d, tb)];
+    if (t.npos < npos) {
+        size_t want = t.npos * 2 > npos ? t.npos * 2 : npos;
+        if (want < 256) want = 256;
+        const size_t half = d / 2;
+        std::vector<uint16_t> hc(want * half), hs(want * half);
+        for (size_t p = 0; p < want; p++) {
+            const float pf = (float)p;
+            for (size_t i = 0; i < half; i++) {
+                const float freq = 1.0f / powf(theta, (2.0f * (float)i) / (float)d);
+                const float ang = pf * freq;
+                const float c = cosf(ang), s = sinf(ang);
+                hc[p * half + i] = host_f2h(c);
+                hs[p * half + i] = host_f2h(s);
+            }
+        }
+        RopeTable nt;
+        CH_HIP(hipMalloc(&nt.cos_d, hc.size() * 2 + 2));
+        CH_HIP(hipMalloc(&nt.sin_d, hs.size() * 2 + 2));
+        CH_HIP(hipMemcpy(nt.cos_d, hc.data(), hc.size() * 2, hipMemcpyHostToDevice));
+        CH_HIP(hipMemcpy(nt.sin_d, hs.data(), hs.size() * 2, hipMemcpyHostToDevice));
+        nt.npos = want;
+        t = nt;  // previous buffers intentionally kept (see above)
+    }
+    *out = &t;
+    return CACTUS_HIP_OK;
+}
+
+__global__ void rope_kernel(const uint16_t* __restrict__ X, uint16_t* __restrict__ Y,
+                            const uint16_t* __restrict__ ct, const uint16_t* __restrict__ st,
+                            size_t total_pairs, int S, int H, int d, size_t start_pos) {
+    const int half = d / 2;
+    const int vh = (half / 8) * 8;
+    for (size_t p = (size_t)blockIdx.x * blockDim.x + threadIdx.x; p < total_pairs;
+         p += (size_t)gridDim.x * blockDim.x) {
+        const int i = (int)(p % half);
+        const size_t rowi = p / half;               // (b*S + s)*H + h
+        const int s = (int)((rowi / H) % S);
+        const size_t off = rowi * d;
+        const size_t toff = (start_pos + s) * half + i;
+        const uint16_t c = ct[toff], sn = st[toff];
+        const uint16_t x1 = X[off + i], x2 = X[off + i + half];
+        if (i < vh) {
+            Y[off + i] = hfma(x2 ^ 0x8000u, sn, hmul(x1, c));
+            Y[off + i + half] = hfma(x1, sn, hmul(x2, c));
+        } else {
+            const float a = h2f(x1), b = h2f(x2), cf = h2f(c), sf = h2f(sn);
+            Y[off + i] = f2h(a * cf - b * sf);
+            Y[off + i + half] = f2h(b * cf + a * sf);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- softmax
+// One workgroup per row.  Max is order-free; the sum runs the reference's
+// 32 fp32 chains (element i -> sum_vec[(i%32)/4] lane i%4, kernel_nn.cpp:
+// 191-214), combined sequentially over the 8 vectors then pairwise over lanes.
+__global__ void __launch_bounds__(256) softmax_kernel(const uint16_t* __restrict__ X,
+                                                      uint16_t* __restrict__ Y, int V) {
+    __shared__ float red[4];
+    __shared__ float chains[32];
+    const size_t row = blockIdx.x;
+    const uint16_t* x = X + row * (size_t)V;
+    uint16_t* y = Y + row * (size_t)V;
+    const int tid = threadIdx.x;
+    float m = -__builtin_inff();
+    for (int i = tid; i < V; i += 256) m = __builtin_fmaxf(m, h2f(x[i]));
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const int vv = (V / 32) * 32;
+    for (int i = tid; i < vv; i += 256) y[i] = f2h(fast_exp(h2f(x[i]) - mx));
+    for (int i = vv + tid; i < V; i += 256) y[i] = f2h(cactus_expf(h2f(x[i]) - mx));
+    if (tid < 32) {
+        float s = 0.0f;
+        for (int i = tid; i < vv; i += 32) s = s + fast_exp(h2f(x[i]) - mx);
+        chains[tid] = s;
+    }
+    __syncthreads();
+    float sum = 0.0f;
+    {
+        float t[4];
+        for (int l = 0; l < 4; l++) {
+            float a = chains[l];
+            for (int u = 1; u < 8; u++) a = a + chains[u * 4 + l];
+            t[l] = a;
+        }
+        sum = (t[0] + t[1]) + (t[2] + t[3]);
+        for (int i = vv; i < V; i++) sum = sum + cactus_expf(h2f(x[i]) - mx);
+    }
+    const float inv = 1.0f / sum;
+    const uint16_t hinv = f2h(inv);
+    __syncthreads();  // all fp16 exps written before they are rescaled
+    for (int i = tid; i < vv; i += 256) y[i] = hmul(y[i], hinv);
+    for (int i = vv + tid; i < V; i += 256) y[i] = f2h(h2f(y[i]) * inv);
+}
+
+// ---------------------------------------------------------------- SiLU, add, mul
+__global__ void silu_kernel(const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, size_t n) {
+    const size_t body = (n / 8) * 8;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const float x = h2f(X[i]);
+        const float e = (i < body) ? fast_exp(-x) : cactus_expf(-x);
+        const float sig = 1.0f / (1.0f + e);
+        Y[i] = f2h(x * sig);
+    }
+}
+
+__global__ void add_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                           uint16_t* __restrict__ Y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        Y[i] = hadd(A[i], B[i]);
+}
+
+__global__ void mul_kernel(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+                           uint16_t* __restrict__ Y, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        Y[i] = hmul(A[i], B[i]);
+}
+
+// ---------------------------------------------------------------- embedding
+__global__ void embedding_kernel(const uint16_t* __restrict__ table, const float* __restrict__ ids,
+                                 uint16_t* __restrict__ out, size_t n, int hidden, size_t vocab,
+                                 int* err) {
+    const size_t row = blockIdx.x;
+    if (row >= n) return;
+    const float f = ids[row];
+    const bool ok = (f >= 0.0f) && (f < (float)vocab) && ((size_t)f < vocab);
+    uint16_t* o = out + row * (size_t)hidden;
+    if (!ok) {
+        for (int j = threadIdx.x; j < hidden; j += blockDim.x) o[j] = 0;
+        if (err && threadIdx.x == 0) *err = 1;
+        return;
+    }
+    const uint16_t* src = table + (size_t)f * hidden;
+    for (int j = threadIdx.x; j < hidden; j += blockDim.x) o[j] = src[j];
+}
+
+// ---------------------------------------------------------------- greedy sample
+// First index of the maximum of (float)logit (kernel_nn.cpp:451-466): each
+// thread scans an increasing index range keeping a strict '>' winner; the
+// combine takes the larger value and, on equal values, the smaller index.
+__global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* __restrict__ L, size_t V,
+                                                      uint32_t* out) {
+    __shared__ float bv_s[1024];
+    __shared__ uint32_t bi_s[1024];
+    const int tid = threadIdx.x;
+    const size_t per = (V + 1023) / 1024;
+    const size_t s0 = tid * per;
+    const size_t s1 = (s0 + per < V) ? s0 + per : V;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu;
+    for (size_t i = s0; i < s1; i++) {
+        const float v = h2f(L[i]);
+        if (bi == 0xFFFFFFFFu || v > bv) { bv = v; bi = (uint32_t)i; }
+    }
+    bv_s[tid] = bv;
+    bi_s[tid] = bi;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (tid < w) {
+            const float ov = bv_s[tid + w];
+            const uint32_t oi = bi_s[tid + w];
+            const float mv = bv_s[tid];
+            const uint32_t mi = bi_s[tid];
+            bool take;
+            if (oi == 0xFFFFFFFFu) take = false;
+            else if (mi == 0xFFFFFFFFu) take = true;
+            else take = (ov > mv) || (ov == mv && oi < mi);
+            if (take) { bv_s[tid] = ov; bi_s[tid] = oi; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) *out = (bi_s[0] == 0xFFFFFFFFu) ? 0u : bi_s[0];
+}
+
+static unsigned grid_for(size_t n, unsigned block) {
+    size_t g = (n + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > 65535) g = 65535;
+    return (unsigned)g;
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+extern "C" {
+
+int cactus_hip_rms_norm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t rows,
+                            size_t dims, float eps, void* stream) {
+    if (rows == 0 || dims == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && w && y, "rms_norm: null pointer");
+    CH_REQUIRE(dims <= (size_t)RMS_MAX_DIMS, "rms_norm: dims > 8192 not supported");
+    CH_REQUIRE(rows < (1ull << 33), "rms_norm: too many rows");
+    const size_t smem = 4 * dims * sizeof(uint16_t);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(ceil_div(rows, 4)), dim3(256), smem, as_stream(stream),
+                       x, w, y, rows, (int)dims, eps);
+    return check_launch("rms_norm");
+}
+
+int cactus_hip_rope_reserve(size_t max_pos, size_t head_dim, float theta) {
+    CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope: head_dim must be even");
+    const RopeTable* t = nullptr;
+    return rope_table(max_pos, head_dim, theta, &t);
+}
+
+int cactus_hip_rope_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq_len,
+                        size_t num_heads, size_t head_dim, size_t start_pos, float theta,
+                        void* stream) {
+    if (batch == 0 || seq_len == 0 || num_heads == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && y, "rope: null pointer");
+    CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim < (1u << 16),
+               "rope: head_dim must be even");
+    const RopeTable* t = nullptr;
+    int rc = rope_table(seq_len + start_pos, head_dim, theta, &t);
+    if (rc) return rc;
+    const size_t pairs = batch * seq_len * num_heads * (head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, as_stream(stream), x,
+                       y, t->cos_d, t->sin_d, pairs, (int)seq_len, (int)num_heads, (int)head_dim,
+                       start_pos);
+    return check_launch("rope");
+}
+
+int cactus_hip_softmax_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq_len,
+                           size_t vocab, void* stream) {
+    const size_t rows = batch * seq_len;
+    if (rows == 0 || vocab == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && y, "softmax: null pointer");
+    CH_REQUIRE(vocab < (1u << 30) && rows < (1u << 31), "softmax: shape too large");
+    hipLaunchKernelGGL(softmax_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), x, y,
+                       (int)vocab);
+    return check_launch("softmax");
+}
+
+int cactus_hip_silu_f16(const uint16_t* x, uint16_t* y, size_t n, void* stream) {
+    if (n == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && y, "silu: null pointer");
+    hipLaunchKernelGGL(silu_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), x, y, n);
+    return check_launch("silu");
+}
+
+int cactus_hip_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n, void* stream) {
+    if (n == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(a && b && y, "add: null pointer");
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), a, b, y, n);
+    return check_launch("add");
+}
+
+int cactus_hip_multiply_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n,
+                            void* stream) {
+    if (n == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(a && b && y, "multiply: null pointer");
+    hipLaunchKernelGGL(mul_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), a, b, y, n);
+    return check_launch("multiply");
+}
+
+int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* out,
+                             size_t num_ids, size_t hidden, size_t vocab, int* error_flag,
+                             void* stream) {
+    if (num_ids == 0 || hidden == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(table && ids && out, "embedding: null pointer");
+    CH_REQUIRE(num_ids <= 0x7FFFFFFF && hidden < (1u << 30), "embedding: shape too large");
+    hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)num_ids), dim3(256), 0, as_stream(stream),
+                       table, ids, out, num_ids, (int)hidden, vocab, error_flag);
+    return check_launch("embedding");
+}
+
+int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, float temperature,
+                          float top_p, size_t top_k, size_t random_seed, void* stream) {
+    (void)random_seed;
+    CH_REQUIRE(out, "sample: null output");
+    if (!(temperature == 0.0f && top_p <= 0.0f && top_k == 0))
+        return fail(CACTUS_HIP_EUNSUPPORTED,
+                    "sample: only greedy decoding (temperature=0, top_p<=0, top_k=0) is built");
+    CH_REQUIRE(vocab == 0 || logits, "sample: null logits");
+    if (vocab == 0) return cactus_hip_memset(out, 0, 4, stream);
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
+    return check_launch("sample");
+}
+
+}  // extern "C"

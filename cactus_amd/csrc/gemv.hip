@@ -1,0 +1,316 @@
+// gemv.hip -- grouped INT8 / packed-INT4 matmul for small M (decode GEMV).
+//
+// Weights are streamed as a flat run of 16-byte chunks: one workgroup owns
+// `rows` consecutive weight rows ([rows][K] int8, or [rows][K/2] packed INT4),
+// so its loads are fully coalesced whatever K is.  Each chunk is dotted with
+// the int8 activation codes held in LDS (v_dot4_i32_i8); the lanes that share
+// one quantization group are summed exactly in int32 with cross-lane shuffles
+// and the group sum goes to LDS.  One thread per output then runs the
+// reference epilogue (kernel_gemm.cpp:311-324):
+//     r = fma((float)acc_g, (float)B_scale[n][g], r)   for g = 0..G-1
+//     C = fp16(r * A_scale[m])
+// With an FP16 activation input the per-row quantization of
+// graph_ops_nn.cpp:35-66 runs in the workgroup prologue (every workgroup
+// recomputes it from L2; it is a K-element pass against rows*K weight bytes).
+#include "quant_device.h"
+
+namespace cactus_hip {
+
+struct GemvArgs {
+    const uint16_t* A16;    // fp16 activations [M][K]      (F16ACT)
+    const int8_t* A8;       // int8 codes [M][K]             (!F16ACT)
+    const float* As;        // row scales [M]                (!F16ACT)
+    const uint8_t* B;       // weights, int8 [N][K] or packed int4 [N][K/2]
+    const uint16_t* Bs;     // fp16 group scales [N][G]
+    uint16_t* C;            // fp16 out [M][N]
+    int M, K, N, gs, rows;
+    size_t sA, sB, sBs, sC; // batch strides: elements of A/Bs/C, bytes of B
+};
+
+constexpr int GEMV_THREADS = 256;
+
+// position of activation element i in LDS; INT4 stores each 8-element run as
+// its 4 even elements followed by its 4 odd elements so that one dword pairs
+// with the low nibbles and the next with the high nibbles of a weight dword
+template <bool INT4>
+__device__ __forceinline__ int act_pos(int i) {
+    if (!INT4) return i;
+    const int j = i & 7;
+    return (i & ~7) + ((j & 1) ? 4 : 0) + (j >> 1);
+}
+
+// dot product of one 16-byte weight chunk with the matching activation codes
+template <bool INT4>
+__device__ __forceinline__ int chunk_dot(const int8_t* act, int col, i32x4 w) {
+    int s = 0;
+    if (!INT4) {
+        const i32x4 av = *reinterpret_cast<const i32x4*>(act + col * 16);
+        s = __builtin_amdgcn_sdot4(av.x, w.x, s, false);
+        s = __builtin_amdgcn_sdot4(av.y, w.y, s, false);
+        s = __builtin_amdgcn_sdot4(av.z, w.z, s, false);
+        s = __builtin_amdgcn_sdot4(av.w, w.w, s, false);
+    } else {
+        const i32x4* ap = reinterpret_cast<const i32x4*>(act + col * 32);
+        const i32x4 a0 = ap[0], a1 = ap[1];
+        const uint32_t wv[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
+        const int ae[4] = {a0.x, a0.z, a1.x, a1.z};
+        const int ao[4] = {a0.y, a0.w, a1.y, a1.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            // nibbles moved to the top of each byte: 16 * code
+            const int lo = (int)((wv[j] << 4) & 0xF0F0F0F0u);
+            const int hi = (int)(wv[j] & 0xF0F0F0F0u);
+            s = __builtin_amdgcn_sdot4(ae[j], lo, s, false);
+            s = __builtin_amdgcn_sdot4(ao[j], hi, s, false);
+        }
+        s >>= 4;  // exact: every product carried a factor 16
+    }
+    return s;
+}
+
+// CH: 16-byte weight chunks each thread loads before the activation
+// prologue, so the weight stream is in flight while the row is quantized.
+template <int MR, bool F16ACT, bool INT4, int CH>
+__global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, int m0) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = a.K, gs = a.gs, G = K / gs;
+    const int rows = a.rows;
+    const int n0 = blockIdx.x * rows;
+    const int nr = min(rows, a.N - n0);
+    const size_t bi = blockIdx.y;
+    const int mr = min(MR, a.M - m0);
+    const int tid = threadIdx.x;
+
+    int8_t* actq = reinterpret_cast<int8_t*>(smem);                       // MR*K
+    int32_t* acc = reinterpret_cast<int32_t*>(smem + ((MR * K + 15) & ~15)); // MR*rows*G
+    uint16_t* scl = reinterpret_cast<uint16_t*>(acc + MR * rows * G);     // rows*G
+    float* rsc = reinterpret_cast<float*>(scl + ((rows * G + 1) & ~1));  // MR
+    float* red = rsc + MR;                                                // 4
+
+    const int cpr = INT4 ? K / 32 : K / 16;       // 16-byte chunks per row
+    const int P = INT4 ? gs / 32 : gs / 16;       // chunks per group (power of 2)
+    const int total = nr * cpr;
+    const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
+    const uint8_t* Bw = a.B + bi * a.sB + (size_t)n0 * row_bytes;
+
+    // 1. weight stream first (streaming data: non-temporal loads)
+    i32x4 wreg[CH];
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + i * GEMV_THREADS;
+        wreg[i] = (i32x4){0, 0, 0, 0};
+        if (c < total)
+            wreg[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                Bw + (size_t)(c / cpr) * row_bytes + (size_t)(c % cpr) * 16));
+    }
+
+    // 2. group scales of this workgroup's rows (contiguous) and activation codes
+    const uint16_t* Bs = a.Bs + bi * a.sBs + (size_t)n0 * G;
+    for (int i = tid; i < nr * G; i += GEMV_THREADS) scl[i] = Bs[i];
+    const int body = (K / 8) * 8;
+    for (int m = 0; m < mr; m++) {
+        if (F16ACT) {
+            const uint16_t* x = a.A16 + bi * a.sA + (size_t)(m0 + m) * K;
+            const float mx = block_max_abs_f16(x, K, red);
+            const float s = row_scale_from_max(mx);
+            const float inv = 1.0f / s;
+            for (int i = tid; i < K; i += GEMV_THREADS)
+                actq[m * K + act_pos<INT4>(i)] = quant_code(h2f(x[i]), inv, i >= body);
+            if (tid == 0) rsc[m] = s;
+        } else {
+            const int8_t* x = a.A8 + bi * a.sA + (size_t)(m0 + m) * K;
+            for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + act_pos<INT4>(i)] = x[i];
+            if (tid == 0) rsc[m] = a.As[bi * (a.sA / K) + m0 + m];
+        }
+    }
+    __syncthreads();
+
+    // 3. dot products; the P lanes of one group are summed exactly in int32
+    auto consume = [&](int c, const i32x4& w) {
+        const bool valid = c < total;
+        const int r = valid ? c / cpr : 0;
+        const int col = valid ? c % cpr : 0;
+        int dot[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++)
+            dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, col, w) : 0;
+        for (int off = 1; off < P; off <<= 1) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) dot[m] += __shfl_xor(dot[m], off, 64);
+        }
+        if (valid && (c & (P - 1)) == 0) {
+            const int g = (col * (INT4 ? 32 : 16)) / gs;
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                if (m < mr) acc[(m * rows + r) * G + g] = dot[m];
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < CH; i++) consume(tid + i * GEMV_THREADS, wreg[i]);
+    for (int base = CH * GEMV_THREADS; base < total; base += GEMV_THREADS) {
+        const int c = base + tid;
+        i32x4 w = (i32x4){0, 0, 0, 0};
+        if (c < total)
+            w = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                Bw + (size_t)(c / cpr) * row_bytes + (size_t)(c % cpr) * 16));
+        consume(c, w);
+    }
+    __syncthreads();
+
+    // 4. reference epilogue, one thread per output
+    for (int t = tid; t < mr * nr; t += GEMV_THREADS) {
+        const int m = t / nr, r = t % nr;
+        const int32_t* ag = acc + (m * rows + r) * G;
+        const uint16_t* sg = scl + r * G;
+        float rs = 0.0f;
+        for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+        a.C[bi * a.sC + (size_t)(m0 + m) * a.N + n0 + r] = f2h(rs * rsc[m]);
+    }
+}
+
+static size_t gemv_smem(int MR, int K, int rows, int G) {
+    size_t s = (size_t)((MR * K + 15) & ~15);
+    s += (size_t)MR * rows * G * 4;
+    s += (size_t)((rows * G + 1) & ~1) * 2;
+    s += (size_t)MR * 4 + 16;
+    return s;
+}
+
+template <int MR, bool F16ACT, bool INT4, int CH>
+static int launch_gemv_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st) {
+    dim3 grid(ceil_div(a.N, a.rows), (unsigned)batch);
+    hipLaunchKernelGGL((gemv_grouped_kernel<MR, F16ACT, INT4, CH>), grid, dim3(GEMV_THREADS), smem,
+                       st, a, m0);
+    return check_launch("gemv_grouped");
+}
+
+template <int MR, bool F16ACT, bool INT4>
+static int launch_gemv_ch(const GemvArgs& a, size_t batch, int m0, size_t smem, int ch,
+                          hipStream_t st) {
+    switch (ch) {
+        case 1: return launch_gemv_t<MR, F16ACT, INT4, 1>(a, batch, m0, smem, st);
+        case 2: return launch_gemv_t<MR, F16ACT, INT4, 2>(a, batch, m0, smem, st);
+        case 4: return launch_gemv_t<MR, F16ACT, INT4, 4>(a, batch, m0, smem, st);
+        default: return launch_gemv_t<MR, F16ACT, INT4, 8>(a, batch, m0, smem, st);
+    }
+}
+
+template <bool F16ACT, bool INT4>
+static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
+    const int G = a.K / a.gs;
+    const int cpr = INT4 ? a.K / 32 : a.K / 16;
+    const int MR = a.M >= 4 ? 4 : (a.M >= 2 ? 2 : 1);
+    // as many rows as 8 prefetched chunks per thread cover, then fewer while
+    // the grid would leave CUs idle (256 CUs, aim for >= 4 workgroups each)
+    int rows = (8 * GEMV_THREADS) / cpr;
+    if (rows < 1) rows = 1;
+    if (rows > a.N) rows = a.N;
+    while (rows > 1 && (size_t)ceil_div(a.N, rows) * batch < 1024) rows = (rows + 1) / 2;
+    while (rows > 1 && gemv_smem(MR, a.K, rows, G) > 60 * 1024) rows = (rows + 1) / 2;
+    if (gemv_smem(MR, a.K, rows, G) > 60 * 1024)
+        return fail(CACTUS_HIP_EUNSUPPORTED, "grouped matmul: K too large for the GEMV path");
+    const int chunks = (rows * cpr + GEMV_THREADS - 1) / GEMV_THREADS;
+    const int ch = chunks <= 1 ? 1 : chunks <= 2 ? 2 : chunks <= 4 ? 4 : 8;
+    a.rows = rows;
+    const size_t smem = gemv_smem(MR, a.K, rows, G);
+    for (int m0 = 0; m0 < a.M; m0 += MR) {
+        int rc;
+        if (MR == 4) rc = launch_gemv_ch<4, F16ACT, INT4>(a, batch, m0, smem, ch, st);
+        else if (MR == 2) rc = launch_gemv_ch<2, F16ACT, INT4>(a, batch, m0, smem, ch, st);
+        else rc = launch_gemv_ch<1, F16ACT, INT4>(a, batch, m0, smem, ch, st);
+        if (rc) return rc;
+    }
+    return CACTUS_HIP_OK;
+}
+
+static bool is_pow2(size_t v) { return v && !(v & (v - 1)); }
+
+int check_grouped_shape(size_t M, size_t K, size_t N, size_t gs, bool int4) {
+    CH_REQUIRE(gs > 0 && K % gs == 0, "grouped matmul: group_size must divide K");
+    CH_REQUIRE(is_pow2(gs) && gs >= (int4 ? 32u : 16u) && gs <= (int4 ? 2048u : 1024u),
+               "grouped matmul: group_size must be a power of two in [16,1024] (INT8) or "
+               "[32,2048] (INT4)");
+    CH_REQUIRE(M < (1u << 30) && K < (1u << 20) && N < (1u << 30), "grouped matmul: shape too large");
+    return CACTUS_HIP_OK;
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+// Internal dispatch shared with the MFMA prefill path (gemm.hip).
+namespace cactus_hip {
+int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
+                      const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
+                      bool int4, hipStream_t st, bool* handled);
+
+static int grouped_dispatch(const uint16_t* A16, const int8_t* A8, const float* As,
+                            const uint8_t* B, const uint16_t* Bs, uint16_t* C, size_t M, size_t K,
+                            size_t N, size_t gs, bool int4, hipStream_t st) {
+    if (M == 0 || K == 0 || N == 0) return CACTUS_HIP_OK;
+    int rc = check_grouped_shape(M, K, N, gs, int4);
+    if (rc) return rc;
+    CH_REQUIRE(B && Bs && C && (A16 || (A8 && As)), "grouped matmul: null pointer");
+    CH_REQUIRE(((uintptr_t)B & 15) == 0, "grouped matmul: weights must be 16-byte aligned");
+    bool handled = false;
+    rc = gemm_grouped_mfma(A16, A8, As, B, Bs, C, M, K, N, gs, int4, st, &handled);
+    if (rc || handled) return rc;
+    GemvArgs a{};
+    a.A16 = A16; a.A8 = A8; a.As = As; a.B = B; a.Bs = Bs; a.C = C;
+    a.M = (int)M; a.K = (int)K; a.N = (int)N; a.gs = (int)gs;
+    a.sA = M * K; a.sB = 0; a.sBs = 0; a.sC = 0;
+    if (A16) return int4 ? launch_gemv<true, true>(a, 1, st) : launch_gemv<true, false>(a, 1, st);
+    return int4 ? launch_gemv<false, true>(a, 1, st) : launch_gemv<false, false>(a, 1, st);
+}
+}  // namespace cactus_hip
+
+extern "C" {
+
+int cactus_hip_matmul_int8(const int8_t* A, const float* A_scales, const int8_t* B,
+                           const uint16_t* B_scales, uint16_t* C, size_t M, size_t K, size_t N,
+                           size_t group_size, void* stream) {
+    return grouped_dispatch(nullptr, A, A_scales, reinterpret_cast<const uint8_t*>(B), B_scales, C,
+                            M, K, N, group_size, false, as_stream(stream));
+}
+
+int cactus_hip_matmul_int4(const int8_t* A, const float* A_scales, const uint8_t* B_packed,
+                           const uint16_t* B_scales, uint16_t* C, size_t M, size_t K, size_t N,
+                           size_t group_size, void* stream) {
+    return grouped_dispatch(nullptr, A, A_scales, B_packed, B_scales, C, M, K, N, group_size, true,
+                            as_stream(stream));
+}
+
+int cactus_hip_matmul_int8_f16act(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                  uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,
+                                  void* stream) {
+    return grouped_dispatch(A, nullptr, nullptr, reinterpret_cast<const uint8_t*>(B), B_scales, C,
+                            M, K, N, group_size, false, as_stream(stream));
+}
+
+int cactus_hip_matmul_int4_f16act(const uint16_t* A, const uint8_t* B_packed,
+                                  const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
+                                  size_t N, size_t group_size, void* stream) {
+    return grouped_dispatch(A, nullptr, nullptr, B_packed, B_scales, C, M, K, N, group_size, true,
+                            as_stream(stream));
+}
+
+int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,
+                                          const uint16_t* B_scales, uint16_t* C, size_t M,
+                                          size_t K, size_t N, size_t group_size, size_t batch,
+                                          size_t stride_a, size_t stride_b, size_t stride_bs,
+                                          size_t stride_c, void* stream) {
+    if (M == 0 || K == 0 || N == 0 || batch == 0) return CACTUS_HIP_OK;
+    int rc = check_grouped_shape(M, K, N, group_size, false);
+    if (rc) return rc;
+    CH_REQUIRE(A && B && B_scales && C, "matmul_int8_f16act_batched: null pointer");
+    CH_REQUIRE(batch <= 65535, "matmul_int8_f16act_batched: batch must be <= 65535");
+    CH_REQUIRE(((uintptr_t)B & 15) == 0 && stride_b % 16 == 0,
+               "matmul_int8_f16act_batched: weights must be 16-byte aligned");
+    GemvArgs a{};
+    a.A16 = A; a.B = reinterpret_cast<const uint8_t*>(B); a.Bs = B_scales; a.C = C;
+    a.M = (int)M; a.K = (int)K; a.N = (int)N; a.gs = (int)group_size;
+    a.sA = stride_a; a.sB = stride_b; a.sBs = stride_bs; a.sC = stride_c;
+    return launch_gemv<true, false>(a, batch, as_stream(stream));
+}
+
+}  // extern "C"

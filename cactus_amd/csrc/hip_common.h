@@ -1,0 +1,187 @@
+// hip_common.h -- shared device helpers and host-side error plumbing for the
+// gfx950 kernel library.  Compiled with -ffp-contract=off: every fused
+// multiply-add below is written explicitly, matching where the reference
+// fuses; every other fp operation rounds on its own.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+#include <string>
+#include <cstring>
+
+#include "../../include/cactus_hip.h"
+
+namespace cactus_hip {
+
+// ----------------------------------------------------------------- host side
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+#define CH_REQUIRE(cond, msg)                                                   \
+    do {                                                                        \
+        if (!(cond)) return ::cactus_hip::fail(CACTUS_HIP_EINVAL, msg);         \
+    } while (0)
+
+#define CH_HIP(call)                                                            \
+    do {                                                                        \
+        hipError_t e_ = (call);                                                 \
+        if (e_ != hipSuccess)                                                   \
+            return ::cactus_hip::fail(CACTUS_HIP_ERUNTIME,                      \
+                                      std::string(#call) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+// fp32 -> fp16 bit pattern on the host: round to nearest even with one
+// rounding step (subnormals, overflow to inf, quiet NaN).  Used for tables
+// built on the host.
+inline uint16_t host_f2h(float f) {
+    const double d = (double)f;  // exact
+    uint64_t b;
+    memcpy(&b, &d, 8);
+    const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    const uint64_t a = b & 0x7FFFFFFFFFFFFFFFull;
+    const int e = (int)(a >> 52);
+    if (e == 0x7FF) return sign | ((a & 0xFFFFFFFFFFFFFull) ? 0x7E00 : 0x7C00);
+    if (a == 0) return sign;
+    const uint64_t mant = (a & 0xFFFFFFFFFFFFFull) | (1ull << 52);  // f is normal as a double
+    const int ex = e - 1023;
+    if (ex > 15) return sign | 0x7C00;
+    const int shift = ex >= -14 ? 42 : 42 + (-14 - ex);
+    if (shift > 63) return sign;
+    uint64_t q = mant >> shift;
+    const uint64_t rem = mant & ((1ull << shift) - 1);
+    const uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    const uint32_t r = ex >= -14 ? ((uint32_t)(ex + 15) << 10) + (uint32_t)(q - 1024) : (uint32_t)q;
+    if (r >= 0x7C00) return sign | 0x7C00;
+    return sign | (uint16_t)r;
+}
+
+// --------------------------------------------------------------- device side
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(f16, h); }
+// fp32 -> fp16, round to nearest even, applied to an already-rounded fp32
+// value.  The empty asm keeps the compiler from folding the producing fp32
+// multiply/add into v_fma_mixlo_f16, which would round only once (to fp16)
+// where the reference rounds twice (to fp32, then to fp16).
+__device__ __forceinline__ float fp32_barrier(float f) {
+    asm volatile("" : "+v"(f));
+    return f;
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (f16)fp32_barrier(f));
+}
+__device__ __forceinline__ f16 hbits(uint16_t h) { return __builtin_bit_cast(f16, h); }
+__device__ __forceinline__ uint16_t bitsh(f16 h) { return __builtin_bit_cast(uint16_t, h); }
+// native fp16 ops: one IEEE rounding each (v_add_f16 / v_mul_f16 / v_fma_f16)
+__device__ __forceinline__ uint16_t hadd(uint16_t a, uint16_t b) { return bitsh(hbits(a) + hbits(b)); }
+__device__ __forceinline__ uint16_t hmul(uint16_t a, uint16_t b) { return bitsh(hbits(a) * hbits(b)); }
+__device__ __forceinline__ uint16_t hfma(uint16_t a, uint16_t b, uint16_t c) {
+    return bitsh(__builtin_fmaf16(hbits(a), hbits(b), hbits(c)));
+}
+
+__device__ __forceinline__ float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+// NEON vcvtq_s32_f32: truncate toward zero, saturating, NaN -> 0
+__device__ __forceinline__ int32_t cvt_trunc_sat(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)x;
+}
+// NEON vcvtnq_s32_f32: round to nearest even, saturating, NaN -> 0
+__device__ __forceinline__ int32_t cvt_rne_sat(float x) {
+    if (x != x) return 0;
+    if (x >= 2147483648.0f) return INT32_MAX;
+    if (x <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)__builtin_rintf(x);
+}
+__device__ __forceinline__ int32_t sat8(int32_t v) { return v > 127 ? 127 : (v < -128 ? -128 : v); }
+__device__ __forceinline__ float exp2_bits(int32_t zi) {
+    return bits_f((uint32_t)((uint32_t)zi + 127u) << 23);
+}
+
+// expf used wherever the reference calls libm expf: x = k*ln2 + r (Cody-Waite,
+// two-part ln2), e^r by its degree-12 Taylor polynomial in double (Horner,
+// fused), one rounding to float.  Relative error of the double result is a
+// few 1e-16, so the float result is the correctly rounded e^x except when
+// e^x lies within ~1e-15 (relative) of a float rounding boundary.
+__device__ __forceinline__ float cactus_expf(float xf) {
+    if (xf != xf) return xf;
+    if (xf > 100.0f) return __builtin_inff();
+    if (xf < -110.0f) return 0.0f;
+    const double LN2_HI = 6.93147180369123816490e-01;
+    const double LN2_LO = 1.90821492927058770002e-10;
+    double x = (double)xf;
+    double k = __builtin_rint(x * 1.44269504088896338700e+00);
+    double r = __builtin_fma(-k, LN2_HI, x);
+    r = __builtin_fma(-k, LN2_LO, r);
+    double p = 1.0 / 479001600.0;
+    p = __builtin_fma(p, r, 1.0 / 39916800.0);
+    p = __builtin_fma(p, r, 1.0 / 3628800.0);
+    p = __builtin_fma(p, r, 1.0 / 362880.0);
+    p = __builtin_fma(p, r, 1.0 / 40320.0);
+    p = __builtin_fma(p, r, 1.0 / 5040.0);
+    p = __builtin_fma(p, r, 1.0 / 720.0);
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    uint64_t sb = (uint64_t)((int64_t)k + 1023) << 52;
+    return (float)(p * __builtin_bit_cast(double, sb));
+}
+
+// fast_exp_f32x4 lane (reference kernel_utils.h:108-141)
+__device__ __forceinline__ float fast_exp(float x) {
+    x = __builtin_fmaxf(x, -87.0f);
+    x = __builtin_fminf(x, 87.0f);
+    float z = x * 1.4426950408889634f;
+    int32_t zi = cvt_trunc_sat(z);
+    float zf = z - (float)zi;
+    if (zf < 0.0f) { zi -= 1; zf = zf + 1.0f; }
+    float u = zf * 0.6931471805599453f;
+    float p = 0.009618129842071803f;
+    p = __builtin_fmaf(p, u, 0.05550410866482158f);
+    p = __builtin_fmaf(p, u, 0.2402265069591007f);
+    p = __builtin_fmaf(p, u, 0.6931471805599453f);
+    p = __builtin_fmaf(p, u, 1.0f);
+    return p * exp2_bits(zi);
+}
+
+// second-order 2^x block weight of cactus_attention_f16
+// (reference kernel_attention.cpp:174-195); masked scores give 0
+__device__ __forceinline__ float poly_exp_weight(float s, float bm) {
+    if (s == -__builtin_inff()) return 0.0f;
+    float x = s - bm;
+    x = x * 1.442695f;
+    int32_t xi = cvt_trunc_sat(x);
+    float xf = x - (float)xi;
+    float y = __builtin_fmaf(xf, 0.6931472f, 1.0f);
+    float xf2 = xf * xf;
+    y = __builtin_fmaf(xf2, 0.2402265f, y);
+    return y * exp2_bits(xi);
+}
+
+// ---------------------------------------------------------- wave reductions
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+}  // namespace cactus_hip

@@ -1,0 +1,154 @@
+// quant.hip -- activation quantization (a1), KV-cache quantization (a7) and
+// INT4 unpacking.
+#include "quant_device.h"
+
+namespace cactus_hip {
+
+// One workgroup computes max|src| over the whole buffer.
+__global__ void __launch_bounds__(1024) max_abs_kernel(const uint16_t* __restrict__ src,
+                                                       size_t count, float* out) {
+    __shared__ float red[16];
+    float m = 0.0f;
+    for (size_t i = threadIdx.x; i < count; i += blockDim.x)
+        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(src[i])));
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float r = red[0];
+        for (unsigned i = 1; i < blockDim.x / 64; i++) r = __builtin_fmaxf(r, red[i]);
+        *out = r;
+    }
+}
+
+// cactus_fp16_to_int8 with a host-provided inv = 1.0f / scale.
+__global__ void fp16_to_int8_kernel(const uint16_t* __restrict__ src, int8_t* __restrict__ dst,
+                                    size_t count, float inv) {
+    const size_t body = (count / 8) * 8;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = quant_code(h2f(src[i]), inv, i >= body);
+}
+
+// One workgroup per row: scale and codes of quantize_activations_fp16_to_int8.
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x,
+                                                            int8_t* __restrict__ q,
+                                                            float* __restrict__ scales, int K) {
+    __shared__ float red[4];
+    const size_t row = blockIdx.x;
+    const uint16_t* xr = x + row * (size_t)K;
+    const float m = block_max_abs_f16(xr, K, red);
+    const float s = row_scale_from_max(m);
+    const float inv = 1.0f / s;
+    const int body = (K / 8) * 8;
+    int8_t* qr = q + row * (size_t)K;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) qr[i] = quant_code(h2f(xr[i]), inv, i >= body);
+    if (threadIdx.x == 0) scales[row] = s;
+}
+
+// cactus_quantize_kv_fp16_to_int8: one wave per (token, head, group).
+// Body codes: sat8(rne(x * inv)) without a clamp; the count%8 tail of a
+// group uses roundf (kernel_quants.cpp:223-264).
+__global__ void __launch_bounds__(256) quantize_kv_kernel(const uint16_t* __restrict__ src,
+                                                          int8_t* __restrict__ dst,
+                                                          float* __restrict__ scales,
+                                                          size_t rows, int d, int gs, int ng) {
+    const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63;
+    if (wave >= rows * (size_t)ng) return;
+    const size_t row = wave / ng;
+    const int g = (int)(wave % ng);
+    const int g0 = g * gs;
+    const int cnt = (gs < d - g0) ? gs : d - g0;
+    const uint16_t* s = src + row * d + g0;
+    int8_t* o = dst + row * d + g0;
+    float m = 0.0f;
+    for (int i = lane; i < cnt; i += 64) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(s[i])));
+    m = wave_max(m);
+    const float sc = row_scale_from_max(m);
+    const float inv = 1.0f / sc;
+    const int body = (cnt / 8) * 8;
+    for (int i = lane; i < cnt; i += 64) {
+        const float v = h2f(s[i]) * inv;
+        int32_t c = (i < body) ? cvt_rne_sat(v) : (int32_t)__builtin_roundf(v);
+        o[i] = (int8_t)sat8(c);
+    }
+    if (lane == 0) scales[row * ng + g] = sc;
+}
+
+__global__ void unpack_int4_kernel(const uint8_t* __restrict__ p, int8_t* __restrict__ u,
+                                   size_t count) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint8_t b = p[i >> 1];
+        int v = (i & 1) ? (b >> 4) : (b & 0x0F);
+        u[i] = (int8_t)(v > 7 ? v - 16 : v);
+    }
+}
+
+static unsigned grid_for(size_t n, unsigned block) {
+    size_t g = (n + block - 1) / block;
+    if (g < 1) g = 1;
+    if (g > 65535) g = 65535;
+    return (unsigned)g;
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+extern "C" {
+
+int cactus_hip_fp16_max_abs(const uint16_t* src, size_t count, float* out, void* stream) {
+    CH_REQUIRE(out, "fp16_max_abs: null output");
+    CH_REQUIRE(count == 0 || src, "fp16_max_abs: null input");
+    hipLaunchKernelGGL(max_abs_kernel, dim3(1), dim3(1024), 0, as_stream(stream), src, count, out);
+    return check_launch("fp16_max_abs");
+}
+
+int cactus_hip_fp16_to_int8(const uint16_t* src, int8_t* dst, size_t count, float scale,
+                            void* stream) {
+    if (count == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(src && dst, "fp16_to_int8: null pointer");
+    const float inv = 1.0f / scale;  // reference computes this once on the host side too
+    hipLaunchKernelGGL(fp16_to_int8_kernel, dim3(grid_for(count, 256)), dim3(256), 0,
+                       as_stream(stream), src, dst, count, inv);
+    return check_launch("fp16_to_int8");
+}
+
+int cactus_hip_quantize_activations(const uint16_t* x, int8_t* q, float* scales, size_t M,
+                                    size_t K, void* stream) {
+    if (M == 0 || K == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && q && scales, "quantize_activations: null pointer");
+    CH_REQUIRE(K < (1u << 30) && M < (1u << 31), "quantize_activations: shape too large");
+    hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x,
+                       q, scales, (int)K);
+    return check_launch("quantize_activations");
+}
+
+int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,
+                                        size_t seq_len, size_t kv_heads, size_t head_dim,
+                                        size_t group_size, void* stream) {
+    const size_t rows = seq_len * kv_heads;
+    if (rows == 0 || head_dim == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(src && dst && scales, "quantize_kv: null pointer");
+    CH_REQUIRE(group_size > 0, "quantize_kv: group_size must be > 0");
+    CH_REQUIRE(head_dim < (1u << 20), "quantize_kv: head_dim too large");
+    const int ng = (int)((head_dim + group_size - 1) / group_size);
+    const size_t waves = rows * (size_t)ng;
+    hipLaunchKernelGGL(quantize_kv_kernel, dim3(ceil_div(waves, 4)), dim3(256), 0,
+                       as_stream(stream), src, dst, scales, rows, (int)head_dim, (int)group_size,
+                       ng);
+    return check_launch("quantize_kv");
+}
+
+int cactus_hip_unpack_int4_to_int8(const uint8_t* packed, int8_t* unpacked, size_t count,
+                                   void* stream) {
+    if (count == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(packed && unpacked, "unpack_int4: null pointer");
+    hipLaunchKernelGGL(unpack_int4_kernel, dim3(grid_for(count, 256)), dim3(256), 0,
+                       as_stream(stream), packed, unpacked, count);
+    return check_launch("unpack_int4");
+}
+
+}  // extern "C"

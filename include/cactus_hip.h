@@ -1,0 +1,201 @@
+/*
+ * cactus_hip.h -- C ABI of the MI355X (gfx950) kernel layer.
+ *
+ * Each kernel entry point replaces one free function of the reference's
+ * kernel layer (cactus/kernel/kernel.h) or one graph node executor that
+ * wraps it (cactus/graph/graph_ops_nn.cpp); the citation on each
+ * declaration names the reference interface it stands in for.
+ *
+ * Conventions (differences from kernel.h are deliberate):
+ *   - fp16 values are passed as uint16_t bit patterns (IEEE binary16).
+ *   - Every tensor pointer is a DEVICE pointer unless stated otherwise;
+ *     memory is owned by the caller (cactus_hip_malloc or any HIP allocation).
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Kernels are
+ *     enqueued on it and the call returns without waiting, except the
+ *     memcpy_d2h / memcpy_h2d helpers, which wait for the copy.
+ *   - Every call returns 0 on success or a negative CACTUS_HIP_E* code;
+ *     cactus_hip_last_error() then holds a message for the calling thread.
+ *     Bad shapes are rejected on the host before anything is launched (the
+ *     reference kernels return silently on M|K|N == 0; so do these).
+ *   - Results are bit-identical to the reference's arithmetic where the
+ *     reference defines it (integer sums, quantized codes, fp16 roundings,
+ *     operation order); see the comment on each entry point.
+ */
+#ifndef CACTUS_HIP_H
+#define CACTUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CACTUS_HIP_OK              0
+#define CACTUS_HIP_EINVAL        (-1)   /* bad argument / shape */
+#define CACTUS_HIP_EUNSUPPORTED  (-2)   /* valid in the reference, not built here */
+#define CACTUS_HIP_ERUNTIME      (-3)   /* HIP runtime error */
+#define CACTUS_HIP_ENOMEM        (-4)
+
+/* ---------------------------------------------------------------- runtime */
+int         cactus_hip_init(int device);
+const char* cactus_hip_last_error(void);
+int         cactus_hip_device_count(int* count);
+int         cactus_hip_malloc(void** ptr, size_t bytes);
+int         cactus_hip_free(void* ptr);
+int         cactus_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int         cactus_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int         cactus_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int         cactus_hip_memset(void* dst, int byte_value, size_t bytes, void* stream);
+int         cactus_hip_stream_create(void** stream);
+int         cactus_hip_stream_destroy(void* stream);
+int         cactus_hip_stream_sync(void* stream);
+int         cactus_hip_event_create(void** event);
+int         cactus_hip_event_destroy(void* event);
+int         cactus_hip_event_record(void* event, void* stream);
+int         cactus_hip_event_elapsed_ms(void* start, void* end, float* ms);
+
+/* ------------------------------------------------ a1: activation quantization */
+/* cactus_fp16_max_abs (kernel/kernel.h:147, kernel_quants.cpp:196):
+ * writes max|src| as one float to *out (device). */
+int cactus_hip_fp16_max_abs(const uint16_t* src, size_t count, float* out, void* stream);
+/* cactus_fp16_to_int8 (kernel/kernel.h:146, kernel_quants.cpp:158):
+ * q = sat8(rne(clamp(x * (1/scale), -128, 127))); count%8 tail rounds ties away. */
+int cactus_hip_fp16_to_int8(const uint16_t* src, int8_t* dst, size_t count, float scale,
+                            void* stream);
+/* quantize_activations_fp16_to_int8 (graph/graph_ops_nn.cpp:35-66) and
+ * compute_quantize_activations_node (:78-127): per row m of x[M][K],
+ * scales[m] = max(max|x|/127, 1e-10), codes as cactus_fp16_to_int8. */
+int cactus_hip_quantize_activations(const uint16_t* x, int8_t* q, float* scales,
+                                    size_t M, size_t K, void* stream);
+
+/* ------------------------------------------------ a2/a3: grouped matmul */
+/* cactus_matmul_int8 (kernel/kernel.h:43, kernel_gemm.cpp:128-327):
+ *   C[m][n] = fp16( fma-chain over g ascending of (float)acc[m][n][g] * Bs[n][g]
+ *                   , times A_scales[m] )
+ * acc = exact int32 sum over group g of A[m][k]*B[n][k].
+ * A [M][K] int8, A_scales [M] f32, B [N][K] int8 (pretransposed),
+ * B_scales [N][K/group_size] fp16, C [M][N] fp16.  group_size must divide K
+ * and be a multiple of 16. */
+int cactus_hip_matmul_int8(const int8_t* A, const float* A_scales, const int8_t* B,
+                           const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
+                           size_t N, size_t group_size, void* stream);
+/* cactus_matmul_int4 (kernel/kernel.h:47, kernel_gemm.cpp:329-529): B_packed
+ * [N][K/2], byte n*K/2 + k/2 holds k even in the low nibble, k odd in the high
+ * nibble, two's-complement 4-bit.  group_size as above (multiple of 32). */
+int cactus_hip_matmul_int4(const int8_t* A, const float* A_scales, const uint8_t* B_packed,
+                           const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
+                           size_t N, size_t group_size, void* stream);
+/* compute_matmul_node with FP16 lhs (graph/graph_ops_nn.cpp:129-231): the
+ * activation quantization of cactus_hip_quantize_activations fused into the
+ * matmul; results identical to the unfused pair. */
+int cactus_hip_matmul_int8_f16act(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                  uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,
+                                  void* stream);
+int cactus_hip_matmul_int4_f16act(const uint16_t* A, const uint8_t* B_packed,
+                                  const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
+                                  size_t N, size_t group_size, void* stream);
+/* Strided-batched form of cactus_hip_matmul_int8_f16act: `batch` independent
+ * problems, problem i at A + i*stride_a, B + i*stride_b, B_scales +
+ * i*stride_bs, C + i*stride_c (strides in elements).  No reference
+ * counterpart: it lets one launch stream many distinct weight sets (layers,
+ * experts, or a cache-defeating rotation). */
+int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,
+                                          const uint16_t* B_scales, uint16_t* C, size_t M,
+                                          size_t K, size_t N, size_t group_size, size_t batch,
+                                          size_t stride_a, size_t stride_b, size_t stride_bs,
+                                          size_t stride_c, void* stream);
+/* cactus_unpack_int4_to_int8 (kernel/kernel.h:162, kernel_quants.cpp:295-351) */
+int cactus_hip_unpack_int4_to_int8(const uint8_t* packed, int8_t* unpacked, size_t count,
+                                   void* stream);
+
+/* ------------------------------------------------ a4: FP16 matmul */
+/* cactus_matmul_f16 (kernel/kernel.h:51, kernel_gemm.cpp:17-126): FP16
+ * accumulation, 8 lanes (lane j takes k = j mod 8 in increasing k, fp16 fma),
+ * final sum ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) in fp16.  a [M][K],
+ * b_transposed [N][K], c [M][N]. */
+int cactus_hip_matmul_f16(const uint16_t* a, const uint16_t* b_transposed, uint16_t* c,
+                          size_t M, size_t K, size_t N, void* stream);
+/* LM head + greedy sample fused (engine_model.cpp:241-247 then
+ * cactus_sample_f16 greedy branch): logits = cactus_hip_matmul_f16(a[1][K],
+ * b_transposed) written to `logits` (may be NULL) and token = argmax with
+ * the first index winning ties. */
+int cactus_hip_lm_head_argmax_f16(const uint16_t* a, const uint16_t* b_transposed,
+                                  uint16_t* logits, uint32_t* token, size_t K, size_t N,
+                                  void* stream);
+
+/* ------------------------------------------------ a5/a6: attention */
+/* cactus_attention_f16 (kernel/kernel.h:95, kernel_attention.cpp:10-255).
+ * q [B][S][Hq][d], k/v [B][Skv][Hkv][d], o like q; mask (may be NULL)
+ * [B][S][Skv] fp16, 0 = masked.  Reference order of operations: 32-key
+ * blocks, running max = last block max, second-order 2^x weights for the
+ * first floor(n/4)*4 keys of a block and expf for the rest. */
+int cactus_hip_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             uint16_t* o, size_t batch, size_t seq_len, size_t kv_seq_len,
+                             size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                             float scale, const uint16_t* mask, size_t position_offset,
+                             size_t window_size, int is_causal, void* stream);
+/* cactus_attention_hybrid_int8_fp16 (kernel/kernel.h:100,
+ * kernel_attention.cpp:257-482): positions < cache_len read the INT8 cache
+ * (k_cached/v_cached [B][cache_len][Hkv][d], scales [B][cache_len][Hkv][G]),
+ * later positions read k_new/v_new [B][new_len][Hkv][d] fp16. expf weights. */
+int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cached,
+                                          const int8_t* v_cached, const float* k_scales,
+                                          const float* v_scales, const uint16_t* k_new,
+                                          const uint16_t* v_new, uint16_t* o, size_t batch,
+                                          size_t seq_len, size_t cache_len, size_t new_len,
+                                          size_t num_q_heads, size_t num_kv_heads,
+                                          size_t head_dim, float scale, size_t position_offset,
+                                          int is_causal, size_t quant_group_size, void* stream);
+
+/* ------------------------------------------------ a7: KV quantization */
+/* cactus_quantize_kv_fp16_to_int8 (kernel/kernel.h:150, kernel_quants.cpp:223-293)
+ * src [S][Hkv][d] fp16 -> dst int8 same shape, scales [S][Hkv][ceil(d/g)] f32. */
+int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,
+                                        size_t seq_len, size_t kv_heads, size_t head_dim,
+                                        size_t group_size, void* stream);
+
+/* ------------------------------------------------ a8-a12 */
+/* cactus_rms_norm_f16 (kernel/kernel.h:79, kernel_attention.cpp:484-563) */
+int cactus_hip_rms_norm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t rows,
+                            size_t dims, float eps, void* stream);
+/* cactus_rope_f16 (kernel/kernel.h:82, kernel_attention.cpp:565-676): NeoX
+ * half-split pairing with fp16 cos/sin tables built on the host
+ * (freq = 1/powf(theta, 2i/d), angle = pos*freq) and cached per device. */
+int cactus_hip_rope_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq_len,
+                        size_t num_heads, size_t head_dim, size_t start_pos, float theta,
+                        void* stream);
+/* Grows the cached RoPE table to at least max_pos positions so that later
+ * cactus_hip_rope_f16 calls up to that position do no host work (required
+ * before capturing them into a HIP graph). */
+int cactus_hip_rope_reserve(size_t max_pos, size_t head_dim, float theta);
+/* cactus_softmax_f16 (kernel/kernel.h:85, kernel_nn.cpp:152-251) */
+int cactus_hip_softmax_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq_len,
+                           size_t vocab, void* stream);
+/* cactus_silu_f16 (kernel/kernel.h:88, kernel_nn.cpp:12-44) */
+int cactus_hip_silu_f16(const uint16_t* x, uint16_t* y, size_t n, void* stream);
+/* cactus_add_f16 / cactus_multiply_f16 (kernel/kernel.h:22,25, kernel_blas.cpp:187,291) */
+int cactus_hip_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n,
+                       void* stream);
+int cactus_hip_multiply_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n,
+                            void* stream);
+
+/* ------------------------------------------------ a13/a14 */
+/* compute_embedding_node, FP16 table with FP32 ids
+ * (graph/graph_ops_tensor.cpp:301-329): out[i] = table[(size_t)ids[i]].
+ * Out-of-range ids (the reference throws) produce zero rows and set
+ * *error_flag = 1 when error_flag is non-NULL (device int). */
+int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* out,
+                             size_t num_ids, size_t hidden, size_t vocab, int* error_flag,
+                             void* stream);
+/* cactus_sample_f16 (kernel/kernel.h:127, kernel_nn.cpp:446-466): only the
+ * greedy branch (temperature == 0, top_p <= 0, top_k == 0) is built; other
+ * settings return CACTUS_HIP_EUNSUPPORTED.  Writes one uint32 to *out. */
+int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
+                          float temperature, float top_p, size_t top_k, size_t random_seed,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

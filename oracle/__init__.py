@@ -1,0 +1,208 @@
+"""ctypes binding of the CPU restatement (oracle/_build/libcactus_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker or the timed CPU
+baseline, never as part of the product path.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "_build" / "libcactus_oracle.so"
+
+_lib = None
+
+P = ctypes.c_void_p
+SZ = ctypes.c_size_t
+F = ctypes.c_float
+I = ctypes.c_int
+
+_SIGS = {
+    "orc_h2f": (F, [ctypes.c_uint16]),
+    "orc_f2h": (ctypes.c_uint16, [F]),
+    "orc_d2h": (ctypes.c_uint16, [ctypes.c_double]),
+    "orc_hadd": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
+    "orc_hmul": (ctypes.c_uint16, [ctypes.c_uint16, ctypes.c_uint16]),
+    "orc_hfma": (ctypes.c_uint16, [ctypes.c_uint16] * 3),
+    "orc_expf": (F, [F]),
+    "orc_fast_exp": (F, [F]),
+    "orc_poly_exp_weight": (F, [F, F]),
+    "orc_fp16_max_abs": (F, [P, SZ]),
+    "orc_fp16_to_int8": (None, [P, P, SZ, F]),
+    "orc_quantize_activations": (None, [P, P, P, SZ, SZ]),
+    "orc_matmul_int8": (None, [P, P, P, P, P, SZ, SZ, SZ, SZ]),
+    "orc_matmul_int4": (None, [P, P, P, P, P, SZ, SZ, SZ, SZ]),
+    "orc_group_sums_int8": (None, [P, P, P, SZ, SZ, SZ, SZ]),
+    "orc_unpack_int4_to_int8": (None, [P, P, SZ]),
+    "orc_matmul_int8_mt": (None, [P, P, P, P, P, SZ, SZ, SZ, SZ, I]),
+    "orc_matmul_f16": (None, [P, P, P, SZ, SZ, SZ]),
+    "orc_attention_f16": (None, [P, P, P, P, SZ, SZ, SZ, SZ, SZ, SZ, F, P, SZ, SZ, I]),
+    "orc_attention_hybrid_int8_fp16": (None, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, SZ, SZ, SZ,
+                                              SZ, F, SZ, I, SZ]),
+    "orc_quantize_kv_fp16_to_int8": (None, [P, P, P, SZ, SZ, SZ, SZ]),
+    "orc_rms_norm_f16": (None, [P, P, P, SZ, SZ, F]),
+    "orc_rope_tables": (None, [P, P, SZ, SZ, F]),
+    "orc_rope_f16": (None, [P, P, SZ, SZ, SZ, SZ, SZ, F]),
+    "orc_softmax_f16": (None, [P, P, SZ, SZ]),
+    "orc_silu_f16": (None, [P, P, SZ]),
+    "orc_add_f16": (None, [P, P, P, SZ]),
+    "orc_multiply_f16": (None, [P, P, P, SZ]),
+    "orc_embedding_f16": (I, [P, P, P, SZ, SZ, SZ]),
+    "orc_argmax_f16": (ctypes.c_uint32, [P, SZ]),
+    "orc_qwen_create": (P, [P, P, P, P]),
+    "orc_qwen_destroy": (None, [P]),
+    "orc_qwen_reset": (None, [P]),
+    "orc_qwen_prefill": (I, [P, P, SZ, SZ]),
+    "orc_qwen_decode": (ctypes.c_uint32, [P, ctypes.c_uint32, P]),
+    "orc_qwen_last_hidden": (P, [P, P]),
+    "orc_qwen_cache_len": (SZ, [P]),
+    "orc_qwen_kv": (None, [P, SZ, P, P, P, P]),
+}
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        _lib = ctypes.CDLL(str(LIB))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(_lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    return _lib
+
+
+def ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+# ---- numpy conveniences (fp16 arrays travel as uint16 bit patterns) ----------
+def f16bits(x) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(x, dtype=np.float16)).view(np.uint16)
+
+
+def bits2f(u: np.ndarray) -> np.ndarray:
+    return np.asarray(u, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def quantize_activations(x16: np.ndarray):
+    M, K = x16.shape
+    q = np.empty((M, K), np.int8)
+    s = np.empty(M, np.float32)
+    lib().orc_quantize_activations(ptr(x16), ptr(q), ptr(s), M, K)
+    return q, s
+
+
+def matmul_int8(A, As, B, Bs, gs):
+    M, K = A.shape
+    N = B.shape[0]
+    C = np.empty((M, N), np.uint16)
+    lib().orc_matmul_int8(ptr(A), ptr(As), ptr(B), ptr(Bs), ptr(C), M, K, N, gs)
+    return C
+
+
+def matmul_int4(A, As, Bp, Bs, gs):
+    M, K = A.shape
+    N = Bp.shape[0]
+    C = np.empty((M, N), np.uint16)
+    lib().orc_matmul_int4(ptr(A), ptr(As), ptr(Bp), ptr(Bs), ptr(C), M, K, N, gs)
+    return C
+
+
+def group_sums_int8(A, B, gs):
+    M, K = A.shape
+    N = B.shape[0]
+    acc = np.empty((M, N, K // gs), np.int32)
+    lib().orc_group_sums_int8(ptr(A), ptr(B), ptr(acc), M, K, N, gs)
+    return acc
+
+
+def matmul_f16(a, bT):
+    M, K = a.shape
+    N = bT.shape[0]
+    c = np.empty((M, N), np.uint16)
+    lib().orc_matmul_f16(ptr(a), ptr(bT), ptr(c), M, K, N)
+    return c
+
+
+def attention_f16(q, k, v, scale, mask=None, pos_off=0, window=0, causal=True):
+    B, S, Hq, d = q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    o = np.empty_like(q)
+    lib().orc_attention_f16(ptr(q), ptr(k), ptr(v), ptr(o), B, S, Skv, Hq, Hkv, d, scale,
+                            ptr(mask), pos_off, window, 1 if causal else 0)
+    return o
+
+
+def attention_hybrid(q, kc, vc, ks, vs, kn, vn, scale, pos_off, causal=True, qgs=128):
+    B, S, Hq, d = q.shape
+    cache_len = kc.shape[1] if kc is not None else 0
+    new_len = kn.shape[1] if kn is not None else 0
+    Hkv = (kc if kc is not None else kn).shape[2]
+    o = np.empty_like(q)
+    lib().orc_attention_hybrid_int8_fp16(ptr(q), ptr(kc), ptr(vc), ptr(ks), ptr(vs), ptr(kn),
+                                         ptr(vn), ptr(o), B, S, cache_len, new_len, Hq, Hkv, d,
+                                         scale, pos_off, 1 if causal else 0, qgs)
+    return o
+
+
+def quantize_kv(src, gs=128):
+    S, H, d = src.shape
+    ng = (d + gs - 1) // gs
+    dst = np.empty((S, H, d), np.int8)
+    sc = np.empty((S, H, ng), np.float32)
+    lib().orc_quantize_kv_fp16_to_int8(ptr(src), ptr(dst), ptr(sc), S, H, d, gs)
+    return dst, sc
+
+
+def rms_norm(x, w, eps):
+    rows, dims = x.shape
+    y = np.empty_like(x)
+    lib().orc_rms_norm_f16(ptr(x), ptr(w), ptr(y), rows, dims, eps)
+    return y
+
+
+def rope(x, start_pos, theta):
+    B, S, H, d = x.shape
+    y = np.empty_like(x)
+    lib().orc_rope_f16(ptr(x), ptr(y), B, S, H, d, start_pos, theta)
+    return y
+
+
+def softmax(x):
+    rows, V = x.shape
+    y = np.empty_like(x)
+    lib().orc_softmax_f16(ptr(x), ptr(y), rows, V)
+    return y
+
+
+def silu(x):
+    y = np.empty_like(x)
+    lib().orc_silu_f16(ptr(x), ptr(y), x.size)
+    return y
+
+
+def add(a, b):
+    y = np.empty_like(a)
+    lib().orc_add_f16(ptr(a), ptr(b), ptr(y), a.size)
+    return y
+
+
+def multiply(a, b):
+    y = np.empty_like(a)
+    lib().orc_multiply_f16(ptr(a), ptr(b), ptr(y), a.size)
+    return y
+
+
+def argmax(logits):
+    return int(lib().orc_argmax_f16(ptr(logits), logits.size))

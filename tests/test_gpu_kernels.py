@@ -1,0 +1,389 @@
+"""GPU parity of every kernel-layer entry point against the oracle.
+
+Each test prints the case it runs (flushed) before touching the GPU.  The bar
+is bit-equality of every output (quantized codes, scales, fp16 results): the
+HIP kernels follow the reference's order of operations exactly.
+"""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from _data import activations, f16, grouped_int4_weights, grouped_int8_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+class Dev:
+    """Small helper: numpy <-> device buffers through the C ABI."""
+
+    def __init__(self, cm):
+        self.cm = cm
+        self.bufs = []
+
+    def put(self, arr):
+        b = self.cm.DeviceBuffer.from_numpy(np.ascontiguousarray(arr))
+        self.bufs.append(b)
+        return b.ptr
+
+    def empty(self, nbytes):
+        b = self.cm.DeviceBuffer(nbytes)
+        self.bufs.append(b)
+        return b
+
+    def get(self, buf, dtype, shape):
+        self.cm.call("cactus_hip_stream_sync", None)
+        return buf.to_numpy(dtype, shape)
+
+
+@pytest.fixture
+def dev(hip_ready):
+    d = Dev(hip_ready)
+    yield d
+    for b in d.bufs:
+        b.free()
+
+
+def assert_bits(got, ref, what):
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    bad = np.flatnonzero(got.ravel() != ref.ravel())
+    assert bad.size == 0, f"{what}: {bad.size}/{ref.size} mismatches, first at {bad[:5]}: " \
+                          f"got {got.ravel()[bad[:5]]} ref {ref.ravel()[bad[:5]]}"
+
+
+# ------------------------------------------------------------------ a1
+@pytest.mark.parametrize("M,K", [(1, 640), (1, 1024), (3, 1001), (512, 1024), (2, 3072)])
+def test_quantize_activations(dev, orc, M, K):
+    say("quantize_activations", M, K)
+    rng = np.random.default_rng(M * 7 + K)
+    x = activations(rng, M, K)
+    x[0, :5] = f16([0.0, -0.0, 65504.0, -3.5, 1e-8])
+    q = dev.empty(M * K)
+    s = dev.empty(M * 4)
+    dev.cm.call("cactus_hip_quantize_activations", dev.put(x), q.ptr, s.ptr, M, K, None)
+    rq, rs = orc.quantize_activations(x)
+    assert_bits(dev.get(s, np.float32, M).view(np.uint32), rs.view(np.uint32), "scales")
+    assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
+
+
+def test_max_abs_and_fp16_to_int8(dev, orc):
+    say("fp16_max_abs / fp16_to_int8")
+    rng = np.random.default_rng(1)
+    x = f16(rng.normal(0, 2, 1003))
+    out = dev.empty(4)
+    xp = dev.put(x)
+    dev.cm.call("cactus_hip_fp16_max_abs", xp, 1003, out.ptr, None)
+    assert dev.get(out, np.float32, 1)[0] == orc.lib().orc_fp16_max_abs(orc.ptr(x), 1003)
+    q = dev.empty(1003)
+    dev.cm.call("cactus_hip_fp16_to_int8", xp, q.ptr, 1003, ctypes.c_float(0.031), None)
+    ref = np.empty(1003, np.int8)
+    orc.lib().orc_fp16_to_int8(orc.ptr(x), orc.ptr(ref), 1003, 0.031)
+    assert_bits(dev.get(q, np.int8, 1003), ref, "codes")
+
+
+# ------------------------------------------------------------------ a2/a3
+GEMM_CASES = [
+    (1, 640, 2048, 32),     # Gemma-3-270m up-proj GEMV (the headline GEMV)
+    (1, 1024, 3072, 32),
+    (1, 2048, 1024, 32),
+    (2, 1024, 512, 64),
+    (3, 512, 384, 128),
+    (5, 256, 200, 32),
+    (17, 1024, 256, 32),
+    (64, 1024, 512, 32),
+    (512, 1024, 3072, 32),  # Qwen3-0.6B gate/up prefill GEMM
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs", GEMM_CASES)
+def test_matmul_int8(dev, orc, M, K, N, gs):
+    say("matmul_int8", M, K, N, gs)
+    rng = np.random.default_rng(M + K + N + gs)
+    x = activations(rng, M, K)
+    B, Bs = grouped_int8_weights(rng, N, K, gs)
+    rq, rs = orc.quantize_activations(x)
+    ref = orc.matmul_int8(rq, rs, B, Bs, gs)
+    Bp, Bsp = dev.put(B), dev.put(Bs)
+    C = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8", dev.put(rq), dev.put(rs), Bp, Bsp, C.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C, np.uint16, (M, N)), ref, "matmul_int8 (pre-quantized)")
+    C2 = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8_f16act", dev.put(x), Bp, Bsp, C2.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C2, np.uint16, (M, N)), ref, "matmul_int8_f16act")
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 3072, 1024, 32), (256, 3072, 1024, 32), (1, 1024, 3072, 32),
+                                      (4, 1024, 640, 64), (2, 512, 96, 128)])
+def test_matmul_int4(dev, orc, M, K, N, gs):
+    say("matmul_int4", M, K, N, gs)
+    rng = np.random.default_rng(M * 3 + K + N)
+    x = activations(rng, M, K)
+    codes, packed, Bs = grouped_int4_weights(rng, N, K, gs)
+    packed[0, :2] = [0x88, 0x77]     # extremes -8 and 7
+    rq, rs = orc.quantize_activations(x)
+    ref = orc.matmul_int4(rq, rs, packed, Bs, gs)
+    Bp, Bsp = dev.put(packed), dev.put(Bs)
+    C = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int4", dev.put(rq), dev.put(rs), Bp, Bsp, C.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C, np.uint16, (M, N)), ref, "matmul_int4")
+    C2 = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int4_f16act", dev.put(x), Bp, Bsp, C2.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C2, np.uint16, (M, N)), ref, "matmul_int4_f16act")
+
+
+def test_int32_accumulator_exact(dev, orc):
+    """Scales of 1 and |acc| <= 2048 make C = fp16(acc) exact: the group sums
+    themselves are compared."""
+    say("int32 accumulators")
+    rng = np.random.default_rng(3)
+    M, K, N, gs = 4, 16, 300, 16
+    A = rng.integers(-8, 9, (M, K), dtype=np.int8)
+    B = rng.integers(-8, 9, (N, K), dtype=np.int8)
+    As = np.ones(M, np.float32)
+    Bs = f16(np.ones((N, 1)))
+    C = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8", dev.put(A), dev.put(As), dev.put(B), dev.put(Bs), C.ptr,
+                M, K, N, gs, None)
+    acc = orc.group_sums_int8(A, B, gs)[:, :, 0]
+    got = dev.get(C, np.uint16, (M, N)).view(np.float16).astype(np.int64)
+    assert (got == acc).all()
+
+
+def test_matmul_int8_batched(dev, orc):
+    say("matmul_int8_f16act_batched")
+    rng = np.random.default_rng(4)
+    M, K, N, gs, R = 1, 640, 2048, 32, 6
+    xs = [activations(rng, M, K) for _ in range(R)]
+    ws = [grouped_int8_weights(rng, N, K, gs) for _ in range(R)]
+    A = np.stack(xs)
+    B = np.stack([w[0] for w in ws])
+    Bs = np.stack([w[1] for w in ws])
+    C = dev.empty(R * M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8_f16act_batched", dev.put(A), dev.put(B), dev.put(Bs), C.ptr,
+                M, K, N, gs, R, M * K, N * K, N * (K // gs), M * N, None)
+    got = dev.get(C, np.uint16, (R, M, N))
+    for r in range(R):
+        rq, rs = orc.quantize_activations(xs[r])
+        assert_bits(got[r], orc.matmul_int8(rq, rs, ws[r][0], ws[r][1], gs), f"batch {r}")
+
+
+def test_unpack_int4(dev, orc):
+    say("unpack_int4")
+    rng = np.random.default_rng(5)
+    codes, packed, _ = grouped_int4_weights(rng, 3, 64, 32)
+    out = dev.empty(3 * 64)
+    dev.cm.call("cactus_hip_unpack_int4_to_int8", dev.put(packed), out.ptr, 3 * 64, None)
+    assert_bits(dev.get(out, np.int8, (3, 64)), codes, "unpack")
+
+
+# ------------------------------------------------------------------ a4
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 4096), (2, 3, 2), (3, 1024, 1000), (5, 520, 77), (1, 24, 9)])
+def test_matmul_f16(dev, orc, M, K, N):
+    say("matmul_f16", M, K, N)
+    rng = np.random.default_rng(M + K + N)
+    a = f16(rng.normal(0, 1, (M, K)))
+    b = f16(rng.normal(0, 0.02, (N, K)))
+    if K == 3:
+        a = f16([[1, 2, 3], [4, 5, 6]])
+        b = f16([[1, 3, 5], [2, 4, 6]])
+    c = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_f16", dev.put(a), dev.put(b), c.ptr, M, K, N, None)
+    if K == 3:   # tests/test_graph.cpp:75-90 known answer
+        assert (dev.get(c, np.uint16, (M, N)).view(np.float16) == [[22, 28], [49, 64]]).all()
+    assert_bits(dev.get(c, np.uint16, (M, N)), orc.matmul_f16(a, b), "matmul_f16")
+
+
+def test_lm_head_argmax_qwen_vocab(dev, orc):
+    say("lm_head_argmax K=1024 N=151936")
+    rng = np.random.default_rng(6)
+    K, N = 1024, 151936
+    a = f16(rng.normal(0, 1, (1, K)))
+    b = f16(rng.normal(0, 0.02, (N, K)))
+    logits = dev.empty(N * 2)
+    tok = dev.empty(4)
+    bp, ap = dev.put(b), dev.put(a)
+    dev.cm.call("cactus_hip_lm_head_argmax_f16", ap, bp, logits.ptr, tok.ptr, K, N, None)
+    ref = orc.matmul_f16(a, b)
+    assert_bits(dev.get(logits, np.uint16, (1, N)), ref, "logits")
+    assert dev.get(tok, np.uint32, 1)[0] == orc.argmax(ref[0])
+    # twice more (the argmax scratch resets itself), logits not stored
+    for _ in range(2):
+        dev.cm.call("cactus_hip_lm_head_argmax_f16", ap, bp, None, tok.ptr, K, N, None)
+        assert dev.get(tok, np.uint32, 1)[0] == orc.argmax(ref[0])
+
+
+# ------------------------------------------------------------------ a5/a6
+def _attn_inputs(rng, B, S, Skv, Hq, Hkv, d):
+    q = f16(rng.normal(0, 1, (B, S, Hq, d)))
+    k = f16(rng.normal(0, 1, (B, Skv, Hkv, d)))
+    v = f16(rng.normal(0, 1, (B, Skv, Hkv, d)))
+    return q, k, v
+
+
+@pytest.mark.parametrize("B,S,Skv,Hq,Hkv,d,pos,window", [
+    (1, 1, 4096, 16, 8, 128, 4095, 0),     # KV-cache decode attention (FP16 KV)
+    (1, 64, 64, 16, 8, 128, 0, 0),          # prefill chunk, causal
+    (2, 5, 37, 4, 2, 64, 32, 0),
+    (1, 9, 100, 4, 4, 128, 91, 20),         # sliding window
+    (1, 3, 50, 2, 1, 40, 47, 0),            # head_dim not a multiple of 8
+])
+def test_attention_f16(dev, orc, B, S, Skv, Hq, Hkv, d, pos, window):
+    say("attention_f16", B, S, Skv, Hq, Hkv, d, pos, window)
+    rng = np.random.default_rng(S + Skv + d)
+    q, k, v = _attn_inputs(rng, B, S, Skv, Hq, Hkv, d)
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_f16(q, k, v, scale, pos_off=pos, window=window)
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_attention_f16", dev.put(q), dev.put(k), dev.put(v), o.ptr, B, S, Skv, Hq,
+                Hkv, d, ctypes.c_float(scale), None, pos, window, 1, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_f16")
+
+
+def test_attention_f16_mask_noncausal(dev, orc):
+    say("attention_f16 mask, non-causal")
+    rng = np.random.default_rng(7)
+    B, S, Skv, Hq, Hkv, d = 1, 4, 45, 2, 2, 64
+    q, k, v = _attn_inputs(rng, B, S, Skv, Hq, Hkv, d)
+    mask = f16((rng.random((B, S, Skv)) > 0.3).astype(np.float32))
+    ref = orc.attention_f16(q, k, v, 0.0, mask=mask, causal=False)
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_attention_f16", dev.put(q), dev.put(k), dev.put(v), o.ptr, B, S, Skv, Hq,
+                Hkv, d, ctypes.c_float(0.0), dev.put(mask), 0, 0, 0, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_f16 masked")
+
+
+@pytest.mark.parametrize("S,cache,new,Hq,Hkv,d", [
+    (1, 4095, 1, 16, 8, 128),      # KV-cache decode attention (INT8 cache)
+    (64, 256, 64, 16, 8, 128),     # second prefill chunk
+    (3, 33, 3, 4, 2, 64),
+    (2, 0, 2, 4, 2, 128),
+])
+def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
+    say("attention_hybrid", S, cache, new, Hq, Hkv, d)
+    rng = np.random.default_rng(cache + new + d)
+    kf = f16(rng.normal(0, 1, (max(cache, 1), Hkv, d)))
+    vf = f16(rng.normal(0, 1, (max(cache, 1), Hkv, d)))
+    kc, ks = orc.quantize_kv(kf)
+    vc, vs = orc.quantize_kv(vf)
+    kc, vc, ks, vs = kc[:cache], vc[:cache], ks[:cache], vs[:cache]
+    kn = f16(rng.normal(0, 1, (1, new, Hkv, d)))
+    vn = f16(rng.normal(0, 1, (1, new, Hkv, d)))
+    q = f16(rng.normal(0, 1, (1, S, Hq, d)))
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_hybrid(q, kc[None] if cache else None, vc[None] if cache else None,
+                               ks[None] if cache else None, vs[None] if cache else None, kn, vn,
+                               scale, pos_off=cache)
+    o = dev.empty(q.nbytes)
+    P = lambda a: dev.put(a) if cache else None
+    dev.cm.call("cactus_hip_attention_hybrid_int8_fp16", dev.put(q), P(kc), P(vc), P(ks), P(vs),
+                dev.put(kn), dev.put(vn), o.ptr, 1, S, cache, new, Hq, Hkv, d, ctypes.c_float(scale),
+                cache, 1, 128, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid")
+
+
+# ------------------------------------------------------------------ a7
+@pytest.mark.parametrize("S,H,d,gs", [(256, 8, 128, 128), (3, 2, 100, 128), (5, 4, 256, 128), (2, 2, 64, 32)])
+def test_quantize_kv(dev, orc, S, H, d, gs):
+    say("quantize_kv", S, H, d, gs)
+    rng = np.random.default_rng(S + d)
+    x = f16(rng.normal(0, 1, (S, H, d)))
+    ng = (d + gs - 1) // gs
+    q = dev.empty(S * H * d)
+    sc = dev.empty(S * H * ng * 4)
+    dev.cm.call("cactus_hip_quantize_kv_fp16_to_int8", dev.put(x), q.ptr, sc.ptr, S, H, d, gs, None)
+    rq, rs = orc.quantize_kv(x, gs)
+    assert_bits(dev.get(sc, np.float32, (S, H, ng)).view(np.uint32), rs.view(np.uint32), "kv scales")
+    assert_bits(dev.get(q, np.int8, (S, H, d)), rq, "kv codes")
+
+
+# ------------------------------------------------------------------ a8-a14
+@pytest.mark.parametrize("rows,dims,eps", [(1, 1024, 1e-6), (256, 1024, 1e-6), (4096, 128, 1e-6),
+                                           (3, 1000, 1e-5), (2, 1004, 1e-5), (1, 8, 1e-5)])
+def test_rms_norm(dev, orc, rows, dims, eps):
+    say("rms_norm", rows, dims)
+    rng = np.random.default_rng(rows + dims)
+    x = f16(rng.normal(0, 1, (rows, dims)))
+    w = f16(1 + rng.normal(0, 0.02, dims))
+    y = dev.empty(x.nbytes)
+    dev.cm.call("cactus_hip_rms_norm_f16", dev.put(x), dev.put(w), y.ptr, rows, dims,
+                ctypes.c_float(eps), None)
+    assert_bits(dev.get(y, np.uint16, x.shape), orc.rms_norm(x, w, eps), "rms_norm")
+
+
+@pytest.mark.parametrize("B,S,H,d,start,theta", [(1, 256, 16, 128, 0, 1e6), (1, 1, 8, 128, 4095, 1e6),
+                                                 (2, 3, 2, 36, 7, 1e4), (1, 64, 8, 128, 3900, 1e6)])
+def test_rope(dev, orc, B, S, H, d, start, theta):
+    say("rope", B, S, H, d, start, theta)
+    rng = np.random.default_rng(S + start)
+    x = f16(rng.normal(0, 1, (B, S, H, d)))
+    y = dev.empty(x.nbytes)
+    dev.cm.call("cactus_hip_rope_f16", dev.put(x), y.ptr, B, S, H, d, start, ctypes.c_float(theta), None)
+    assert_bits(dev.get(y, np.uint16, x.shape), orc.rope(x, start, theta), "rope")
+
+
+@pytest.mark.parametrize("rows,V", [(2, 3), (4, 96), (3, 1000), (1, 151936)])
+def test_softmax(dev, orc, rows, V):
+    say("softmax", rows, V)
+    rng = np.random.default_rng(V)
+    x = f16(rng.normal(0, 3, (rows, V)))
+    y = dev.empty(x.nbytes)
+    dev.cm.call("cactus_hip_softmax_f16", dev.put(x), y.ptr, 1, rows, V, None)
+    assert_bits(dev.get(y, np.uint16, x.shape), orc.softmax(x), "softmax")
+
+
+@pytest.mark.parametrize("n", [3072, 786432, 1003])
+def test_silu_add_multiply(dev, orc, n):
+    say("silu/add/multiply", n)
+    rng = np.random.default_rng(n)
+    a = f16(rng.normal(0, 3, n))
+    b = f16(rng.normal(0, 3, n))
+    ap, bp = dev.put(a), dev.put(b)
+    y = dev.empty(a.nbytes)
+    dev.cm.call("cactus_hip_silu_f16", ap, y.ptr, n, None)
+    assert_bits(dev.get(y, np.uint16, n), orc.silu(a), "silu")
+    dev.cm.call("cactus_hip_add_f16", ap, bp, y.ptr, n, None)
+    assert_bits(dev.get(y, np.uint16, n), orc.add(a, b), "add")
+    dev.cm.call("cactus_hip_multiply_f16", ap, bp, y.ptr, n, None)
+    assert_bits(dev.get(y, np.uint16, n), orc.multiply(a, b), "multiply")
+
+
+def test_embedding(dev, orc):
+    say("embedding")
+    rng = np.random.default_rng(8)
+    V, Hd = 1000, 1024
+    table = f16(rng.normal(0, 0.02, (V, Hd)))
+    ids = np.array([5, 999, 0, 5, 123], np.float32)
+    out = dev.empty(5 * Hd * 2)
+    err = dev.empty(4)
+    dev.cm.call("cactus_hip_memset", err.ptr, 0, 4, None)
+    tp = dev.put(table)
+    dev.cm.call("cactus_hip_embedding_f16", tp, dev.put(ids), out.ptr, 5, Hd, V, err.ptr, None)
+    assert_bits(dev.get(out, np.uint16, (5, Hd)), table[ids.astype(int)], "embedding")
+    assert dev.get(err, np.int32, 1)[0] == 0
+    dev.cm.call("cactus_hip_embedding_f16", tp, dev.put(np.array([1000], np.float32)), out.ptr, 1, Hd,
+                V, err.ptr, None)
+    assert dev.get(err, np.int32, 1)[0] == 1
+
+
+def test_sample_greedy(dev, orc):
+    say("sample greedy")
+    rng = np.random.default_rng(9)
+    V = 151936
+    logits = f16(rng.normal(0, 1, V))
+    logits[[77, 150000]] = f16([9.0, 9.0])       # planted tie: first index wins
+    out = dev.empty(4)
+    lp = dev.put(logits)
+    dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.0), ctypes.c_float(0.0), 0, 0,
+                None)
+    assert dev.get(out, np.uint32, 1)[0] == orc.argmax(logits) == 77
+    rc = dev.cm.hip().cactus_hip_sample_f16(lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 20,
+                                            1, None)
+    assert rc == -2  # CACTUS_HIP_EUNSUPPORTED: only greedy decoding is built
