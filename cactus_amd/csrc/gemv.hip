@@ -23,7 +23,7 @@ struct GemvArgs {
     const uint8_t* B;       // weights, int8 [N][K] or packed int4 [N][K/2]
     const uint16_t* Bs;     // fp16 group scales [N][G]
     uint16_t* C;            // fp16 out [M][N]
-    int M, K, N, gs, rows;
+    int M, K, N, gs, rows, tiles;
     size_t sA, sB, sBs, sC; // batch strides: elements of A/Bs/C, bytes of B
 };
 
@@ -68,45 +68,74 @@ __device__ __forceinline__ int chunk_dot(const int8_t* act, int col, i32x4 w) {
     return s;
 }
 
-// CH: 16-byte weight chunks each thread loads before the activation
-// prologue, so the weight stream is in flight while the row is quantized.
+// exact int32 sum over aligned groups of P consecutive lanes (P = 1..64)
+__device__ __forceinline__ int group_lane_sum(int v, int P) {
+    if (P >= 2) v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // lane ^ 1
+    if (P >= 4) v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // lane ^ 2
+    for (int off = 4; off < P; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Streaming grouped GEMV for M <= 4 activation rows.
+//
+// Grid (blocks_per_problem, batch).  A workgroup owns `tiles` consecutive
+// row tiles of one problem; a tile is `rows` weight rows = rows*cpr 16-byte
+// chunks, at most CH per thread.  The loads of tile t+1 are in flight while
+// tile t is dotted, and the activation prologue runs while tile 0 loads.
+// Group sums of a tile go to one of two LDS buffers; after a barrier the
+// tile's epilogue (one thread per output) runs the reference fma chain.
 template <int MR, bool F16ACT, bool INT4, int CH>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, int m0) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, gs = a.gs, G = K / gs;
     const int rows = a.rows;
-    const int n0 = blockIdx.x * rows;
-    const int nr = min(rows, a.N - n0);
     const size_t bi = blockIdx.y;
     const int mr = min(MR, a.M - m0);
     const int tid = threadIdx.x;
+    const int tile0 = blockIdx.x * a.tiles;
+    const int ntiles_all = (a.N + rows - 1) / rows;
+    const int tile_end = min(tile0 + a.tiles, ntiles_all);
+    if (tile0 >= tile_end) return;
 
-    int8_t* actq = reinterpret_cast<int8_t*>(smem);                       // MR*K
-    int32_t* acc = reinterpret_cast<int32_t*>(smem + ((MR * K + 15) & ~15)); // MR*rows*G
-    uint16_t* scl = reinterpret_cast<uint16_t*>(acc + MR * rows * G);     // rows*G
-    float* rsc = reinterpret_cast<float*>(scl + ((rows * G + 1) & ~1));  // MR
-    float* red = rsc + MR;                                                // 4
+    int8_t* actq = reinterpret_cast<int8_t*>(smem);                           // MR*K
+    int32_t* acc = reinterpret_cast<int32_t*>(smem + ((MR * K + 15) & ~15));  // 2*MR*rows*G
+    uint16_t* scl = reinterpret_cast<uint16_t*>(acc + 2 * MR * rows * G);     // 2*rows*G
+    float* rsc = reinterpret_cast<float*>(scl + 2 * rows * G);                // MR
+    float* red = rsc + MR;                                                    // 4
 
     const int cpr = INT4 ? K / 32 : K / 16;       // 16-byte chunks per row
     const int P = INT4 ? gs / 32 : gs / 16;       // chunks per group (power of 2)
-    const int total = nr * cpr;
     const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
-    const uint8_t* Bw = a.B + bi * a.sB + (size_t)n0 * row_bytes;
+    const uint8_t* Bbase = a.B + bi * a.sB;
+    const uint16_t* Bsbase = a.Bs + bi * a.sBs;
 
-    // 1. weight stream first (streaming data: non-temporal loads)
-    i32x4 wreg[CH];
+    // per-thread chunk coordinates inside a full tile (the same for every tile)
+    int crow[CH], ccol[CH];
 #pragma unroll
     for (int i = 0; i < CH; i++) {
         const int c = tid + i * GEMV_THREADS;
-        wreg[i] = (i32x4){0, 0, 0, 0};
-        if (c < total)
-            wreg[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
-                Bw + (size_t)(c / cpr) * row_bytes + (size_t)(c % cpr) * 16));
+        crow[i] = c / cpr;
+        ccol[i] = c - crow[i] * cpr;
     }
+    auto load_tile = [&](int t, i32x4 (&w)[CH]) {
+        const int n0 = t * rows;
+        const int total = min(rows, a.N - n0) * cpr;
+        const uint8_t* Bw = Bbase + (size_t)n0 * row_bytes;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            w[i] = (i32x4){0, 0, 0, 0};
+            if (tid + i * GEMV_THREADS < total)
+                w[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                    Bw + (size_t)crow[i] * row_bytes + (size_t)ccol[i] * 16));
+        }
+    };
 
-    // 2. group scales of this workgroup's rows (contiguous) and activation codes
-    const uint16_t* Bs = a.Bs + bi * a.sBs + (size_t)n0 * G;
-    for (int i = tid; i < nr * G; i += GEMV_THREADS) scl[i] = Bs[i];
+    i32x4 wcur[CH], wnext[CH];
+    load_tile(tile0, wcur);
+    for (int i = tid; i < min(rows, a.N - tile0 * rows) * G; i += GEMV_THREADS)
+        scl[i] = Bsbase[(size_t)tile0 * rows * G + i];
+
+    // activation codes (the per-row quantization of the matmul node)
     const int body = (K / 8) * 8;
     for (int m = 0; m < mr; m++) {
         if (F16ACT) {
@@ -125,60 +154,69 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
     }
     __syncthreads();
 
-    // 3. dot products; the P lanes of one group are summed exactly in int32
-    auto consume = [&](int c, const i32x4& w) {
-        const bool valid = c < total;
-        const int r = valid ? c / cpr : 0;
-        const int col = valid ? c % cpr : 0;
-        int dot[MR];
+    // One barrier per tile: the dot products of tile t fill accumulator
+    // buffer t%2; after the barrier the epilogue of tile t reads it while
+    // other waves already dot tile t+1 into the other buffer.
+    for (int t = tile0; t < tile_end; t++) {
+        const int buf = (t - tile0) & 1;
+        const int n0 = t * rows;
+        const int nr = min(rows, a.N - n0);
+        const int total = nr * cpr;
+        int32_t* accb = acc + buf * MR * rows * G;
+        uint16_t* sclb = scl + buf * rows * G;
+        if (t + 1 < tile_end) load_tile(t + 1, wnext);
 #pragma unroll
-        for (int m = 0; m < MR; m++)
-            dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, col, w) : 0;
-        for (int off = 1; off < P; off <<= 1) {
+        for (int i = 0; i < CH; i++) {
+            const bool valid = tid + i * GEMV_THREADS < total;
+            int dot[MR];
 #pragma unroll
-            for (int m = 0; m < MR; m++) dot[m] += __shfl_xor(dot[m], off, 64);
+            for (int m = 0; m < MR; m++) {
+                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], wcur[i]) : 0;
+                dot[m] = group_lane_sum(dot[m], P);
+            }
+            if (valid && ((tid + i * GEMV_THREADS) & (P - 1)) == 0) {
+                const int g = (ccol[i] * (INT4 ? 32 : 16)) / gs;
+#pragma unroll
+                for (int m = 0; m < MR; m++)
+                    if (m < mr) accb[(m * rows + crow[i]) * G + g] = dot[m];
+            }
         }
-        if (valid && (c & (P - 1)) == 0) {
-            const int g = (col * (INT4 ? 32 : 16)) / gs;
-#pragma unroll
-            for (int m = 0; m < MR; m++)
-                if (m < mr) acc[(m * rows + r) * G + g] = dot[m];
+        __syncthreads();
+        // scales of tile t+1 into the other buffer: its last reader, the
+        // epilogue of tile t-1, finished before the barrier above
+        if (t + 1 < tile_end) {
+            const int n1 = n0 + rows;
+            uint16_t* scln = scl + (buf ^ 1) * rows * G;
+            for (int i = tid; i < min(rows, a.N - n1) * G; i += GEMV_THREADS)
+                scln[i] = Bsbase[(size_t)n1 * G + i];
         }
-    };
-#pragma unroll
-    for (int i = 0; i < CH; i++) consume(tid + i * GEMV_THREADS, wreg[i]);
-    for (int base = CH * GEMV_THREADS; base < total; base += GEMV_THREADS) {
-        const int c = base + tid;
-        i32x4 w = (i32x4){0, 0, 0, 0};
-        if (c < total)
-            w = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
-                Bw + (size_t)(c / cpr) * row_bytes + (size_t)(c % cpr) * 16));
-        consume(c, w);
-    }
-    __syncthreads();
 
-    // 4. reference epilogue, one thread per output
-    for (int t = tid; t < mr * nr; t += GEMV_THREADS) {
-        const int m = t / nr, r = t % nr;
-        const int32_t* ag = acc + (m * rows + r) * G;
-        const uint16_t* sg = scl + r * G;
-        float rs = 0.0f;
-        for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
-        a.C[bi * a.sC + (size_t)(m0 + m) * a.N + n0 + r] = f2h(rs * rsc[m]);
+        // reference epilogue, one thread per output of this tile
+        for (int o = tid; o < mr * nr; o += GEMV_THREADS) {
+            const int m = o / nr, r = o % nr;
+            const int32_t* ag = accb + (m * rows + r) * G;
+            const uint16_t* sg = sclb + r * G;
+            float rs = 0.0f;
+            for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+            a.C[bi * a.sC + (size_t)(m0 + m) * a.N + n0 + r] = f2h(rs * rsc[m]);
+        }
+#pragma unroll
+        for (int i = 0; i < CH; i++) wcur[i] = wnext[i];
     }
 }
 
 static size_t gemv_smem(int MR, int K, int rows, int G) {
     size_t s = (size_t)((MR * K + 15) & ~15);
-    s += (size_t)MR * rows * G * 4;
-    s += (size_t)((rows * G + 1) & ~1) * 2;
+    s += (size_t)2 * MR * rows * G * 4;
+    s += (size_t)2 * rows * G * 2;
     s += (size_t)MR * 4 + 16;
-    return s;
+    return (s + 15) & ~(size_t)15;
 }
 
 template <int MR, bool F16ACT, bool INT4, int CH>
 static int launch_gemv_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st) {
-    dim3 grid(ceil_div(a.N, a.rows), (unsigned)batch);
+    const int ntiles = (a.N + a.rows - 1) / a.rows;
+    dim3 grid(ceil_div(ntiles, a.tiles), (unsigned)batch);
     hipLaunchKernelGGL((gemv_grouped_kernel<MR, F16ACT, INT4, CH>), grid, dim3(GEMV_THREADS), smem,
                        st, a, m0);
     return check_launch("gemv_grouped");
@@ -191,6 +229,7 @@ static int launch_gemv_ch(const GemvArgs& a, size_t batch, int m0, size_t smem, 
         case 1: return launch_gemv_t<MR, F16ACT, INT4, 1>(a, batch, m0, smem, st);
         case 2: return launch_gemv_t<MR, F16ACT, INT4, 2>(a, batch, m0, smem, st);
         case 4: return launch_gemv_t<MR, F16ACT, INT4, 4>(a, batch, m0, smem, st);
+        case 6: return launch_gemv_t<MR, F16ACT, INT4, 6>(a, batch, m0, smem, st);
         default: return launch_gemv_t<MR, F16ACT, INT4, 8>(a, batch, m0, smem, st);
     }
 }
@@ -200,18 +239,25 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
     const int G = a.K / a.gs;
     const int cpr = INT4 ? a.K / 32 : a.K / 16;
     const int MR = a.M >= 4 ? 4 : (a.M >= 2 ? 2 : 1);
-    // as many rows as 8 prefetched chunks per thread cover, then fewer while
-    // the grid would leave CUs idle (256 CUs, aim for >= 4 workgroups each)
-    int rows = (8 * GEMV_THREADS) / cpr;
+    // a tile is about 4 chunks per thread (measured best: more registers per
+    // thread cost occupancy); fewer rows when the whole problem would leave
+    // CUs idle (256 CUs, aim for >= 4 workgroups each)
+    int rows = (4 * GEMV_THREADS) / cpr;
     if (rows < 1) rows = 1;
     if (rows > a.N) rows = a.N;
     while (rows > 1 && (size_t)ceil_div(a.N, rows) * batch < 1024) rows = (rows + 1) / 2;
     while (rows > 1 && gemv_smem(MR, a.K, rows, G) > 60 * 1024) rows = (rows + 1) / 2;
-    if (gemv_smem(MR, a.K, rows, G) > 60 * 1024)
+    if (gemv_smem(MR, a.K, rows, G) > 60 * 1024 || rows * cpr > 8 * GEMV_THREADS)
         return fail(CACTUS_HIP_EUNSUPPORTED, "grouped matmul: K too large for the GEMV path");
     const int chunks = (rows * cpr + GEMV_THREADS - 1) / GEMV_THREADS;
-    const int ch = chunks <= 1 ? 1 : chunks <= 2 ? 2 : chunks <= 4 ? 4 : 8;
+    const int ch = chunks <= 1 ? 1 : chunks <= 2 ? 2 : chunks <= 4 ? 4 : chunks <= 6 ? 6 : 8;
+    // tiles per workgroup: up to 8 once there are >= 2048 tiles in flight
+    const size_t ntiles = ceil_div(a.N, rows);
+    size_t per = ntiles * batch / 2048;
+    if (per < 1) per = 1;
+    if (per > 8) per = 8;
     a.rows = rows;
+    a.tiles = (int)per;
     const size_t smem = gemv_smem(MR, a.K, rows, G);
     for (int m0 = 0; m0 < a.M; m0 += MR) {
         int rc;
