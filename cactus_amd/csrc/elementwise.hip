@@ -210,6 +210,22 @@ __global__ void mul_kernel(const uint16_t* __restrict__ A, const uint16_t* __res
         Y[i] = hmul(A[i], B[i]);
 }
 
+// ---------------------------------------------------------------- transpose
+__global__ void transpose_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                 size_t rows, size_t cols) {
+    __shared__ uint16_t tile[32][33];
+    const size_t c0 = (size_t)blockIdx.x * 32, r0 = (size_t)blockIdx.y * 32;
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const size_t r = r0 + i, c = c0 + threadIdx.x;
+        if (r < rows && c < cols) tile[i][threadIdx.x] = src[r * cols + c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const size_t c = c0 + i, r = r0 + threadIdx.x;
+        if (r < rows && c < cols) dst[c * rows + r] = tile[threadIdx.x][i];
+    }
+}
+
 // ---------------------------------------------------------------- embedding
 __global__ void embedding_kernel(const uint16_t* __restrict__ table, const float* __restrict__ ids,
                                  uint16_t* __restrict__ out, size_t n, int hidden, size_t vocab,
@@ -345,6 +361,16 @@ int cactus_hip_multiply_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, s
     CH_REQUIRE(a && b && y, "multiply: null pointer");
     hipLaunchKernelGGL(mul_kernel, dim3(grid_for(n, 256)), dim3(256), 0, as_stream(stream), a, b, y, n);
     return check_launch("multiply");
+}
+
+int cactus_hip_transpose_2d_f16(const uint16_t* src, uint16_t* dst, size_t rows, size_t cols,
+                                void* stream) {
+    if (rows == 0 || cols == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(src && dst, "transpose: null pointer");
+    CH_REQUIRE(rows / 32 < 65535 && cols / 32 < (1u << 30), "transpose: shape too large");
+    hipLaunchKernelGGL(transpose_kernel, dim3(ceil_div(cols, 32), ceil_div(rows, 32)), dim3(32, 8), 0,
+                       as_stream(stream), src, dst, rows, cols);
+    return check_launch("transpose");
 }
 
 int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* out,

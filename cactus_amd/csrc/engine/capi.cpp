@@ -1,0 +1,315 @@
+// capi.cpp -- extern "C" entry points of include/cactus_engine.h, random
+// weight generation, and the FFI-style generate loop
+// (cactus/ffi/cactus_complete.cpp:185-298).
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "cactus_hip.h"
+#include "engine.h"
+
+namespace cactus {
+
+static thread_local std::string g_engine_error;
+
+template <typename F>
+static int guarded(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception& e) {
+        g_engine_error = e.what();
+        return -1;
+    }
+}
+
+// ---------------------------------------------------------------- random init
+static inline uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+static uint16_t f2h_host(float f) {
+    const double d = (double)f;
+    uint64_t b;
+    std::memcpy(&b, &d, 8);
+    const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    const uint64_t a = b & 0x7FFFFFFFFFFFFFFFull;
+    const int e = (int)(a >> 52);
+    if (e == 0x7FF) return sign | ((a & 0xFFFFFFFFFFFFFull) ? 0x7E00 : 0x7C00);
+    if (a == 0) return sign;
+    const uint64_t mant = (a & 0xFFFFFFFFFFFFFull) | (1ull << 52);
+    const int ex = e - 1023;
+    if (ex > 15) return sign | 0x7C00;
+    const int shift = ex >= -14 ? 42 : 42 + (-14 - ex);
+    if (shift > 63) return sign;
+    uint64_t q = mant >> shift;
+    const uint64_t rem = mant & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    const uint32_t r = ex >= -14 ? ((uint32_t)(ex + 15) << 10) + (uint32_t)(q - 1024) : (uint32_t)q;
+    return r >= 0x7C00 ? (sign | 0x7C00) : (sign | (uint16_t)r);
+}
+
+// Deterministic parallel fill: element i of tensor `tag` draws from stream
+// (seed, tag, i / 65536), so the values do not depend on the thread count.
+template <typename Fn>
+static void parallel_fill(size_t n, uint64_t seed, uint64_t tag, Fn fn) {
+    const size_t blk = 65536;
+    const size_t nblk = (n + blk - 1) / blk;
+    unsigned nt = std::thread::hardware_concurrency();
+    if (nt == 0) nt = 4;
+    if (nt > 16) nt = 16;
+    std::vector<std::thread> th;
+    for (unsigned t = 0; t < nt; t++) {
+        th.emplace_back([&, t] {
+            for (size_t b = t; b < nblk; b += nt) {
+                uint64_t s = seed * 0x100000001B3ull ^ (tag << 40) ^ (b * 0x9E3779B97F4A7C15ull);
+                const size_t e = std::min(n, (b + 1) * blk);
+                for (size_t i = b * blk; i < e; i++) fn(i, s);
+            }
+        });
+    }
+    for (auto& x : th) x.join();
+}
+
+static inline double unif01(uint64_t& s) { return (double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0); }
+static inline double normal(uint64_t& s) {
+    double u1 = unif01(s), u2 = unif01(s);
+    if (u1 < 1e-300) u1 = 1e-300;
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+}
+
+struct HostWeights {
+    std::vector<std::vector<int8_t>> q_w, k_w, v_w, o_w;
+    std::vector<std::vector<uint8_t>> gate_w, up_w, down_w;
+    std::vector<std::vector<uint16_t>> q_s, k_s, v_s, o_s, gate_s, up_s, down_s;
+    std::vector<std::vector<uint16_t>> in_norm, post_norm, q_norm, k_norm;
+    std::vector<uint16_t> emb, out_norm;
+    std::vector<cactus_qwen_layer_weights> layers;
+};
+
+static void make_random(const cactus_qwen_config& c, uint64_t seed, HostWeights& w) {
+    const size_t H = c.hidden, F = c.ffn, hd = c.head_dim, gs = c.group_size;
+    const size_t nq = (size_t)c.heads * hd, nkv = (size_t)c.kv_heads * hd;
+    uint64_t tag = 1;
+    auto codes8 = [&](size_t n) {
+        std::vector<int8_t> v(n);
+        parallel_fill(n, seed, tag++, [&](size_t i, uint64_t& s) { v[i] = (int8_t)((int)(splitmix64(s) % 255) - 127); });
+        return v;
+    };
+    auto codes4 = [&](size_t rows, size_t cols) {  // packed, low nibble = even column
+        std::vector<uint8_t> v(rows * cols / 2);
+        parallel_fill(v.size(), seed, tag++, [&](size_t i, uint64_t& s) {
+            const int lo = (int)(splitmix64(s) % 15) - 7, hi = (int)(splitmix64(s) % 15) - 7;
+            v[i] = (uint8_t)((lo & 0x0F) | ((hi & 0x0F) << 4));
+        });
+        return v;
+    };
+    auto scales = [&](size_t n, double qmax) {
+        std::vector<uint16_t> v(n);
+        parallel_fill(n, seed, tag++, [&](size_t i, uint64_t& s) { v[i] = f2h_host((float)(std::fabs(normal(s) * 0.02) / qmax)); });
+        return v;
+    };
+    auto gauss = [&](size_t n, double mean, double sd) {
+        std::vector<uint16_t> v(n);
+        parallel_fill(n, seed, tag++, [&](size_t i, uint64_t& s) { v[i] = f2h_host((float)(mean + sd * normal(s))); });
+        return v;
+    };
+    const uint32_t L = c.num_layers;
+    for (uint32_t l = 0; l < L; l++) {
+        w.in_norm.push_back(gauss(H, 1.0, 0.02));
+        w.post_norm.push_back(gauss(H, 1.0, 0.02));
+        w.q_norm.push_back(gauss(hd, 1.0, 0.02));
+        w.k_norm.push_back(gauss(hd, 1.0, 0.02));
+        w.q_w.push_back(codes8(nq * H));
+        w.q_s.push_back(scales(nq * (H / gs), 127.0));
+        w.k_w.push_back(codes8(nkv * H));
+        w.k_s.push_back(scales(nkv * (H / gs), 127.0));
+        w.v_w.push_back(codes8(nkv * H));
+        w.v_s.push_back(scales(nkv * (H / gs), 127.0));
+        w.o_w.push_back(codes8(H * nq));
+        w.o_s.push_back(scales(H * (nq / gs), 127.0));
+        w.gate_w.push_back(codes4(F, H));
+        w.gate_s.push_back(scales(F * (H / gs), 7.0));
+        w.up_w.push_back(codes4(F, H));
+        w.up_s.push_back(scales(F * (H / gs), 7.0));
+        w.down_w.push_back(codes4(H, F));
+        w.down_s.push_back(scales(H * (F / gs), 7.0));
+    }
+    w.emb = gauss((size_t)c.vocab * H, 0.0, 0.02);
+    w.out_norm = gauss(H, 1.0, 0.02);
+    w.layers.resize(L);
+    for (uint32_t l = 0; l < L; l++) {
+        cactus_qwen_layer_weights& x = w.layers[l];
+        x.input_norm = w.in_norm[l].data();
+        x.post_norm = w.post_norm[l].data();
+        x.q_norm = w.q_norm[l].data();
+        x.k_norm = w.k_norm[l].data();
+        x.q_w = w.q_w[l].data(); x.q_s = w.q_s[l].data();
+        x.k_w = w.k_w[l].data(); x.k_s = w.k_s[l].data();
+        x.v_w = w.v_w[l].data(); x.v_s = w.v_s[l].data();
+        x.o_w = w.o_w[l].data(); x.o_s = w.o_s[l].data();
+        x.gate_w = w.gate_w[l].data(); x.gate_s = w.gate_s[l].data();
+        x.up_w = w.up_w[l].data(); x.up_s = w.up_s[l].data();
+        x.down_w = w.down_w[l].data(); x.down_s = w.down_s[l].data();
+    }
+}
+
+static void validate(const cactus_qwen_config* c) {
+    if (!c) throw std::runtime_error("null config");
+    if (!c->num_layers || !c->hidden || !c->ffn || !c->heads || !c->kv_heads || !c->head_dim ||
+        !c->vocab || !c->group_size || !c->max_seq)
+        throw std::runtime_error("config fields must be non-zero");
+}
+
+}  // namespace cactus
+
+using namespace cactus;
+
+extern "C" {
+
+const char* cactus_engine_last_error(void) { return g_engine_error.c_str(); }
+
+int cactus_qwen_create(const cactus_qwen_config* cfg, const cactus_qwen_layer_weights* layers,
+                       const uint16_t* embedding, const uint16_t* output_norm, void** model) {
+    return guarded([&] {
+        validate(cfg);
+        if (!model || !layers || !embedding || !output_norm) throw std::runtime_error("null argument");
+        *model = new QwenModel(*cfg, layers, embedding, output_norm);
+    });
+}
+
+int cactus_qwen_create_random(const cactus_qwen_config* cfg, uint64_t seed, void** model) {
+    return guarded([&] {
+        validate(cfg);
+        if (!model) throw std::runtime_error("null argument");
+        HostWeights w;
+        make_random(*cfg, seed, w);
+        *model = new QwenModel(*cfg, w.layers.data(), w.emb.data(), w.out_norm.data());
+    });
+}
+
+int cactus_qwen_destroy(void* model) {
+    return guarded([&] { delete static_cast<QwenModel*>(model); });
+}
+
+int cactus_qwen_reset(void* model) {
+    return guarded([&] { static_cast<QwenModel*>(model)->reset(); });
+}
+
+int cactus_qwen_set_decode_mode(void* model, int mode) {
+    return guarded([&] { static_cast<QwenModel*>(model)->set_decode_mode(mode); });
+}
+
+int cactus_qwen_prefill(void* model, const uint32_t* tokens, size_t n) {
+    return guarded([&] {
+        static_cast<QwenModel*>(model)->prefill(std::vector<uint32_t>(tokens, tokens + n));
+    });
+}
+
+int cactus_qwen_decode(void* model, uint32_t token, uint32_t* next) {
+    return guarded([&] { *next = static_cast<QwenModel*>(model)->decode(token); });
+}
+
+int cactus_qwen_generate(void* model, const uint32_t* prompt, size_t n, size_t max_new,
+                         uint32_t* out, cactus_qwen_timing* timing) {
+    return guarded([&] {
+        if (n == 0) throw std::runtime_error("Cannot generate from empty prompt");
+        QwenModel* m = static_cast<QwenModel*>(model);
+        using clk = std::chrono::steady_clock;
+        auto ms = [](clk::time_point a, clk::time_point b) {
+            return std::chrono::duration<double, std::milli>(b - a).count();
+        };
+        auto t0 = clk::now();
+        if (n > 1) m->prefill(std::vector<uint32_t>(prompt, prompt + n - 1));
+        check_hip(cactus_hip_stream_sync(m->stream()), "sync");
+        auto t1 = clk::now();
+        uint32_t tok = max_new ? m->decode(prompt[n - 1]) : 0;
+        if (max_new) out[0] = tok;
+        auto t2 = clk::now();
+        for (size_t i = 1; i < max_new; i++) {
+            tok = m->decode(tok);
+            out[i] = tok;
+        }
+        check_hip(cactus_hip_stream_sync(m->stream()), "sync");
+        auto t3 = clk::now();
+        if (timing) {
+            timing->prefill_ms = ms(t0, t1);
+            timing->first_decode_ms = ms(t1, t2);
+            timing->decode_ms = ms(t2, t3);
+            timing->prefill_tokens = (uint32_t)(n - 1);
+            timing->decode_tokens = (uint32_t)(max_new ? max_new - 1 : 0);
+        }
+    });
+}
+
+int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t* rows) {
+    return guarded([&] {
+        QwenModel* m = static_cast<QwenModel*>(model);
+        if (m->last_hidden_node() == SIZE_MAX) throw std::runtime_error("no forward has run");
+        const BufferDesc& b = m->graph().get_output_buffer(m->last_hidden_node());
+        const size_t r = b.shape[0];
+        if (rows) *rows = r;
+        const size_t n = std::min(r, max_rows) * m->config().hidden;
+        check_hip(cactus_hip_memcpy_d2h(out, b.data, n * 2, m->stream()), "last_hidden");
+    });
+}
+
+int cactus_qwen_last_logits(void* model, uint16_t* out) {
+    return guarded([&] {
+        QwenModel* m = static_cast<QwenModel*>(model);
+        if (m->last_logits_node() == SIZE_MAX || m->decode_mode() != 0)
+            throw std::runtime_error("logits are kept by decode mode 0 only");
+        const BufferDesc& b = m->graph().get_output_buffer(m->last_logits_node());
+        check_hip(cactus_hip_memcpy_d2h(out, b.data, b.byte_size, m->stream()), "last_logits");
+    });
+}
+
+int cactus_qwen_cache_len(void* model, size_t* len) {
+    return guarded([&] { *len = static_cast<QwenModel*>(model)->cache().current_seq_len; });
+}
+
+int cactus_qwen_read_kv(void* model, size_t layer, int8_t* k, int8_t* v, float* ks, float* vs) {
+    return guarded([&] {
+        QwenModel* m = static_cast<QwenModel*>(model);
+        KVCache& c = m->cache();
+        if (layer >= c.num_layers) throw std::runtime_error("layer out of range");
+        const size_t n = c.current_seq_len * c.num_kv_heads * c.head_dim;
+        const size_t ns = c.current_seq_len * c.num_kv_heads * c.groups() * sizeof(float);
+        check_hip(cactus_hip_memcpy_d2h(k, c.keys(layer), n, m->stream()), "read_kv");
+        check_hip(cactus_hip_memcpy_d2h(v, c.values(layer), n, m->stream()), "read_kv");
+        check_hip(cactus_hip_memcpy_d2h(ks, c.key_scales(layer), ns, m->stream()), "read_kv");
+        check_hip(cactus_hip_memcpy_d2h(vs, c.value_scales(layer), ns, m->stream()), "read_kv");
+    });
+}
+
+int cactus_qwen_read_weights(void* model, cactus_qwen_layer_weights* lw, uint16_t* emb,
+                             uint16_t* out_norm) {
+    return guarded([&] {
+        QwenModel* m = static_cast<QwenModel*>(model);
+        void* st = m->stream();
+        auto rd = [&](const void* dst, const DevBuf& b) {
+            if (dst) check_hip(cactus_hip_memcpy_d2h(const_cast<void*>(dst), b.ptr, b.bytes, st), "read_weights");
+        };
+        if (emb) rd(emb, m->embedding());
+        if (out_norm) rd(out_norm, m->output_norm());
+        if (!lw) return;
+        for (uint32_t l = 0; l < m->config().num_layers; l++) {
+            const QwenLayer& L = m->layer(l);
+            const cactus_qwen_layer_weights& w = lw[l];
+            rd(w.input_norm, L.input_norm); rd(w.post_norm, L.post_norm);
+            rd(w.q_norm, L.q_norm); rd(w.k_norm, L.k_norm);
+            rd(w.q_w, L.q_w); rd(w.q_s, L.q_s); rd(w.k_w, L.k_w); rd(w.k_s, L.k_s);
+            rd(w.v_w, L.v_w); rd(w.v_s, L.v_s); rd(w.o_w, L.o_w); rd(w.o_s, L.o_s);
+            rd(w.gate_w, L.gate_w); rd(w.gate_s, L.gate_s); rd(w.up_w, L.up_w); rd(w.up_s, L.up_s);
+            rd(w.down_w, L.down_w); rd(w.down_s, L.down_s);
+        }
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// engine.h -- device KV cache and the Qwen3 model over the device graph
+// (reference: cactus/engine/engine.h KVCache :325-382, Model :473-577;
+// cactus/models/model_qwen.cpp).
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+#include "cactus_engine.h"
+#include "graph.h"
+
+namespace cactus {
+
+// Device buffer owned by the engine (weights, cache).
+struct DevBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    DevBuf() = default;
+    explicit DevBuf(size_t n);
+    ~DevBuf();
+    DevBuf(const DevBuf&) = delete;
+    DevBuf& operator=(const DevBuf&) = delete;
+    DevBuf(DevBuf&& o) noexcept : ptr(o.ptr), bytes(o.bytes) { o.ptr = nullptr; o.bytes = 0; }
+    DevBuf& operator=(DevBuf&& o) noexcept;
+    void upload(const void* host, size_t n, void* stream);
+    template <typename T> T* as() const { return static_cast<T*>(ptr); }
+};
+
+// INT8 KV cache, one per-token/per-kv-head scale per 128 dims
+// (KV_QUANT_GROUP_SIZE, kernel.h:18; engine_cache.cpp:234-267).  Append-only:
+// capacity must cover the sequence (the sliding window is not built).
+class KVCache {
+public:
+    static constexpr size_t GROUP = 128;
+    void init(size_t layers, size_t max_seq, size_t kv_heads, size_t head_dim);
+    void reset() { current_seq_len = 0; total_seq_len = 0; }
+    bool is_empty() const { return current_seq_len == 0; }
+    // quantize `seq` new fp16 tokens [seq][kv_heads][head_dim] of one layer
+    void append(size_t layer, const void* k_fp16, const void* v_fp16, size_t seq, void* stream);
+    void commit(size_t seq) { current_seq_len += seq; total_seq_len += seq; }
+    const int8_t* keys(size_t l) const { return k_[l].as<int8_t>(); }
+    const int8_t* values(size_t l) const { return v_[l].as<int8_t>(); }
+    const float* key_scales(size_t l) const { return ks_[l].as<float>(); }
+    const float* value_scales(size_t l) const { return vs_[l].as<float>(); }
+    int8_t* keys_mut(size_t l) { return k_[l].as<int8_t>(); }
+    int8_t* values_mut(size_t l) { return v_[l].as<int8_t>(); }
+    float* key_scales_mut(size_t l) { return ks_[l].as<float>(); }
+    float* value_scales_mut(size_t l) { return vs_[l].as<float>(); }
+    size_t groups() const { return (head_dim + GROUP - 1) / GROUP; }
+
+    size_t current_seq_len = 0, total_seq_len = 0;
+    size_t max_seq_len = 0, num_layers = 0, num_kv_heads = 0, head_dim = 0;
+
+private:
+    std::vector<DevBuf> k_, v_, ks_, vs_;
+};
+
+struct QwenLayer {
+    DevBuf input_norm, q_w, q_s, k_w, k_s, v_w, v_s, o_w, o_s, q_norm, k_norm, post_norm;
+    DevBuf gate_w, gate_s, up_w, up_s, down_w, down_s;
+    // graph node ids of the weights
+    size_t n_input_norm, n_q, n_k, n_v, n_o, n_q_norm, n_k_norm, n_post_norm, n_gate, n_up, n_down;
+};
+
+class FusedDecoder;  // fused per-layer decode path (decode_fused.cpp)
+
+class QwenModel {
+public:
+    QwenModel(const cactus_qwen_config& cfg, const cactus_qwen_layer_weights* layers,
+              const uint16_t* embedding, const uint16_t* output_norm);
+    ~QwenModel();
+
+    void reset();
+    void prefill(const std::vector<uint32_t>& tokens);
+    uint32_t decode(uint32_t token);
+    void set_decode_mode(int mode);
+    int decode_mode() const { return decode_mode_; }
+
+    const cactus_qwen_config& config() const { return cfg_; }
+    KVCache& cache() { return cache_; }
+    CactusGraph& graph() { return *graph_; }
+    void* stream() const { return stream_; }
+    size_t last_hidden_node() const { return last_hidden_; }
+    size_t last_logits_node() const { return last_logits_; }
+    const QwenLayer& layer(size_t i) const { return layers_[i]; }
+    const DevBuf& embedding() const { return embedding_; }
+    const DevBuf& output_norm() const { return out_norm_; }
+    float attention_scale() const { return attn_scale_; }
+
+private:
+    size_t forward(const std::vector<uint32_t>& tokens);
+    size_t build_attention(size_t x, uint32_t l, size_t pos);
+    size_t build_mlp(size_t x, uint32_t l);
+    size_t build_block(size_t h, uint32_t l, size_t pos);
+    void update_kv_cache(size_t seq);
+
+    cactus_qwen_config cfg_;
+    void* stream_ = nullptr;
+    std::unique_ptr<CactusGraph> graph_;
+    std::vector<QwenLayer> layers_;
+    DevBuf embedding_, out_norm_;
+    size_t n_embedding_ = 0, n_out_norm_ = 0;
+    KVCache cache_;
+    float attn_scale_ = 0.0f;
+    std::vector<size_t> k_nodes_, v_nodes_;
+    size_t last_hidden_ = SIZE_MAX, last_logits_ = SIZE_MAX;
+    int decode_mode_ = 0;
+    std::unique_ptr<FusedDecoder> fused_;
+    friend class FusedDecoder;
+};
+
+}  // namespace cactus

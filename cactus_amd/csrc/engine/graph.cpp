@@ -1,0 +1,529 @@
+// graph.cpp -- builder and serial executor of the device-resident CactusGraph.
+//
+// Shape/precision inference follows graph_builder.cpp; node execution follows
+// the per-op executors of graph_ops_nn.cpp, graph_ops_math.cpp,
+// graph_ops_tensor.cpp and graph_ops_sample.cpp, with every compute step a
+// call into the kernel C ABI.  RESHAPE and INDEX(dim 0) are views here (the
+// reference copies for RESHAPE, graph_ops_math.cpp:265-281); values are
+// identical.
+#include "graph.h"
+
+#include <algorithm>
+#include <cstring>
+#include <numeric>
+
+#include "cactus_hip.h"
+
+namespace cactus {
+
+void check_hip(int rc, const char* what) {
+    if (rc != CACTUS_HIP_OK)
+        throw std::runtime_error(std::string(what) + ": " + cactus_hip_last_error());
+}
+
+size_t precision_size(Precision p) {
+    switch (p) {
+        case Precision::INT8: return 1;
+        case Precision::FP16: return 2;
+        case Precision::FP32: return 4;
+        case Precision::INT4: return 1;
+    }
+    return 1;
+}
+
+static size_t numel(const std::vector<size_t>& s) {
+    return std::accumulate(s.begin(), s.end(), (size_t)1, std::multiplies<size_t>());
+}
+
+// ------------------------------------------------------------------ BufferPool
+size_t BufferPool::round_up(size_t b) {
+    if (b <= 256) return 256;
+    size_t p = 256;
+    while (p < b) p <<= 1;
+    return p;
+}
+
+void* BufferPool::acquire(size_t bytes) {
+    const size_t b = round_up(bytes);
+    auto& fl = free_[b];
+    if (!fl.empty()) {
+        void* p = fl.back();
+        fl.pop_back();
+        return p;
+    }
+    void* p = nullptr;
+    check_hip(cactus_hip_malloc(&p, b), "BufferPool::acquire");
+    pool_bytes_ += b;
+    return p;
+}
+
+void BufferPool::release(void* ptr, size_t bytes) {
+    if (ptr) free_[round_up(bytes)].push_back(ptr);
+}
+
+void BufferPool::clear() {
+    for (auto& kv : free_)
+        for (void* p : kv.second) cactus_hip_free(p);
+    free_.clear();
+    pool_bytes_ = 0;
+}
+
+BufferPool::~BufferPool() { clear(); }
+
+// ------------------------------------------------------------------ CactusGraph
+CactusGraph::CactusGraph(void* stream) : stream_(stream) {}
+
+CactusGraph::~CactusGraph() {
+    cactus_hip_stream_sync(stream_);
+    hard_reset();
+    if (quant_codes_) cactus_hip_free(quant_codes_);
+    if (quant_scales_) cactus_hip_free(quant_scales_);
+    if (embed_err_) cactus_hip_free(embed_err_);
+}
+
+GraphNode& CactusGraph::node(size_t id) {
+    auto it = index_.find(id);
+    if (it == index_.end()) throw std::runtime_error("unknown node " + std::to_string(id));
+    return *nodes_[it->second];
+}
+const GraphNode& CactusGraph::node(size_t id) const {
+    auto it = index_.find(id);
+    if (it == index_.end()) throw std::runtime_error("unknown node " + std::to_string(id));
+    return *nodes_[it->second];
+}
+
+size_t CactusGraph::add_node(OpType op, const std::vector<size_t>& inputs,
+                             const std::vector<size_t>& shape, Precision precision,
+                             const OpParams& params) {
+    auto n = std::make_unique<GraphNode>();
+    n->id = next_id_++;
+    n->op = op;
+    n->inputs = inputs;
+    n->params = params;
+    n->out.shape = shape;
+    n->out.precision = precision;
+    n->out.total_size = numel(shape);
+    n->out.byte_size = n->out.total_size * precision_size(precision);
+    index_[n->id] = nodes_.size();
+    nodes_.push_back(std::move(n));
+    return nodes_.back()->id;
+}
+
+const BufferDesc& CactusGraph::get_output_buffer(size_t id) const { return node(id).out; }
+
+size_t CactusGraph::input(const std::vector<size_t>& shape, Precision precision) {
+    return add_node(OpType::INPUT, {}, shape, precision);
+}
+
+size_t CactusGraph::matmul(size_t a, size_t b, bool pretransposed_rhs) {
+    const auto& as = node(a).out.shape;
+    const auto& bs = node(b).out.shape;
+    if (as.size() < 2 || bs.size() != 2) throw std::runtime_error("matmul expects [.., M, K] x 2D");
+    const size_t K = as.back();
+    const size_t N = pretransposed_rhs ? bs[0] : bs[1];
+    const size_t Kb = pretransposed_rhs ? bs[1] : bs[0];
+    if (K != Kb) throw std::runtime_error("matmul: inner dimensions differ");
+    std::vector<size_t> out(as.begin(), as.end() - 1);
+    out.push_back(N);
+    OpParams p;
+    p.pretransposed_rhs = pretransposed_rhs;
+    return add_node(OpType::MATMUL, {a, b}, out, Precision::FP16, p);
+}
+
+size_t CactusGraph::quantize_activations(size_t input) {
+    return add_node(OpType::QUANTIZE_ACTIVATIONS, {input}, node(input).out.shape, Precision::INT8);
+}
+
+size_t CactusGraph::rms_norm(size_t input, size_t weight, float epsilon) {
+    OpParams p;
+    p.epsilon = epsilon;
+    return add_node(OpType::RMS_NORM, {input, weight}, node(input).out.shape, Precision::FP16, p);
+}
+
+size_t CactusGraph::rope(size_t input, float theta, size_t position_offset) {
+    OpParams p;
+    p.theta = theta;
+    p.position_offset = position_offset;
+    return add_node(OpType::ROPE, {input}, node(input).out.shape, Precision::FP16, p);
+}
+
+size_t CactusGraph::softmax(size_t input, int axis) {
+    OpParams p;
+    p.axis = axis;
+    return add_node(OpType::SOFTMAX, {input}, node(input).out.shape, Precision::FP16, p);
+}
+
+size_t CactusGraph::attention(size_t q, size_t k, size_t v, float scale, size_t position_offset,
+                              size_t window_size, bool is_causal) {
+    OpParams p;
+    p.scale = scale;
+    p.position_offset = position_offset;
+    p.window_size = window_size;
+    p.is_causal = is_causal;
+    return add_node(OpType::ATTENTION, {q, k, v}, node(q).out.shape, Precision::FP16, p);
+}
+
+size_t CactusGraph::attention_int8_hybrid(size_t q, size_t k_new, size_t v_new, float scale,
+                                          size_t position_offset, const int8_t* ck,
+                                          const int8_t* cv, const float* ks, const float* vs,
+                                          size_t cache_len, size_t num_kv_heads, size_t head_dim) {
+    OpParams p;
+    p.scale = scale;
+    p.position_offset = position_offset;
+    p.cached_keys_int8 = ck;
+    p.cached_values_int8 = cv;
+    p.cached_k_scales = ks;
+    p.cached_v_scales = vs;
+    p.cache_seq_len = cache_len;
+    p.num_kv_heads = num_kv_heads;
+    p.head_dim = head_dim;
+    return add_node(OpType::ATTENTION_INT8_HYBRID, {q, k_new, v_new}, node(q).out.shape,
+                    Precision::FP16, p);
+}
+
+size_t CactusGraph::silu(size_t input) {
+    return add_node(OpType::SILU, {input}, node(input).out.shape, Precision::FP16);
+}
+
+size_t CactusGraph::add(size_t a, size_t b) {
+    if (node(a).out.total_size != node(b).out.total_size)
+        throw std::runtime_error("add: broadcasting is not built (shapes must match)");
+    return add_node(OpType::ADD, {a, b}, node(a).out.shape, Precision::FP16);
+}
+
+size_t CactusGraph::multiply(size_t a, size_t b) {
+    if (node(a).out.total_size != node(b).out.total_size)
+        throw std::runtime_error("multiply: broadcasting is not built (shapes must match)");
+    return add_node(OpType::MULTIPLY, {a, b}, node(a).out.shape, Precision::FP16);
+}
+
+size_t CactusGraph::embedding(size_t table, size_t indices) {
+    const auto& ts = node(table).out.shape;
+    if (ts.size() != 2) throw std::runtime_error("embedding table must be 2D");
+    return add_node(OpType::EMBEDDING, {table, indices}, {node(indices).out.total_size, ts[1]},
+                    Precision::FP16);
+}
+
+size_t CactusGraph::index(size_t input, size_t index_value, int dim) {
+    const auto& s = node(input).out.shape;
+    if (dim != 0 || s.empty()) throw std::runtime_error("index: only dim 0 is built");
+    if (index_value >= s[0]) throw std::runtime_error("index out of range");
+    OpParams p;
+    p.index_value = index_value;
+    p.axis = dim;
+    std::vector<size_t> out(s.begin() + 1, s.end());
+    if (out.empty()) out.push_back(1);
+    return add_node(OpType::INDEX, {input}, out, node(input).out.precision, p);
+}
+
+size_t CactusGraph::reshape(size_t input, const std::vector<size_t>& new_shape) {
+    if (numel(new_shape) != node(input).out.total_size)
+        throw std::runtime_error("reshape: element count changes");
+    OpParams p;
+    p.new_shape = new_shape;
+    return add_node(OpType::RESHAPE, {input}, new_shape, node(input).out.precision, p);
+}
+
+size_t CactusGraph::sample(size_t logits, float temperature, float top_p, size_t top_k) {
+    OpParams p;
+    p.temperature = temperature;
+    p.top_p = top_p;
+    p.top_k = top_k;
+    return add_node(OpType::SAMPLE, {logits}, {1}, Precision::FP32, p);
+}
+
+// ------------------------------------------------------------------ data
+void CactusGraph::set_input(size_t id, const void* host, Precision precision) {
+    GraphNode& n = node(id);
+    if (n.op != OpType::INPUT) throw std::runtime_error("set_input on a non-input node");
+    n.out.precision = precision;
+    n.out.byte_size = n.out.total_size * precision_size(precision);
+    if (!n.out.data || n.out.external) {
+        n.out.data = pool_.acquire(n.out.byte_size);
+        n.out.pooled_bytes = n.out.byte_size;
+        n.out.external = false;
+    }
+    check_hip(cactus_hip_memcpy_h2d(n.out.data, host, n.out.byte_size, stream_), "set_input");
+}
+
+void CactusGraph::set_external_input(size_t id, void* dev, Precision precision) {
+    GraphNode& n = node(id);
+    if (n.op != OpType::INPUT) throw std::runtime_error("set_external_input on a non-input node");
+    n.out.precision = precision;
+    n.out.byte_size = n.out.total_size * precision_size(precision);
+    n.out.data = dev;
+    n.out.external = true;
+}
+
+void CactusGraph::set_grouped_scales(size_t id, size_t group_size, size_t num_groups,
+                                     const void* scales) {
+    BufferDesc& b = node(id).out;
+    b.group_size = group_size;
+    b.num_groups = num_groups;
+    b.scales = scales;
+}
+
+void CactusGraph::set_packed_int4(size_t id, const void* packed, size_t packed_size) {
+    BufferDesc& b = node(id).out;
+    b.packed_int4 = packed;
+    b.packed_int4_size = packed_size;
+}
+
+void* CactusGraph::get_output(size_t id) {
+    const BufferDesc& b = node(id).out;
+    if (!b.data) throw std::runtime_error("get_output: node has no data (not executed?)");
+    auto& m = host_mirror_[id];
+    m.resize(b.byte_size);
+    check_hip(cactus_hip_memcpy_d2h(m.data(), b.data, b.byte_size, stream_), "get_output");
+    return m.data();
+}
+
+// ------------------------------------------------------------------ execution
+void CactusGraph::allocate(GraphNode& n) {
+    if (n.op == OpType::INPUT) {
+        if (!n.out.data) throw std::runtime_error("input node " + std::to_string(n.id) + " has no data");
+        return;
+    }
+    if (n.op == OpType::RESHAPE) {
+        const BufferDesc& src = node(n.inputs[0]).out;
+        n.out.data = src.data;
+        n.out.external = true;
+        n.out.group_size = src.group_size;
+        n.out.num_groups = src.num_groups;
+        n.out.scales = src.scales;
+        n.out.activation_scales = src.activation_scales;
+        return;
+    }
+    if (n.op == OpType::INDEX) {  // dim 0: a view (graph_ops_tensor.cpp:357-361)
+        const BufferDesc& src = node(n.inputs[0]).out;
+        const size_t slice = src.total_size / src.shape[0];
+        n.out.data = static_cast<char*>(src.data) + n.params.index_value * slice * precision_size(src.precision);
+        n.out.external = true;
+        return;
+    }
+    if (!n.out.data) {
+        n.out.data = pool_.acquire(n.out.byte_size);
+        n.out.pooled_bytes = n.out.byte_size;
+    }
+    if (n.op == OpType::QUANTIZE_ACTIVATIONS && !n.out.activation_scales) {
+        const auto& s = n.out.shape;
+        const size_t rows = n.out.total_size / s.back();
+        n.out.activation_scales = pool_.acquire(rows * sizeof(float));
+    }
+}
+
+void CactusGraph::compute(GraphNode& n) {
+    void* st = stream_;
+    auto in = [&](int i) -> const BufferDesc& { return node(n.inputs[i]).out; };
+    auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+    uint16_t* out16 = static_cast<uint16_t*>(n.out.data);
+    switch (n.op) {
+        case OpType::INPUT:
+        case OpType::RESHAPE:
+        case OpType::INDEX:
+            return;
+        case OpType::QUANTIZE_ACTIVATIONS: {  // graph_ops_nn.cpp:78-127
+            const BufferDesc& x = in(0);
+            if (x.precision != Precision::FP16) throw std::runtime_error("QUANTIZE_ACTIVATIONS requires FP16 input");
+            const size_t K = x.shape.back(), M = x.total_size / K;
+            check_hip(cactus_hip_quantize_activations(u16(x.data), static_cast<int8_t*>(n.out.data),
+                                                      static_cast<float*>(n.out.activation_scales), M, K, st),
+                      "quantize_activations");
+            return;
+        }
+        case OpType::MATMUL: {  // graph_ops_nn.cpp:129-231
+            const BufferDesc& a = in(0);
+            const BufferDesc& b = in(1);
+            const size_t K = a.shape.back();
+            const size_t M = a.total_size / K;
+            const size_t N = n.out.shape.back();
+            const bool preq = a.precision == Precision::INT8 && a.activation_scales;
+            if (b.is_packed_int4() || b.is_grouped_int8()) {
+                if (!n.params.pretransposed_rhs)
+                    throw std::runtime_error("grouped INT8/INT4 matmul requires pretransposed weights");
+                if (!preq && a.precision != Precision::FP16)
+                    throw std::runtime_error("grouped matmul requires INT8 (pre-quantized) or FP16 activations");
+                const uint16_t* bs = u16(b.scales);
+                if (b.is_packed_int4()) {
+                    const uint8_t* bp = static_cast<const uint8_t*>(b.packed_int4);
+                    if (preq)
+                        check_hip(cactus_hip_matmul_int4(static_cast<const int8_t*>(a.data),
+                                                         static_cast<const float*>(a.activation_scales),
+                                                         bp, bs, out16, M, K, N, b.group_size, st),
+                                  "matmul_int4");
+                    else
+                        check_hip(cactus_hip_matmul_int4_f16act(u16(a.data), bp, bs, out16, M, K, N,
+                                                                b.group_size, st),
+                                  "matmul_int4_f16act");
+                } else {
+                    const int8_t* bw = static_cast<const int8_t*>(b.data);
+                    if (preq)
+                        check_hip(cactus_hip_matmul_int8(static_cast<const int8_t*>(a.data),
+                                                         static_cast<const float*>(a.activation_scales),
+                                                         bw, bs, out16, M, K, N, b.group_size, st),
+                                  "matmul_int8");
+                    else
+                        check_hip(cactus_hip_matmul_int8_f16act(u16(a.data), bw, bs, out16, M, K, N,
+                                                                b.group_size, st),
+                                  "matmul_int8_f16act");
+                }
+                return;
+            }
+            if (a.precision != Precision::FP16 || b.precision != Precision::FP16)
+                throw std::runtime_error("FP16 matmul requires FP16 operands");
+            if (n.params.pretransposed_rhs) {
+                check_hip(cactus_hip_matmul_f16(u16(a.data), u16(b.data), out16, M, K, N, st), "matmul_f16");
+            } else {
+                void* t = pool_.acquire(b.byte_size);
+                check_hip(cactus_hip_transpose_2d_f16(u16(b.data), static_cast<uint16_t*>(t), b.shape[0],
+                                                      b.shape[1], st),
+                          "transpose");
+                check_hip(cactus_hip_matmul_f16(u16(a.data), u16(t), out16, M, K, N, st), "matmul_f16");
+                check_hip(cactus_hip_stream_sync(st), "matmul_f16 sync");
+                pool_.release(t, b.byte_size);
+            }
+            return;
+        }
+        case OpType::RMS_NORM: {  // graph_ops_nn.cpp:233-251
+            const BufferDesc& x = in(0);
+            if (x.shape.size() != 2) throw std::runtime_error("RMS normalization requires 2D input tensor");
+            check_hip(cactus_hip_rms_norm_f16(u16(x.data), u16(in(1).data), out16, x.shape[0], x.shape[1],
+                                              n.params.epsilon, st),
+                      "rms_norm");
+            return;
+        }
+        case OpType::ROPE: {  // graph_ops_nn.cpp:253-277
+            const auto& s = in(0).shape;
+            if (s.size() < 4) throw std::runtime_error("RoPE operation requires 4D tensor");
+            check_hip(cactus_hip_rope_f16(u16(in(0).data), out16, s[0], s[1], s[2], s[3],
+                                          n.params.position_offset, n.params.theta, st),
+                      "rope");
+            return;
+        }
+        case OpType::SOFTMAX: {  // graph_ops_nn.cpp:279-300
+            const auto& s = in(0).shape;
+            if (s.size() < 2) throw std::runtime_error("Softmax operation requires at least 2D tensor");
+            const size_t V = s.back();
+            check_hip(cactus_hip_softmax_f16(u16(in(0).data), out16, in(0).total_size / V, 1, V, st),
+                      "softmax");
+            return;
+        }
+        case OpType::ATTENTION: {  // graph_ops_nn.cpp:302-338
+            const auto& q = in(0).shape;
+            const auto& k = in(1).shape;
+            if (q.size() < 4) throw std::runtime_error("Attention operation requires 4D tensors");
+            check_hip(cactus_hip_attention_f16(u16(in(0).data), u16(in(1).data), u16(in(2).data), out16,
+                                               q[0], q[1], k[1], q[2], k[2], q[3], n.params.scale, nullptr,
+                                               n.params.position_offset, n.params.window_size,
+                                               n.params.is_causal ? 1 : 0, st),
+                      "attention");
+            return;
+        }
+        case OpType::ATTENTION_INT8_HYBRID: {  // graph_ops_nn.cpp:340-371
+            const auto& q = in(0).shape;
+            const auto& p = n.params;
+            check_hip(cactus_hip_attention_hybrid_int8_fp16(
+                          u16(in(0).data), p.cached_keys_int8, p.cached_values_int8, p.cached_k_scales,
+                          p.cached_v_scales, u16(in(1).data), u16(in(2).data), out16, q[0], q[1],
+                          p.cache_seq_len, in(1).shape[1], q[2], p.num_kv_heads, p.head_dim, p.scale,
+                          p.position_offset, 1, 128, st),
+                      "attention_int8_hybrid");
+            return;
+        }
+        case OpType::SILU:
+            check_hip(cactus_hip_silu_f16(u16(in(0).data), out16, in(0).total_size, st), "silu");
+            return;
+        case OpType::ADD:
+            check_hip(cactus_hip_add_f16(u16(in(0).data), u16(in(1).data), out16, n.out.total_size, st), "add");
+            return;
+        case OpType::MULTIPLY:
+            check_hip(cactus_hip_multiply_f16(u16(in(0).data), u16(in(1).data), out16, n.out.total_size, st),
+                      "multiply");
+            return;
+        case OpType::EMBEDDING: {  // graph_ops_tensor.cpp:301-329 (FP16 table, FP32 ids)
+            const BufferDesc& t = in(0);
+            const BufferDesc& ids = in(1);
+            if (t.precision != Precision::FP16 || ids.precision != Precision::FP32)
+                throw std::runtime_error("embedding: FP16 table with FP32 indices only");
+            if (!embed_err_) check_hip(cactus_hip_malloc(reinterpret_cast<void**>(&embed_err_), 4), "malloc");
+            check_hip(cactus_hip_memset(embed_err_, 0, 4, st), "memset");
+            check_hip(cactus_hip_embedding_f16(u16(t.data), static_cast<const float*>(ids.data), out16,
+                                               ids.total_size, t.shape[1], t.shape[0], embed_err_, st),
+                      "embedding");
+            return;
+        }
+        case OpType::SAMPLE: {  // graph_ops_sample.cpp:8-39
+            const BufferDesc& l = in(0);
+            if (l.shape.size() != 2) throw std::runtime_error("Sample expects 2D logits tensor [seq_len, vocab_size]");
+            const size_t V = l.shape[1];
+            const uint16_t* last = u16(l.data) + (l.shape[0] - 1) * V;
+            check_hip(cactus_hip_sample_f16(last, static_cast<uint32_t*>(n.out.data), V, n.params.temperature,
+                                            n.params.top_p, n.params.top_k, 0, st),
+                      "sample");
+            return;
+        }
+    }
+}
+
+void CactusGraph::execute() {
+    for (auto& n : nodes_) {
+        allocate(*n);
+        compute(*n);
+    }
+    if (embed_err_) {
+        int err = 0;
+        check_hip(cactus_hip_memcpy_d2h(&err, embed_err_, 4, stream_), "embedding check");
+        if (err) throw std::runtime_error("Embedding index out of bounds");
+    }
+}
+
+void CactusGraph::release_outputs() {
+    for (auto& n : nodes_) {
+        if (n->out.pooled_bytes && !n->out.external) {
+            pool_.release(n->out.data, n->out.pooled_bytes);
+            n->out.data = nullptr;
+            n->out.pooled_bytes = 0;
+        }
+        if (n->op == OpType::QUANTIZE_ACTIVATIONS && n->out.activation_scales) {
+            const size_t rows = n->out.total_size / n->out.shape.back();
+            pool_.release(n->out.activation_scales, rows * sizeof(float));
+            n->out.activation_scales = nullptr;
+        }
+    }
+}
+
+void CactusGraph::soft_reset() {
+    // graph_execute.cpp:640-675: keep INPUT nodes whose data is external
+    // (weights), drop everything else; buffers go back to the pool
+    check_hip(cactus_hip_stream_sync(stream_), "soft_reset sync");
+    std::vector<std::unique_ptr<GraphNode>> keep;
+    size_t max_id = 0;
+    bool any = false;
+    for (auto& n : nodes_) {
+        if (n->op == OpType::INPUT && n->out.external) {
+            max_id = std::max(max_id, n->id);
+            any = true;
+            keep.push_back(std::move(n));
+        } else if (n->out.pooled_bytes && !n->out.external) {
+            pool_.release(n->out.data, n->out.pooled_bytes);
+            if (n->op == OpType::QUANTIZE_ACTIVATIONS && n->out.activation_scales)
+                pool_.release(n->out.activation_scales, n->out.total_size / n->out.shape.back() * sizeof(float));
+        }
+    }
+    nodes_ = std::move(keep);
+    index_.clear();
+    for (size_t i = 0; i < nodes_.size(); i++) index_[nodes_[i]->id] = i;
+    next_id_ = any ? max_id + 1 : 0;
+    host_mirror_.clear();
+}
+
+void CactusGraph::hard_reset() {
+    release_outputs();
+    nodes_.clear();
+    index_.clear();
+    host_mirror_.clear();
+    next_id_ = 0;
+    pool_.clear();
+}
+
+}  // namespace cactus

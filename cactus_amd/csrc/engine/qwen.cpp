@@ -1,0 +1,289 @@
+// qwen.cpp -- KV cache and the Qwen3 block over the device graph.
+//
+//   QwenModel::build_attention/build_mlp/build_transformer_block/forward
+//                                   models/model_qwen.cpp:51-172
+//   Model::prefill                  engine/engine_model.cpp:170-219
+//   Model::decode (greedy)          engine/engine_model.cpp:221-297
+//   KVCache::update_from_graph      engine/engine_cache.cpp:101-337 (append)
+#include <cmath>
+#include <cstring>
+
+#include "cactus_hip.h"
+#include "engine.h"
+#include "fused.h"
+
+namespace cactus {
+
+// ------------------------------------------------------------------ DevBuf
+DevBuf::DevBuf(size_t n) : bytes(n) {
+    check_hip(cactus_hip_malloc(&ptr, n ? n : 1), "DevBuf");
+}
+DevBuf::~DevBuf() {
+    if (ptr) cactus_hip_free(ptr);
+}
+DevBuf& DevBuf::operator=(DevBuf&& o) noexcept {
+    if (this != &o) {
+        if (ptr) cactus_hip_free(ptr);
+        ptr = o.ptr;
+        bytes = o.bytes;
+        o.ptr = nullptr;
+        o.bytes = 0;
+    }
+    return *this;
+}
+void DevBuf::upload(const void* host, size_t n, void* stream) {
+    check_hip(cactus_hip_memcpy_h2d(ptr, host, n, stream), "upload");
+}
+
+// ------------------------------------------------------------------ KVCache
+void KVCache::init(size_t layers, size_t max_seq, size_t kv_heads, size_t hd) {
+    num_layers = layers;
+    max_seq_len = max_seq;
+    num_kv_heads = kv_heads;
+    head_dim = hd;
+    const size_t codes = max_seq * kv_heads * hd;
+    const size_t scales = max_seq * kv_heads * groups() * sizeof(float);
+    k_.clear(); v_.clear(); ks_.clear(); vs_.clear();
+    for (size_t l = 0; l < layers; l++) {
+        k_.emplace_back(codes);
+        v_.emplace_back(codes);
+        ks_.emplace_back(scales);
+        vs_.emplace_back(scales);
+    }
+    reset();
+}
+
+void KVCache::append(size_t l, const void* kf, const void* vf, size_t seq, void* stream) {
+    if (current_seq_len + seq > max_seq_len)
+        throw std::runtime_error("KV cache capacity exceeded (sliding window not built)");
+    const size_t off = current_seq_len * num_kv_heads * head_dim;
+    const size_t soff = current_seq_len * num_kv_heads * groups();
+    check_hip(cactus_hip_quantize_kv_fp16_to_int8(static_cast<const uint16_t*>(kf), keys_mut(l) + off,
+                                                  key_scales_mut(l) + soff, seq, num_kv_heads, head_dim,
+                                                  GROUP, stream),
+              "kv append (keys)");
+    check_hip(cactus_hip_quantize_kv_fp16_to_int8(static_cast<const uint16_t*>(vf), values_mut(l) + off,
+                                                  value_scales_mut(l) + soff, seq, num_kv_heads, head_dim,
+                                                  GROUP, stream),
+              "kv append (values)");
+}
+
+// ------------------------------------------------------------------ QwenModel
+static DevBuf upload_buf(const void* host, size_t bytes, void* stream) {
+    if (!host) throw std::runtime_error("missing weight tensor");
+    DevBuf b(bytes);
+    b.upload(host, bytes, stream);
+    return b;
+}
+
+QwenModel::QwenModel(const cactus_qwen_config& cfg, const cactus_qwen_layer_weights* lw,
+                     const uint16_t* embedding, const uint16_t* output_norm)
+    : cfg_(cfg) {
+    if (cfg.hidden % cfg.group_size || cfg.ffn % cfg.group_size ||
+        (cfg.heads * cfg.head_dim) % cfg.group_size)
+        throw std::runtime_error("group_size must divide every projection's input dimension");
+    if (cfg.heads % cfg.kv_heads) throw std::runtime_error("heads must be a multiple of kv_heads");
+    check_hip(cactus_hip_stream_create(&stream_), "stream_create");
+    graph_ = std::make_unique<CactusGraph>(stream_);
+    const size_t H = cfg.hidden, F = cfg.ffn, hd = cfg.head_dim, gs = cfg.group_size;
+    const size_t nq = (size_t)cfg.heads * hd, nkv = (size_t)cfg.kv_heads * hd;
+    // engine_model.cpp:125-129
+    attn_scale_ = 1.0f / std::sqrt(static_cast<float>(hd));
+
+    CactusGraph& g = *graph_;
+    auto weight = [&](const std::vector<size_t>& shape, Precision p, void* dev) {
+        size_t id = g.input(shape, p);
+        g.set_external_input(id, dev, p);
+        return id;
+    };
+    embedding_ = upload_buf(embedding, (size_t)cfg.vocab * H * 2, stream_);
+    out_norm_ = upload_buf(output_norm, H * 2, stream_);
+    n_embedding_ = weight({cfg.vocab, H}, Precision::FP16, embedding_.ptr);
+    n_out_norm_ = weight({H}, Precision::FP16, out_norm_.ptr);
+    layers_.resize(cfg.num_layers);
+    for (uint32_t l = 0; l < cfg.num_layers; l++) {
+        const cactus_qwen_layer_weights& w = lw[l];
+        QwenLayer& L = layers_[l];
+        L.input_norm = upload_buf(w.input_norm, H * 2, stream_);
+        L.post_norm = upload_buf(w.post_norm, H * 2, stream_);
+        L.q_norm = upload_buf(w.q_norm, hd * 2, stream_);
+        L.k_norm = upload_buf(w.k_norm, hd * 2, stream_);
+        L.q_w = upload_buf(w.q_w, nq * H, stream_);
+        L.q_s = upload_buf(w.q_s, nq * (H / gs) * 2, stream_);
+        L.k_w = upload_buf(w.k_w, nkv * H, stream_);
+        L.k_s = upload_buf(w.k_s, nkv * (H / gs) * 2, stream_);
+        L.v_w = upload_buf(w.v_w, nkv * H, stream_);
+        L.v_s = upload_buf(w.v_s, nkv * (H / gs) * 2, stream_);
+        L.o_w = upload_buf(w.o_w, H * nq, stream_);
+        L.o_s = upload_buf(w.o_s, H * (nq / gs) * 2, stream_);
+        L.gate_w = upload_buf(w.gate_w, F * H / 2, stream_);
+        L.gate_s = upload_buf(w.gate_s, F * (H / gs) * 2, stream_);
+        L.up_w = upload_buf(w.up_w, F * H / 2, stream_);
+        L.up_s = upload_buf(w.up_s, F * (H / gs) * 2, stream_);
+        L.down_w = upload_buf(w.down_w, H * F / 2, stream_);
+        L.down_s = upload_buf(w.down_s, H * (F / gs) * 2, stream_);
+        // QwenModel::load_weights_to_graph (model_qwen.cpp:17-49)
+        L.n_input_norm = weight({H}, Precision::FP16, L.input_norm.ptr);
+        L.n_post_norm = weight({H}, Precision::FP16, L.post_norm.ptr);
+        L.n_q_norm = weight({hd}, Precision::FP16, L.q_norm.ptr);
+        L.n_k_norm = weight({hd}, Precision::FP16, L.k_norm.ptr);
+        L.n_q = weight({nq, H}, Precision::INT8, L.q_w.ptr);
+        g.set_grouped_scales(L.n_q, gs, H / gs, L.q_s.ptr);
+        L.n_k = weight({nkv, H}, Precision::INT8, L.k_w.ptr);
+        g.set_grouped_scales(L.n_k, gs, H / gs, L.k_s.ptr);
+        L.n_v = weight({nkv, H}, Precision::INT8, L.v_w.ptr);
+        g.set_grouped_scales(L.n_v, gs, H / gs, L.v_s.ptr);
+        L.n_o = weight({H, nq}, Precision::INT8, L.o_w.ptr);
+        g.set_grouped_scales(L.n_o, gs, nq / gs, L.o_s.ptr);
+        // packed INT4 MLP weights keep their shape in elements
+        L.n_gate = weight({F, H}, Precision::INT8, L.gate_w.ptr);
+        g.set_grouped_scales(L.n_gate, gs, H / gs, L.gate_s.ptr);
+        g.set_packed_int4(L.n_gate, L.gate_w.ptr, F * H / 2);
+        L.n_up = weight({F, H}, Precision::INT8, L.up_w.ptr);
+        g.set_grouped_scales(L.n_up, gs, H / gs, L.up_s.ptr);
+        g.set_packed_int4(L.n_up, L.up_w.ptr, F * H / 2);
+        L.n_down = weight({H, F}, Precision::INT8, L.down_w.ptr);
+        g.set_grouped_scales(L.n_down, gs, F / gs, L.down_s.ptr);
+        g.set_packed_int4(L.n_down, L.down_w.ptr, H * F / 2);
+    }
+    cache_.init(cfg.num_layers, cfg.max_seq, cfg.kv_heads, hd);
+    check_hip(cactus_hip_rope_reserve(cfg.max_seq + 1, hd, cfg.rope_theta), "rope_reserve");
+    check_hip(cactus_hip_stream_sync(stream_), "init sync");
+    k_nodes_.assign(cfg.num_layers, SIZE_MAX);
+    v_nodes_.assign(cfg.num_layers, SIZE_MAX);
+}
+
+QwenModel::~QwenModel() {
+    cactus_hip_stream_sync(stream_);
+    fused_.reset();
+    graph_.reset();
+    layers_.clear();
+    cactus_hip_stream_destroy(stream_);
+}
+
+void QwenModel::reset() {
+    cache_.reset();
+    graph_->soft_reset();
+}
+
+// model_qwen.cpp:51-106
+size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
+    CactusGraph& g = *graph_;
+    const QwenLayer& L = layers_[l];
+    const size_t hd = cfg_.head_dim, nh = cfg_.heads, nkv = cfg_.kv_heads;
+    size_t q = g.matmul(x, L.n_q, true);
+    size_t k = g.matmul(x, L.n_k, true);
+    size_t v = g.matmul(x, L.n_v, true);
+    const size_t S = g.get_output_buffer(q).shape[0];
+    q = g.reshape(q, {S * nh, hd});
+    q = g.rms_norm(q, L.n_q_norm, cfg_.eps);
+    q = g.reshape(q, {S, nh * hd});
+    k = g.reshape(k, {S * nkv, hd});
+    k = g.rms_norm(k, L.n_k_norm, cfg_.eps);
+    k = g.reshape(k, {S, nkv * hd});
+    size_t q4 = g.reshape(q, {1, S, nh, hd});
+    size_t k4 = g.reshape(k, {1, S, nkv, hd});
+    size_t v4 = g.reshape(v, {1, S, nkv, hd});
+    if (cfg_.rope_theta > 0) {
+        q4 = g.rope(q4, cfg_.rope_theta, pos);
+        k4 = g.rope(k4, cfg_.rope_theta, pos);
+    }
+    k_nodes_[l] = k4;
+    v_nodes_[l] = v4;
+    size_t att;
+    if (!cache_.is_empty())
+        att = g.attention_int8_hybrid(q4, k4, v4, attn_scale_, pos, cache_.keys(l), cache_.values(l),
+                                      cache_.key_scales(l), cache_.value_scales(l),
+                                      cache_.current_seq_len, nkv, hd);
+    else
+        att = g.attention(q4, k4, v4, attn_scale_, pos);
+    att = g.reshape(att, {S, hd * nh});
+    return g.matmul(att, L.n_o, true);
+}
+
+// model_qwen.cpp:109-117
+size_t QwenModel::build_mlp(size_t x, uint32_t l) {
+    CactusGraph& g = *graph_;
+    const QwenLayer& L = layers_[l];
+    size_t gate = g.matmul(x, L.n_gate, true);
+    size_t up = g.matmul(x, L.n_up, true);
+    size_t act = g.silu(gate);
+    size_t m = g.multiply(act, up);
+    return g.matmul(m, L.n_down, true);
+}
+
+// model_qwen.cpp:120-129
+size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
+    CactusGraph& g = *graph_;
+    const QwenLayer& L = layers_[l];
+    size_t x = g.rms_norm(h, L.n_input_norm, cfg_.eps);
+    size_t att = build_attention(x, l, pos);
+    size_t h1 = g.add(h, att);
+    size_t x2 = g.rms_norm(h1, L.n_post_norm, cfg_.eps);
+    size_t mlp = build_mlp(x2, l);
+    return g.add(h1, mlp);
+}
+
+// model_qwen.cpp:132-172 (use_cache = true)
+size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
+    if (tokens.empty()) throw std::runtime_error("Token sequence cannot be empty");
+    CactusGraph& g = *graph_;
+    g.soft_reset();
+    const size_t S = tokens.size();
+    const size_t pos = cache_.total_seq_len;
+    size_t ids = g.input({S}, Precision::FP32);
+    size_t h = g.embedding(n_embedding_, ids);
+    std::vector<float> idf(S);
+    for (size_t i = 0; i < S; i++) idf[i] = static_cast<float>(tokens[i]);
+    g.set_input(ids, idf.data(), Precision::FP32);
+    for (uint32_t l = 0; l < cfg_.num_layers; l++) h = build_block(h, l, pos);
+    return g.rms_norm(h, n_out_norm_, cfg_.eps);
+}
+
+// engine_model.cpp:317-321 -> engine_cache.cpp:234-267 (append branch)
+void QwenModel::update_kv_cache(size_t seq) {
+    for (uint32_t l = 0; l < cfg_.num_layers; l++)
+        cache_.append(l, graph_->get_output_buffer(k_nodes_[l]).data,
+                      graph_->get_output_buffer(v_nodes_[l]).data, seq, stream_);
+    cache_.commit(seq);
+}
+
+// engine_model.cpp:170-219
+void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
+    if (tokens.empty()) return;
+    const size_t chunk = cfg_.prefill_chunk ? cfg_.prefill_chunk : 256;
+    auto process = [&](size_t b, size_t e) {
+        std::vector<uint32_t> c(tokens.begin() + b, tokens.begin() + e);
+        last_hidden_ = forward(c);
+        graph_->execute();
+        update_kv_cache(c.size());
+    };
+    if (tokens.size() <= chunk) {
+        process(0, tokens.size());
+        return;
+    }
+    const size_t full = (tokens.size() - 1) / chunk;
+    for (size_t i = 0; i < full; i++) process(i * chunk, (i + 1) * chunk);
+    process(full * chunk, tokens.size());
+}
+
+// engine_model.cpp:221-297, greedy
+uint32_t QwenModel::decode(uint32_t token) {
+    if (decode_mode_ == 1 && fused_) {
+        return fused_decode(*this, *fused_, token);
+    }
+    CactusGraph& g = *graph_;
+    size_t fin = forward({token});
+    last_hidden_ = fin;
+    size_t last = g.index(fin, 0, 0);
+    last = g.reshape(last, {1, cfg_.hidden});
+    last_logits_ = g.matmul(last, n_embedding_, true);
+    size_t tok = g.sample(last_logits_, 0.0f, 0.0f, 0);
+    g.execute();
+    update_kv_cache(1);
+    uint32_t id = 0;
+    std::memcpy(&id, g.get_output(tok), 4);
+    return id;
+}
+
+}  // namespace cactus

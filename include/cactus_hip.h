@@ -180,6 +180,11 @@ int cactus_hip_add_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t
 int cactus_hip_multiply_f16(const uint16_t* a, const uint16_t* b, uint16_t* y, size_t n,
                             void* stream);
 
+/* cactus_transpose_2d_f16 (kernel/kernel.h:54, kernel_blas.cpp): dst[c][r] = src[r][c]
+ * for src [rows][cols]; used by the graph for a non-pretransposed FP16 rhs. */
+int cactus_hip_transpose_2d_f16(const uint16_t* src, uint16_t* dst, size_t rows, size_t cols,
+                                void* stream);
+
 /* ------------------------------------------------ a13/a14 */
 /* compute_embedding_node, FP16 table with FP32 ids
  * (graph/graph_ops_tensor.cpp:301-329): out[i] = table[(size_t)ids[i]].

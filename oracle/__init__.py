@@ -206,3 +206,86 @@ def multiply(a, b):
 
 def argmax(logits):
     return int(lib().orc_argmax_f16(ptr(logits), logits.size))
+
+
+# ---- Qwen3 forward restatement ---------------------------------------------
+QWEN_LAYER_FIELDS = ["input_norm", "q_w", "q_s", "k_w", "k_s", "v_w", "v_s", "o_w", "o_s", "q_norm",
+                     "k_norm", "post_norm", "gate_w", "gate_s", "up_w", "up_s", "down_w", "down_s"]
+
+
+class _Cfg(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in
+                ("num_layers", "hidden", "ffn", "heads", "kv_heads", "head_dim", "vocab", "group_size")] + \
+               [("eps", ctypes.c_float), ("rope_theta", ctypes.c_float), ("max_seq", ctypes.c_uint32)]
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in QWEN_LAYER_FIELDS]
+
+
+class OracleQwen:
+    """orc_qwen_* (qwen_oracle.c): the reference's Qwen3 block and engine flow."""
+
+    def __init__(self, cfg: dict, layers, embedding, output_norm):
+        L = lib()
+        self.cfg = cfg
+        c = _Cfg(**{k: cfg[k] for k in ("num_layers", "hidden", "ffn", "heads", "kv_heads", "head_dim",
+                                        "vocab", "group_size", "eps", "rope_theta", "max_seq")})
+        self._keep = [{k: np.ascontiguousarray(v) for k, v in Lw.items()} for Lw in layers]
+        self._emb = np.ascontiguousarray(embedding)
+        self._on = np.ascontiguousarray(output_norm)
+        arr = (_Layer * len(layers))()
+        for i, Lw in enumerate(self._keep):
+            for k in QWEN_LAYER_FIELDS:
+                setattr(arr[i], k, Lw[k].ctypes.data)
+        self.h = L.orc_qwen_create(ctypes.byref(c), arr, self._emb.ctypes.data, self._on.ctypes.data)
+
+    def prefill(self, tokens, chunk=256):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        rc = lib().orc_qwen_prefill(self.h, t.ctypes.data, t.size, chunk)
+        assert rc == 0
+
+    def decode(self, token, logits=None):
+        return int(lib().orc_qwen_decode(self.h, int(token), None if logits is None else logits.ctypes.data))
+
+    def generate(self, prompt, max_new, chunk=256):
+        """The FFI order: prefill prompt[:-1], then decode from prompt[-1]."""
+        if len(prompt) > 1:
+            self.prefill(prompt[:-1], chunk)
+        out, tok = [], int(prompt[-1])
+        for _ in range(max_new):
+            tok = self.decode(tok)
+            out.append(tok)
+        return np.array(out, np.uint32)
+
+    def last_hidden(self):
+        rows = ctypes.c_size_t()
+        p = lib().orc_qwen_last_hidden(self.h, ctypes.byref(rows))
+        n = rows.value * self.cfg["hidden"]
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_uint16)), (n,)).reshape(
+            rows.value, self.cfg["hidden"]).copy()
+
+    def cache_len(self):
+        return int(lib().orc_qwen_cache_len(self.h))
+
+    def read_kv(self, layer):
+        n = self.cache_len()
+        kvh, hd = self.cfg["kv_heads"], self.cfg["head_dim"]
+        ng = (hd + 127) // 128
+        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        lib().orc_qwen_kv(self.h, layer, *[ctypes.byref(p) for p in ptrs])
+        arr = lambda p, dt, shape: np.ctypeslib.as_array(
+            ctypes.cast(p, ctypes.POINTER(dt)), (int(np.prod(shape)),)).reshape(shape).copy()
+        return (arr(ptrs[0], ctypes.c_int8, (n, kvh, hd)), arr(ptrs[1], ctypes.c_int8, (n, kvh, hd)),
+                arr(ptrs[2], ctypes.c_float, (n, kvh, ng)), arr(ptrs[3], ctypes.c_float, (n, kvh, ng)))
+
+    def close(self):
+        if self.h:
+            lib().orc_qwen_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -34,3 +34,33 @@ def grouped_int4_weights(rng, N, K, gs):
 
 def activations(rng, M, K):
     return f16(rng.normal(0, 1, size=(M, K)))
+
+
+def qwen_small_config(**over):
+    """Reduced Qwen3-architecture config the oracle runs in seconds."""
+    c = dict(num_layers=2, hidden=256, ffn=768, heads=4, kv_heads=2, head_dim=128, vocab=2048,
+             group_size=32, eps=1e-6, rope_theta=1e6, max_seq=640, prefill_chunk=256)
+    c.update(over)
+    return c
+
+
+def qwen_weights(rng, c):
+    """Random-init weights of the architecture: INT8 g-grouped attention
+    projections, packed INT4 MLP, fp16 norms 1+N(0,0.02), embeddings N(0,0.02)."""
+    H, F, hd, gs = c["hidden"], c["ffn"], c["head_dim"], c["group_size"]
+    nq, nkv = c["heads"] * hd, c["kv_heads"] * hd
+    layers = []
+    for _ in range(c["num_layers"]):
+        L = {}
+        L["input_norm"] = f16(1 + rng.normal(0, 0.02, H))
+        L["post_norm"] = f16(1 + rng.normal(0, 0.02, H))
+        L["q_norm"] = f16(1 + rng.normal(0, 0.02, hd))
+        L["k_norm"] = f16(1 + rng.normal(0, 0.02, hd))
+        for name, (n, k) in {"q": (nq, H), "k": (nkv, H), "v": (nkv, H), "o": (H, nq)}.items():
+            L[name + "_w"], L[name + "_s"] = grouped_int8_weights(rng, n, k, gs)
+        for name, (n, k) in {"gate": (F, H), "up": (F, H), "down": (H, F)}.items():
+            _, L[name + "_w"], L[name + "_s"] = grouped_int4_weights(rng, n, k, gs)
+        layers.append(L)
+    emb = f16(rng.normal(0, 0.02, (c["vocab"], H)))
+    out_norm = f16(1 + rng.normal(0, 0.02, H))
+    return layers, emb, out_norm
