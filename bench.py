@@ -110,12 +110,55 @@ def cpu_baseline(seconds: float = 10.0):
                       f"x86 build of the CPU restatement, {threads} threads"}
 
 
+def bench_decode(prompt_len: int = 4096, new_tokens: int = 128, mode: int = 0):
+    """Qwen3-0.6B-architecture forward, random-init weights (INT4 MLP, INT8
+    attention projections, FP16 embeddings/norms): prefill of a 4096-token
+    random prompt through the reference's FFI flow, then greedy decode."""
+    from cactus_amd.engine import Qwen, qwen3_0p6b
+    cfg = qwen3_0p6b(max_seq=prompt_len + new_tokens + 64)
+    t0 = time.perf_counter()
+    m = Qwen(cfg, seed=6)
+    if mode:
+        m.set_decode_mode(mode)
+    init_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], prompt_len).astype(np.uint32)
+    toks, t = m.generate(prompt, new_tokens)
+    decode_steps = t.decode_tokens + 1
+    decode_s = (t.decode_ms + t.first_decode_ms) / 1e3
+    ctx = prompt_len - 1 + new_tokens / 2
+    # bytes per decoded token: every weight once (INT8 attention, INT4 MLP,
+    # fp16 scales/norms), the tied FP16 LM head, and the INT8 KV cache at the
+    # mean context
+    H, F, hd = cfg["hidden"], cfg["ffn"], cfg["head_dim"]
+    nq, nkv, gs = cfg["heads"] * hd, cfg["kv_heads"] * hd, cfg["group_size"]
+    per_layer = (nq * H + 2 * nkv * H + H * nq) * (1 + 2 / gs) + 3 * F * H * (0.5 + 2 / gs) + 4 * H + 4 * hd
+    kv = cfg["num_layers"] * 2 * cfg["kv_heads"] * (hd + 4) * ctx
+    bytes_tok = cfg["num_layers"] * per_layer + cfg["vocab"] * H * 2 + kv
+    m.close()
+    return {
+        "decode_tok_s": round(decode_steps / decode_s, 2),
+        "prefill_tok_s": round(t.prefill_tokens / (t.prefill_ms / 1e3), 1),
+        "decode_ms_per_token": round(decode_s * 1e3 / decode_steps, 3),
+        "decode_hbm_fraction": round(bytes_tok * decode_steps / decode_s / 1e9 / HBM_PEAK_GBS, 4),
+        "bytes_per_token": int(bytes_tok),
+        "decode_mode": mode,
+        "prompt_tokens": prompt_len,
+        "new_tokens": new_tokens,
+        "first_tokens": [int(x) for x in toks[:8]],
+        "init_s": round(init_s, 1),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--decode-mode", type=int, default=0)
+    ap.add_argument("--skip-decode", action="store_true")
+    ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--new-tokens", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -124,7 +167,11 @@ def main():
 
     import cactus_amd as cm
     cm.call("cactus_hip_init", 0)
+    if args.decode_only:
+        print(json.dumps(bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)), flush=True)
+        return
     g = bench_gemv(args.steps, args.warmup)
+    dec = None if args.skip_decode else bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)
     cpu = cpu_baseline(args.cpu_seconds)
     out = {
         "metric": "INT8 GEMV GB/s (% HBM peak) + Qwen3-0.6B-shape decode tok/s, 1 MI355X",
@@ -155,6 +202,7 @@ def main():
             "traffic": None,
         },
         "cpu_baseline": cpu,
+        "qwen3_0p6b_decode": dec,
     }
     print(json.dumps(out), flush=True)
 

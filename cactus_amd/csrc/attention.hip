@@ -1,33 +1,35 @@
 // attention.hip -- KV-cache attention (a5 FP16 KV, a6 INT8 cache + FP16 new)
-// in the reference's order of operations (kernel_attention.cpp:10-482).
+// with the reference's exact order of operations (kernel_attention.cpp:10-482).
 //
-// One wave per (batch, query position, query head).  Keys are walked in the
-// reference's 32-key blocks; for each block:
-//   * lane j (< 32) runs the "low" FMA chains of key j's score (dims 8c+0..3)
-//     and lane j+32 the "high" chains (dims 8c+4..7); the pair is combined as
-//     (t0+t1)+(t2+t3) with t_l = low_l + high_l, then multiplied by `scale`;
-//   * the block max becomes the running max (even when smaller), the running
-//     sum and accumulators are rescaled by expf(old_max - block_max);
-//   * weights are the second-order 2^x polynomial for the first
-//     floor(n/4)*4 keys and expf for the rest (FP16 variant), or expf for all
-//     keys (hybrid variant); the block sum adds ((y0+y1)+(y2+y3)) per group of
-//     four in order, then the tail;
-//   * each lane owns head_dim/64 output dims and applies acc = fma(v, w, acc)
-//     key by key in increasing position.
-// Output = fp16(acc * (1/sum)) on the 8-aligned prefix of head_dim, zero
-// elsewhere or when the sum is not positive.
+// The reference walks each (query, head) serially through 32-key blocks.  Only
+// two of its steps carry a dependence from one key to the next: the running
+// sum and the weighted-value accumulators.  Everything else is independent
+// per key or per block, so it runs here in two kernels:
+//
+//  A. scores  -- one lane per key, a wave per 64 keys (two reference blocks)
+//     and per query/KV-head group.  Each lane computes the score exactly as
+//     the reference does: fp32 FMA chains on dims 8c+j, combined as
+//     ((c0+c4)+(c1+c5)) + ((c2+c6)+(c3+c7)), times `scale`, masked to -inf.
+//     The block max, the weights (second-order 2^x polynomial on the first
+//     floor(n/4)*4 keys of a FP16 block and expf elsewhere; expf everywhere
+//     for the INT8 hybrid) and the block sum in the reference's order are
+//     written to scratch.
+//  B. values  -- one lane per output dim.  The rescale factors
+//     expf(previous_max - block_max) are computed in parallel, the running
+//     sum is chained once per (query, head), and every lane then applies
+//     acc = acc * corr at each block start and acc = fma(v, w, acc) key by
+//     key, in increasing position, exactly as the reference.  The output is
+//     fp16(acc * (1/sum)) on the 8-aligned prefix of head_dim.
 #include "hip_common.h"
+
+#include <map>
+#include <mutex>
 
 namespace cactus_hip {
 
 constexpr int ATT_BLOCK = 32;
 constexpr int ATT_MAX_D = 256;
-constexpr int ATT_DPL = ATT_MAX_D / 64;   // max dims per lane
-
-// value of v in lane j (j wave-uniform), via v_readlane_b32
-__device__ __forceinline__ float lane_f(float v, int j) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
-}
+constexpr int ATT_MAX_GQ = 8;      // query heads per KV head
 
 struct AttnArgs {
     const uint16_t* q;
@@ -39,40 +41,55 @@ struct AttnArgs {
     const float* vs;
     const uint16_t* mask;     // [B][S][Skv] or null
     uint16_t* o;
-    int B, S, Hq, Hkv, d;
+    float* w;                 // scratch: weights [B*S*Hq][wstride]
+    float* bmax;              // scratch: block max [B*S*Hq][nbstride]
+    float* bsum;              // scratch: block sums
+    size_t wstride;
+    int nbstride;
+    int B, S, Hq, Hkv, d, gq;
     size_t Skv;               // FP16: kv_seq_len; hybrid: cache_len + new_len
     size_t cache_len, new_len;
     size_t pos_off, window;
     int causal, qgs, nqg;
     float scale;
+    // decode-step form: when set, cache_len = dyn[2] and position_offset =
+    // dyn[1] are read from device memory (the step state of the fused
+    // decode path), and the launch is sized for max_cache keys
+    const uint32_t* dyn;
+    size_t max_cache;
+    // fp32 value-product tiles of the INT8 cache (kv_shadow.hip), or null
+    const float* vsh;
+    size_t sh_ntile;
 };
 
-template <bool HYBRID>
-__global__ void __launch_bounds__(256) attention_ref_kernel(AttnArgs a) {
-    __shared__ float qsh[4][ATT_MAX_D];
-    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const size_t item = (size_t)blockIdx.x * 4 + wid;
-    const size_t total = (size_t)a.B * a.S * a.Hq;
-    const bool live = item < total;
-    // work order of the reference: batch, then head, then query position
-    const size_t b = live ? item / ((size_t)a.Hq * a.S) : 0;
-    const size_t rem = live ? item % ((size_t)a.Hq * a.S) : 0;
-    const int h = (int)(rem / a.S);
-    const size_t qp = rem % a.S;
-    const int kvh = h / (a.Hq / a.Hkv);
-    const int d = a.d, da = (d / 8) * 8;
-    float* qs = qsh[wid];
-    const uint16_t* qv = a.q + ((b * a.S + qp) * a.Hq + h) * (size_t)d;
-    if (live)
-        for (int i = lane; i < d; i += 64) qs[i] = h2f(qv[i]);
-    __syncthreads();
-    if (!live) return;
+__device__ __forceinline__ AttnArgs resolve(const AttnArgs& in) {
+    AttnArgs a = in;
+    if (a.dyn) {
+        a.cache_len = a.dyn[2];
+        a.pos_off = a.dyn[1];
+        a.Skv = a.cache_len + a.new_len;
+    }
+    return a;
+}
 
-    const bool high = lane >= 32;
-    const int jl = lane & 31;
+// sign bit set on a non-negative float: a flag carried by a block sum
+__device__ __forceinline__ float set_sign(float x) {
+    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) | 0x80000000u);
+}
+
+__device__ __forceinline__ float lane_f(float v, int j) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
+}
+
+// Key range and block limit of query position qp (kernel_attention.cpp:78-96
+// for FP16, :328-337 for the hybrid).
+template <bool HYBRID>
+__device__ __forceinline__ void kv_range(const AttnArgs& a, size_t qp, size_t& kv_start,
+                                         size_t& kv_end, size_t& blk_limit) {
     const size_t aq = a.pos_off + qp;
-    const bool is_decode = (!HYBRID) && (qp == (size_t)a.S - 1) && a.S > 1;
-    size_t kv_start = 0, kv_end = a.Skv, blk_limit = a.Skv;
+    kv_start = 0;
+    kv_end = a.Skv;
+    blk_limit = a.Skv;
     if (!HYBRID) {
         if (a.window > 0 && a.window < a.Skv) {
             if (aq > a.window) kv_start = aq - a.window;
@@ -84,60 +101,110 @@ __global__ void __launch_bounds__(256) attention_ref_kernel(AttnArgs a) {
         if (a.causal && aq + 1 < kv_end) kv_end = aq + 1;
         blk_limit = kv_end;
     }
+}
 
-    float acc[ATT_DPL];
-#pragma unroll
-    for (int i = 0; i < ATT_DPL; i++) acc[i] = 0.0f;
-    float rmax = -__builtin_inff(), rsum = 0.0f;
+// ----------------------------------------------------------------- kernel A
+// grid.x: 64-key chunks (4 per workgroup), grid.y: (b, qp, kv head)
+template <bool HYBRID>
+__global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
+    const AttnArgs a = resolve(a_in);
+    __shared__ float qsh[ATT_MAX_GQ][ATT_MAX_D];
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t row = blockIdx.y;                    // (b, qp, kvh)
+    const int kvh = (int)(row % a.Hkv);
+    const size_t qp = (row / a.Hkv) % a.S;
+    const size_t b = row / ((size_t)a.Hkv * a.S);
+    const int d = a.d, da = (d / 8) * 8, gq = a.gq;
+    const int h0 = kvh * gq;
+    for (int i = threadIdx.x; i < gq * d; i += 256) {
+        const int hh = i / d, dim = i % d;
+        qsh[hh][dim] = h2f(a.q[((b * a.S + qp) * a.Hq + h0 + hh) * (size_t)d + dim]);
+    }
+    __syncthreads();
+
+    size_t kv_start, kv_end, blk_limit;
+    kv_range<HYBRID>(a, qp, kv_start, kv_end, blk_limit);
+    const size_t chunk = (size_t)blockIdx.x * 4 + wid;
+    const size_t bs0 = kv_start + chunk * 64 + (lane & 32);   // this lane's block start
+    if (kv_start + chunk * 64 >= kv_end) return;              // wave-uniform
+    const int jl = lane & 31;
+    const bool block_live = bs0 < kv_end;
+    const size_t be = block_live ? ((bs0 + ATT_BLOCK < blk_limit) ? bs0 + ATT_BLOCK : blk_limit) : bs0;
+    const int bsz = (int)(be - bs0);
+    const size_t kp = bs0 + jl;
+    const size_t aq = a.pos_off + qp;
+    const bool is_decode = (!HYBRID) && (qp == (size_t)a.S - 1) && a.S > 1;
     const float NEG_INF = -__builtin_inff();
+    // FP16: a block wholly in the future of a non-last query is skipped by the
+    // reference (kernel_attention.cpp:100-105): it contributes nothing
+    const bool block_skipped = !HYBRID && !is_decode && a.causal && bs0 > aq;
+    const bool in_block = block_live && jl < bsz && !block_skipped;
+    bool computed = in_block;
+    if (computed && a.causal && kp > aq && (HYBRID || !is_decode)) computed = false;
 
-    for (size_t bs0 = kv_start; bs0 < kv_end; bs0 += ATT_BLOCK) {
-        const size_t be = (bs0 + ATT_BLOCK < blk_limit) ? bs0 + ATT_BLOCK : blk_limit;
-        const int bsz = (int)(be - bs0);
-        if (!HYBRID && !is_decode && a.causal && bs0 > aq) continue;
-        // ---- scores: lane jl computes key bs0+jl, low or high half
-        const size_t kp = bs0 + jl;
-        bool masked = jl >= bsz;
-        if (!masked && a.causal && kp > aq && (HYBRID || !is_decode)) masked = true;
-        float c[4] = {0.f, 0.f, 0.f, 0.f};
-        if (!masked) {
-            const int off = high ? 4 : 0;
-            if (HYBRID && kp < a.cache_len) {
-                const int8_t* kr = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
-                const float* sr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
-                for (int cb = 0; cb < da; cb += 8) {
-                    const float s = sr[cb / a.qgs];
-                    const uint32_t w = *reinterpret_cast<const uint32_t*>(kr + cb + off);
+    float score[ATT_MAX_GQ];
 #pragma unroll
-                    for (int l = 0; l < 4; l++) {
-                        const float kk = (float)(int8_t)((w >> (8 * l)) & 0xFF) * s;
-                        c[l] = __builtin_fmaf(qs[cb + off + l], kk, c[l]);
-                    }
+    for (int hh = 0; hh < ATT_MAX_GQ; hh++) score[hh] = NEG_INF;
+    if (computed) {
+        float ch[ATT_MAX_GQ][8];
+#pragma unroll
+        for (int hh = 0; hh < ATT_MAX_GQ; hh++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) ch[hh][c] = 0.0f;
+        if (HYBRID && kp < a.cache_len) {
+            const int8_t* kr = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
+            const float* sr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
+            for (int cb = 0; cb < da; cb += 8) {
+                const float s = sr[cb / a.qgs];
+                const uint2 w = *reinterpret_cast<const uint2*>(kr + cb);
+                float kk[8];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    kk[c] = (float)(int8_t)((w.x >> (8 * c)) & 0xFF) * s;
+                    kk[4 + c] = (float)(int8_t)((w.y >> (8 * c)) & 0xFF) * s;
                 }
-            } else {
-                const size_t kpos = HYBRID ? kp - a.cache_len : kp;
-                const size_t klen = HYBRID ? a.new_len : a.Skv;
-                const uint16_t* kr = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
-                for (int cb = 0; cb < da; cb += 8) {
-                    const uint2 w = *reinterpret_cast<const uint2*>(kr + cb + off);
-                    c[0] = __builtin_fmaf(qs[cb + off + 0], h2f((uint16_t)(w.x & 0xFFFF)), c[0]);
-                    c[1] = __builtin_fmaf(qs[cb + off + 1], h2f((uint16_t)(w.x >> 16)), c[1]);
-                    c[2] = __builtin_fmaf(qs[cb + off + 2], h2f((uint16_t)(w.y & 0xFFFF)), c[2]);
-                    c[3] = __builtin_fmaf(qs[cb + off + 3], h2f((uint16_t)(w.y >> 16)), c[3]);
+#pragma unroll
+                for (int hh = 0; hh < ATT_MAX_GQ; hh++)
+                    if (hh < gq)
+#pragma unroll
+                        for (int c = 0; c < 8; c++) ch[hh][c] = __builtin_fmaf(qsh[hh][cb + c], kk[c], ch[hh][c]);
+            }
+        } else {
+            const size_t kpos = HYBRID ? kp - a.cache_len : kp;
+            const size_t klen = HYBRID ? a.new_len : a.Skv;
+            const uint16_t* kr = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
+            for (int cb = 0; cb < da; cb += 8) {
+                uint32_t wv[4];
+                if ((d & 7) == 0) {
+                    const uint4 w = *reinterpret_cast<const uint4*>(kr + cb);
+                    wv[0] = w.x; wv[1] = w.y; wv[2] = w.z; wv[3] = w.w;
+                } else {
+                    const uint2 w0 = *reinterpret_cast<const uint2*>(kr + cb);
+                    const uint2 w1 = *reinterpret_cast<const uint2*>(kr + cb + 4);
+                    wv[0] = w0.x; wv[1] = w0.y; wv[2] = w1.x; wv[3] = w1.y;
                 }
+                float kk[8];
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    kk[2 * c] = h2f((uint16_t)(wv[c] & 0xFFFF));
+                    kk[2 * c + 1] = h2f((uint16_t)(wv[c] >> 16));
+                }
+#pragma unroll
+                for (int hh = 0; hh < ATT_MAX_GQ; hh++)
+                    if (hh < gq)
+#pragma unroll
+                        for (int c = 0; c < 8; c++) ch[hh][c] = __builtin_fmaf(qsh[hh][cb + c], kk[c], ch[hh][c]);
             }
         }
-        // combine low (lane jl) with high (lane jl+32)
-        float hi0 = __shfl(c[0], jl + 32, 64), hi1 = __shfl(c[1], jl + 32, 64);
-        float hi2 = __shfl(c[2], jl + 32, 64), hi3 = __shfl(c[3], jl + 32, 64);
-        float score = NEG_INF;
-        if (!high && !masked) {
-            const float t0 = c[0] + hi0, t1 = c[1] + hi1, t2 = c[2] + hi2, t3 = c[3] + hi3;
+#pragma unroll
+        for (int hh = 0; hh < ATT_MAX_GQ; hh++) {
+            if (hh >= gq) break;
+            const float t0 = ch[hh][0] + ch[hh][4], t1 = ch[hh][1] + ch[hh][5];
+            const float t2 = ch[hh][2] + ch[hh][6], t3 = ch[hh][3] + ch[hh][7];
             float s = (t0 + t1) + (t2 + t3);
             if (!HYBRID) {
-                // dims beyond the 8-aligned prefix (kernel_attention.cpp:139-141)
                 const uint16_t* kr = a.k + ((b * a.Skv + kp) * a.Hkv + kvh) * (size_t)d;
-                for (int i = da; i < d; i++) s = __builtin_fmaf(qs[i], h2f(kr[i]), s);
+                for (int i = da; i < d; i++) s = __builtin_fmaf(qsh[hh][i], h2f(kr[i]), s);
             }
             s = s * a.scale;
             if (!HYBRID) {
@@ -145,74 +212,1050 @@ __global__ void __launch_bounds__(256) attention_ref_kernel(AttnArgs a) {
                 else if (a.window > 0 && kp < aq && (aq - kp) > a.window) s = NEG_INF;
                 else if (a.mask && h2f(a.mask[(b * a.S + qp) * a.Skv + kp]) == 0.0f) s = NEG_INF;
             }
-            score = s;
+            score[hh] = s;
         }
-        // ---- block max (lanes 0..31 hold scores, others -inf)
-        const float bmax = wave_max(score);
-        if (bmax > NEG_INF) {
-            const float corr = cactus_expf(rmax - bmax);
-            rsum = rsum * corr;
+    }
+
+    // per head of the group: block max, weights, block sum, stores
+    const int blk = (int)((bs0 - kv_start) / ATT_BLOCK);
+    const int vs4 = HYBRID ? 0 : (bsz / 4) * 4;
+    const int half = lane & 32;
+    for (int hh = 0; hh < gq; hh++) {
+        float s = score[hh];
+        // max over the 32 lanes of this block (half-wave reduction)
+        float m = s;
 #pragma unroll
-            for (int i = 0; i < ATT_DPL; i++) acc[i] = acc[i] * corr;
-            rmax = bmax;
-        }
-        // ---- weights
+        for (int off = 16; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
         float w = 0.0f;
-        const int vs4 = HYBRID ? 0 : (bsz / 4) * 4;
-        if (!high && jl < bsz) {
-            if (jl < vs4) w = poly_exp_weight(score, bmax);
-            else w = (score != NEG_INF) ? cactus_expf(score - bmax) : 0.0f;
+        if (in_block) {
+            if (jl < vs4) w = poly_exp_weight(s, m);
+            else w = (s != NEG_INF) ? cactus_expf(s - m) : 0.0f;
         }
-        // block sum: ((y0+y1)+(y2+y3)) per group of four in order, then the
-        // tail; weights are broadcast from lane j with v_readlane
-        float bsum = 0.0f;
-        for (int j = 0; j < vs4; j += 4) {
-            const float y0 = lane_f(w, j), y1 = lane_f(w, j + 1);
-            const float y2 = lane_f(w, j + 2), y3 = lane_f(w, j + 3);
-            bsum = bsum + ((y0 + y1) + (y2 + y3));
+        // block sum in the reference's order, for both half-wave blocks
+        float sumA = 0.0f, sumB = 0.0f;
+        const int bszA = __builtin_amdgcn_readlane(bsz, 0);
+        const int bszB = __builtin_amdgcn_readlane(bsz, 32);
+        {
+            const int v4 = HYBRID ? 0 : (bszA / 4) * 4;
+            for (int j = 0; j < v4; j += 4)
+                sumA = sumA + ((lane_f(w, j) + lane_f(w, j + 1)) + (lane_f(w, j + 2) + lane_f(w, j + 3)));
+            for (int j = v4; j < bszA; j++) sumA = sumA + lane_f(w, j);
         }
-        for (int j = vs4; j < bsz; j++) bsum = bsum + lane_f(w, j);
-        // ---- weighted values
-        for (int j = 0; j < bsz; j++) {
-            const float wj = lane_f(w, j);
-            if (wj == 0.0f) continue;
-            const size_t vp = bs0 + j;
-            if (HYBRID && vp < a.cache_len) {
-                const int8_t* vr = a.vc + ((b * a.cache_len + vp) * a.Hkv + kvh) * (size_t)d;
-                const float* sr = a.vs + ((b * a.cache_len + vp) * a.Hkv + kvh) * (size_t)a.nqg;
+        {
+            const int v4 = HYBRID ? 0 : (bszB / 4) * 4;
+            for (int j = 0; j < v4; j += 4)
+                sumB = sumB + ((lane_f(w, 32 + j) + lane_f(w, 33 + j)) + (lane_f(w, 34 + j) + lane_f(w, 35 + j)));
+            for (int j = v4; j < bszB; j++) sumB = sumB + lane_f(w, 32 + j);
+        }
+        const size_t r = (b * a.S + qp) * a.Hq + h0 + hh;
+        // every key of a live block gets its weight (0 when not computed);
+        // a block holding a zero weight is flagged by the sign of its sum
+        const bool wlane = block_live && jl < bsz;
+        const uint64_t zb = __ballot(wlane && !(w != 0.0f));
+        const bool has_zero = ((zb >> half) & 0xFFFFFFFFull) != 0;
+        if (wlane) a.w[r * a.wstride + (kp - kv_start)] = w;
+        if (block_live && jl == 0) {
+            a.bmax[r * a.nbstride + blk] = block_skipped ? NEG_INF : m;
+            const float bs = block_skipped ? 0.0f : (half ? sumB : sumA);
+            a.bsum[r * a.nbstride + blk] = has_zero ? set_sign(bs) : bs;
+        }
+    }
+}
+
+// ----------------------------------------------------------------- kernel B
+// The value accumulation is one fp32 FMA chain per (query, head, dimension)
+// over the keys in order, rescaled at every block whose max is finite
+// (kernel_attention.cpp:160-169 and :199-217 for FP16, :396-455 for the
+// hybrid), so it is latency-bound: the chains must run at FMA cadence.
+//
+// One workgroup per (b, group of `qpg` query positions, kv head, 64-dim
+// slice).  Waves 0..nc-1 (nc = qpg * gq) are chain waves: wave c owns query
+// position qp0 + c / gq and head kvh * gq + c % gq, each lane one output
+// dimension.  The CH_NP stage waves convert value rows into the reference's
+// fp32 operands (INT8 code * per-key group scale, or fp16 -> fp32) and stage
+// them, with the chain waves' weights, in LDS one CH_T-key tile ahead of the
+// chains, so a chain step is one broadcast LDS read and one FMA.
+constexpr int CH_T = 128;              // keys per staged tile
+constexpr int CH_NP = 2;               // stage waves
+constexpr int CH_PS = CH_T + 4;        // floats per staged dimension row (bank skew)
+constexpr int CH_MAX_THREADS = 64 * (ATT_MAX_GQ + CH_NP);
+
+template <bool HYBRID>
+__global__ void __launch_bounds__(CH_MAX_THREADS) attn_chain_kernel(AttnArgs a_in, int qpg, int nbmax,
+                                                                     int vec_ok) {
+    const AttnArgs a = resolve(a_in);
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int gq = a.gq, nc = qpg * gq;
+    float* prod = reinterpret_cast<float*>(smem);            // [2][64][CH_PS]
+    float* wts = prod + 2 * 64 * CH_PS;                      // [2][nc][CH_T]
+    float* corr_s = wts + 2 * nc * CH_T;                     // [nc][nbmax]
+    float* bsum_s = corr_s + (size_t)nc * nbmax;             // [nc][nbmax]
+    const float NEG_INF = -__builtin_inff();
+
+    const int d = a.d, da = (d / 8) * 8;
+    const int nsl = (d + 63) / 64;
+    size_t g = blockIdx.x;
+    const int sl = (int)(g % nsl);
+    g /= nsl;
+    const int kvh = (int)(g % a.Hkv);
+    g /= a.Hkv;
+    const int ngrp = (a.S + qpg - 1) / qpg;
+    const int qp0 = (int)(g % ngrp) * qpg;
+    const size_t b = g / ngrp;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+
+    // keys of the group: every row starts at the same kv_start (the host
+    // uses qpg = 1 for a sliding window); the last position reaches furthest
+    size_t ks, ke_first, bl_first;
+    kv_range<HYBRID>(a, (size_t)qp0, ks, ke_first, bl_first);
+    const int qlast = min(qp0 + qpg, a.S) - 1;
+    size_t ks_l, ke_l, bl_l;
+    kv_range<HYBRID>(a, (size_t)qlast, ks_l, ke_l, bl_l);
+    size_t kneed = ks;
+    if (ke_l > ks) {
+        kneed = ks + ((ke_l - ks + ATT_BLOCK - 1) / ATT_BLOCK) * ATT_BLOCK;
+        if (kneed > bl_l) kneed = bl_l;
+    }
+    const int nst = (int)((kneed - ks + CH_T - 1) / CH_T);
+
+    // ---- stage waves: tile t -> buffer t & 1
+    auto stage = [&](int t) {
+        const int pl = (int)threadIdx.x - nc * 64;
+        const size_t tb = ks + (size_t)t * CH_T;
+        float* pbuf = prod + (t & 1) * 64 * CH_PS;
+        for (int item = pl; item < (CH_T / 4) * 16; item += CH_NP * 64) {
+            const int dq = item & 15, kq = item >> 4;
+            const int dim0 = sl * 64 + dq * 4;
+            float pr[4][4];
 #pragma unroll
-                for (int i = 0; i < ATT_DPL; i++) {
-                    const int dim = lane + 64 * i;
-                    if (dim < da) {
-                        const float vv = (float)vr[dim] * sr[((dim / 8) * 8) / a.qgs];
-                        acc[i] = __builtin_fmaf(vv, wj, acc[i]);
+            for (int e = 0; e < 4; e++) {
+                const size_t kp = tb + kq * 4 + e;
+#pragma unroll
+                for (int c = 0; c < 4; c++) pr[e][c] = 0.0f;
+                if (kp >= kneed || dim0 >= da) continue;
+                if (HYBRID && kp < a.cache_len) {
+                    const size_t off = (b * a.cache_len + kp) * a.Hkv + kvh;
+                    const int8_t* src = a.vc + off * d + dim0;
+                    const float sc = a.vs[off * a.nqg + dim0 / a.qgs];
+                    int8_t cd[4];
+                    if (vec_ok) {
+                        const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+#pragma unroll
+                        for (int c = 0; c < 4; c++) cd[c] = (int8_t)((w >> (8 * c)) & 0xFF);
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; c++) cd[c] = src[c];
+                    }
+#pragma unroll
+                    for (int c = 0; c < 4; c++) pr[e][c] = (float)cd[c] * sc;
+                } else {
+                    const size_t vpos = HYBRID ? kp - a.cache_len : kp;
+                    const size_t vlen = HYBRID ? a.new_len : a.Skv;
+                    const uint16_t* src = a.v + ((b * vlen + vpos) * a.Hkv + kvh) * (size_t)d + dim0;
+                    if (vec_ok) {
+                        const uint2 w = *reinterpret_cast<const uint2*>(src);
+                        pr[e][0] = h2f((uint16_t)(w.x & 0xFFFF));
+                        pr[e][1] = h2f((uint16_t)(w.x >> 16));
+                        pr[e][2] = h2f((uint16_t)(w.y & 0xFFFF));
+                        pr[e][3] = h2f((uint16_t)(w.y >> 16));
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; c++) pr[e][c] = h2f(src[c]);
                     }
                 }
-            } else {
-                const size_t vpos = HYBRID ? vp - a.cache_len : vp;
-                const size_t vlen = HYBRID ? a.new_len : a.Skv;
-                const uint16_t* vr = a.v + ((b * vlen + vpos) * a.Hkv + kvh) * (size_t)d;
+            }
 #pragma unroll
-                for (int i = 0; i < ATT_DPL; i++) {
-                    const int dim = lane + 64 * i;
-                    if (dim < da) acc[i] = __builtin_fmaf(h2f(vr[dim]), wj, acc[i]);
+            for (int c = 0; c < 4; c++)
+                *reinterpret_cast<float4*>(pbuf + (dq * 4 + c) * CH_PS + kq * 4) =
+                    make_float4(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+        }
+        // weights of the chain rows for this tile (columns beyond a row's
+        // keys are never read by its chain)
+        float* wbuf = wts + (t & 1) * nc * CH_T;
+        for (int i = pl; i < nc * (CH_T / 4); i += CH_NP * 64) {
+            const int c = i / (CH_T / 4), j4 = (i % (CH_T / 4)) * 4;
+            const int qp = qp0 + c / gq;
+            float4 w4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const size_t col = (size_t)t * CH_T + j4;
+            if (qp < a.S && col + 4 <= a.wstride) {
+                const size_t row = (b * a.S + qp) * a.Hq + kvh * gq + (c % gq);
+                w4 = *reinterpret_cast<const float4*>(a.w + row * a.wstride + col);
+            }
+            *reinterpret_cast<float4*>(wbuf + c * CH_T + j4) = w4;
+        }
+    };
+
+    // ---- chain waves: block rescale factors of the row
+    const bool is_chain = wv < nc;
+    const int qp = qp0 + (is_chain ? wv / gq : 0);
+    const bool row_ok = is_chain && qp < a.S;
+    const size_t row = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + (is_chain ? wv % gq : 0);
+    size_t rks = 0, rke = 0, rbl = 0;
+    int nb = 0;
+    if (row_ok) {
+        kv_range<HYBRID>(a, (size_t)qp, rks, rke, rbl);
+        nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
+    }
+    if (row_ok) {
+        // corr[blk] = expf(running max before blk - block max) when the block
+        // max is finite (the running max is the last finite block max), else
+        // NEG_INF: the block leaves the accumulators unscaled
+        const float* bm = a.bmax + row * a.nbstride;
+        const float* bsm = a.bsum + row * a.nbstride;
+        float carry = NEG_INF;
+        for (int c0 = 0; c0 < nb; c0 += 64) {
+            const int i = c0 + lane;
+            const float m = i < nb ? bm[i] : NEG_INF;
+            const float bs = i < nb ? bsm[i] : 0.0f;
+            const bool fin = m > NEG_INF;
+            int idx = fin ? lane : -1;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const int o = __shfl_up(idx, off, 64);
+                if (lane >= off) idx = max(idx, o);
+            }
+            int ex = __shfl_up(idx, 1, 64);
+            if (lane == 0) ex = -1;
+            const float pm = __shfl(m, ex < 0 ? 0 : ex, 64);
+            const float prev = ex >= 0 ? pm : carry;
+            if (i < nb) {
+                corr_s[wv * nbmax + i] = fin ? cactus_expf(prev - m) : NEG_INF;
+                bsum_s[wv * nbmax + i] = bs;
+            }
+            const int last = __shfl(idx, 63, 64);
+            if (last >= 0) carry = __shfl(m, last, 64);
+        }
+    }
+    if (!is_chain && nst > 0) stage(0);
+
+    float acc = 0.0f, rs = 0.0f;
+    const int dim = sl * 64 + lane;
+    for (int t = 0; t < nst; t++) {
+        __syncthreads();
+        if (!is_chain) {
+            if (t + 1 < nst) stage(t + 1);
+            continue;
+        }
+        if (!row_ok) continue;
+        const float* pt = prod + (t & 1) * 64 * CH_PS + lane * CH_PS;
+        const float* wt = wts + ((t & 1) * nc + wv) * CH_T;
+        const int b0 = t * (CH_T / ATT_BLOCK);
+        const int b1 = min(nb, b0 + CH_T / ATT_BLOCK);
+        for (int blk = b0; blk < b1; blk++) {
+            const float c = corr_s[wv * nbmax + blk];
+            const float bse = bsum_s[wv * nbmax + blk];
+            if (c != NEG_INF) {
+                acc = acc * c;
+                rs = rs * c;
+            }
+            const size_t bs0 = rks + (size_t)blk * ATT_BLOCK;
+            const size_t be = bs0 + ATT_BLOCK < rbl ? bs0 + ATT_BLOCK : rbl;
+            const int bsz = (int)(be - bs0);
+            const int jo = (blk - b0) * ATT_BLOCK;
+            if (bsz == ATT_BLOCK && !__builtin_signbit(bse)) {
+                float4 pv[8], wv4[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    pv[j] = *reinterpret_cast<const float4*>(pt + jo + 4 * j);
+                    wv4[j] = *reinterpret_cast<const float4*>(wt + jo + 4 * j);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    acc = __builtin_fmaf(pv[j].x, wv4[j].x, acc);
+                    acc = __builtin_fmaf(pv[j].y, wv4[j].y, acc);
+                    acc = __builtin_fmaf(pv[j].z, wv4[j].z, acc);
+                    acc = __builtin_fmaf(pv[j].w, wv4[j].w, acc);
+                }
+            } else {
+                // a zero weight is skipped (kernel_attention.cpp:200-201): an
+                // FMA with it could turn an accumulator of -0 into +0
+                for (int j = 0; j < bsz; j++) {
+                    const float w = wt[jo + j];
+                    if (w != 0.0f) acc = __builtin_fmaf(pt[jo + j], w, acc);
+                }
+            }
+            rs = rs + __builtin_fabsf(bse);
+        }
+    }
+    if (row_ok && dim < d) {
+        uint16_t* ov = a.o + row * (size_t)d;
+        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
+        else ov[dim] = f2h(acc * (1.0f / rs));
+    }
+}
+
+// ------------------------------------------------ kernel B, LDS-DMA form
+// The same chains as attn_chain_kernel with the value tiles fetched by
+// gfx950 LDS DMA (global_load_lds_dword[x4]): the stage waves keep
+// CdCfg::D - 1 tiles of raw value rows, scales and weights in flight in an
+// LDS ring without holding them in registers, convert one tile per step and
+// never wait for more than the oldest tile.  Keys outside the tiles (the
+// hybrid's new fp16 rows) are read by the chains directly.
+//
+// The DMA is issued from inline assembly so that the compiler does not make
+// every LDS read wait for every outstanding DMA; the waits are explicit
+// (s_waitcnt vmcnt) and the step barrier waits for LDS only.  M0 carries
+// the LDS destination; nothing else in these kernels uses M0.
+constexpr int CD_T = 64;               // keys per tile
+constexpr int CD_PS = CD_T + 4;        // floats per product row (bank skew)
+constexpr int CD_NP = 4;               // stage waves
+constexpr int CD_KPW = CD_T / CD_NP;   // keys of a tile per stage wave
+constexpr int CD_WR = ATT_MAX_GQ / CD_NP;  // weight rows per stage wave
+
+template <bool HYBRID, int DW>
+struct CdCfg {
+    static constexpr int D = DW == 16 ? 8 : 5;                  // ring depth (tiles)
+    static constexpr int ROW_B = HYBRID ? 64 : 128;             // bytes of a 64-dim key row
+    static constexpr int ROWS_LPT = CD_KPW * ROW_B / (64 * DW); // DMA per stage wave per tile
+    static constexpr int SC_LPT = HYBRID ? 1 : 0;
+    static constexpr int W_LPT = (CD_WR * 256 + 64 * DW - 1) / (64 * DW);
+    static constexpr int LPT = ROWS_LPT + SC_LPT + W_LPT;
+    static constexpr int VM_WAIT = (D - 2) * LPT;               // DMA younger than the next tile
+    static constexpr int ROWS_OFF = 0;
+    static constexpr int SC_OFF = CD_T * ROW_B;
+    static constexpr int W_OFF = SC_OFF + (HYBRID ? CD_T * 4 : 0);
+    static constexpr int SLOT = W_OFF + ATT_MAX_GQ * CD_T * 4;
+    static_assert(VM_WAIT <= 63, "vmcnt range");
+    static_assert(ROWS_LPT * 64 * DW == CD_KPW * ROW_B, "row chunks");
+};
+
+template <int DW>
+__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds) {
+    if constexpr (DW == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
+                     : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// workgroup barrier that orders LDS only (outstanding DMA keeps flying)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Block rescale factors of one chain row, into LDS: corr[blk] =
+// expf(running max before blk - block max) when the block max is finite
+// (the running max is the last finite block max), else NEG_INF (the block
+// leaves the accumulators unscaled); bsum[blk] is the block's flagged sum.
+// One whole wave.
+__device__ __forceinline__ void chain_corr(const AttnArgs& a, size_t row, int nb, float* corr, float* bsum) {
+    const int lane = threadIdx.x & 63;
+    const float NEG_INF = -__builtin_inff();
+    const float* bm = a.bmax + row * a.nbstride;
+    const float* bsm = a.bsum + row * a.nbstride;
+#pragma unroll 4
+    for (int i = lane; i < nb; i += 64) {
+        corr[i] = bm[i];
+        bsum[i] = bsm[i];
+    }
+    float carry = NEG_INF;
+    for (int c0 = 0; c0 < nb; c0 += 64) {
+        const int i = c0 + lane;
+        const float m = i < nb ? corr[i] : NEG_INF;
+        const bool fin = m > NEG_INF;
+        int idx = fin ? lane : -1;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int o = __shfl_up(idx, off, 64);
+            if (lane >= off) idx = max(idx, o);
+        }
+        int ex = __shfl_up(idx, 1, 64);
+        if (lane == 0) ex = -1;
+        const float pm = __shfl(m, ex < 0 ? 0 : ex, 64);
+        const float prev = ex >= 0 ? pm : carry;
+        if (i < nb) corr[i] = fin ? cactus_expf(prev - m) : NEG_INF;
+        const int last = __shfl(idx, 63, 64);
+        if (last >= 0) carry = __shfl(m, last, 64);
+    }
+}
+
+// One tile of a chain row: blocks [b0, b1), all keys inside the tile; pt
+// is this lane's product row of the tile, wt the row's weights.
+__device__ __forceinline__ void chain_tile(const float* pt, const float* wt, int b0, int b1, size_t rks,
+                                           size_t rbl, const float* cw, const float* cb, float& acc,
+                                           float& rs) {
+    const float NEG_INF = -__builtin_inff();
+    // both blocks of the tile full: every LDS read of the tile at once
+    if (b1 - b0 == 2 && rks + (size_t)(b0 + 2) * ATT_BLOCK <= rbl) {
+        const float c0 = cw[b0], c1 = cw[b0 + 1];
+        const float s0 = cb[b0], s1 = cb[b0 + 1];
+        float4 pv[16], wq[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            pv[j] = *reinterpret_cast<const float4*>(pt + 4 * j);
+            wq[j] = *reinterpret_cast<const float4*>(wt + 4 * j);
+        }
+        if (!__builtin_signbit(s0) && !__builtin_signbit(s1)) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float c = h ? c1 : c0;
+                if (c != NEG_INF) {
+                    acc = acc * c;
+                    rs = rs * c;
+                }
+#pragma unroll
+                for (int j = 8 * h; j < 8 * h + 8; j++) {
+                    acc = __builtin_fmaf(pv[j].x, wq[j].x, acc);
+                    acc = __builtin_fmaf(pv[j].y, wq[j].y, acc);
+                    acc = __builtin_fmaf(pv[j].z, wq[j].z, acc);
+                    acc = __builtin_fmaf(pv[j].w, wq[j].w, acc);
+                }
+                rs = rs + (h ? s1 : s0);
+            }
+            return;
+        }
+    }
+    for (int blk = b0; blk < b1; blk++) {
+        const float c = cw[blk];
+        const float bse = cb[blk];
+        if (c != NEG_INF) {
+            acc = acc * c;
+            rs = rs * c;
+        }
+        const size_t bs0 = rks + (size_t)blk * ATT_BLOCK;
+        const size_t be = bs0 + ATT_BLOCK < rbl ? bs0 + ATT_BLOCK : rbl;
+        const int bsz = (int)(be - bs0);
+        const int jo = (blk - b0) * ATT_BLOCK;
+        if (bsz == ATT_BLOCK && !__builtin_signbit(bse)) {
+            float4 pv[8], wq[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                pv[j] = *reinterpret_cast<const float4*>(pt + jo + 4 * j);
+                wq[j] = *reinterpret_cast<const float4*>(wt + jo + 4 * j);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                acc = __builtin_fmaf(pv[j].x, wq[j].x, acc);
+                acc = __builtin_fmaf(pv[j].y, wq[j].y, acc);
+                acc = __builtin_fmaf(pv[j].z, wq[j].z, acc);
+                acc = __builtin_fmaf(pv[j].w, wq[j].w, acc);
+            }
+        } else {
+            // a zero weight is skipped (kernel_attention.cpp:200-201): an
+            // FMA with it could turn an accumulator of -0 into +0
+            for (int j = 0; j < bsz; j++) {
+                const float w = wt[jo + j];
+                if (w != 0.0f) acc = __builtin_fmaf(pt[jo + j], w, acc);
+            }
+        }
+        rs = rs + __builtin_fabsf(bse);
+    }
+}
+
+// Blocks of a chain row reaching past the tiles: tile keys from the last
+// tile (tbase: its first key; pt, wt as in chain_tile), the hybrid's new
+// rows read directly (pf: the first new row, loaded early).
+template <bool HYBRID>
+__device__ __forceinline__ void chain_tail(const AttnArgs& a, size_t b, int kvh, int dim, size_t row, int nb_tile,
+                                           int nb, size_t rks, size_t rbl, size_t kt_end, size_t tbase,
+                                           const float* pt, const float* wt, bool pf, float pf_p, float pf_w,
+                                           const float* cw, const float* cb, float& acc, float& rs) {
+    const float NEG_INF = -__builtin_inff();
+    const int d = a.d;
+    for (int blk = nb_tile; blk < nb; blk++) {
+        const float c = cw[blk];
+        const float bse = cb[blk];
+        if (c != NEG_INF) {
+            acc = acc * c;
+            rs = rs * c;
+        }
+        const size_t bs0 = rks + (size_t)blk * ATT_BLOCK;
+        const size_t be = bs0 + ATT_BLOCK < rbl ? bs0 + ATT_BLOCK : rbl;
+        const int bsz = (int)(be - bs0);
+        // new rows past the prefetched one: one batch of loads per block
+        float gp[ATT_BLOCK], gw[ATT_BLOCK];
+#pragma unroll
+        for (int j = 0; j < ATT_BLOCK; j++) {
+            gp[j] = 0.0f;
+            gw[j] = 0.0f;
+        }
+        if constexpr (HYBRID) {
+            const size_t covered = pf ? (size_t)a.cache_len + 1 : kt_end;
+            if (be > (covered > kt_end ? covered : kt_end)) {
+                const int dimc = dim < d ? dim : d - 1;
+#pragma unroll
+                for (int j = 0; j < ATT_BLOCK; j++) {
+                    size_t kp = bs0 + j;
+                    if (kp >= be) kp = be - 1;
+                    if (kp < a.cache_len) kp = a.cache_len;
+                    gw[j] = a.w[row * a.wstride + (kp - rks)];
+                    gp[j] = h2f(a.v[((b * a.new_len + (kp - a.cache_len)) * a.Hkv + kvh) * (size_t)d + dimc]);
                 }
             }
         }
-        rsum = rsum + bsum;
-    }
-
-    uint16_t* ov = a.o + ((b * a.S + qp) * a.Hq + h) * (size_t)d;
-    if (rsum > 0.0f) {
-        const float inv = 1.0f / rsum;
+        float pv[ATT_BLOCK], wq[ATT_BLOCK];
 #pragma unroll
-        for (int i = 0; i < ATT_DPL; i++) {
-            const int dim = lane + 64 * i;
-            if (dim < d) ov[dim] = dim < da ? f2h(acc[i] * inv) : (uint16_t)0;
+        for (int j = 0; j < ATT_BLOCK; j++) {
+            pv[j] = 0.0f;
+            wq[j] = 0.0f;
+            const size_t kp = bs0 + j;
+            if (j < bsz) {
+                if (kp < kt_end) {
+                    pv[j] = pt[kp - tbase];
+                    wq[j] = wt[kp - tbase];
+                } else if (pf && kp == a.cache_len) {
+                    pv[j] = pf_p;
+                    wq[j] = pf_w;
+                } else {
+                    pv[j] = gp[j];
+                    wq[j] = gw[j];
+                }
+            }
         }
-    } else {
-        for (int dim = lane; dim < d; dim += 64) ov[dim] = 0;
+#pragma unroll
+        for (int j = 0; j < ATT_BLOCK; j++)
+            if (j < bsz && wq[j] != 0.0f) acc = __builtin_fmaf(pv[j], wq[j], acc);
+        rs = rs + __builtin_fabsf(bse);
     }
+}
+
+template <bool HYBRID, int DW>
+__global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_dma_kernel(AttnArgs a_in, int qpg,
+                                                                                    int nbmax) {
+    using C = CdCfg<HYBRID, DW>;
+    const AttnArgs a = resolve(a_in);
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int gq = a.gq, nc = qpg * gq;
+    unsigned char* ring = smem;                                            // [D][SLOT]
+    float* prod = reinterpret_cast<float*>(smem + C::D * C::SLOT);         // [2][64][CD_PS]
+    float* corr_s = prod + 2 * 64 * CD_PS;                                 // [nc][nbmax]
+    float* bsum_s = corr_s + (size_t)nc * nbmax;                           // [nc][nbmax]
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
+    const float NEG_INF = -__builtin_inff();
+
+    const int d = a.d, da = (d / 8) * 8;
+    const int nsl = (d + 63) / 64;
+    size_t g = blockIdx.x;
+    const int sl = (int)(g % nsl);
+    g /= nsl;
+    const int kvh = (int)(g % a.Hkv);
+    g /= a.Hkv;
+    const int ngrp = (a.S + qpg - 1) / qpg;
+    const int qp0 = (int)(g % ngrp) * qpg;
+    const size_t b = g / ngrp;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+
+    size_t ks, ke_f, bl_f;
+    kv_range<HYBRID>(a, (size_t)qp0, ks, ke_f, bl_f);
+    const int qlast = min(qp0 + qpg, a.S) - 1;
+    size_t ks_l, ke_l, bl_l;
+    kv_range<HYBRID>(a, (size_t)qlast, ks_l, ke_l, bl_l);
+    size_t kneed = ks;
+    if (ke_l > ks) {
+        kneed = ks + ((ke_l - ks + ATT_BLOCK - 1) / ATT_BLOCK) * ATT_BLOCK;
+        if (kneed > bl_l) kneed = bl_l;
+    }
+    // keys served by tiles: the INT8 cache for the hybrid, all for FP16
+    const size_t kt_end = HYBRID ? (kneed < a.cache_len ? kneed : (size_t)a.cache_len) : kneed;
+    const int nst = kt_end > ks ? (int)((kt_end - ks + CD_T - 1) / CD_T) : 0;
+    const bool is_chain = wv < nc;
+    const int pw = wv - nc;
+
+    // DMA sources of tile 0 per lane; a tile further is a fixed stride on
+    // (the last tile clamps keys to the tile range instead)
+    const size_t krow = (size_t)a.Hkv * d;                     // elements between keys
+    const size_t vlen = HYBRID ? a.cache_len : a.Skv;
+    const char* vbase = HYBRID ? reinterpret_cast<const char*>(a.vc) : reinterpret_cast<const char*>(a.v);
+    constexpr int ESZ = HYBRID ? 1 : 2;
+    auto row_src = [&](int i, size_t kp) -> const char* {
+        const int o = i * 64 * DW + lane * DW;
+        int cel = (o % C::ROW_B) / ESZ;
+        if (sl * 64 + cel + DW / ESZ > d) cel = 0;   // beyond the row: any chunk inside it
+        return vbase + (((b * vlen + kp) * a.Hkv + kvh) * (size_t)d + sl * 64 + cel) * ESZ;
+    };
+    auto scale_src = [&](size_t kp) -> const float* {
+        return a.vs + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg + (sl * 64) / a.qgs;
+    };
+    auto w_src = [&](int i) -> const float* {
+        const int o = i * 64 * DW + lane * DW;
+        int r = pw * CD_WR + o / 256;
+        int qp = qp0 + r / gq;
+        if (r >= nc || qp >= a.S) {
+            r = 0;
+            qp = qp0;
+        }
+        const size_t row = (b * a.S + qp) * a.Hq + kvh * gq + r % gq;
+        return a.w + row * a.wstride + (o % 256) / 4;
+    };
+    // rolling DMA sources, one tile further per issue (tiles are issued in
+    // order); the last tile clamps its keys to the tile range instead
+    const char* rp[C::ROWS_LPT];
+    const float* sp = nullptr;
+    const float* wp[C::W_LPT];
+    if (!is_chain) {
+#pragma unroll
+        for (int i = 0; i < C::ROWS_LPT; i++)
+            rp[i] = row_src(i, ks + pw * CD_KPW + (i * 64 * DW + lane * DW) / C::ROW_B);
+        if (HYBRID) sp = scale_src(ks + pw * CD_KPW + (lane & (CD_KPW - 1)));
+#pragma unroll
+        for (int i = 0; i < C::W_LPT; i++) wp[i] = w_src(i);
+    }
+    const size_t rstep = (size_t)CD_T * krow * ESZ;
+    const size_t sstep = (size_t)CD_T * a.Hkv * a.nqg;
+    const int kt_len = (int)(kt_end - ks);
+    auto issue = [&](int t) {
+        const uint32_t slot = ring_lds + (uint32_t)((t % C::D) * C::SLOT);
+        const uint32_t rdst = slot + C::ROWS_OFF + pw * CD_KPW * C::ROW_B;
+        const uint32_t sdst = slot + C::SC_OFF + pw * CD_KPW * 4;
+        if ((t + 1) * CD_T <= kt_len) {
+#pragma unroll
+            for (int i = 0; i < C::ROWS_LPT; i++) lds_dma<DW>(rp[i], rdst + i * 64 * DW);
+            if (HYBRID && lane < CD_KPW) lds_dma<4>(sp, sdst);
+        } else {
+            const size_t tb = ks + (size_t)t * CD_T;
+            const size_t klast = kt_end - 1;
+#pragma unroll
+            for (int i = 0; i < C::ROWS_LPT; i++) {
+                size_t kp = tb + pw * CD_KPW + (i * 64 * DW + lane * DW) / C::ROW_B;
+                if (kp > klast) kp = klast;
+                lds_dma<DW>(row_src(i, kp), rdst + i * 64 * DW);
+            }
+            if (HYBRID && lane < CD_KPW) {
+                size_t kp = tb + pw * CD_KPW + lane;
+                if (kp > klast) kp = klast;
+                lds_dma<4>(scale_src(kp), sdst);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::W_LPT; i++)
+            if (i * 64 * DW + lane * DW < CD_WR * 256)
+                lds_dma<DW>(wp[i], slot + C::W_OFF + pw * CD_WR * 256 + i * 64 * DW);
+#pragma unroll
+        for (int i = 0; i < C::ROWS_LPT; i++) rp[i] += rstep;
+        if (HYBRID) sp += sstep;
+#pragma unroll
+        for (int i = 0; i < C::W_LPT; i++) wp[i] += CD_T;
+    };
+    auto convert = [&](int t) {
+        const unsigned char* slot = ring + (t % C::D) * C::SLOT;
+        float* pb = prod + (t & 1) * 64 * CD_PS;
+        const int dq = lane & 15, kq = lane >> 4;
+        // all LDS reads first, then the products, then the stores
+        uint32_t r8[4];
+        uint2 r16[4];
+        float sc[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int kl = pw * CD_KPW + kq * 4 + e;
+            if (HYBRID) {
+                r8[e] = *reinterpret_cast<const uint32_t*>(slot + C::ROWS_OFF + kl * 64 + dq * 4);
+                sc[e] = *reinterpret_cast<const float*>(slot + C::SC_OFF + kl * 4);
+            } else {
+                r16[e] = *reinterpret_cast<const uint2*>(slot + C::ROWS_OFF + kl * 128 + dq * 8);
+            }
+        }
+        float pr[4][4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (HYBRID) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) pr[e][c] = (float)(int8_t)((r8[e] >> (8 * c)) & 0xFF) * sc[e];
+            } else {
+                pr[e][0] = h2f((uint16_t)(r16[e].x & 0xFFFF));
+                pr[e][1] = h2f((uint16_t)(r16[e].x >> 16));
+                pr[e][2] = h2f((uint16_t)(r16[e].y & 0xFFFF));
+                pr[e][3] = h2f((uint16_t)(r16[e].y >> 16));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            *reinterpret_cast<float4*>(pb + (dq * 4 + c) * CD_PS + pw * CD_KPW + kq * 4) =
+                make_float4(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+    };
+
+    // ---- chain row
+    const int qp = qp0 + (is_chain ? wv / gq : 0);
+    const bool row_ok = is_chain && qp < a.S;
+    const size_t row = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + (is_chain ? wv % gq : 0);
+    size_t rks = 0, rke = 0, rbl = 0;
+    int nb = 0, nb_tile = 0;
+    if (row_ok) {
+        kv_range<HYBRID>(a, (size_t)qp, rks, rke, rbl);
+        nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
+        nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
+    }
+    const int dim = sl * 64 + lane;
+    // the first new row of the hybrid (the decode step's own key), early
+    float pf_p = 0.0f, pf_w = 0.0f;
+    const bool pf = HYBRID && row_ok && a.cache_len < rke;
+    if (pf) {
+        pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
+        if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
+    }
+    if (row_ok) chain_corr(a, row, nb, corr_s + wv * nbmax, bsum_s + wv * nbmax);
+
+    if (!is_chain && nst > 0) {
+        for (int t = 0; t < C::D - 1; t++)
+            if (t < nst) issue(t);
+        if (nst >= C::D - 1) wait_dma<C::VM_WAIT>();
+        else wait_dma<0>();
+        convert(0);
+    }
+    const float* cw = corr_s + wv * nbmax;
+    const float* cb = bsum_s + wv * nbmax;
+    float acc = 0.0f, rs = 0.0f;
+    for (int t = 0; t < nst; t++) {
+        lds_barrier();
+        if (!is_chain) {
+            if (t + C::D - 1 < nst) issue(t + C::D - 1);
+            if (t + 1 < nst) {
+                if (t + C::D - 1 < nst) wait_dma<C::VM_WAIT>();
+                else wait_dma<0>();
+                convert(t + 1);
+            }
+            continue;
+        }
+        if (!row_ok) continue;
+        const float* pt = prod + (t & 1) * 64 * CD_PS + lane * CD_PS;
+        const float* wt = reinterpret_cast<const float*>(ring + (t % C::D) * C::SLOT + C::W_OFF) + wv * CD_T;
+        const int b0 = t * (CD_T / ATT_BLOCK);
+        const int b1 = min(nb_tile, b0 + CD_T / ATT_BLOCK);
+        chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc, rs);
+    }
+    if (!row_ok) return;
+    // blocks reaching past the tiles: tile keys from the last tile (still
+    // resident), new rows read directly
+    const int tl = nst - 1;
+    const size_t tbase = ks + (size_t)(tl > 0 ? tl : 0) * CD_T;
+    const float* pt = prod + ((tl > 0 ? tl : 0) & 1) * 64 * CD_PS + lane * CD_PS;
+    const float* wt =
+        reinterpret_cast<const float*>(ring + ((tl > 0 ? tl : 0) % C::D) * C::SLOT + C::W_OFF) + wv * CD_T;
+    chain_tail<HYBRID>(a, b, kvh, dim, row, nb_tile, nb, rks, rbl, kt_end, tbase, pt, wt, pf, pf_p, pf_w, cw, cb,
+                       acc, rs);
+    if (dim < d) {
+        uint16_t* ov = a.o + row * (size_t)d;
+        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
+        else ov[dim] = f2h(acc * (1.0f / rs));
+    }
+}
+
+// ------------------------------------------------ kernel B, product tiles
+// With the INT8 value cache mirrored as fp32 product tiles (every cached
+// (float)code * scale already rounded, kv_shadow.hip), the stage waves only
+// move memory: each tile is 17 KB of products in the chains' LDS layout
+// plus the weights, fetched by LDS DMA D - 1 tiles ahead.  Tile layout, per
+// (batch, kv head, 64-dim slice, 64-key tile): [64 dims][SH_PS keys].
+constexpr int SH_PS = CD_T + 4;                    // keys per dim row (4 of them padding)
+constexpr int SH_TILE_B = 64 * SH_PS * 4;          // 17408 bytes
+constexpr int SH_PCHUNKS = SH_TILE_B / 1024;       // 1 KB DMA per tile
+constexpr int SH_W_OFF = SH_TILE_B;
+constexpr int SH_SLOT = SH_TILE_B + ATT_MAX_GQ * CD_T * 4;
+static_assert(SH_PCHUNKS * 1024 == SH_TILE_B, "tile chunks");
+
+template <int D>
+__global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_kernel(AttnArgs a_in, int qpg,
+                                                                                       int nbmax) {
+    const AttnArgs a = resolve(a_in);
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int gq = a.gq, nc = qpg * gq;
+    unsigned char* ring = smem;                                            // [D][SH_SLOT]
+    float* corr_s = reinterpret_cast<float*>(smem + D * SH_SLOT);          // [nc][nbmax]
+    float* bsum_s = corr_s + (size_t)nc * nbmax;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
+
+    const int d = a.d, da = (d / 8) * 8;
+    const int nsl = (d + 63) / 64;
+    size_t g = blockIdx.x;
+    const int sl = (int)(g % nsl);
+    g /= nsl;
+    const int kvh = (int)(g % a.Hkv);
+    g /= a.Hkv;
+    const int ngrp = (a.S + qpg - 1) / qpg;
+    const int qp0 = (int)(g % ngrp) * qpg;
+    const size_t b = g / ngrp;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+
+    size_t ks, ke_l, bl_l;
+    const int qlast = min(qp0 + qpg, a.S) - 1;
+    kv_range<true>(a, (size_t)qlast, ks, ke_l, bl_l);
+    size_t kneed = ks;
+    if (ke_l > ks) {
+        kneed = ks + ((ke_l - ks + ATT_BLOCK - 1) / ATT_BLOCK) * ATT_BLOCK;
+        if (kneed > bl_l) kneed = bl_l;
+    }
+    const size_t kt_end = kneed < a.cache_len ? kneed : (size_t)a.cache_len;
+    const int nst = kt_end > 0 ? (int)((kt_end + CD_T - 1) / CD_T) : 0;
+    const bool is_chain = wv < nc;
+    const int pw = wv - nc;
+
+    // stage wave pw: product chunks pw, pw + CD_NP, ...; the weights of
+    // rows 4k..4k+3 go to stage wave 1 + k
+    const int wn = (nc + 3) / 4;
+    const bool my_w = pw >= 1 && pw <= wn;
+    const int lpt = (SH_PCHUNKS - pw + CD_NP - 1) / CD_NP + (my_w ? 1 : 0);
+    const char* psrc = nullptr;
+    const float* wsrc = nullptr;
+    if (!is_chain) {
+        psrc = reinterpret_cast<const char*>(a.vsh) +
+               (((b * a.Hkv + kvh) * nsl + sl) * a.sh_ntile) * (size_t)SH_TILE_B + lane * 16;
+        if (my_w) {
+            int r = (pw - 1) * 4 + lane / 16;
+            int qp = qp0 + r / gq;
+            if (r >= nc || qp >= a.S) {
+                r = 0;
+                qp = qp0;
+            }
+            const size_t row = (b * a.S + qp) * a.Hq + kvh * gq + r % gq;
+            wsrc = a.w + row * a.wstride + (lane % 16) * 4;
+        }
+    }
+    auto issue = [&](int t) {
+        const uint32_t slot = ring_lds + (uint32_t)((t % D) * SH_SLOT);
+        const char* src = psrc + (size_t)t * SH_TILE_B;
+        for (int c = pw; c < SH_PCHUNKS; c += CD_NP) lds_dma<16>(src + c * 1024, slot + c * 1024);
+        if (my_w) lds_dma<16>(wsrc + (size_t)t * CD_T, slot + SH_W_OFF + (pw - 1) * 1024);
+    };
+    auto wait_next = [&](bool all_issued) {
+        if (!all_issued) wait_dma<0>();
+        else if (lpt == 5) wait_dma<(D - 2) * 5>();
+        else wait_dma<(D - 2) * 4>();
+    };
+
+    // ---- chain row
+    const int qp = qp0 + (is_chain ? wv / gq : 0);
+    const bool row_ok = is_chain && qp < a.S;
+    const size_t row = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + (is_chain ? wv % gq : 0);
+    size_t rks = 0, rke = 0, rbl = 0;
+    int nb = 0, nb_tile = 0;
+    if (row_ok) {
+        kv_range<true>(a, (size_t)qp, rks, rke, rbl);
+        nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
+        nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
+    }
+    const int dim = sl * 64 + lane;
+    float pf_p = 0.0f, pf_w = 0.0f;
+    const bool pf = row_ok && a.cache_len < rke;
+    if (pf) {
+        pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
+        if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
+    }
+    if (row_ok) chain_corr(a, row, nb, corr_s + wv * nbmax, bsum_s + wv * nbmax);
+
+    if (!is_chain && nst > 0) {
+        for (int t = 0; t < D - 1; t++)
+            if (t < nst) issue(t);
+        wait_next(nst >= D - 1);
+    }
+    const float* cw = corr_s + wv * nbmax;
+    const float* cb = bsum_s + wv * nbmax;
+    float acc = 0.0f, rs = 0.0f;
+    for (int t = 0; t < nst; t++) {
+        lds_barrier();
+        if (!is_chain) {
+            if (t + D - 1 < nst) issue(t + D - 1);
+            if (t + 1 < nst) wait_next(t + D - 1 < nst);
+            continue;
+        }
+        if (!row_ok) continue;
+        const unsigned char* slot = ring + (t % D) * SH_SLOT;
+        const float* pt = reinterpret_cast<const float*>(slot) + lane * SH_PS;
+        const float* wt = reinterpret_cast<const float*>(slot + SH_W_OFF) + wv * CD_T;
+        const int b0 = t * (CD_T / ATT_BLOCK);
+        const int b1 = min(nb_tile, b0 + CD_T / ATT_BLOCK);
+        chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc, rs);
+    }
+    if (!row_ok) return;
+    const int tl = nst > 0 ? nst - 1 : 0;
+    const unsigned char* slot = ring + (tl % D) * SH_SLOT;
+    chain_tail<true>(a, b, kvh, dim, row, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
+                     reinterpret_cast<const float*>(slot) + lane * SH_PS,
+                     reinterpret_cast<const float*>(slot + SH_W_OFF) + wv * CD_T, pf, pf_p, pf_w, cw, cb, acc,
+                     rs);
+    if (dim < d) {
+        uint16_t* ov = a.o + row * (size_t)d;
+        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
+        else ov[dim] = f2h(acc * (1.0f / rs));
+    }
+}
+
+// ------------------------------------------------ per-(device, stream) scratch
+struct AttnScratch {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+static std::mutex g_att_mu;
+static std::map<std::pair<int, void*>, AttnScratch> g_att_scratch;
+
+static int attn_scratch(void* stream, size_t bytes, void** out) {
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_att_mu);
+    AttnScratch& s = g_att_scratch[std::make_pair(dev, stream)];
+    if (s.bytes < bytes) {
+        // the previous buffer is kept: kernels queued on the stream may use it
+        size_t want = bytes + bytes / 4;
+        void* p = nullptr;
+        CH_HIP(hipMalloc(&p, want));
+        s.ptr = p;
+        s.bytes = want;
+    }
+    *out = s.ptr;
+    return CACTUS_HIP_OK;
+}
+
+template <bool HYBRID>
+static int launch_attention(AttnArgs a, void* stream) {
+    // largest key range over the launch (query 0 .. S-1)
+    size_t maxr = 0;
+    for (int qp : {0, a.S - 1}) {
+        const size_t aq = a.pos_off + qp;
+        size_t s0 = 0, e = a.Skv;
+        if (!HYBRID) {
+            if (a.window > 0 && a.window < a.Skv) {
+                if (aq > a.window) s0 = aq - a.window;
+                if (a.causal && aq + 1 < e) e = aq + 1;
+            } else if (a.causal && aq + 1 < e) {
+                e = aq + 1;
+            }
+        } else if (a.causal && aq + 1 < e) {
+            e = aq + 1;
+        }
+        if (e > s0 && e - s0 > maxr) maxr = e - s0;
+    }
+    if (!HYBRID && a.window > 0 && a.window < a.Skv) maxr = a.Skv;  // conservative
+    if (a.dyn) maxr = a.max_cache + a.new_len;
+    const size_t rows = (size_t)a.B * a.S * a.Hq;
+    const int nb = (int)((maxr + ATT_BLOCK - 1) / ATT_BLOCK);
+    CH_REQUIRE(nb <= 1024, "attention: key range above 32768 is not supported");
+    a.wstride = (maxr + 63) & ~(size_t)63;
+    a.nbstride = nb > 0 ? nb : 1;
+    const size_t wbytes = rows * a.wstride * sizeof(float);
+    const size_t bbytes = rows * (size_t)a.nbstride * sizeof(float);
+    void* scratch = nullptr;
+    int rc = attn_scratch(stream, wbytes + 2 * bbytes + 256, &scratch);
+    if (rc) return rc;
+    a.w = static_cast<float*>(scratch);
+    a.bmax = reinterpret_cast<float*>(static_cast<char*>(scratch) + wbytes);
+    a.bsum = a.bmax + rows * a.nbstride;
+    const size_t chunks = (maxr + 63) / 64;
+    if (chunks > 0) {
+        dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * a.S * a.Hkv));
+        hipLaunchKernelGGL(attn_scores_kernel<HYBRID>, ga, dim3(256), 0, as_stream(stream), a);
+        rc = check_launch("attention scores");
+        if (rc) return rc;
+    }
+    // chain kernel: rows sharing a kv head are grouped so that their value
+    // tiles are staged once; a sliding window gives every row its own start
+    const bool windowed = !HYBRID && a.window > 0 && a.window < a.Skv;
+    int qpg = windowed ? 1 : ATT_MAX_GQ / a.gq;
+    if (qpg > a.S) qpg = a.S;
+    if (qpg < 1) qpg = 1;
+    const int nbmax = a.nbstride;
+    const size_t nsl = (size_t)(a.d + 63) / 64;
+    if (HYBRID && a.vsh) {
+        // product tiles: ring depth 8, or 5 where the rows' block data needs the room
+        auto sh_smem = [&](int q, int depth) {
+            return (size_t)depth * SH_SLOT + 2 * (size_t)q * a.gq * nbmax * sizeof(float);
+        };
+        int depth = 8;
+        while (qpg > 1 && sh_smem(qpg, depth) > 160 * 1024) qpg = (qpg + 1) / 2;
+        if (sh_smem(qpg, depth) > 160 * 1024) depth = 5;
+        const size_t smem = sh_smem(qpg, depth);
+        CH_REQUIRE(smem <= 160 * 1024, "attention: key range too long for the product-tile kernel");
+        static bool sh_attr[2] = {false, false};
+        const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
+        const size_t groups = (size_t)a.B * ngrp * a.Hkv * nsl;
+        const dim3 blk(64 * (qpg * a.gq + CD_NP));
+        if (depth == 8) {
+            if (!sh_attr[0]) {
+                CH_HIP(hipFuncSetAttribute((const void*)attn_chain_shadow_kernel<8>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                sh_attr[0] = true;
+            }
+            hipLaunchKernelGGL(attn_chain_shadow_kernel<8>, dim3((unsigned)groups), blk, smem, as_stream(stream), a,
+                               qpg, nbmax);
+        } else {
+            if (!sh_attr[1]) {
+                CH_HIP(hipFuncSetAttribute((const void*)attn_chain_shadow_kernel<5>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                sh_attr[1] = true;
+            }
+            hipLaunchKernelGGL(attn_chain_shadow_kernel<5>, dim3((unsigned)groups), blk, smem, as_stream(stream), a,
+                               qpg, nbmax);
+        }
+        return check_launch("attention values");
+    }
+    // LDS-DMA form: value rows in 16- or 4-byte chunks, one scale group per
+    // 64-dim slice; otherwise the register-staged form
+    const uintptr_t vp = HYBRID ? (uintptr_t)a.vc : (uintptr_t)a.v;
+    const bool g64 = !HYBRID || (a.qgs % 64 == 0);
+    const bool w16 = g64 && (HYBRID ? a.d % 16 == 0 : a.d % 8 == 0) && vp % 16 == 0 &&
+                     (!HYBRID || (uintptr_t)a.vs % 4 == 0);
+    const bool w4 = g64 && a.d % 4 == 0 && vp % 4 == 0 && (!HYBRID || (uintptr_t)a.vs % 4 == 0);
+    auto dma_smem = [&](int q) -> size_t {
+        const size_t slot = w16 ? CdCfg<HYBRID, 16>::SLOT : CdCfg<HYBRID, 4>::SLOT;
+        const size_t depth = w16 ? CdCfg<HYBRID, 16>::D : CdCfg<HYBRID, 4>::D;
+        return depth * slot + (2 * 64 * CD_PS + 2 * (size_t)q * a.gq * nbmax) * sizeof(float);
+    };
+    if (w16 || w4) {
+        while (qpg > 1 && dma_smem(qpg) > 160 * 1024) qpg = (qpg + 1) / 2;
+        if (dma_smem(qpg) <= 160 * 1024) {
+            static bool attr_set[2][2] = {{false, false}, {false, false}};
+            const size_t smem = dma_smem(qpg);
+            const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
+            const size_t groups = (size_t)a.B * ngrp * a.Hkv * nsl;
+            const dim3 blk(64 * (qpg * a.gq + CD_NP));
+            if (w16) {
+                if (!attr_set[HYBRID][1]) {
+                    CH_HIP(hipFuncSetAttribute((const void*)attn_chain_dma_kernel<HYBRID, 16>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                    attr_set[HYBRID][1] = true;
+                }
+                hipLaunchKernelGGL((attn_chain_dma_kernel<HYBRID, 16>), dim3((unsigned)groups), blk, smem,
+                                   as_stream(stream), a, qpg, nbmax);
+            } else {
+                if (!attr_set[HYBRID][0]) {
+                    CH_HIP(hipFuncSetAttribute((const void*)attn_chain_dma_kernel<HYBRID, 4>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                    attr_set[HYBRID][0] = true;
+                }
+                hipLaunchKernelGGL((attn_chain_dma_kernel<HYBRID, 4>), dim3((unsigned)groups), blk, smem,
+                                   as_stream(stream), a, qpg, nbmax);
+            }
+            return check_launch("attention values");
+        }
+        qpg = 1;
+    }
+    const int nc = qpg * a.gq;
+    const uintptr_t hp = (uintptr_t)a.v;
+    const int vec_ok = (a.d % 4 == 0) && ((HYBRID ? (uintptr_t)a.vc : 0) % 4 == 0) && (hp % 8 == 0);
+    const size_t smem = (2 * 64 * CH_PS + 2 * (size_t)nc * CH_T + 2 * (size_t)nc * nbmax) * sizeof(float);
+    CH_REQUIRE(smem <= 160 * 1024, "attention: key range too long for the chain kernel");
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[HYBRID]) {
+        CH_HIP(hipFuncSetAttribute((const void*)attn_chain_kernel<HYBRID>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+        attr_set[HYBRID] = true;
+    }
+    const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
+    const size_t groups = (size_t)a.B * ngrp * a.Hkv * nsl;
+    hipLaunchKernelGGL(attn_chain_kernel<HYBRID>, dim3((unsigned)groups), dim3(64 * (nc + CH_NP)), smem,
+                       as_stream(stream), a, qpg, nbmax, vec_ok);
+    return check_launch("attention values");
+}
+
+// Hybrid attention of one decode step whose cache length and position are
+// read from the device step state (see AttnArgs::dyn).
+int attention_hybrid_decode(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                            const float* vs, const uint16_t* k_new, const uint16_t* v_new,
+                            uint16_t* o, int Hq, int Hkv, int d, float scale, const uint32_t* state,
+                            size_t max_cache, const float* v_shadow, size_t shadow_tiles, void* stream) {
+    AttnArgs a{};
+    a.q = q; a.k = k_new; a.v = v_new; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.o = o;
+    a.B = 1; a.S = 1; a.Hq = Hq; a.Hkv = Hkv; a.gq = Hq / Hkv; a.d = d;
+    a.new_len = 1; a.cache_len = max_cache; a.Skv = max_cache + 1; a.pos_off = max_cache;
+    a.causal = 1; a.scale = scale; a.qgs = 128; a.nqg = (d + 127) / 128;
+    a.dyn = state; a.max_cache = max_cache;
+    a.vsh = v_shadow; a.sh_ntile = shadow_tiles;
+    CH_REQUIRE(!v_shadow || shadow_tiles * CD_T >= max_cache, "decode attention: product tiles too short");
+    return launch_attention<true>(a, stream);
 }
 
 }  // namespace cactus_hip
@@ -230,18 +1273,19 @@ int cactus_hip_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_
     CH_REQUIRE(q && o && (kv_seq_len == 0 || (k && v)), "attention_f16: null pointer");
     CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
                "attention_f16: num_q_heads must be a multiple of num_kv_heads");
+    CH_REQUIRE(num_q_heads / num_kv_heads <= (size_t)ATT_MAX_GQ,
+               "attention_f16: more than 8 query heads per KV head is not supported");
     CH_REQUIRE(head_dim <= (size_t)ATT_MAX_D, "attention_f16: head_dim > 256 not supported");
     CH_REQUIRE(head_dim % 4 == 0, "attention_f16: head_dim must be a multiple of 4");
+    CH_REQUIRE(batch * seq_len * num_kv_heads < (1u << 31), "attention_f16: too many rows");
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)head_dim);
     AttnArgs a{};
     a.q = q; a.k = k; a.v = v; a.o = o; a.mask = mask;
     a.B = (int)batch; a.S = (int)seq_len; a.Hq = (int)num_q_heads; a.Hkv = (int)num_kv_heads;
+    a.gq = (int)(num_q_heads / num_kv_heads);
     a.d = (int)head_dim; a.Skv = kv_seq_len; a.pos_off = position_offset; a.window = window_size;
     a.causal = is_causal ? 1 : 0; a.scale = scale; a.qgs = 1; a.nqg = 1;
-    const size_t items = batch * seq_len * num_q_heads;
-    hipLaunchKernelGGL(attention_ref_kernel<false>, dim3(ceil_div(items, 4)), dim3(256), 0,
-                       as_stream(stream), a);
-    return check_launch("attention_f16");
+    return launch_attention<false>(a, stream);
 }
 
 int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cached,
@@ -259,22 +1303,23 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
     CH_REQUIRE(new_len == 0 || (k_new && v_new), "attention_hybrid: null new K/V pointer");
     CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
                "attention_hybrid: num_q_heads must be a multiple of num_kv_heads");
+    CH_REQUIRE(num_q_heads / num_kv_heads <= (size_t)ATT_MAX_GQ,
+               "attention_hybrid: more than 8 query heads per KV head is not supported");
     CH_REQUIRE(head_dim <= (size_t)ATT_MAX_D && head_dim % 8 == 0,
                "attention_hybrid: head_dim must be a multiple of 8 and <= 256");
     CH_REQUIRE(quant_group_size > 0, "attention_hybrid: quant_group_size must be > 0");
+    CH_REQUIRE(batch * seq_len * num_kv_heads < (1u << 31), "attention_hybrid: too many rows");
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)head_dim);
     AttnArgs a{};
     a.q = q; a.k = k_new; a.v = v_new; a.kc = k_cached; a.vc = v_cached; a.ks = k_scales;
     a.vs = v_scales; a.o = o;
     a.B = (int)batch; a.S = (int)seq_len; a.Hq = (int)num_q_heads; a.Hkv = (int)num_kv_heads;
+    a.gq = (int)(num_q_heads / num_kv_heads);
     a.d = (int)head_dim; a.Skv = cache_len + new_len; a.cache_len = cache_len; a.new_len = new_len;
     a.pos_off = position_offset; a.causal = is_causal ? 1 : 0; a.scale = scale;
     a.qgs = (int)quant_group_size;
     a.nqg = (int)((head_dim + quant_group_size - 1) / quant_group_size);
-    const size_t items = batch * seq_len * num_q_heads;
-    hipLaunchKernelGGL(attention_ref_kernel<true>, dim3(ceil_div(items, 4)), dim3(256), 0,
-                       as_stream(stream), a);
-    return check_launch("attention_hybrid");
+    return launch_attention<true>(a, stream);
 }
 
 }  // extern "C"

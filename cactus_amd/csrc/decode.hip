@@ -1,0 +1,588 @@
+// decode.hip -- fused kernels of one Qwen3 decode step (batch 1, one token).
+//
+// Each kernel computes a run of consecutive graph nodes of
+// QwenModel::forward (models/model_qwen.cpp:51-172) for one token with
+// exactly the reference's arithmetic, reading the step's token, position
+// and cache length from a small device "step state" so that a whole decode
+// step can be captured once into a HIP graph and replayed:
+//
+//   state[0] token    state[1] position    state[2] cache length    state[3] step
+//
+//   embed       h = embedding[token]                          (graph_ops_tensor.cpp:301-329)
+//   qkv         x = rms_norm(h); q|k|v = matmul(x, Wq|Wk|Wv)  (graph_ops_nn.cpp:129-251)
+//   attn_prep   q/k head RMSNorm, RoPE at `position`, INT8 append of k and v
+//               at `cache length` (kernel_attention.cpp:484-676, kernel_quants.cpp:223-293)
+//   attention   hybrid INT8-cache attention            (attention.hip)
+//   residual    h = h + matmul(x, W)                      (o-proj, MLP down)
+//   mlp_up      x = rms_norm(h); m = silu(x Wg) * (x Wu)  (kernel_nn.cpp:12-44, kernel_blas.cpp:291-316)
+//   lm_head     token = argmax(rms_norm(h) E^T); the last workgroup advances
+//               the step state (engine_model.cpp:221-297)
+#include "gemv_device.h"
+#include "lm_device.h"
+
+namespace cactus_hip {
+
+int attention_hybrid_decode(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                            const float* vs, const uint16_t* k_new, const uint16_t* v_new,
+                            uint16_t* o, int Hq, int Hkv, int d, float scale, const uint32_t* state,
+                            size_t max_cache, const float* v_shadow, size_t shadow_tiles, void* stream);
+
+// ----------------------------------------------------------------- RMSNorm
+// 1/rms of an fp16 row held in LDS, in the reference's order (16 fp32 FMA
+// chains, kernel_attention.cpp:500-538).  Called by one whole wave; every
+// lane returns inv and fp16(inv).
+__device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float eps, float& inv,
+                                               uint16_t& hinv) {
+    const int lane = threadIdx.x & 63;
+    float chain = 0.0f;
+    const int n16 = n / 16, end8 = (n / 8) * 8;
+    if (lane < 16) {
+        for (int i = 0; i < n16; i++) {
+            const float a = h2f(xs[i * 16 + lane]);
+            chain = __builtin_fmaf(a, a, chain);
+        }
+        if (lane < 8 && n16 * 16 + 8 <= n) {
+            const float a = h2f(xs[n16 * 16 + lane]);
+            chain = __builtin_fmaf(a, a, chain);
+        }
+    }
+    const float c4 = __shfl(chain, (lane + 4) & 63, 64);
+    const float c8 = __shfl(chain, (lane + 8) & 63, 64);
+    const float c12 = __shfl(chain, (lane + 12) & 63, 64);
+    const float t = ((chain + c4) + c8) + c12;
+    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    float ss = (t0 + t1) + (t2 + t3);
+    for (int k = end8; k < n; k++) {
+        const float a = h2f(xs[k]);
+        ss = __builtin_fmaf(a, a, ss);
+    }
+    const float rms = __builtin_sqrtf(ss / (float)n + eps);
+    inv = 1.0f / rms;
+    hinv = f2h(inv);
+}
+
+__device__ __forceinline__ uint16_t rms_apply(uint16_t x, uint16_t w, int i, int end8, float inv,
+                                              uint16_t hinv) {
+    return i < end8 ? hmul(hmul(x, hinv), w) : f2h((h2f(x) * inv) * h2f(w));
+}
+
+// ----------------------------------------------------------------- embed
+__global__ void dec_embed_kernel(const uint16_t* __restrict__ table, const uint32_t* __restrict__ st,
+                                 uint16_t* __restrict__ h, int hidden, uint32_t vocab) {
+    const uint32_t tok = st[0];
+    const bool ok = tok < vocab;
+    for (int i = threadIdx.x; i < hidden; i += blockDim.x)
+        h[i] = ok ? table[(size_t)tok * hidden + i] : (uint16_t)0;
+}
+
+// ----------------------------------------------------------------- GEMV
+enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILUMUL = 2 };
+
+struct DecSeg {
+    const uint8_t* B;        // weights [N][K] int8 or [N][K/2] packed int4
+    const uint16_t* Bs;      // [N][K/gs] fp16
+    uint16_t* out;           // [N]
+    int N;
+};
+
+struct DecGemvArgs {
+    const uint16_t* x;       // activation [K]
+    const uint16_t* norm_w;  // RMSNorm weight [K] (PRO_NORM)
+    const uint16_t* res;     // residual [N] (EPI_RESID); may alias seg[0].out
+    float eps;
+    int K, gs, rows;
+    DecSeg seg[3];
+};
+
+// grid.x: row tiles, grid.y: segment (EPI_SILUMUL: one tile covers `rows`
+// gate rows of seg[0] and the same rows of the up projection seg[1])
+template <int PRO, int EPI, bool INT4, int CH>
+__global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = a.K, gs = a.gs, G = K / gs;
+    const int rows = a.rows;
+    const int tid = threadIdx.x;
+    const int si = EPI == EPI_SILUMUL ? 0 : (int)blockIdx.y;
+    const DecSeg sg = si == 0 ? a.seg[0] : (si == 1 ? a.seg[1] : a.seg[2]);
+    const int n0 = blockIdx.x * rows;
+    if (n0 >= sg.N) return;
+    const int nr = min(rows, sg.N - n0);
+    const int vrows = EPI == EPI_SILUMUL ? 2 * rows : rows;   // virtual rows of the tile
+
+    int8_t* actq = reinterpret_cast<int8_t*>(smem);                          // K
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem + ((K + 15) & ~15));     // K
+    uint16_t* ys = xs + ((K + 7) & ~7);                                      // K
+    int32_t* acc = reinterpret_cast<int32_t*>(ys + ((K + 7) & ~7));         // vrows*G
+    uint16_t* scl = reinterpret_cast<uint16_t*>(acc + vrows * G);           // vrows*G
+    float* red = reinterpret_cast<float*>(scl + ((vrows * G + 1) & ~1));    // 8
+
+    const int cpr = INT4 ? K / 32 : K / 16;
+    const int P = INT4 ? gs / 32 : gs / 16;
+    const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
+    auto row_ptr = [&](int vr) -> const uint8_t* {
+        if (EPI == EPI_SILUMUL && vr >= rows) return a.seg[1].B + (size_t)(n0 + vr - rows) * row_bytes;
+        return sg.B + (size_t)(n0 + vr) * row_bytes;
+    };
+    auto vrow_valid = [&](int vr) { return EPI == EPI_SILUMUL ? ((vr < rows ? vr : vr - rows) < nr) : vr < nr; };
+
+    // 1. weights in flight first
+    i32x4 wreg[CH];
+    int crow[CH], ccol[CH];
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + i * GEMV_THREADS;
+        crow[i] = c / cpr;
+        ccol[i] = c - crow[i] * cpr;
+        wreg[i] = (i32x4){0, 0, 0, 0};
+        if (crow[i] < vrows && vrow_valid(crow[i]))
+            wreg[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const i32x4*>(row_ptr(crow[i]) + (size_t)ccol[i] * 16));
+    }
+    // 2. group scales
+    for (int i = tid; i < vrows * G; i += GEMV_THREADS) {
+        const int vr = i / G, g = i % G;
+        uint16_t v = 0;
+        if (vrow_valid(vr)) {
+            if (EPI == EPI_SILUMUL && vr >= rows) v = a.seg[1].Bs[(size_t)(n0 + vr - rows) * G + g];
+            else v = sg.Bs[(size_t)(n0 + vr) * G + g];
+        }
+        scl[i] = v;
+    }
+    // 3. activation: optional RMSNorm, then per-row quantization
+    for (int i = tid; i < K; i += GEMV_THREADS) xs[i] = a.x[i];
+    __syncthreads();
+    const uint16_t* act = xs;
+    if (PRO == PRO_NORM) {
+        if (tid < 64) {
+            float inv;
+            uint16_t hinv;
+            rms_stats_wave(xs, K, a.eps, inv, hinv);
+            if (tid == 0) { red[4] = inv; red[5] = __builtin_bit_cast(float, (uint32_t)hinv); }
+        }
+        __syncthreads();
+        const float inv = red[4];
+        const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, red[5]);
+        const int end8 = (K / 8) * 8;
+        for (int i = tid; i < K; i += GEMV_THREADS) ys[i] = rms_apply(xs[i], a.norm_w[i], i, end8, inv, hinv);
+        __syncthreads();
+        act = ys;
+    }
+    float m = 0.0f;
+    for (int i = tid; i < K; i += GEMV_THREADS) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(act[i])));
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float as = row_scale_from_max(mx);
+    const float inv_s = 1.0f / as;
+    const int body = (K / 8) * 8;
+    for (int i = tid; i < K; i += GEMV_THREADS)
+        actq[act_pos<INT4>(i)] = quant_code(h2f(act[i]), inv_s, i >= body);
+    __syncthreads();
+
+    // 4. dot products and exact group sums
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const bool valid = crow[i] < vrows && vrow_valid(crow[i]);
+        int dot = valid ? chunk_dot<INT4>(actq, ccol[i], wreg[i]) : 0;
+        dot = group_lane_sum(dot, P);
+        if (valid && ((tid + i * GEMV_THREADS) & (P - 1)) == 0)
+            acc[crow[i] * G + (ccol[i] * (INT4 ? 32 : 16)) / gs] = dot;
+    }
+    __syncthreads();
+
+    // 5. reference epilogue
+    auto chain = [&](int vr) {
+        float rs = 0.0f;
+        for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)acc[vr * G + g], h2f(scl[vr * G + g]), rs);
+        return f2h(rs * as);
+    };
+    for (int r = tid; r < nr; r += GEMV_THREADS) {
+        const uint16_t val = chain(r);
+        if (EPI == EPI_STORE) {
+            sg.out[n0 + r] = val;
+        } else if (EPI == EPI_RESID) {
+            sg.out[n0 + r] = hadd(a.res[n0 + r], val);
+        } else {
+            const uint16_t up = chain(rows + r);
+            const float gx = h2f(val);
+            // silu's vector body uses fast_exp, its n % 8 tail expf (kernel_nn.cpp:12-44)
+            const float e = n0 + r < (sg.N / 8) * 8 ? fast_exp(-gx) : cactus_expf(-gx);
+            const float sig = 1.0f / (1.0f + e);
+            sg.out[n0 + r] = hmul(f2h(gx * sig), up);
+        }
+    }
+}
+
+static size_t dec_gemv_smem(int K, int vrows, int G) {
+    size_t s = (size_t)((K + 15) & ~15) + 2 * (size_t)((K + 7) & ~7) * 2;
+    s += (size_t)vrows * G * 4 + (size_t)((vrows * G + 1) & ~1) * 2 + 8 * 4;
+    return (s + 15) & ~(size_t)15;
+}
+
+template <int PRO, int EPI, bool INT4>
+static int launch_dec_gemv(DecGemvArgs a, int nseg, hipStream_t st) {
+    const int G = a.K / a.gs;
+    const int cpr = INT4 ? a.K / 32 : a.K / 16;
+    const int vmul = EPI == EPI_SILUMUL ? 2 : 1;
+    int maxN = 0, totalN = 0;
+    for (int s = 0; s < nseg; s++) { maxN = max(maxN, a.seg[s].N); totalN += a.seg[s].N; }
+    // at most 2 chunks per thread; as few rows as keep >= 512 workgroups
+    int rows = (2 * GEMV_THREADS) / (cpr * vmul);
+    if (rows < 1) rows = 1;
+    while (rows > 1 && (size_t)ceil_div(totalN, rows) < 512) rows = (rows + 1) / 2;
+    CH_REQUIRE(rows * cpr * vmul <= 2 * GEMV_THREADS, "decode matmul: K too large");
+    a.rows = rows;
+    const int ch = (rows * cpr * vmul + GEMV_THREADS - 1) / GEMV_THREADS;
+    const size_t smem = dec_gemv_smem(a.K, rows * vmul, G);
+    CH_REQUIRE(smem <= 60 * 1024, "decode matmul: K too large for LDS");
+    dim3 grid(ceil_div(maxN, rows), EPI == EPI_SILUMUL ? 1 : nseg);
+    if (ch <= 1)
+        hipLaunchKernelGGL((dec_gemv_kernel<PRO, EPI, INT4, 1>), grid, dim3(GEMV_THREADS), smem, st, a);
+    else
+        hipLaunchKernelGGL((dec_gemv_kernel<PRO, EPI, INT4, 2>), grid, dim3(GEMV_THREADS), smem, st, a);
+    return check_launch("decode matmul");
+}
+
+// ----------------------------------------------------------------- attn prep
+// grid: Hq + Hkv workgroups of one wave.  Workgroup h < Hq: q head h
+// (RMSNorm, RoPE).  Workgroup Hq + g: k head g (RMSNorm, RoPE, INT8 append)
+// and v head g (INT8 append), at the cache length of the step state.
+struct PrepArgs {
+    const uint16_t* q_raw; const uint16_t* k_raw; const uint16_t* v_raw;
+    const uint16_t* q_norm; const uint16_t* k_norm;
+    uint16_t* q_out; uint16_t* k_out;
+    int8_t* kc; int8_t* vc; float* ks; float* vs;
+    const uint16_t* cos_t; const uint16_t* sin_t;
+    const uint32_t* st;
+    float eps;
+    int Hq, Hkv, d;
+    uint32_t max_cache;
+    uint32_t table_pos;      // positions held by the RoPE tables
+    float* vsh;              // value product tiles or null
+    size_t sh_ntile;
+};
+
+// quantize_group_fp16_to_int8 per 128-dim group (kernel_quants.cpp:223-264);
+// with `sh`, also the row's fp32 products (float)code * scale into the
+// product tiles (kv_shadow.hip layout, key `key`, kv head `h`)
+__device__ __forceinline__ void kv_append_row(const uint16_t* src, int8_t* dst, float* scales, int d,
+                                              float* sh = nullptr, size_t ntile = 0, size_t key = 0, int h = 0) {
+    const int lane = threadIdx.x & 63;
+    const int nsl = (d + 63) / 64, da = (d / 8) * 8;
+    for (int g0 = 0, g = 0; g0 < d; g0 += 128, g++) {
+        const int cnt = min(128, d - g0);
+        float m = 0.0f;
+        for (int i = lane; i < cnt; i += 64) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(src[g0 + i])));
+        m = wave_max(m);
+        const float s = row_scale_from_max(m);
+        const float inv = 1.0f / s;
+        const int body = (cnt / 8) * 8;
+        for (int i = lane; i < cnt; i += 64) {
+            const float v = h2f(src[g0 + i]) * inv;
+            const int32_t c = i < body ? cvt_rne_sat(v) : (int32_t)__builtin_roundf(v);
+            const int8_t code = (int8_t)sat8(c);
+            dst[g0 + i] = code;
+            if (sh) {
+                const int dim = g0 + i;
+                const float p = dim < da ? (float)code * s : 0.0f;
+                sh[(((size_t)h * nsl + dim / 64) * ntile + key / 64) * (64 * 68) + (dim % 64) * 68 + key % 64] = p;
+            }
+        }
+        if (lane == 0) scales[g] = s;
+    }
+}
+
+__global__ void __launch_bounds__(64) dec_attn_prep_kernel(PrepArgs a) {
+    __shared__ uint16_t xs[256];
+    __shared__ uint16_t ys[256];
+    const int lane = threadIdx.x;
+    const int d = a.d, half = d / 2, end8 = (d / 8) * 8;
+    const uint32_t pos = a.st[1];
+    const uint32_t clen = a.st[2];
+    if (pos >= a.table_pos) return;   // the host keeps positions inside the table
+    const bool is_q = (int)blockIdx.x < a.Hq;
+    const int h = is_q ? blockIdx.x : blockIdx.x - a.Hq;
+    const uint16_t* src = is_q ? a.q_raw + (size_t)h * d : a.k_raw + (size_t)h * d;
+    const uint16_t* nw = is_q ? a.q_norm : a.k_norm;
+    uint16_t* out = is_q ? a.q_out + (size_t)h * d : a.k_out + (size_t)h * d;
+    for (int i = lane; i < d; i += 64) xs[i] = src[i];
+    __syncthreads();
+    float inv;
+    uint16_t hinv;
+    rms_stats_wave(xs, d, a.eps, inv, hinv);
+    for (int i = lane; i < d; i += 64) ys[i] = rms_apply(xs[i], nw[i], i, end8, inv, hinv);
+    __syncthreads();
+    // RoPE (kernel_attention.cpp:640-671) at absolute position `pos`
+    const uint16_t* ct = a.cos_t + (size_t)pos * half;
+    const uint16_t* stb = a.sin_t + (size_t)pos * half;
+    const int vh = (half / 8) * 8;
+    for (int i = lane; i < half; i += 64) {
+        const uint16_t x1 = ys[i], x2 = ys[i + half], c = ct[i], s = stb[i];
+        uint16_t o1, o2;
+        if (i < vh) {
+            o1 = hfma(x2 ^ 0x8000u, s, hmul(x1, c));
+            o2 = hfma(x1, s, hmul(x2, c));
+        } else {
+            const float fa = h2f(x1), fb = h2f(x2), cf = h2f(c), sf = h2f(s);
+            o1 = f2h(fa * cf - fb * sf);
+            o2 = f2h(fb * cf + fa * sf);
+        }
+        out[i] = o1;
+        out[i + half] = o2;
+        xs[i] = o1;          // keep the roped row for the cache append
+        xs[i + half] = o2;
+    }
+    __syncthreads();
+    if (!is_q && clen < a.max_cache) {
+        const int ng = (d + 127) / 128;
+        const size_t row = (size_t)clen * a.Hkv + h;
+        kv_append_row(xs, a.kc + row * d, a.ks + row * ng, d);
+        kv_append_row(a.v_raw + (size_t)h * d, a.vc + row * d, a.vs + row * ng, d, a.vsh, a.sh_ntile, clen, h);
+    }
+}
+
+// ----------------------------------------------------------------- LM head
+// RMSNorm of h in every workgroup's prologue, then the FP16-accumulation
+// GEMV of kernel_gemm.cpp:17-126 against the tied embedding and the greedy
+// argmax (first index wins); the last workgroup also advances the state.
+struct LmDecArgs {
+    const uint16_t* h; const uint16_t* norm_w; const uint16_t* b;
+    float eps;
+    int K, N;
+    float* part_val; uint32_t* part_idx; uint32_t* counter;
+    uint32_t* st;            // token, pos, cache_len, step
+    uint32_t* tokens_out;    // [max_steps] or null
+    uint32_t max_steps;
+};
+
+__global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = p.K;
+    const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                // K
+    uint16_t* as = xs + K;                                          // K (normed)
+    unsigned char* stage = smem + 4 * (size_t)K + wid * LM_ROWS_PER_WAVE * LM_ROW_STRIDE;
+    __shared__ float stats[2];
+    for (int i = threadIdx.x; i < K; i += LM_THREADS) xs[i] = p.h[i];
+    __syncthreads();
+    if (wid == 0) {
+        float inv;
+        uint16_t hinv;
+        rms_stats_wave(xs, K, p.eps, inv, hinv);
+        if (lane == 0) { stats[0] = inv; stats[1] = __builtin_bit_cast(float, (uint32_t)hinv); }
+    }
+    __syncthreads();
+    {
+        const float inv = stats[0];
+        const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, stats[1]);
+        const int end8 = (K / 8) * 8;
+        for (int i = threadIdx.x; i < K; i += LM_THREADS) as[i] = rms_apply(xs[i], p.norm_w[i], i, end8, inv, hinv);
+    }
+    __syncthreads();
+
+    const int row0 = (blockIdx.x * (LM_THREADS / 64) + wid) * LM_ROWS_PER_WAVE;
+    const int my_row = row0 + lane;
+    h2v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = (h2v){(f16)0.0f, (f16)0.0f};
+    for (int k0 = 0; k0 < K; k0 += LM_KC) {
+        const int kc = min(LM_KC, K - k0);
+        const int cpr = kc / 8;
+        for (int i = lane; i < LM_ROWS_PER_WAVE * cpr; i += 64) {
+            const int r = i / cpr, ch = i % cpr;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (row0 + r < p.N)
+                v = *reinterpret_cast<const uint4*>(p.b + (size_t)(row0 + r) * K + k0 + ch * 8);
+            *reinterpret_cast<uint4*>(stage + r * LM_ROW_STRIDE + ch * 16) = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int ch = 0; ch < cpr; ch++) {
+            const uint4 bv = *reinterpret_cast<const uint4*>(stage + lane * LM_ROW_STRIDE + ch * 16);
+            const uint4 av = *reinterpret_cast<const uint4*>(as + k0 + ch * 8);
+            f16_step(acc, av, bv);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    float best = -__builtin_inff();
+    uint32_t best_i = 0xFFFFFFFFu;
+    if (my_row < p.N) {
+        best = h2f(f16_hsum(acc));
+        best_i = (uint32_t)my_row;
+    }
+    __shared__ float bv_s[LM_THREADS];
+    __shared__ uint32_t bi_s[LM_THREADS];
+    __shared__ bool last;
+    auto reduce = [&]() {
+        for (int w = LM_THREADS / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w) {
+                const float ov = bv_s[threadIdx.x + w];
+                const uint32_t oi = bi_s[threadIdx.x + w];
+                const float mv = bv_s[threadIdx.x];
+                const uint32_t mi = bi_s[threadIdx.x];
+                const bool take = oi != 0xFFFFFFFFu && (mi == 0xFFFFFFFFu || ov > mv || (ov == mv && oi < mi));
+                if (take) { bv_s[threadIdx.x] = ov; bi_s[threadIdx.x] = oi; }
+            }
+            __syncthreads();
+        }
+    };
+    bv_s[threadIdx.x] = best;
+    bi_s[threadIdx.x] = best_i;
+    __syncthreads();
+    reduce();
+    if (threadIdx.x == 0) {
+        p.part_val[blockIdx.x] = bv_s[0];
+        p.part_idx[blockIdx.x] = bi_s[0];
+        __threadfence();
+        last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu;
+    for (unsigned i = threadIdx.x; i < gridDim.x; i += LM_THREADS) {
+        const float v = p.part_val[i];
+        const uint32_t ix = p.part_idx[i];
+        if (ix != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && ix < bi))) { bv = v; bi = ix; }
+    }
+    bv_s[threadIdx.x] = bv;
+    bi_s[threadIdx.x] = bi;
+    __syncthreads();
+    reduce();
+    if (threadIdx.x == 0) {
+        const uint32_t tok = bi_s[0] == 0xFFFFFFFFu ? 0u : bi_s[0];
+        const uint32_t step = p.st[3];
+        if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
+        p.st[0] = tok;
+        p.st[1] = p.st[1] + 1;
+        p.st[2] = p.st[2] + 1;
+        p.st[3] = step + 1;
+        *p.counter = 0u;
+    }
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+extern "C" {
+
+int cactus_hip_decode_embed(const uint16_t* table, const uint32_t* state, uint16_t* h, size_t hidden,
+                            size_t vocab, void* stream) {
+    CH_REQUIRE(table && state && h && hidden > 0 && vocab > 0, "decode_embed: bad argument");
+    hipLaunchKernelGGL(dec_embed_kernel, dim3(1), dim3(256), 0, as_stream(stream), table, state, h,
+                       (int)hidden, (uint32_t)vocab);
+    return check_launch("decode_embed");
+}
+
+int cactus_hip_decode_qkv(const uint16_t* h, const uint16_t* norm_w, float eps, size_t K,
+                          size_t group_size, const int8_t* wq, const uint16_t* sq, uint16_t* q,
+                          size_t nq, const int8_t* wk, const uint16_t* sk, uint16_t* k, size_t nk,
+                          const int8_t* wv, const uint16_t* sv, uint16_t* v, size_t nv, void* stream) {
+    CH_REQUIRE(h && norm_w && wq && sq && q && wk && sk && k && wv && sv && v, "decode_qkv: null pointer");
+    CH_REQUIRE(group_size >= 16 && K % group_size == 0 && (group_size & (group_size - 1)) == 0 &&
+               group_size <= 1024 && K <= 8192, "decode_qkv: bad K / group_size");
+    DecGemvArgs a{};
+    a.x = h; a.norm_w = norm_w; a.eps = eps; a.K = (int)K; a.gs = (int)group_size;
+    a.seg[0] = {reinterpret_cast<const uint8_t*>(wq), sq, q, (int)nq};
+    a.seg[1] = {reinterpret_cast<const uint8_t*>(wk), sk, k, (int)nk};
+    a.seg[2] = {reinterpret_cast<const uint8_t*>(wv), sv, v, (int)nv};
+    return launch_dec_gemv<PRO_NORM, EPI_STORE, false>(a, 3, as_stream(stream));
+}
+
+int cactus_hip_decode_matmul_residual(const uint16_t* x, size_t K, size_t group_size, const void* w,
+                                      const uint16_t* s, size_t N, int int4, uint16_t* h,
+                                      void* stream) {
+    CH_REQUIRE(x && w && s && h, "decode_matmul_residual: null pointer");
+    CH_REQUIRE(group_size >= (int4 ? 32u : 16u) && K % group_size == 0 &&
+               (group_size & (group_size - 1)) == 0 && group_size <= 1024 && K <= 8192,
+               "decode_matmul_residual: bad K / group_size");
+    DecGemvArgs a{};
+    a.x = x; a.res = h; a.K = (int)K; a.gs = (int)group_size;
+    a.seg[0] = {static_cast<const uint8_t*>(w), s, h, (int)N};
+    if (int4) return launch_dec_gemv<PRO_PLAIN, EPI_RESID, true>(a, 1, as_stream(stream));
+    return launch_dec_gemv<PRO_PLAIN, EPI_RESID, false>(a, 1, as_stream(stream));
+}
+
+int cactus_hip_decode_mlp_up(const uint16_t* h, const uint16_t* norm_w, float eps, size_t K,
+                             size_t group_size, const uint8_t* wg, const uint16_t* sg,
+                             const uint8_t* wu, const uint16_t* su, size_t N, uint16_t* m,
+                             void* stream) {
+    CH_REQUIRE(h && norm_w && wg && sg && wu && su && m, "decode_mlp_up: null pointer");
+    CH_REQUIRE(group_size >= 32 && K % group_size == 0 && (group_size & (group_size - 1)) == 0 &&
+               group_size <= 1024 && K <= 8192, "decode_mlp_up: bad K / group_size");
+    DecGemvArgs a{};
+    a.x = h; a.norm_w = norm_w; a.eps = eps; a.K = (int)K; a.gs = (int)group_size;
+    a.seg[0] = {wg, sg, m, (int)N};
+    a.seg[1] = {wu, su, nullptr, (int)N};
+    return launch_dec_gemv<PRO_NORM, EPI_SILUMUL, true>(a, 2, as_stream(stream));
+}
+
+int cactus_hip_decode_attn_prep(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float theta,
+                                const uint32_t* state, uint16_t* q_out, uint16_t* k_out,
+                                int8_t* k_cache, int8_t* v_cache, float* k_scales, float* v_scales,
+                                size_t max_cache, float* v_shadow, void* stream) {
+    CH_REQUIRE(q_raw && k_raw && v_raw && q_norm && k_norm && state && q_out && k_out && k_cache &&
+               v_cache && k_scales && v_scales, "decode_attn_prep: null pointer");
+    CH_REQUIRE(head_dim >= 8 && head_dim <= 256 && head_dim % 2 == 0, "decode_attn_prep: head_dim");
+    const RopeTable* t = nullptr;
+    int rc = rope_table(max_cache + 1, head_dim, theta, &t);
+    if (rc) return rc;
+    PrepArgs a{};
+    a.q_raw = q_raw; a.k_raw = k_raw; a.v_raw = v_raw; a.q_norm = q_norm; a.k_norm = k_norm;
+    a.q_out = q_out; a.k_out = k_out; a.kc = k_cache; a.vc = v_cache; a.ks = k_scales; a.vs = v_scales;
+    a.cos_t = t->cos_d; a.sin_t = t->sin_d; a.st = state; a.eps = eps;
+    a.Hq = (int)num_q_heads; a.Hkv = (int)num_kv_heads; a.d = (int)head_dim;
+    a.max_cache = (uint32_t)max_cache;
+    a.table_pos = (uint32_t)t->npos;
+    a.vsh = v_shadow;
+    a.sh_ntile = (max_cache + 63) / 64;
+    hipLaunchKernelGGL(dec_attn_prep_kernel, dim3((unsigned)(num_q_heads + num_kv_heads)), dim3(64), 0,
+                       as_stream(stream), a);
+    return check_launch("decode_attn_prep");
+}
+
+int cactus_hip_decode_attention(const uint16_t* q, const int8_t* k_cache, const int8_t* v_cache,
+                                const float* k_scales, const float* v_scales, const uint16_t* k_new,
+                                const uint16_t* v_new, uint16_t* o, size_t num_q_heads,
+                                size_t num_kv_heads, size_t head_dim, float scale,
+                                const uint32_t* state, size_t max_cache, const float* v_shadow,
+                                void* stream) {
+    CH_REQUIRE(q && k_cache && v_cache && k_scales && v_scales && k_new && v_new && o && state,
+               "decode_attention: null pointer");
+    CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && num_q_heads / num_kv_heads <= 8,
+               "decode_attention: bad head counts");
+    CH_REQUIRE(head_dim % 8 == 0 && head_dim <= 256, "decode_attention: head_dim");
+    return attention_hybrid_decode(q, k_cache, v_cache, k_scales, v_scales, k_new, v_new, o,
+                                   (int)num_q_heads, (int)num_kv_heads, (int)head_dim, scale, state,
+                                   max_cache, v_shadow, (max_cache + 63) / 64, stream);
+}
+
+int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
+                              const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
+                              uint32_t* tokens_out, size_t max_steps, void* scratch,
+                              size_t scratch_bytes, void* stream) {
+    CH_REQUIRE(h && norm_w && embedding && state && scratch, "decode_lm_head: null pointer");
+    CH_REQUIRE(K % 8 == 0 && K <= 4096 && ((uintptr_t)embedding & 15) == 0, "decode_lm_head: bad K");
+    const unsigned blocks = ceil_div(N, (LM_THREADS / 64) * LM_ROWS_PER_WAVE);
+    CH_REQUIRE(scratch_bytes >= (size_t)blocks * 8 + 256, "decode_lm_head: scratch too small");
+    LmDecArgs p{};
+    p.h = h; p.norm_w = norm_w; p.b = embedding; p.eps = eps; p.K = (int)K; p.N = (int)N;
+    p.counter = static_cast<uint32_t*>(scratch);
+    p.part_val = reinterpret_cast<float*>(static_cast<char*>(scratch) + 256);
+    p.part_idx = reinterpret_cast<uint32_t*>(p.part_val + blocks);
+    p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps;
+    const size_t smem = 4 * K + (size_t)(LM_THREADS / 64) * LM_ROWS_PER_WAVE * LM_ROW_STRIDE;
+    hipLaunchKernelGGL(dec_lm_head_kernel, dim3(blocks), dim3(LM_THREADS), smem, as_stream(stream), p);
+    return check_launch("decode_lm_head");
+}
+
+}  // extern "C"

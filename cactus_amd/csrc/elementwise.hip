@@ -69,18 +69,14 @@ __global__ void __launch_bounds__(256) rms_norm_kernel(const uint16_t* __restric
 }
 
 // ---------------------------------------------------------------- RoPE
-struct RopeTable {
-    uint16_t* cos_d = nullptr;
-    uint16_t* sin_d = nullptr;
-    size_t npos = 0;
-};
+// RopeTable is declared in hip_common.h
 static std::mutex g_rope_mu;
 static std::map<std::tuple<int, size_t, uint32_t>, RopeTable> g_rope;
 
 // Table of precompute_rope_tables_f16 (kernel_attention.cpp:588-612), built
 // on the host with the host libm and uploaded.  Tables only grow; a replaced
 // table stays allocated because queued kernels may still read it.
-static int rope_table(size_t npos, size_t d, float theta, const RopeTable** out) {
+int rope_table(size_t npos, size_t d, float theta, const RopeTable** out) {
     int dev = 0;
     CH_HIP(hipGetDevice(&dev));
     uint32_t tb;

@@ -232,10 +232,7 @@ int cactus_qwen_generate(void* model, const uint32_t* prompt, size_t n, size_t m
         uint32_t tok = max_new ? m->decode(prompt[n - 1]) : 0;
         if (max_new) out[0] = tok;
         auto t2 = clk::now();
-        for (size_t i = 1; i < max_new; i++) {
-            tok = m->decode(tok);
-            out[i] = tok;
-        }
+        if (max_new > 1) m->decode_many(tok, max_new - 1, out + 1);
         check_hip(cactus_hip_stream_sync(m->stream()), "sync");
         auto t3 = clk::now();
         if (timing) {
@@ -251,7 +248,8 @@ int cactus_qwen_generate(void* model, const uint32_t* prompt, size_t n, size_t m
 int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t* rows) {
     return guarded([&] {
         QwenModel* m = static_cast<QwenModel*>(model);
-        if (m->last_hidden_node() == SIZE_MAX) throw std::runtime_error("no forward has run");
+        if (m->last_hidden_node() == SIZE_MAX)
+            throw std::runtime_error("no graph forward has run since the last reset or fused decode step");
         const BufferDesc& b = m->graph().get_output_buffer(m->last_hidden_node());
         const size_t r = b.shape[0];
         if (rows) *rows = r;

@@ -1,13 +1,137 @@
-// decode_fused.cpp -- decode-step path selection of QwenModel.
+// decode_fused.cpp -- fused decode path of QwenModel (decode mode 1).
+//
+// Per layer: qkv (RMSNorm + INT8 GEMV x3), attn_prep (q/k RMSNorm, RoPE,
+// INT8 KV append), attention (scores + value chains), o-proj + residual,
+// mlp_up (RMSNorm + INT4 gate/up + SiLU*mul), down + residual.  Then the LM
+// head with the fused argmax advances the device step state.  Bit-identical
+// to decode mode 0 (the node-by-node graph).
+#include <cstring>
+#include <stdexcept>
+
+#include "cactus_hip.h"
 #include "fused.h"
 
 namespace cactus {
 
-FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {}
-FusedDecoder::~FusedDecoder() = default;
+FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
+    const cactus_qwen_config& c = m.config();
+    const size_t H = c.hidden, F = c.ffn, hd = c.head_dim;
+    const size_t nq = (size_t)c.heads * hd, nkv = (size_t)c.kv_heads * hd;
+    state_ = DevBuf(16);
+    h_ = DevBuf(H * 2);
+    q_raw_ = DevBuf(nq * 2);
+    k_raw_ = DevBuf(nkv * 2);
+    v_raw_ = DevBuf(nkv * 2);
+    q_rot_ = DevBuf(nq * 2);
+    k_rot_ = DevBuf(nkv * 2);
+    attn_ = DevBuf(nq * 2);
+    mlp_ = DevBuf(F * 2);
+    max_steps_ = c.max_seq + 1;
+    tokens_ = DevBuf(max_steps_ * 4);
+    const size_t blocks = (c.vocab + 255) / 256;
+    lm_scratch_ = DevBuf(256 + 8 * blocks);
+    check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
+    check_hip(cactus_hip_rope_reserve(c.max_seq + 1, hd, c.rope_theta), "rope_reserve");
+    check_hip(cactus_hip_stream_sync(m.stream()), "sync");
+}
+
+FusedDecoder::~FusedDecoder() {
+    if (graph_) cactus_hip_graph_destroy(graph_);
+}
+
+void FusedDecoder::enqueue() {
+    const cactus_qwen_config& c = m_.config();
+    void* st = m_.stream();
+    const size_t H = c.hidden, F = c.ffn, hd = c.head_dim, gs = c.group_size;
+    const size_t nq = (size_t)c.heads * hd, nkv = (size_t)c.kv_heads * hd;
+    uint32_t* state = state_.as<uint32_t>();
+    uint16_t* h = h_.as<uint16_t>();
+    KVCache& kv = m_.cache();
+    auto u16 = [](const DevBuf& b) { return b.as<uint16_t>(); };
+    check_hip(cactus_hip_decode_embed(u16(m_.embedding()), state, h, H, c.vocab, st), "decode_embed");
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        const QwenLayer& L = m_.layer(l);
+        check_hip(cactus_hip_decode_qkv(h, u16(L.input_norm), c.eps, H, gs, L.q_w.as<int8_t>(), u16(L.q_s),
+                                        q_raw_.as<uint16_t>(), nq, L.k_w.as<int8_t>(), u16(L.k_s),
+                                        k_raw_.as<uint16_t>(), nkv, L.v_w.as<int8_t>(), u16(L.v_s),
+                                        v_raw_.as<uint16_t>(), nkv, st),
+                  "decode_qkv");
+        check_hip(cactus_hip_decode_attn_prep(q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(),
+                                              u16(L.q_norm), u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd,
+                                              c.rope_theta, state, q_rot_.as<uint16_t>(), k_rot_.as<uint16_t>(),
+                                              kv.keys_mut(l), kv.values_mut(l), kv.key_scales_mut(l),
+                                              kv.value_scales_mut(l), kv.max_seq_len, kv.value_products(l), st),
+                  "decode_attn_prep");
+        check_hip(cactus_hip_decode_attention(q_rot_.as<uint16_t>(), kv.keys(l), kv.values(l), kv.key_scales(l),
+                                              kv.value_scales(l), k_rot_.as<uint16_t>(), v_raw_.as<uint16_t>(),
+                                              attn_.as<uint16_t>(), c.heads, c.kv_heads, hd, m_.attention_scale(),
+                                              state, kv.max_seq_len, kv.value_products(l), st),
+                  "decode_attention");
+        check_hip(cactus_hip_decode_matmul_residual(attn_.as<uint16_t>(), nq, gs, L.o_w.ptr, u16(L.o_s), H, 0, h,
+                                                    st),
+                  "decode_o_proj");
+        check_hip(cactus_hip_decode_mlp_up(h, u16(L.post_norm), c.eps, H, gs, L.gate_w.as<uint8_t>(),
+                                           u16(L.gate_s), L.up_w.as<uint8_t>(), u16(L.up_s), F,
+                                           mlp_.as<uint16_t>(), st),
+                  "decode_mlp_up");
+        check_hip(cactus_hip_decode_matmul_residual(mlp_.as<uint16_t>(), F, gs, L.down_w.ptr, u16(L.down_s), H, 1,
+                                                    h, st),
+                  "decode_down");
+    }
+    check_hip(cactus_hip_decode_lm_head(h, u16(m_.output_norm()), c.eps, u16(m_.embedding()), H, c.vocab, state,
+                                        tokens_.as<uint32_t>(), max_steps_, lm_scratch_.ptr, lm_scratch_.bytes, st),
+              "decode_lm_head");
+}
+
+void FusedDecoder::set_state(uint32_t token) {
+    const KVCache& kv = m_.cache();
+    const uint32_t s[4] = {token, (uint32_t)kv.total_seq_len, (uint32_t)kv.current_seq_len, 0u};
+    check_hip(cactus_hip_memcpy_h2d(state_.ptr, s, sizeof(s), m_.stream()), "state upload");
+}
+
+void FusedDecoder::ensure_graph() {
+    if (graph_) return;
+    void* st = m_.stream();
+    check_hip(cactus_hip_graph_capture_begin(st), "capture begin");
+    try {
+        enqueue();
+    } catch (...) {
+        void* g = nullptr;
+        cactus_hip_graph_capture_end(st, &g);
+        if (g) cactus_hip_graph_destroy(g);
+        throw;
+    }
+    check_hip(cactus_hip_graph_capture_end(st, &graph_), "capture end");
+}
+
+void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
+    if (n == 0) return;
+    KVCache& kv = m_.cache();
+    if (kv.current_seq_len + n > kv.max_seq_len)
+        throw std::runtime_error("KV cache capacity exceeded (sliding window not built)");
+    set_state(token);
+    // the fused step keeps neither the final hidden state nor the logits
+    m_.last_hidden_ = SIZE_MAX;
+    m_.last_logits_ = SIZE_MAX;
+    size_t done = 0;
+    if (!warmed_) {
+        // the first step runs eagerly: it allocates the library's scratch
+        // buffers outside of any capture; later steps replay the graph
+        enqueue();
+        warmed_ = true;
+        done = 1;
+    }
+    if (done < n) ensure_graph();
+    for (; done < n; done++) check_hip(cactus_hip_graph_launch(graph_, m_.stream()), "graph launch");
+    check_hip(cactus_hip_memcpy_d2h(out, tokens_.ptr, n * 4, m_.stream()), "tokens");
+    kv.current_seq_len += n;
+    kv.total_seq_len += n;
+}
+
 uint32_t FusedDecoder::step(uint32_t token) {
-    (void)token;
-    throw std::runtime_error("fused decode path is not built");
+    uint32_t t = 0;
+    run(token, 1, &t);
+    return t;
 }
 
 uint32_t fused_decode(QwenModel& m, FusedDecoder& f, uint32_t token) {
@@ -16,8 +140,21 @@ uint32_t fused_decode(QwenModel& m, FusedDecoder& f, uint32_t token) {
 }
 
 void QwenModel::set_decode_mode(int mode) {
-    if (mode != 0) throw std::runtime_error("decode mode " + std::to_string(mode) + " is not built");
+    if (mode != 0 && mode != 1) throw std::runtime_error("decode mode must be 0 or 1");
+    check_hip(cactus_hip_stream_sync(stream_), "sync");
+    if (mode == 1 && !fused_) fused_ = std::make_unique<FusedDecoder>(*this);
     decode_mode_ = mode;
+}
+
+void QwenModel::decode_many(uint32_t token, size_t n, uint32_t* out) {
+    if (decode_mode_ == 1 && fused_) {
+        fused_->run(token, n, out);
+        return;
+    }
+    for (size_t i = 0; i < n; i++) {
+        token = decode(token);
+        out[i] = token;
+    }
 }
 
 }  // namespace cactus

@@ -47,13 +47,15 @@ public:
     int8_t* values_mut(size_t l) { return v_[l].as<int8_t>(); }
     float* key_scales_mut(size_t l) { return ks_[l].as<float>(); }
     float* value_scales_mut(size_t l) { return vs_[l].as<float>(); }
+    // fp32 product tiles of the values (cactus_hip_kv_shadow_update)
+    float* value_products(size_t l) { return vsh_[l].as<float>(); }
     size_t groups() const { return (head_dim + GROUP - 1) / GROUP; }
 
     size_t current_seq_len = 0, total_seq_len = 0;
     size_t max_seq_len = 0, num_layers = 0, num_kv_heads = 0, head_dim = 0;
 
 private:
-    std::vector<DevBuf> k_, v_, ks_, vs_;
+    std::vector<DevBuf> k_, v_, ks_, vs_, vsh_;
 };
 
 struct QwenLayer {
@@ -74,6 +76,8 @@ public:
     void reset();
     void prefill(const std::vector<uint32_t>& tokens);
     uint32_t decode(uint32_t token);
+    // n greedy steps from `token` (decode mode 1 keeps them on the device)
+    void decode_many(uint32_t token, size_t n, uint32_t* out);
     void set_decode_mode(int mode);
     int decode_mode() const { return decode_mode_; }
 

@@ -43,12 +43,15 @@ void KVCache::init(size_t layers, size_t max_seq, size_t kv_heads, size_t hd) {
     head_dim = hd;
     const size_t codes = max_seq * kv_heads * hd;
     const size_t scales = max_seq * kv_heads * groups() * sizeof(float);
-    k_.clear(); v_.clear(); ks_.clear(); vs_.clear();
+    size_t shadow = 0;
+    check_hip(cactus_hip_kv_shadow_bytes(max_seq, kv_heads, hd, &shadow), "kv shadow size");
+    k_.clear(); v_.clear(); ks_.clear(); vs_.clear(); vsh_.clear();
     for (size_t l = 0; l < layers; l++) {
         k_.emplace_back(codes);
         v_.emplace_back(codes);
         ks_.emplace_back(scales);
         vs_.emplace_back(scales);
+        vsh_.emplace_back(shadow);
     }
     reset();
 }
@@ -66,6 +69,9 @@ void KVCache::append(size_t l, const void* kf, const void* vf, size_t seq, void*
                                                   value_scales_mut(l) + soff, seq, num_kv_heads, head_dim,
                                                   GROUP, stream),
               "kv append (values)");
+    check_hip(cactus_hip_kv_shadow_update(values(l), value_scales(l), value_products(l), current_seq_len, seq,
+                                          num_kv_heads, head_dim, GROUP, max_seq_len, stream),
+              "kv append (value products)");
 }
 
 // ------------------------------------------------------------------ QwenModel

@@ -35,6 +35,15 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Device RoPE tables (fp16 cos/sin [npos][head_dim/2]) built on the host,
+// cached per (device, head_dim, theta); grows to at least npos positions.
+struct RopeTable {
+    uint16_t* cos_d = nullptr;
+    uint16_t* sin_d = nullptr;
+    size_t npos = 0;
+};
+int rope_table(size_t npos, size_t head_dim, float theta, const RopeTable** out);
+
 // fp32 -> fp16 bit pattern on the host: round to nearest even with one
 // rounding step (subnormals, overflow to inf, quiet NaN).  Used for tables
 // built on the host.

@@ -152,4 +152,32 @@ int cactus_hip_event_elapsed_ms(void* start, void* end, float* ms) {
     return CACTUS_HIP_OK;
 }
 
+int cactus_hip_graph_capture_begin(void* stream) {
+    CH_REQUIRE(stream, "graph capture needs a non-default stream");
+    CH_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal));
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_graph_capture_end(void* stream, void** graph_exec) {
+    CH_REQUIRE(graph_exec, "graph_capture_end: null out pointer");
+    hipGraph_t g = nullptr;
+    CH_HIP(hipStreamEndCapture(as_stream(stream), &g));
+    hipGraphExec_t ge = nullptr;
+    hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return fail(CACTUS_HIP_ERUNTIME, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    *graph_exec = ge;
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_graph_launch(void* graph_exec, void* stream) {
+    CH_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), as_stream(stream)));
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_graph_destroy(void* graph_exec) {
+    if (graph_exec) CH_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    return CACTUS_HIP_OK;
+}
+
 }  // extern "C"

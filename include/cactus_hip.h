@@ -54,6 +54,12 @@ int         cactus_hip_event_create(void** event);
 int         cactus_hip_event_destroy(void* event);
 int         cactus_hip_event_record(void* event, void* stream);
 int         cactus_hip_event_elapsed_ms(void* start, void* end, float* ms);
+/* Stream capture into a HIP graph (the fused decode step is captured once
+ * and replayed per token).  No reference counterpart. */
+int         cactus_hip_graph_capture_begin(void* stream);
+int         cactus_hip_graph_capture_end(void* stream, void** graph_exec);
+int         cactus_hip_graph_launch(void* graph_exec, void* stream);
+int         cactus_hip_graph_destroy(void* graph_exec);
 
 /* ------------------------------------------------ a1: activation quantization */
 /* cactus_fp16_max_abs (kernel/kernel.h:147, kernel_quants.cpp:196):
@@ -199,6 +205,70 @@ int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* 
 int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
                           float temperature, float top_p, size_t top_k, size_t random_seed,
                           void* stream);
+
+/* ------------------------------------------------ value product tiles
+ * No reference counterpart: an fp32 mirror of the INT8 value cache holding
+ * each cached (float)code * scale, the operand the hybrid attention's value
+ * accumulation rounds to (kernel_attention.cpp:424-441), tiled
+ * [kv head][64-dim slice][64-key tile][64 dims][68 keys] for the decode
+ * attention.  Batch 1, head_dim % 8 == 0, 128-dim scale groups. */
+int cactus_hip_kv_shadow_bytes(size_t max_seq, size_t kv_heads, size_t head_dim, size_t* bytes);
+/* products of cached keys [start, start + count) from the INT8 values and
+ * scales ([max_seq][kv_heads][head_dim], [max_seq][kv_heads][groups]) */
+int cactus_hip_kv_shadow_update(const int8_t* v_cache, const float* v_scales, float* shadow,
+                                size_t start, size_t count, size_t kv_heads, size_t head_dim,
+                                size_t quant_group_size, size_t max_seq, void* stream);
+
+/* ------------------------------------------------ fused decode step
+ * Each entry point computes a run of consecutive graph nodes of
+ * QwenModel::forward (models/model_qwen.cpp:51-172) for ONE token with the
+ * reference's arithmetic; there is no single reference function for any of
+ * them.  `state` is a device uint32[4] = {token, position, cache_length,
+ * step}, read (and, by the LM head, advanced) on the device so the whole
+ * step can be captured into a HIP graph. */
+/* h = embedding[state.token] */
+int cactus_hip_decode_embed(const uint16_t* table, const uint32_t* state, uint16_t* h,
+                            size_t hidden, size_t vocab, void* stream);
+/* x = rms_norm(h, norm_w, eps); q|k|v = matmul(x, Wq|Wk|Wv) (grouped INT8) */
+int cactus_hip_decode_qkv(const uint16_t* h, const uint16_t* norm_w, float eps, size_t K,
+                          size_t group_size, const int8_t* wq, const uint16_t* sq, uint16_t* q,
+                          size_t nq, const int8_t* wk, const uint16_t* sk, uint16_t* k, size_t nk,
+                          const int8_t* wv, const uint16_t* sv, uint16_t* v, size_t nv,
+                          void* stream);
+/* h = h + matmul(x, W) (grouped INT8, or packed INT4 when int4 != 0) */
+int cactus_hip_decode_matmul_residual(const uint16_t* x, size_t K, size_t group_size,
+                                      const void* w, const uint16_t* s, size_t N, int int4,
+                                      uint16_t* h, void* stream);
+/* x = rms_norm(h); m = silu(matmul(x, Wg)) * matmul(x, Wu) (packed INT4) */
+int cactus_hip_decode_mlp_up(const uint16_t* h, const uint16_t* norm_w, float eps, size_t K,
+                             size_t group_size, const uint8_t* wg, const uint16_t* sg,
+                             const uint8_t* wu, const uint16_t* su, size_t N, uint16_t* m,
+                             void* stream);
+/* q/k head RMSNorm, RoPE at state.position, INT8 append of k and v at
+ * state.cache_length (128-dim groups); with v_shadow (may be null) also the
+ * appended value row's product tiles (cactus_hip_kv_shadow_update) */
+int cactus_hip_decode_attn_prep(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                float theta, const uint32_t* state, uint16_t* q_out,
+                                uint16_t* k_out, int8_t* k_cache, int8_t* v_cache,
+                                float* k_scales, float* v_scales, size_t max_cache,
+                                float* v_shadow, void* stream);
+/* cactus_hip_attention_hybrid_int8_fp16 for one token, cache length and
+ * position from `state`; v_shadow (may be null): the value product tiles of
+ * the cache, capacity max_cache, which the value chains then stream */
+int cactus_hip_decode_attention(const uint16_t* q, const int8_t* k_cache, const int8_t* v_cache,
+                                const float* k_scales, const float* v_scales,
+                                const uint16_t* k_new, const uint16_t* v_new, uint16_t* o,
+                                size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                float scale, const uint32_t* state, size_t max_cache,
+                                const float* v_shadow, void* stream);
+/* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
+ * and advances state.  scratch: >= 256 + 8 * ceil(N/256) bytes, zeroed once. */
+int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
+                              const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
+                              uint32_t* tokens_out, size_t max_steps, void* scratch,
+                              size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -240,6 +240,9 @@ class OracleQwen:
                 setattr(arr[i], k, Lw[k].ctypes.data)
         self.h = L.orc_qwen_create(ctypes.byref(c), arr, self._emb.ctypes.data, self._on.ctypes.data)
 
+    def reset(self):
+        lib().orc_qwen_reset(self.h)
+
     def prefill(self, tokens, chunk=256):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         rc = lib().orc_qwen_prefill(self.h, t.ctypes.data, t.size, chunk)

@@ -233,7 +233,10 @@ def _attn_inputs(rng, B, S, Skv, Hq, Hkv, d):
     (1, 64, 64, 16, 8, 128, 0, 0),          # prefill chunk, causal
     (2, 5, 37, 4, 2, 64, 32, 0),
     (1, 9, 100, 4, 4, 128, 91, 20),         # sliding window
-    (1, 3, 50, 2, 1, 40, 47, 0),            # head_dim not a multiple of 8
+    (1, 3, 50, 2, 1, 40, 47, 0),            # head_dim not a multiple of 16
+    (1, 40, 600, 2, 2, 36, 560, 0),         # 4-byte value chunks, many tiles
+    (1, 2, 40, 2, 1, 12, 38, 0),            # head_dim not a multiple of 8
+    (2, 130, 130, 8, 1, 64, 0, 0),          # 8 query heads per kv head, prefill
 ])
 def test_attention_f16(dev, orc, B, S, Skv, Hq, Hkv, d, pos, window):
     say("attention_f16", B, S, Skv, Hq, Hkv, d, pos, window)
@@ -245,6 +248,24 @@ def test_attention_f16(dev, orc, B, S, Skv, Hq, Hkv, d, pos, window):
     dev.cm.call("cactus_hip_attention_f16", dev.put(q), dev.put(k), dev.put(v), o.ptr, B, S, Skv, Hq,
                 Hkv, d, ctypes.c_float(scale), None, pos, window, 1, None)
     assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_f16")
+
+
+def test_attention_f16_unaligned_values(dev, orc):
+    """Value rows at a 2-byte aligned address take the register-staged form
+    of the value chains."""
+    say("attention_f16 unaligned values")
+    rng = np.random.default_rng(21)
+    B, S, Skv, Hq, Hkv, d = 1, 6, 300, 4, 2, 64
+    q, k, v = _attn_inputs(rng, B, S, Skv, Hq, Hkv, d)
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_f16(q, k, v, scale, pos_off=Skv - S)
+    vb = np.zeros(v.size + 1, np.uint16)
+    vb[1:] = v.reshape(-1)
+    vp = dev.put(vb) + 2
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_attention_f16", dev.put(q), dev.put(k), vp, o.ptr, B, S, Skv, Hq,
+                Hkv, d, ctypes.c_float(scale), None, Skv - S, 0, 1, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_f16 unaligned")
 
 
 def test_attention_f16_mask_noncausal(dev, orc):
@@ -265,6 +286,9 @@ def test_attention_f16_mask_noncausal(dev, orc):
     (64, 256, 64, 16, 8, 128),     # second prefill chunk
     (3, 33, 3, 4, 2, 64),
     (2, 0, 2, 4, 2, 128),
+    (5, 700, 5, 4, 2, 40),         # 4-byte value chunks, new rows past the prefetched one
+    (1, 100, 1, 8, 1, 128),        # 8 query heads per kv head
+    (40, 1000, 40, 16, 8, 128),    # new rows spanning two blocks, cache not block aligned
 ])
 def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
     say("attention_hybrid", S, cache, new, Hq, Hkv, d)
@@ -287,6 +311,59 @@ def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
                 dev.put(kn), dev.put(vn), o.ptr, 1, S, cache, new, Hq, Hkv, d, ctypes.c_float(scale),
                 cache, 1, 128, None)
     assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid")
+
+
+def _shadow_ref(vc, vs, cap, d):
+    """Product tiles [kvh][slice][tile][64 dims][68 keys] of an INT8 cache
+    (numpy float32 products, the rounding the value chain consumes)."""
+    n, H = vc.shape[0], vc.shape[1]
+    nsl, nt = (d + 63) // 64, (cap + 63) // 64
+    ref = np.zeros((H, nsl, nt, 64, 68), np.float32)
+    prod = vc.astype(np.float32) * np.repeat(vs, 128, axis=2)[:, :, :d]
+    for key in range(n):
+        for sl in range(nsl):
+            w = min(64, d - sl * 64)
+            ref[:, sl, key // 64, :w, key % 64] = prod[key, :, sl * 64:sl * 64 + w]
+    return ref
+
+
+@pytest.mark.parametrize("cache,Hq,Hkv,d", [(4095, 16, 8, 128), (700, 4, 2, 64), (63, 8, 1, 128)])
+@pytest.mark.parametrize("shadow", [True, False])
+def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, shadow):
+    """The decode step's attention: cache length and position from the device
+    state, INT8 cache of capacity cache + 37, optionally through the value
+    product tiles; equal to the hybrid attention with one new row."""
+    say("decode_attention", cache, Hq, Hkv, d, "shadow" if shadow else "int8")
+    rng = np.random.default_rng(cache + d)
+    cap = cache + 37
+    kf = f16(rng.normal(0, 1, (cap, Hkv, d)))
+    vf = f16(rng.normal(0, 1, (cap, Hkv, d)))
+    kc, ks = orc.quantize_kv(kf)
+    vc, vs = orc.quantize_kv(vf)
+    kn = f16(rng.normal(0, 1, (1, 1, Hkv, d)))
+    vn = f16(rng.normal(0, 1, (1, 1, Hkv, d)))
+    q = f16(rng.normal(0, 1, (1, 1, Hq, d)))
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_hybrid(q, kc[None, :cache], vc[None, :cache], ks[None, :cache], vs[None, :cache],
+                               kn, vn, scale, pos_off=cache)
+    vcp, vsp = dev.put(vc), dev.put(vs)
+    shp = None
+    if shadow:
+        nbytes = ctypes.c_size_t()
+        dev.cm.call("cactus_hip_kv_shadow_bytes", cap, Hkv, d, ctypes.byref(nbytes))
+        sh = dev.empty(nbytes.value)
+        dev.cm.call("cactus_hip_kv_shadow_update", vcp, vsp, sh.ptr, 0, cache, Hkv, d, 128, cap, None)
+        got = dev.get(sh, np.float32, (Hkv, (d + 63) // 64, (cap + 63) // 64, 64, 68))
+        want = _shadow_ref(vc[:cache], vs[:cache], cap, d)
+        for key in (0, cache // 2, cache - 1):
+            t, j = key // 64, key % 64
+            assert (got[:, :, t, :, j] == want[:, :, t, :, j]).all(), f"products of key {key}"
+        shp = sh.ptr
+    state = np.array([0, cache, cache, 0], np.uint32)
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_decode_attention", dev.put(q), dev.put(kc), vcp, dev.put(ks), vsp, dev.put(kn),
+                dev.put(vn), o.ptr, Hq, Hkv, d, ctypes.c_float(scale), dev.put(state), cap, shp, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "decode attention")
 
 
 # ------------------------------------------------------------------ a7

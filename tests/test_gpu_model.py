@@ -35,17 +35,21 @@ def _run_both(cfg, prompt, steps, mode=0, weights=None, seed=None):
     return gpu, orc, toks, ref
 
 
+@pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("prompt_len,steps", [(300, 16), (40, 8), (1, 4)])
-def test_qwen_small_generate_matches_oracle(prompt_len, steps):
-    say("qwen small", prompt_len, steps)
+def test_qwen_small_generate_matches_oracle(prompt_len, steps, mode):
+    """mode 0: node-by-node graph decode; mode 1: fused kernels replayed as
+    one HIP graph per token with the step state on the device."""
+    say("qwen small", prompt_len, steps, "mode", mode)
     cfg = qwen_small_config()
     rng = np.random.default_rng(prompt_len)
     w = qwen_weights(rng, cfg)
     prompt = rng.integers(0, cfg["vocab"], prompt_len).astype(np.uint32)
-    gpu, orc, toks, ref = _run_both(cfg, prompt, steps, weights=w)
+    gpu, orc, toks, ref = _run_both(cfg, prompt, steps, mode=mode, weights=w)
     assert list(toks) == list(ref)
     assert gpu.cache_len() == orc.cache_len() == prompt_len - 1 + steps
-    assert (gpu.last_hidden() == orc.last_hidden()).all()
+    if mode == 0:
+        assert (gpu.last_hidden() == orc.last_hidden()).all()
     for layer in range(cfg["num_layers"]):
         for a, b in zip(gpu.read_kv(layer), orc.read_kv(layer)):
             assert (a == b).all(), f"kv cache layer {layer}"
@@ -65,3 +69,35 @@ def test_qwen_random_init_and_logits():
     t_orc = orc.decode(int(ref[-1]), lg)
     assert t_gpu == t_orc
     assert (gpu.last_logits() == lg).all()
+
+
+def test_qwen_fused_decode_continues_after_reset():
+    """Fused decode, reset, a second prompt: the captured graph reads the
+    new step state and cache length from the device."""
+    say("qwen fused reset")
+    cfg = qwen_small_config()
+    rng = np.random.default_rng(11)
+    w = qwen_weights(rng, cfg)
+    p1 = rng.integers(0, cfg["vocab"], 70).astype(np.uint32)
+    p2 = rng.integers(0, cfg["vocab"], 130).astype(np.uint32)
+    import cactus_amd
+    from cactus_amd.engine import Qwen
+    import oracle
+    cactus_amd.call("cactus_hip_init", 0)
+    gpu = Qwen(cfg, *w)
+    gpu.set_decode_mode(1)
+    orc = oracle.OracleQwen(cfg, *w)
+    for p, n in ((p1, 9), (p2, 12)):
+        gpu.reset()
+        orc.reset()
+        toks, _ = gpu.generate(p, n)
+        ref = orc.generate(p, n, cfg["prefill_chunk"])
+        assert list(toks) == list(ref)
+        # single steps through the same graph
+        t_gpu = gpu.decode(int(toks[-1]))
+        lg = np.zeros(cfg["vocab"], np.uint16)
+        t_orc = orc.decode(int(ref[-1]), lg)
+        assert t_gpu == t_orc
+    for layer in range(cfg["num_layers"]):
+        for a, b in zip(gpu.read_kv(layer), orc.read_kv(layer)):
+            assert (a == b).all(), f"kv cache layer {layer}"
