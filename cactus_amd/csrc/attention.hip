@@ -23,6 +23,7 @@
 #include "hip_common.h"
 
 #include <map>
+#include <utility>
 #include <mutex>
 
 namespace cactus_hip {
@@ -574,23 +575,49 @@ __device__ __forceinline__ void chain_corr(const AttnArgs& a, size_t row, int nb
     }
 }
 
+// acc = fma(w, p, acc) with w taken from lane k of each 16-lane row of wv
+// (DPP row_newbcast): a row-replicated weight vector feeds 16 chain steps
+// without an LDS broadcast read per step.  One VALU op per step, the same
+// single rounding as fmaf.
+template <int K>
+__device__ __forceinline__ void fmac_row_bcast(float& acc, float wv, float p) {
+    asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "+v"(acc)
+                 : "v"(wv), "v"(p), "n"(K));
+}
+
+// 16 chain steps: keys k = 0..15 with products p[k], weights in lanes k of wv
+template <int... K>
+__device__ __forceinline__ void chain16(float& acc, const float* p, float wv, std::integer_sequence<int, K...>) {
+    asm volatile("s_nop 1");   // DPP source read after a possible VALU write of wv
+    (fmac_row_bcast<K>(acc, wv, p[K]), ...);
+}
+
 // One tile of a chain row: blocks [b0, b1), all keys inside the tile; pt
 // is this lane's product row of the tile, wt the row's weights.
 __device__ __forceinline__ void chain_tile(const float* pt, const float* wt, int b0, int b1, size_t rks,
                                            size_t rbl, const float* cw, const float* cb, float& acc,
                                            float& rs) {
     const float NEG_INF = -__builtin_inff();
-    // both blocks of the tile full: every LDS read of the tile at once
+    // both blocks of the tile full: every LDS read of the tile at once;
+    // weights row-replicated into 4 VGPRs (16 keys each) for the DPP steps
     if (b1 - b0 == 2 && rks + (size_t)(b0 + 2) * ATT_BLOCK <= rbl) {
         const float c0 = cw[b0], c1 = cw[b0 + 1];
         const float s0 = cb[b0], s1 = cb[b0 + 1];
-        float4 pv[16], wq[16];
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            pv[j] = *reinterpret_cast<const float4*>(pt + 4 * j);
-            wq[j] = *reinterpret_cast<const float4*>(wt + 4 * j);
-        }
         if (!__builtin_signbit(s0) && !__builtin_signbit(s1)) {
+            const int lr = threadIdx.x & 15;
+            float pv[64];
+            float wv[4];
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const float4 v = *reinterpret_cast<const float4*>(pt + 4 * q);
+                pv[4 * q] = v.x;
+                pv[4 * q + 1] = v.y;
+                pv[4 * q + 2] = v.z;
+                pv[4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) wv[q] = wt[16 * q + lr];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const float c = h ? c1 : c0;
@@ -598,13 +625,8 @@ __device__ __forceinline__ void chain_tile(const float* pt, const float* wt, int
                     acc = acc * c;
                     rs = rs * c;
                 }
-#pragma unroll
-                for (int j = 8 * h; j < 8 * h + 8; j++) {
-                    acc = __builtin_fmaf(pv[j].x, wq[j].x, acc);
-                    acc = __builtin_fmaf(pv[j].y, wq[j].y, acc);
-                    acc = __builtin_fmaf(pv[j].z, wq[j].z, acc);
-                    acc = __builtin_fmaf(pv[j].w, wq[j].w, acc);
-                }
+                chain16(acc, pv + 32 * h, wv[2 * h], std::make_integer_sequence<int, 16>{});
+                chain16(acc, pv + 32 * h + 16, wv[2 * h + 1], std::make_integer_sequence<int, 16>{});
                 rs = rs + (h ? s1 : s0);
             }
             return;
@@ -948,12 +970,17 @@ constexpr int SH_W_OFF = SH_TILE_B;
 constexpr int SH_SLOT = SH_TILE_B + ATT_MAX_GQ * CD_T * 4;
 static_assert(SH_PCHUNKS * 1024 == SH_TILE_B, "tile chunks");
 
+constexpr int SH_MAX_CHAINS = 4;   // chain waves per workgroup (register budget)
+
 template <int D>
-__global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_kernel(AttnArgs a_in, int qpg,
-                                                                                       int nbmax) {
+__global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shadow_kernel(AttnArgs a_in, int qpg,
+                                                                                          int nbmax) {
+    constexpr int H = 1;
     const AttnArgs a = resolve(a_in);
     extern __shared__ __align__(16) unsigned char smem[];
-    const int gq = a.gq, nc = qpg * gq;
+    const int gq = a.gq, nc = qpg * gq;          // chain rows
+    const int hw = gq / H;                       // chain waves per query position
+    const int ncw = qpg * hw;                    // chain waves
     unsigned char* ring = smem;                                            // [D][SH_SLOT]
     float* corr_s = reinterpret_cast<float*>(smem + D * SH_SLOT);          // [nc][nbmax]
     float* bsum_s = corr_s + (size_t)nc * nbmax;
@@ -982,8 +1009,8 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_k
     }
     const size_t kt_end = kneed < a.cache_len ? kneed : (size_t)a.cache_len;
     const int nst = kt_end > 0 ? (int)((kt_end + CD_T - 1) / CD_T) : 0;
-    const bool is_chain = wv < nc;
-    const int pw = wv - nc;
+    const bool is_chain = wv < ncw;
+    const int pw = wv - ncw;
 
     // stage wave pw: product chunks pw, pw + CD_NP, ...; the weights of
     // rows 4k..4k+3 go to stage wave 1 + k
@@ -1018,10 +1045,13 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_k
         else wait_dma<(D - 2) * 4>();
     };
 
-    // ---- chain row
-    const int qp = qp0 + (is_chain ? wv / gq : 0);
+    // ---- chain wave: query position qp, heads hp*H .. hp*H + H-1, chain
+    // rows wv*H + j (position-major, the weight rows' order)
+    const int qp = qp0 + (is_chain ? wv / hw : 0);
+    const int hp = is_chain ? wv % hw : 0;
     const bool row_ok = is_chain && qp < a.S;
-    const size_t row = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + (is_chain ? wv % gq : 0);
+    const size_t row0 = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + hp * H;
+    const int c0 = (is_chain ? wv : 0) * H;
     size_t rks = 0, rke = 0, rbl = 0;
     int nb = 0, nb_tile = 0;
     if (row_ok) {
@@ -1030,22 +1060,31 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_k
         nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
     }
     const int dim = sl * 64 + lane;
-    float pf_p = 0.0f, pf_w = 0.0f;
+    float pf_p = 0.0f, pf_w[H];
     const bool pf = row_ok && a.cache_len < rke;
+#pragma unroll
+    for (int j = 0; j < H; j++) pf_w[j] = 0.0f;
     if (pf) {
-        pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
+#pragma unroll
+        for (int j = 0; j < H; j++) pf_w[j] = a.w[(row0 + j) * a.wstride + (a.cache_len - rks)];
         if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
     }
-    if (row_ok) chain_corr(a, row, nb, corr_s + wv * nbmax, bsum_s + wv * nbmax);
+    if (row_ok)
+        for (int j = 0; j < H; j++) chain_corr(a, row0 + j, nb, corr_s + (c0 + j) * nbmax, bsum_s + (c0 + j) * nbmax);
 
     if (!is_chain && nst > 0) {
         for (int t = 0; t < D - 1; t++)
             if (t < nst) issue(t);
         wait_next(nst >= D - 1);
     }
-    const float* cw = corr_s + wv * nbmax;
-    const float* cb = bsum_s + wv * nbmax;
-    float acc = 0.0f, rs = 0.0f;
+    const float* cw = corr_s + c0 * nbmax;
+    const float* cb = bsum_s + c0 * nbmax;
+    float acc[H], rs[H];
+#pragma unroll
+    for (int j = 0; j < H; j++) {
+        acc[j] = 0.0f;
+        rs[j] = 0.0f;
+    }
     for (int t = 0; t < nst; t++) {
         lds_barrier();
         if (!is_chain) {
@@ -1056,22 +1095,25 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_shadow_k
         if (!row_ok) continue;
         const unsigned char* slot = ring + (t % D) * SH_SLOT;
         const float* pt = reinterpret_cast<const float*>(slot) + lane * SH_PS;
-        const float* wt = reinterpret_cast<const float*>(slot + SH_W_OFF) + wv * CD_T;
+        const float* wt = reinterpret_cast<const float*>(slot + SH_W_OFF) + c0 * CD_T;
         const int b0 = t * (CD_T / ATT_BLOCK);
         const int b1 = min(nb_tile, b0 + CD_T / ATT_BLOCK);
-        chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc, rs);
+        chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc[0], rs[0]);
     }
     if (!row_ok) return;
     const int tl = nst > 0 ? nst - 1 : 0;
     const unsigned char* slot = ring + (tl % D) * SH_SLOT;
-    chain_tail<true>(a, b, kvh, dim, row, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
-                     reinterpret_cast<const float*>(slot) + lane * SH_PS,
-                     reinterpret_cast<const float*>(slot + SH_W_OFF) + wv * CD_T, pf, pf_p, pf_w, cw, cb, acc,
-                     rs);
-    if (dim < d) {
-        uint16_t* ov = a.o + row * (size_t)d;
-        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
-        else ov[dim] = f2h(acc * (1.0f / rs));
+#pragma unroll
+    for (int j = 0; j < H; j++) {
+        chain_tail<true>(a, b, kvh, dim, row0 + j, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
+                         reinterpret_cast<const float*>(slot) + lane * SH_PS,
+                         reinterpret_cast<const float*>(slot + SH_W_OFF) + (c0 + j) * CD_T, pf, pf_p, pf_w[j],
+                         cw + j * nbmax, cb + j * nbmax, acc[j], rs[j]);
+        if (dim < d) {
+            uint16_t* ov = a.o + (row0 + j) * (size_t)d;
+            if (!(rs[j] > 0.0f) || dim >= da) ov[dim] = 0;
+            else ov[dim] = f2h(acc[j] * (1.0f / rs[j]));
+        }
     }
 }
 
@@ -1149,37 +1191,32 @@ static int launch_attention(AttnArgs a, void* stream) {
     if (qpg < 1) qpg = 1;
     const int nbmax = a.nbstride;
     const size_t nsl = (size_t)(a.d + 63) / 64;
-    if (HYBRID && a.vsh) {
-        // product tiles: ring depth 8, or 5 where the rows' block data needs the room
+    if (HYBRID && a.vsh && a.gq <= SH_MAX_CHAINS) {
+        // product tiles: ring depth 8, or 5 where the rows' block data needs
+        // the room
         auto sh_smem = [&](int q, int depth) {
             return (size_t)depth * SH_SLOT + 2 * (size_t)q * a.gq * nbmax * sizeof(float);
         };
         int depth = 8;
+        while (qpg > 1 && qpg * a.gq > SH_MAX_CHAINS) qpg = (qpg + 1) / 2;
         while (qpg > 1 && sh_smem(qpg, depth) > 160 * 1024) qpg = (qpg + 1) / 2;
         if (sh_smem(qpg, depth) > 160 * 1024) depth = 5;
         const size_t smem = sh_smem(qpg, depth);
         CH_REQUIRE(smem <= 160 * 1024, "attention: key range too long for the product-tile kernel");
-        static bool sh_attr[2] = {false, false};
         const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
         const size_t groups = (size_t)a.B * ngrp * a.Hkv * nsl;
         const dim3 blk(64 * (qpg * a.gq + CD_NP));
-        if (depth == 8) {
-            if (!sh_attr[0]) {
-                CH_HIP(hipFuncSetAttribute((const void*)attn_chain_shadow_kernel<8>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-                sh_attr[0] = true;
+        static bool sh_attr[2] = {false, false};
+        auto launch = [&](auto kern, int di) -> int {
+            if (!sh_attr[di]) {
+                CH_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
+                sh_attr[di] = true;
             }
-            hipLaunchKernelGGL(attn_chain_shadow_kernel<8>, dim3((unsigned)groups), blk, smem, as_stream(stream), a,
-                               qpg, nbmax);
-        } else {
-            if (!sh_attr[1]) {
-                CH_HIP(hipFuncSetAttribute((const void*)attn_chain_shadow_kernel<5>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-                sh_attr[1] = true;
-            }
-            hipLaunchKernelGGL(attn_chain_shadow_kernel<5>, dim3((unsigned)groups), blk, smem, as_stream(stream), a,
-                               qpg, nbmax);
-        }
+            hipLaunchKernelGGL(kern, dim3((unsigned)groups), blk, smem, as_stream(stream), a, qpg, nbmax);
+            return CACTUS_HIP_OK;
+        };
+        const int lrc = depth == 8 ? launch(attn_chain_shadow_kernel<8>, 0) : launch(attn_chain_shadow_kernel<5>, 1);
+        if (lrc) return lrc;
         return check_launch("attention values");
     }
     // LDS-DMA form: value rows in 16- or 4-byte chunks, one scale group per
