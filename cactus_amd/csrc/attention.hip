@@ -748,7 +748,6 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_dma_kern
     float* corr_s = prod + 2 * 64 * CD_PS;                                 // [nc][nbmax]
     float* bsum_s = corr_s + (size_t)nc * nbmax;                           // [nc][nbmax]
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
-    const float NEG_INF = -__builtin_inff();
 
     const int d = a.d, da = (d / 8) * 8;
     const int nsl = (d + 63) / 64;

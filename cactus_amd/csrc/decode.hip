@@ -37,9 +37,18 @@ __device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float 
     float chain = 0.0f;
     const int n16 = n / 16, end8 = (n / 8) * 8;
     if (lane < 16) {
-        for (int i = 0; i < n16; i++) {
-            const float a = h2f(xs[i * 16 + lane]);
-            chain = __builtin_fmaf(a, a, chain);
+        int i = 0;
+        // 16 reads in flight per batch, then the chain steps
+        for (; i + 16 <= n16; i += 16) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = h2f(xs[(i + j) * 16 + lane]);
+#pragma unroll
+            for (int j = 0; j < 16; j++) chain = __builtin_fmaf(v[j], v[j], chain);
+        }
+        for (; i < n16; i++) {
+            const float v = h2f(xs[i * 16 + lane]);
+            chain = __builtin_fmaf(v, v, chain);
         }
         if (lane < 8 && n16 * 16 + 8 <= n) {
             const float a = h2f(xs[n16 * 16 + lane]);
@@ -112,8 +121,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 
     int8_t* actq = reinterpret_cast<int8_t*>(smem);                          // K
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + ((K + 15) & ~15));     // K
-    uint16_t* ys = xs + ((K + 7) & ~7);                                      // K
-    int32_t* acc = reinterpret_cast<int32_t*>(ys + ((K + 7) & ~7));         // vrows*G
+    int32_t* acc = reinterpret_cast<int32_t*>(xs + ((K + 7) & ~7));         // vrows*G
     uint16_t* scl = reinterpret_cast<uint16_t*>(acc + vrows * G);           // vrows*G
     float* red = reinterpret_cast<float*>(scl + ((vrows * G + 1) & ~1));    // 8
 
@@ -149,11 +157,39 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         }
         scl[i] = v;
     }
-    // 3. activation: optional RMSNorm, then per-row quantization
-    for (int i = tid; i < K; i += GEMV_THREADS) xs[i] = a.x[i];
-    __syncthreads();
-    const uint16_t* act = xs;
+    // 3. activation: optional RMSNorm, then per-row quantization.  Thread t
+    // owns the 8-element chunks t + 256 j in registers; the LDS copy feeds
+    // the RMS chains.
+    constexpr int CPT = 4;    // chunks per thread (K <= 8192)
+    const int nch = K / 8;
+    uint4 xv[CPT], wv[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int c = tid + j * GEMV_THREADS;
+        xv[j] = make_uint4(0, 0, 0, 0);
+        wv[j] = make_uint4(0, 0, 0, 0);
+        if (c < nch) {
+            xv[j] = reinterpret_cast<const uint4*>(a.x)[c];
+            if (PRO == PRO_NORM) wv[j] = reinterpret_cast<const uint4*>(a.norm_w)[c];
+        }
+    }
+    uint16_t resv = 0;   // residual of this thread's first row, early
+    if (EPI == EPI_RESID && tid < nr) resv = a.res[n0 + tid];
+    auto elem = [](const uint4& v, int e) -> uint16_t {
+        const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+        return (uint16_t)(e & 1 ? w >> 16 : w & 0xFFFF);
+    };
+    auto set_elem = [](uint4& v, int e, uint16_t h) {
+        uint32_t& w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+        w = e & 1 ? (w & 0xFFFFu) | ((uint32_t)h << 16) : (w & 0xFFFF0000u) | h;
+    };
     if (PRO == PRO_NORM) {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int c = tid + j * GEMV_THREADS;
+            if (c < nch) reinterpret_cast<uint4*>(xs)[c] = xv[j];
+        }
+        __syncthreads();
         if (tid < 64) {
             float inv;
             uint16_t hinv;
@@ -164,12 +200,22 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         const float inv = red[4];
         const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, red[5]);
         const int end8 = (K / 8) * 8;
-        for (int i = tid; i < K; i += GEMV_THREADS) ys[i] = rms_apply(xs[i], a.norm_w[i], i, end8, inv, hinv);
-        __syncthreads();
-        act = ys;
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int c = tid + j * GEMV_THREADS;
+            if (c < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    set_elem(xv[j], e, rms_apply(elem(xv[j], e), elem(wv[j], e), 8 * c + e, end8, inv, hinv));
+            }
+        }
     }
     float m = 0.0f;
-    for (int i = tid; i < K; i += GEMV_THREADS) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(act[i])));
+#pragma unroll
+    for (int j = 0; j < CPT; j++)
+        if (tid + j * GEMV_THREADS < nch)
+#pragma unroll
+            for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(elem(xv[j], e))));
     m = wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
@@ -177,8 +223,17 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     const float as = row_scale_from_max(mx);
     const float inv_s = 1.0f / as;
     const int body = (K / 8) * 8;
-    for (int i = tid; i < K; i += GEMV_THREADS)
-        actq[act_pos<INT4>(i)] = quant_code(h2f(act[i]), inv_s, i >= body);
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int c = tid + j * GEMV_THREADS;
+        if (c < nch) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int i = 8 * c + e;
+                actq[act_pos<INT4>(i)] = quant_code(h2f(elem(xv[j], e)), inv_s, i >= body);
+            }
+        }
+    }
     __syncthreads();
 
     // 4. dot products and exact group sums
@@ -195,7 +250,21 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     // 5. reference epilogue
     auto chain = [&](int vr) {
         float rs = 0.0f;
-        for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)acc[vr * G + g], h2f(scl[vr * G + g]), rs);
+        const int32_t* ar = acc + vr * G;
+        const uint16_t* sr = scl + vr * G;
+        int g = 0;
+        for (; g + 16 <= G; g += 16) {
+            int av[16];
+            uint16_t sv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                av[j] = ar[g + j];
+                sv[j] = sr[g + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; j++) rs = __builtin_fmaf((float)av[j], h2f(sv[j]), rs);
+        }
+        for (; g < G; g++) rs = __builtin_fmaf((float)ar[g], h2f(sr[g]), rs);
         return f2h(rs * as);
     };
     for (int r = tid; r < nr; r += GEMV_THREADS) {
@@ -203,7 +272,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         if (EPI == EPI_STORE) {
             sg.out[n0 + r] = val;
         } else if (EPI == EPI_RESID) {
-            sg.out[n0 + r] = hadd(a.res[n0 + r], val);
+            sg.out[n0 + r] = hadd(r == tid ? resv : a.res[n0 + r], val);
         } else {
             const uint16_t up = chain(rows + r);
             const float gx = h2f(val);
@@ -216,7 +285,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 }
 
 static size_t dec_gemv_smem(int K, int vrows, int G) {
-    size_t s = (size_t)((K + 15) & ~15) + 2 * (size_t)((K + 7) & ~7) * 2;
+    size_t s = (size_t)((K + 15) & ~15) + (size_t)((K + 7) & ~7) * 2;
     s += (size_t)vrows * G * 4 + (size_t)((vrows * G + 1) & ~1) * 2 + 8 * 4;
     return (s + 15) & ~(size_t)15;
 }
@@ -486,6 +555,7 @@ int cactus_hip_decode_qkv(const uint16_t* h, const uint16_t* norm_w, float eps, 
                           size_t nq, const int8_t* wk, const uint16_t* sk, uint16_t* k, size_t nk,
                           const int8_t* wv, const uint16_t* sv, uint16_t* v, size_t nv, void* stream) {
     CH_REQUIRE(h && norm_w && wq && sq && q && wk && sk && k && wv && sv && v, "decode_qkv: null pointer");
+    CH_REQUIRE(((uintptr_t)h | (uintptr_t)norm_w) % 16 == 0, "decode_qkv: h and norm_w must be 16-byte aligned");
     CH_REQUIRE(group_size >= 16 && K % group_size == 0 && (group_size & (group_size - 1)) == 0 &&
                group_size <= 1024 && K <= 8192, "decode_qkv: bad K / group_size");
     DecGemvArgs a{};
@@ -500,6 +570,7 @@ int cactus_hip_decode_matmul_residual(const uint16_t* x, size_t K, size_t group_
                                       const uint16_t* s, size_t N, int int4, uint16_t* h,
                                       void* stream) {
     CH_REQUIRE(x && w && s && h, "decode_matmul_residual: null pointer");
+    CH_REQUIRE((uintptr_t)x % 16 == 0, "decode_matmul_residual: x must be 16-byte aligned");
     CH_REQUIRE(group_size >= (int4 ? 32u : 16u) && K % group_size == 0 &&
                (group_size & (group_size - 1)) == 0 && group_size <= 1024 && K <= 8192,
                "decode_matmul_residual: bad K / group_size");
@@ -515,6 +586,7 @@ int cactus_hip_decode_mlp_up(const uint16_t* h, const uint16_t* norm_w, float ep
                              const uint8_t* wu, const uint16_t* su, size_t N, uint16_t* m,
                              void* stream) {
     CH_REQUIRE(h && norm_w && wg && sg && wu && su && m, "decode_mlp_up: null pointer");
+    CH_REQUIRE(((uintptr_t)h | (uintptr_t)norm_w) % 16 == 0, "decode_mlp_up: h and norm_w must be 16-byte aligned");
     CH_REQUIRE(group_size >= 32 && K % group_size == 0 && (group_size & (group_size - 1)) == 0 &&
                group_size <= 1024 && K <= 8192, "decode_mlp_up: bad K / group_size");
     DecGemvArgs a{};
