@@ -105,8 +105,10 @@ __device__ __forceinline__ void kv_range(const AttnArgs& a, size_t qp, size_t& k
 }
 
 // ----------------------------------------------------------------- kernel A
-// grid.x: 64-key chunks (4 per workgroup), grid.y: (b, qp, kv head)
-template <bool HYBRID>
+// grid.x: 64-key chunks (4 per workgroup), grid.y: (b, qp, kv head).  A lane
+// owns one key: its whole key row is loaded up front (DMAX >= head_dim), so a
+// score costs one memory round trip.
+template <bool HYBRID, int DMAX>
 __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
     const AttnArgs a = resolve(a_in);
     __shared__ float qsh[ATT_MAX_GQ][ATT_MAX_D];
@@ -147,73 +149,90 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
 #pragma unroll
     for (int hh = 0; hh < ATT_MAX_GQ; hh++) score[hh] = NEG_INF;
     if (computed) {
-        float ch[ATT_MAX_GQ][8];
+        constexpr int NC = DMAX / 8;   // 8-dim chunks of a key row
+        const int nca = da / 8;
+        // per chunk: 8 key values as float (INT8 code * scale, or fp16)
+        auto dot_heads = [&](auto chunk_vals) {
 #pragma unroll
-        for (int hh = 0; hh < ATT_MAX_GQ; hh++)
+            for (int hh = 0; hh < ATT_MAX_GQ; hh++) {
+                if (hh >= gq) break;
+                float ch[8];
 #pragma unroll
-            for (int c = 0; c < 8; c++) ch[hh][c] = 0.0f;
+                for (int c = 0; c < 8; c++) ch[c] = 0.0f;
+#pragma unroll
+                for (int cc = 0; cc < NC; cc++) {
+                    if (cc >= nca) break;
+                    float kk[8];
+                    chunk_vals(cc, kk);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) ch[c] = __builtin_fmaf(qsh[hh][cc * 8 + c], kk[c], ch[c]);
+                }
+                const float t0 = ch[0] + ch[4], t1 = ch[1] + ch[5];
+                const float t2 = ch[2] + ch[6], t3 = ch[3] + ch[7];
+                score[hh] = (t0 + t1) + (t2 + t3);
+            }
+        };
         if (HYBRID && kp < a.cache_len) {
             const int8_t* kr = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
             const float* sr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
-            for (int cb = 0; cb < da; cb += 8) {
-                const float s = sr[cb / a.qgs];
-                const uint2 w = *reinterpret_cast<const uint2*>(kr + cb);
-                float kk[8];
+            uint2 kw[NC];
+            float ksc[NC];
+#pragma unroll
+            for (int cc = 0; cc < NC; cc++) {
+                const int cb = cc < nca ? cc * 8 : 0;   // chunks past the row reload chunk 0
+                kw[cc] = *reinterpret_cast<const uint2*>(kr + cb);
+                ksc[cc] = sr[cb / a.qgs];
+            }
+            dot_heads([&](int cc, float* kk) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    kk[c] = (float)(int8_t)((w.x >> (8 * c)) & 0xFF) * s;
-                    kk[4 + c] = (float)(int8_t)((w.y >> (8 * c)) & 0xFF) * s;
+                    kk[c] = (float)(int8_t)((kw[cc].x >> (8 * c)) & 0xFF) * ksc[cc];
+                    kk[4 + c] = (float)(int8_t)((kw[cc].y >> (8 * c)) & 0xFF) * ksc[cc];
                 }
-#pragma unroll
-                for (int hh = 0; hh < ATT_MAX_GQ; hh++)
-                    if (hh < gq)
-#pragma unroll
-                        for (int c = 0; c < 8; c++) ch[hh][c] = __builtin_fmaf(qsh[hh][cb + c], kk[c], ch[hh][c]);
-            }
-        } else {
+            });
+        } else if (nca > 0) {
             const size_t kpos = HYBRID ? kp - a.cache_len : kp;
             const size_t klen = HYBRID ? a.new_len : a.Skv;
             const uint16_t* kr = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
-            for (int cb = 0; cb < da; cb += 8) {
-                uint32_t wv[4];
+            uint32_t kw[NC][4];
+#pragma unroll
+            for (int cc = 0; cc < NC; cc++) {
+                const int cb = cc < nca ? cc * 8 : 0;
                 if ((d & 7) == 0) {
                     const uint4 w = *reinterpret_cast<const uint4*>(kr + cb);
-                    wv[0] = w.x; wv[1] = w.y; wv[2] = w.z; wv[3] = w.w;
+                    kw[cc][0] = w.x; kw[cc][1] = w.y; kw[cc][2] = w.z; kw[cc][3] = w.w;
                 } else {
                     const uint2 w0 = *reinterpret_cast<const uint2*>(kr + cb);
                     const uint2 w1 = *reinterpret_cast<const uint2*>(kr + cb + 4);
-                    wv[0] = w0.x; wv[1] = w0.y; wv[2] = w1.x; wv[3] = w1.y;
+                    kw[cc][0] = w0.x; kw[cc][1] = w0.y; kw[cc][2] = w1.x; kw[cc][3] = w1.y;
                 }
-                float kk[8];
+            }
+            dot_heads([&](int cc, float* kk) {
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
-                    kk[2 * c] = h2f((uint16_t)(wv[c] & 0xFFFF));
-                    kk[2 * c + 1] = h2f((uint16_t)(wv[c] >> 16));
+                    kk[2 * c] = h2f((uint16_t)(kw[cc][c] & 0xFFFF));
+                    kk[2 * c + 1] = h2f((uint16_t)(kw[cc][c] >> 16));
                 }
+            });
+        } else {
 #pragma unroll
-                for (int hh = 0; hh < ATT_MAX_GQ; hh++)
-                    if (hh < gq)
-#pragma unroll
-                        for (int c = 0; c < 8; c++) ch[hh][c] = __builtin_fmaf(qsh[hh][cb + c], kk[c], ch[hh][c]);
-            }
+            for (int hh = 0; hh < ATT_MAX_GQ; hh++) score[hh] = 0.0f;
         }
 #pragma unroll
         for (int hh = 0; hh < ATT_MAX_GQ; hh++) {
             if (hh >= gq) break;
-            const float t0 = ch[hh][0] + ch[hh][4], t1 = ch[hh][1] + ch[hh][5];
-            const float t2 = ch[hh][2] + ch[hh][6], t3 = ch[hh][3] + ch[hh][7];
-            float s = (t0 + t1) + (t2 + t3);
+            float sc = score[hh];
             if (!HYBRID) {
                 const uint16_t* kr = a.k + ((b * a.Skv + kp) * a.Hkv + kvh) * (size_t)d;
-                for (int i = da; i < d; i++) s = __builtin_fmaf(qsh[hh][i], h2f(kr[i]), s);
+                for (int i = da; i < d; i++) sc = __builtin_fmaf(qsh[hh][i], h2f(kr[i]), sc);
             }
-            s = s * a.scale;
+            sc = sc * a.scale;
             if (!HYBRID) {
-                if (a.causal && kp > aq) s = NEG_INF;
-                else if (a.window > 0 && kp < aq && (aq - kp) > a.window) s = NEG_INF;
-                else if (a.mask && h2f(a.mask[(b * a.S + qp) * a.Skv + kp]) == 0.0f) s = NEG_INF;
+                if (a.causal && kp > aq) sc = NEG_INF;
+                else if (a.window > 0 && kp < aq && (aq - kp) > a.window) sc = NEG_INF;
+                else if (a.mask && h2f(a.mask[(b * a.S + qp) * a.Skv + kp]) == 0.0f) sc = NEG_INF;
             }
-            score[hh] = s;
+            score[hh] = sc;
         }
     }
 
@@ -237,16 +256,33 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
         const int bszA = __builtin_amdgcn_readlane(bsz, 0);
         const int bszB = __builtin_amdgcn_readlane(bsz, 32);
         {
-            const int v4 = HYBRID ? 0 : (bszA / 4) * 4;
-            for (int j = 0; j < v4; j += 4)
-                sumA = sumA + ((lane_f(w, j) + lane_f(w, j + 1)) + (lane_f(w, j + 2) + lane_f(w, j + 3)));
-            for (int j = v4; j < bszA; j++) sumA = sumA + lane_f(w, j);
-        }
-        {
-            const int v4 = HYBRID ? 0 : (bszB / 4) * 4;
-            for (int j = 0; j < v4; j += 4)
-                sumB = sumB + ((lane_f(w, 32 + j) + lane_f(w, 33 + j)) + (lane_f(w, 34 + j) + lane_f(w, 35 + j)));
-            for (int j = v4; j < bszB; j++) sumB = sumB + lane_f(w, 32 + j);
+            // the two half-wave blocks' chains interleave; every lane index is
+            // a constant (v_readlane), every bound a uniform branch
+            const int v4A = HYBRID ? 0 : (bszA / 4) * 4;
+            const int v4B = HYBRID ? 0 : (bszB / 4) * 4;
+#pragma unroll
+            for (int j = 0; j < ATT_BLOCK; j += 4) {
+                float xa[4], xb[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    xa[e] = lane_f(w, j + e);
+                    xb[e] = lane_f(w, 32 + j + e);
+                }
+                if (j < v4A) {
+                    sumA = sumA + ((xa[0] + xa[1]) + (xa[2] + xa[3]));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (j + e < bszA) sumA = sumA + xa[e];
+                }
+                if (j < v4B) {
+                    sumB = sumB + ((xb[0] + xb[1]) + (xb[2] + xb[3]));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (j + e < bszB) sumB = sumB + xb[e];
+                }
+            }
         }
         const size_t r = (b * a.S + qp) * a.Hq + h0 + hh;
         // every key of a live block gets its weight (0 when not computed);
@@ -522,7 +558,9 @@ struct CdCfg {
 };
 
 template <int DW>
-__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds) {
+__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds_addr) {
+    // M0 takes a scalar: the destination is uniform over the wave
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
     if constexpr (DW == 16)
         asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
                      : "memory");
@@ -597,13 +635,14 @@ __device__ __forceinline__ void chain16(float& acc, const float* p, float wv, st
 // is this lane's product row of the tile, wt the row's weights.
 __device__ __forceinline__ void chain_tile(const float* pt, const float* wt, int b0, int b1, size_t rks,
                                            size_t rbl, const float* cw, const float* cb, float& acc,
-                                           float& rs) {
+                                           float& rs, const float* meta = nullptr) {
     const float NEG_INF = -__builtin_inff();
     // both blocks of the tile full: every LDS read of the tile at once;
-    // weights row-replicated into 4 VGPRs (16 keys each) for the DPP steps
+    // weights row-replicated into 4 VGPRs (16 keys each) for the DPP steps.
+    // meta: the blocks' {corr, corr, sum, sum} read ahead by the caller
     if (b1 - b0 == 2 && rks + (size_t)(b0 + 2) * ATT_BLOCK <= rbl) {
-        const float c0 = cw[b0], c1 = cw[b0 + 1];
-        const float s0 = cb[b0], s1 = cb[b0 + 1];
+        const float c0 = meta ? meta[0] : cw[b0], c1 = meta ? meta[1] : cw[b0 + 1];
+        const float s0 = meta ? meta[2] : cb[b0], s1 = meta ? meta[3] : cb[b0 + 1];
         if (!__builtin_signbit(s0) && !__builtin_signbit(s1)) {
             const int lr = threadIdx.x & 15;
             float pv[64];
@@ -959,15 +998,21 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_dma_kern
 // ------------------------------------------------ kernel B, product tiles
 // With the INT8 value cache mirrored as fp32 product tiles (every cached
 // (float)code * scale already rounded, kv_shadow.hip), the stage waves only
-// move memory: each tile is 17 KB of products in the chains' LDS layout
-// plus the weights, fetched by LDS DMA D - 1 tiles ahead.  Tile layout, per
-// (batch, kv head, 64-dim slice, 64-key tile): [64 dims][SH_PS keys].
+// move memory: each step stages the 32-dim half of a product tile the
+// workgroup owns (8.5 KB) plus the weights, by LDS DMA D - 1 tiles ahead.
+// A chain wave runs its 32 dimensions on lanes 0-31, which halves the LDS
+// bytes it pulls per key: a chain step is then bound by the FMA latency, not
+// by the wave's LDS delivery.
+// Tile layout, per (batch, kv head, 64-dim slice, 64-key tile):
+// [64 dims][SH_PS keys].
 constexpr int SH_PS = CD_T + 4;                    // keys per dim row (4 of them padding)
 constexpr int SH_TILE_B = 64 * SH_PS * 4;          // 17408 bytes
-constexpr int SH_PCHUNKS = SH_TILE_B / 1024;       // 1 KB DMA per tile
-constexpr int SH_W_OFF = SH_TILE_B;
-constexpr int SH_SLOT = SH_TILE_B + ATT_MAX_GQ * CD_T * 4;
-static_assert(SH_PCHUNKS * 1024 == SH_TILE_B, "tile chunks");
+constexpr int SH_SW = 32;                          // dims per workgroup
+constexpr int SH_HALF_B = SH_SW * SH_PS * 4;       // 8704 bytes staged per step
+constexpr int SH_PCHUNKS = (SH_HALF_B + 1023) / 1024;   // 8 full 1 KB DMA + one half
+constexpr int SH_W_OFF = SH_HALF_B;
+constexpr int SH_SLOT = SH_HALF_B + ATT_MAX_GQ * CD_T * 4;
+static_assert(SH_HALF_B % 512 == 0 && SH_W_OFF % 16 == 0, "tile chunks");
 
 constexpr int SH_MAX_CHAINS = 4;   // chain waves per workgroup (register budget)
 
@@ -986,7 +1031,8 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
     const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
 
     const int d = a.d, da = (d / 8) * 8;
-    const int nsl = (d + 63) / 64;
+    const int nsl = (d + SH_SW - 1) / SH_SW;   // 32-dim slices (workgroups)
+    const int nsl64 = (d + 63) / 64;           // 64-dim slices (tile layout)
     size_t g = blockIdx.x;
     const int sl = (int)(g % nsl);
     g /= nsl;
@@ -1015,12 +1061,13 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
     // rows 4k..4k+3 go to stage wave 1 + k
     const int wn = (nc + 3) / 4;
     const bool my_w = pw >= 1 && pw <= wn;
-    const int lpt = (SH_PCHUNKS - pw + CD_NP - 1) / CD_NP + (my_w ? 1 : 0);
+    const int lpt = (SH_PCHUNKS - pw + CD_NP - 1) / CD_NP + (my_w ? 1 : 0);   // 2 or 3
     const char* psrc = nullptr;
     const float* wsrc = nullptr;
     if (!is_chain) {
         psrc = reinterpret_cast<const char*>(a.vsh) +
-               (((b * a.Hkv + kvh) * nsl + sl) * a.sh_ntile) * (size_t)SH_TILE_B + lane * 16;
+               (((b * a.Hkv + kvh) * nsl64 + sl / 2) * a.sh_ntile) * (size_t)SH_TILE_B + (sl & 1) * SH_HALF_B +
+               lane * 16;
         if (my_w) {
             int r = (pw - 1) * 4 + lane / 16;
             int qp = qp0 + r / gq;
@@ -1035,13 +1082,14 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
     auto issue = [&](int t) {
         const uint32_t slot = ring_lds + (uint32_t)((t % D) * SH_SLOT);
         const char* src = psrc + (size_t)t * SH_TILE_B;
-        for (int c = pw; c < SH_PCHUNKS; c += CD_NP) lds_dma<16>(src + c * 1024, slot + c * 1024);
+        for (int c = pw; c < SH_PCHUNKS; c += CD_NP)
+            if (c * 1024 + lane * 16 < SH_HALF_B) lds_dma<16>(src + c * 1024, slot + c * 1024);
         if (my_w) lds_dma<16>(wsrc + (size_t)t * CD_T, slot + SH_W_OFF + (pw - 1) * 1024);
     };
     auto wait_next = [&](bool all_issued) {
         if (!all_issued) wait_dma<0>();
-        else if (lpt == 5) wait_dma<(D - 2) * 5>();
-        else wait_dma<(D - 2) * 4>();
+        else if (lpt == 3) wait_dma<(D - 2) * 3>();
+        else wait_dma<(D - 2) * 2>();
     };
 
     // ---- chain wave: query position qp, heads hp*H .. hp*H + H-1, chain
@@ -1058,7 +1106,8 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
         nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
         nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
     }
-    const int dim = sl * 64 + lane;
+    const int dim = sl * SH_SW + lane;
+    const bool dlane = lane < SH_SW;   // chain lanes
     float pf_p = 0.0f, pf_w[H];
     const bool pf = row_ok && a.cache_len < rke;
 #pragma unroll
@@ -1066,7 +1115,7 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
     if (pf) {
 #pragma unroll
         for (int j = 0; j < H; j++) pf_w[j] = a.w[(row0 + j) * a.wstride + (a.cache_len - rks)];
-        if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
+        if (dlane && dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
     }
     if (row_ok)
         for (int j = 0; j < H; j++) chain_corr(a, row0 + j, nb, corr_s + (c0 + j) * nbmax, bsum_s + (c0 + j) * nbmax);
@@ -1093,19 +1142,19 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
         }
         if (!row_ok) continue;
         const unsigned char* slot = ring + (t % D) * SH_SLOT;
-        const float* pt = reinterpret_cast<const float*>(slot) + lane * SH_PS;
+        const float* pt = reinterpret_cast<const float*>(slot) + (lane & (SH_SW - 1)) * SH_PS;
         const float* wt = reinterpret_cast<const float*>(slot + SH_W_OFF) + c0 * CD_T;
         const int b0 = t * (CD_T / ATT_BLOCK);
         const int b1 = min(nb_tile, b0 + CD_T / ATT_BLOCK);
-        chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc[0], rs[0]);
+        if (dlane) chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc[0], rs[0]);
     }
-    if (!row_ok) return;
+    if (!row_ok || !dlane) return;
     const int tl = nst > 0 ? nst - 1 : 0;
     const unsigned char* slot = ring + (tl % D) * SH_SLOT;
 #pragma unroll
     for (int j = 0; j < H; j++) {
         chain_tail<true>(a, b, kvh, dim, row0 + j, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
-                         reinterpret_cast<const float*>(slot) + lane * SH_PS,
+                         reinterpret_cast<const float*>(slot) + (lane & (SH_SW - 1)) * SH_PS,
                          reinterpret_cast<const float*>(slot + SH_W_OFF) + (c0 + j) * CD_T, pf, pf_p, pf_w[j],
                          cw + j * nbmax, cb + j * nbmax, acc[j], rs[j]);
         if (dim < d) {
@@ -1178,7 +1227,12 @@ static int launch_attention(AttnArgs a, void* stream) {
     const size_t chunks = (maxr + 63) / 64;
     if (chunks > 0) {
         dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * a.S * a.Hkv));
-        hipLaunchKernelGGL(attn_scores_kernel<HYBRID>, ga, dim3(256), 0, as_stream(stream), a);
+        if (a.d <= 64)
+            hipLaunchKernelGGL((attn_scores_kernel<HYBRID, 64>), ga, dim3(256), 0, as_stream(stream), a);
+        else if (a.d <= 128)
+            hipLaunchKernelGGL((attn_scores_kernel<HYBRID, 128>), ga, dim3(256), 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL((attn_scores_kernel<HYBRID, 256>), ga, dim3(256), 0, as_stream(stream), a);
         rc = check_launch("attention scores");
         if (rc) return rc;
     }
@@ -1196,14 +1250,14 @@ static int launch_attention(AttnArgs a, void* stream) {
         auto sh_smem = [&](int q, int depth) {
             return (size_t)depth * SH_SLOT + 2 * (size_t)q * a.gq * nbmax * sizeof(float);
         };
-        int depth = 8;
+        int depth = 12;
         while (qpg > 1 && qpg * a.gq > SH_MAX_CHAINS) qpg = (qpg + 1) / 2;
         while (qpg > 1 && sh_smem(qpg, depth) > 160 * 1024) qpg = (qpg + 1) / 2;
         if (sh_smem(qpg, depth) > 160 * 1024) depth = 5;
         const size_t smem = sh_smem(qpg, depth);
         CH_REQUIRE(smem <= 160 * 1024, "attention: key range too long for the product-tile kernel");
         const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
-        const size_t groups = (size_t)a.B * ngrp * a.Hkv * nsl;
+        const size_t groups = (size_t)a.B * ngrp * a.Hkv * ((a.d + SH_SW - 1) / SH_SW);
         const dim3 blk(64 * (qpg * a.gq + CD_NP));
         static bool sh_attr[2] = {false, false};
         auto launch = [&](auto kern, int di) -> int {
@@ -1214,7 +1268,7 @@ static int launch_attention(AttnArgs a, void* stream) {
             hipLaunchKernelGGL(kern, dim3((unsigned)groups), blk, smem, as_stream(stream), a, qpg, nbmax);
             return CACTUS_HIP_OK;
         };
-        const int lrc = depth == 8 ? launch(attn_chain_shadow_kernel<8>, 0) : launch(attn_chain_shadow_kernel<5>, 1);
+        const int lrc = depth == 12 ? launch(attn_chain_shadow_kernel<12>, 0) : launch(attn_chain_shadow_kernel<5>, 1);
         if (lrc) return lrc;
         return check_launch("attention values");
     }

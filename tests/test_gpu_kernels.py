@@ -237,6 +237,7 @@ def _attn_inputs(rng, B, S, Skv, Hq, Hkv, d):
     (1, 40, 600, 2, 2, 36, 560, 0),         # 4-byte value chunks, many tiles
     (1, 2, 40, 2, 1, 12, 38, 0),            # head_dim not a multiple of 8
     (2, 130, 130, 8, 1, 64, 0, 0),          # 8 query heads per kv head, prefill
+    (1, 5, 70, 4, 2, 256, 65, 0),           # head_dim 256
 ])
 def test_attention_f16(dev, orc, B, S, Skv, Hq, Hkv, d, pos, window):
     say("attention_f16", B, S, Skv, Hq, Hkv, d, pos, window)
@@ -289,6 +290,7 @@ def test_attention_f16_mask_noncausal(dev, orc):
     (5, 700, 5, 4, 2, 40),         # 4-byte value chunks, new rows past the prefetched one
     (1, 100, 1, 8, 1, 128),        # 8 query heads per kv head
     (40, 1000, 40, 16, 8, 128),    # new rows spanning two blocks, cache not block aligned
+    (2, 100, 2, 4, 2, 256),        # head_dim 256
 ])
 def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
     say("attention_hybrid", S, cache, new, Hq, Hkv, d)
