@@ -84,6 +84,19 @@ def bench_gemv(steps: int, warmup: int, R: int = 768):
     return {"gbs": gbs, "ms_per_step": ms / steps, "wall_s": wall, "R": R}
 
 
+def measured_traffic():
+    """HBM bytes per GEMV launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated),
+    as recorded by the rocprofv3 counter runs summarised in
+    profiles/gemv_int8_traffic.md (line 'traffic_bytes_per_launch: N')."""
+    f = ROOT / "profiles" / "gemv_int8_traffic.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
 def cpu_baseline(seconds: float = 10.0):
     """Reference-restated CPU GEMV (oracle build) on this host."""
     import oracle
@@ -155,10 +168,14 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--decode-mode", type=int, default=0)
+    ap.add_argument("--decode-mode", type=int, default=1,
+                    help="1: fused decode step replayed as one HIP graph (default); 0: node-by-node graph")
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
     ap.add_argument("--new-tokens", type=int, default=128)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -170,6 +187,12 @@ def main():
     if args.decode_only:
         print(json.dumps(bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)), flush=True)
         return
+    if args.copy_calibration:
+        n = 1 << 30
+        src, dst = cm.DeviceBuffer(n), cm.DeviceBuffer(n)
+        cm.call("cactus_hip_memcpy_d2d", dst.ptr, src.ptr, n, None)
+        cm.call("cactus_hip_stream_sync", None)
+        del src, dst
     g = bench_gemv(args.steps, args.warmup)
     dec = None if args.skip_decode else bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)
     cpu = cpu_baseline(args.cpu_seconds)
@@ -199,7 +222,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(g["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
         "qwen3_0p6b_decode": dec,
