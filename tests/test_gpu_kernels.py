@@ -99,7 +99,11 @@ GEMM_CASES = [
     (5, 256, 200, 32),
     (17, 1024, 256, 32),
     (64, 1024, 512, 32),
-    (512, 1024, 3072, 32),  # Qwen3-0.6B gate/up prefill GEMM
+    (33, 640, 200, 32),     # MFMA path, ragged rows and columns
+    (100, 1024, 1024, 64),  # MFMA path, two MFMAs per group
+    (40, 512, 96, 128),
+    (256, 2048, 1024, 32),  # Qwen3-0.6B o-proj prefill chunk
+    (512, 1024, 3072, 32),  # Qwen3-0.6B gate/up prefill GEMM (MFMA, two tiles per wave)
 ]
 
 
@@ -121,7 +125,8 @@ def test_matmul_int8(dev, orc, M, K, N, gs):
 
 
 @pytest.mark.parametrize("M,K,N,gs", [(1, 3072, 1024, 32), (256, 3072, 1024, 32), (1, 1024, 3072, 32),
-                                      (4, 1024, 640, 64), (2, 512, 96, 128)])
+                                      (4, 1024, 640, 64), (2, 512, 96, 128), (70, 1024, 3072, 32),
+                                      (48, 2048, 1024, 64), (512, 1024, 3072, 32)])
 def test_matmul_int4(dev, orc, M, K, N, gs):
     say("matmul_int4", M, K, N, gs)
     rng = np.random.default_rng(M * 3 + K + N)
@@ -153,6 +158,25 @@ def test_int32_accumulator_exact(dev, orc):
     dev.cm.call("cactus_hip_matmul_int8", dev.put(A), dev.put(As), dev.put(B), dev.put(Bs), C.ptr,
                 M, K, N, gs, None)
     acc = orc.group_sums_int8(A, B, gs)[:, :, 0]
+    got = dev.get(C, np.uint16, (M, N)).view(np.float16).astype(np.int64)
+    assert (got == acc).all()
+
+
+@pytest.mark.parametrize("M,N", [(40, 96), (64, 300)])
+def test_int32_accumulator_exact_mfma(dev, orc, M, N):
+    """As test_int32_accumulator_exact at prefill sizes (the MFMA path), two
+    groups of 32: the fp32 chain adds the two exact group sums."""
+    say("int32 accumulators mfma", M, N)
+    rng = np.random.default_rng(M + N)
+    K, gs = 64, 32
+    A = rng.integers(-8, 9, (M, K), dtype=np.int8)
+    B = rng.integers(-8, 9, (N, K), dtype=np.int8)
+    As = np.ones(M, np.float32)
+    Bs = f16(np.ones((N, K // gs)))
+    C = dev.empty(M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8", dev.put(A), dev.put(As), dev.put(B), dev.put(Bs), C.ptr,
+                M, K, N, gs, None)
+    acc = orc.group_sums_int8(A, B, gs).sum(axis=2)
     got = dev.get(C, np.uint16, (M, N)).view(np.float16).astype(np.int64)
     assert (got == acc).all()
 
