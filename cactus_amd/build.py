@@ -40,6 +40,11 @@ HIP_FLAGS = [
     "-Wno-unused-function",
 ]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-ffp-contract=off"]
+# per-source additions: the MFMA matmul keeps its int32 accumulators in
+# ordinary VGPRs, so the fp32 epilogue reads them without v_accvgpr_read copies
+HIP_FILE_FLAGS = {
+    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def _run(cmd: list[str]) -> None:
@@ -58,7 +63,8 @@ def _run(cmd: list[str]) -> None:
 
 def _compile_hip(src: Path) -> Path:
     obj = OBJDIR / (src.stem + ".o")
-    _run([HIPCC, *HIP_FLAGS, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
+    _run([HIPCC, *HIP_FLAGS, *HIP_FILE_FLAGS.get(src.name, []), "-I", str(ROOT / "include"), "-c", str(src),
+          "-o", str(obj)])
     return obj
 
 

@@ -557,26 +557,6 @@ struct CdCfg {
     static_assert(ROWS_LPT * 64 * DW == CD_KPW * ROW_B, "row chunks");
 };
 
-template <int DW>
-__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds_addr) {
-    // M0 takes a scalar: the destination is uniform over the wave
-    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
-    if constexpr (DW == 16)
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-                     : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
-                     : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_dma() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// workgroup barrier that orders LDS only (outstanding DMA keeps flying)
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 // Block rescale factors of one chain row, into LDS: corr[blk] =
 // expf(running max before blk - block max) when the block max is finite
 // (the running max is the last finite block max), else NEG_INF (the block

@@ -22,7 +22,10 @@
 // reference's fma((float)acc, Bs, r) bit for bit.
 #include "hip_common.h"
 
+#include <algorithm>
+#include <cmath>
 #include <map>
+#include <type_traits>
 #include <mutex>
 
 namespace cactus_hip {
@@ -168,6 +171,370 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------ LDS-staged 16x16 tiling
+// v_mfma_i32_16x16x32_i8: lane l holds A[l % 16][8 (l / 16) .. +8) and
+// B[8 (l / 16) .. +8)[l % 16] (8 bytes each); result register i of lane l is
+// C[4 (l / 16) + i][l % 16].  One instruction covers one 32-k chunk of a
+// 16x16 output tile, so an output tile costs 8 VALU instructions per group
+// (4 converts + 4 FMAs) against one MFMA: the epilogue, not the matrix core,
+// sets the pace, and the tiling is chosen to keep every SIMD's VALU busy.
+//
+// Workgroup = WGM x WGN waves, each WM x WN outputs.  A single wave issues
+// at most one VALU instruction per ~7 cycles on gfx950, so the epilogue only
+// reaches the SIMD's rate with two or more waves per SIMD.
+// The K loop runs over stages of SG 32-k chunks.  A stage holds, for each of
+// the workgroup's BM rows of A and BN columns of B, that row's SG * 32 (INT4:
+// SG * 16) contiguous bytes, moved by global_load_lds_dwordx4 with
+// consecutive lanes on consecutive 16-byte pieces of one row (whole cache
+// lines per 8 lanes), and each column's GPS group scales (global_load_lds_dword).
+// NS stages form a ring; loads run NS - 1 stages ahead of the MFMAs.
+// In LDS a row is [pieces][16 B] with piece p stored in slot p ^ (row & 7)
+// (INT4 columns of 4 pieces: p ^ (col & 3)), so the 16 rows one operand read
+// spans land on distinct banks; scales are [col][GPS] fp16.
+template <bool INT4, int WM_, int WN_, int WGM_, int WGN_, int KSUB_>
+struct LdsCfg {
+    static constexpr int WM = WM_, WN = WN_, WGM = WGM_, WGN = WGN_, KSUB = KSUB_;
+    static constexpr int NW = WGM * WGN, NT = 64 * NW;  // waves, threads
+    static constexpr int BM = WGM * WM, BN = WGN * WN;
+    static constexpr int TM = WM / 16, TN = WN / 16;
+    static constexpr int SG = KSUB == 4 ? 8 : 4;        // chunks per stage: an even number of groups
+    static constexpr int GPS = SG / KSUB;               // groups per stage (2 or 4)
+    static constexpr int PA = SG * 2;                   // 16-byte pieces per A row and stage
+    static constexpr int PB = INT4 ? SG : SG * 2;       // per B column and stage
+    static constexpr int BMASK = PB >= 8 ? 7 : 3;       // B piece swizzle
+    static constexpr int NBJ = INT4 ? SG : 4;           // precomputed B read offsets per tile
+    static constexpr int A_U = BM * PA;                 // 16-byte units of A per stage
+    static constexpr int U = A_U + BN * PB;
+    static constexpr int NI = (U + NT - 1) / NT;        // 16-byte DMA instructions per wave per stage
+    static constexpr int OPND = NI * NW * 1024;         // operand bytes per ring slot (padded)
+    static constexpr int SC_U = BN * GPS / 2;           // dword units of scales per stage
+    static constexpr int NSI = (SC_U + NT - 1) / NT;    // dword DMA instructions per wave per stage
+    static constexpr int STAGE = OPND + NSI * NW * 256; // bytes per ring slot
+    static constexpr int VM_STAGE = NI + NSI;           // vmcnt per stage and wave
+    static constexpr int NS = 3;
+    static constexpr int CSTEP_B = INT4 ? 16 : 32;      // B bytes per chunk and column
+    static_assert(WM % 16 == 0 && WN % 16 == 0 && NW <= 16, "tile");
+    static_assert(GPS % 2 == 0, "accumulator parity is static within a stage");
+    static_assert(BM * BN * 2 <= STAGE, "output transpose fits one ring slot");
+    static_assert(VM_STAGE <= 31, "vmcnt range");
+};
+
+template <class C, bool INT4>
+__global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int K = a.K, N = a.N, M = a.M;
+    const int NK = K / 32, G = NK / C::KSUB, NSTAGE = NK / C::SG;
+    const int mb = blockIdx.y * C::BM, nb = blockIdx.x * C::BN;
+    const int wm = wv / C::WGN, wn = wv % C::WGN;
+    const size_t brow = INT4 ? (size_t)K / 2 : (size_t)K;
+    const int q = lane >> 4, l16 = lane & 15;
+
+    // row scales of this lane's output rows, fetched up front
+    float as[C::TM][4];
+#pragma unroll
+    for (int x = 0; x < C::TM; x++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) as[x][e] = a.As[min(mb + wm * C::WM + x * 16 + 4 * q + e, M - 1)];
+
+    // DMA sources: 16-byte instruction i of this wave moves unit u = (wv + NW i) * 64 + lane,
+    // dword instruction i moves scale unit v = (wv + NW i) * 64 + lane
+    const uint8_t* src[C::NI];
+    uint32_t inc[C::NI];
+#pragma unroll
+    for (int i = 0; i < C::NI; i++) {
+        const int u = (wv + C::NW * i) * 64 + lane;
+        src[i] = reinterpret_cast<const uint8_t*>(a.A);
+        inc[i] = 0;
+        if (u < C::A_U) {
+            const int row = u / C::PA, p = (u % C::PA) ^ (row & 7);
+            src[i] = reinterpret_cast<const uint8_t*>(a.A) + (size_t)min(mb + row, M - 1) * K + p * 16;
+            inc[i] = C::SG * 32;
+        } else if (u < C::U) {
+            const int u2 = u - C::A_U;
+            const int col = u2 / C::PB, p = (u2 % C::PB) ^ (col & C::BMASK);
+            src[i] = a.B + (size_t)min(nb + col, N - 1) * brow + p * 16;
+            inc[i] = C::SG * C::CSTEP_B;
+        }
+    }
+    const uint16_t* ssrc[C::NSI];
+    uint32_t sinc[C::NSI];
+#pragma unroll
+    for (int i = 0; i < C::NSI; i++) {
+        const int v = (wv + C::NW * i) * 64 + lane;
+        ssrc[i] = a.Bs;
+        sinc[i] = 0;
+        if (v < C::SC_U) {
+            const int col = v / (C::GPS / 2), d = v % (C::GPS / 2);
+            ssrc[i] = a.Bs + (size_t)min(nb + col, N - 1) * G + 2 * d;
+            sinc[i] = C::GPS;
+        }
+    }
+    const uint32_t ring = (uint32_t)(uintptr_t)smem;
+    auto issue = [&](int s, int slot) {
+        const uint32_t base = ring + (uint32_t)(slot * C::STAGE);
+#pragma unroll
+        for (int i = 0; i < C::NI; i++)
+            lds_dma<16>(src[i] + (size_t)s * inc[i], base + (uint32_t)((wv + C::NW * i) * 1024));
+#pragma unroll
+        for (int i = 0; i < C::NSI; i++)
+            lds_dma<4>(ssrc[i] + (size_t)s * sinc[i], base + (uint32_t)(C::OPND + (wv + C::NW * i) * 256));
+    };
+#pragma unroll
+    for (int s = 0; s < C::NS - 1; s++)
+        if (s < NSTAGE) issue(s, s);
+
+    // operand read offsets within a stage (bytes): A / INT8 B piece
+    // p = 2 j + (q >> 1) of row r sits at slot p ^ (r & 7), i.e. at
+    // 128 (j >> 2) + 32 ((j & 3) ^ ((r >> 1) & 3)) + 16 ((q >> 1) ^ (r & 1))
+    uint32_t ao[C::TM][4], bo[C::TN][C::NBJ], so[C::TN];
+#pragma unroll
+    for (int t = 0; t < C::TM; t++) {
+        const int r = wm * C::WM + t * 16 + l16;
+#pragma unroll
+        for (int m = 0; m < 4; m++)
+            ao[t][m] = (uint32_t)(r * C::PA * 16 + 32 * (m ^ ((r >> 1) & 3)) + 16 * ((q >> 1) ^ (r & 1)) + 8 * (q & 1));
+    }
+#pragma unroll
+    for (int t = 0; t < C::TN; t++) {
+        const int c = wn * C::WN + t * 16 + l16;
+        const uint32_t cb = (uint32_t)(C::A_U * 16 + c * C::PB * 16);
+#pragma unroll
+        for (int m = 0; m < C::NBJ; m++)
+            bo[t][m] = INT4 ? cb + 16 * (m ^ (c & C::BMASK)) + 4 * q
+                            : cb + 32 * (m ^ ((c >> 1) & 3)) + 16 * ((q >> 1) ^ (c & 1)) + 8 * (q & 1);
+        so[t] = (uint32_t)(C::OPND + c * C::GPS * 2);
+    }
+
+    float r[C::TM][C::TN][4];
+#pragma unroll
+    for (int x = 0; x < C::TM; x++)
+#pragma unroll
+        for (int y = 0; y < C::TN; y++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) r[x][y][e] = 0.0f;
+    i32x4 acc[2][C::TM][C::TN];
+    // this stage's and the previous stage's group scales (fp16 pairs)
+    uint32_t scw[2][C::TN][C::GPS / 2];
+
+    struct Frag {
+        long fa[C::TM];
+        long fb[C::TN];
+    };
+    auto read = [&](const uint8_t* stage, int j, Frag& f) {
+#pragma unroll
+        for (int t = 0; t < C::TM; t++)
+            f.fa[t] = *reinterpret_cast<const long*>(stage + ao[t][j & 3] + 128 * (j >> 2));
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            if constexpr (INT4) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(stage + bo[t][j]);
+                const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+                const uint32_t x0 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                const uint32_t x1 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+                f.fb[t] = (long)(((uint64_t)x1 << 32) | x0);
+            } else {
+                f.fb[t] = *reinterpret_cast<const long*>(stage + bo[t][j & 3] + 128 * (j >> 2));
+            }
+        }
+    };
+    auto read_scales = [&](const uint8_t* stage, int sb) {
+#pragma unroll
+        for (int t = 0; t < C::TN; t++) {
+            if constexpr (C::GPS == 4) {
+                const uint2 w = *reinterpret_cast<const uint2*>(stage + so[t]);
+                scw[sb][t][0] = w.x;
+                scw[sb][t][1] = w.y;
+            } else {
+                scw[sb][t][0] = *reinterpret_cast<const uint32_t*>(stage + so[t]);
+            }
+        }
+    };
+    // r = fma((float)acc, Bs, r) per output; for INT4 the MFMA sums are 16 acc
+    // and r carries 16 r (exact: power-of-two scaling), undone at the store
+    auto epilogue = [&](int buf, int sb, int gl) {
+#pragma unroll
+        for (int y = 0; y < C::TN; y++) {
+            const uint32_t w = scw[sb][y][gl >> 1];
+            const float sc = h2f((uint16_t)((gl & 1) ? (w >> 16) : (w & 0xFFFFu)));
+#pragma unroll
+            for (int x = 0; x < C::TM; x++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) r[x][y][e] = __builtin_fmaf((float)acc[buf][x][y][e], sc, r[x][y][e]);
+        }
+    };
+
+    // one stage; the ring slot is a compile-time constant so the LDS offsets
+    // fold into the read instructions
+    auto stage = [&](auto slotc, int s) {
+        constexpr int SL = decltype(slotc)::value;
+        constexpr int SB = SL & 1;   // scale register set of this stage (ring of two)
+        static_assert(SL < 2 * C::NS, "slot index");
+        if (s + 1 < NSTAGE) wait_dma<C::VM_STAGE>();
+        else wait_dma<0>();
+        lds_barrier();
+        if (s + C::NS - 1 < NSTAGE) issue(s + C::NS - 1, (SL + C::NS - 1) % C::NS);
+        const uint8_t* st = smem + (SL % C::NS) * C::STAGE;
+        Frag f[2];
+        read(st, 0, f[0]);
+        read_scales(st, SB);
+#pragma unroll
+        for (int j = 0; j < C::SG; j++) {
+            if (j + 1 < C::SG) read(st, j + 1, f[(j + 1) & 1]);
+            const int gl = j / C::KSUB, buf = gl & 1;
+            const bool first = (j % C::KSUB) == 0;
+#pragma unroll
+            for (int x = 0; x < C::TM; x++)
+#pragma unroll
+                for (int y = 0; y < C::TN; y++)
+                    acc[buf][x][y] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                        f[j & 1].fa[x], f[j & 1].fb[y], first ? (i32x4){0, 0, 0, 0} : acc[buf][x][y], 0, 0, 0);
+            // the previous group's epilogue runs behind this chunk's MFMAs
+            if (first) {
+                if (j == 0) {
+                    if (s > 0) epilogue(1, SB ^ 1, C::GPS - 1);
+                } else {
+                    epilogue(buf ^ 1, SB, gl - 1);
+                }
+            }
+        }
+    };
+    // the ring has 3 slots but the scale registers alternate by stage parity:
+    // unroll by 6 so both are compile-time
+    static_assert(C::NS == 3, "stage loop unrolled by the ring depth");
+    for (int s = 0; s < NSTAGE; s += 6) {
+        stage(std::integral_constant<int, 0>{}, s);
+        if (s + 1 < NSTAGE) stage(std::integral_constant<int, 1>{}, s + 1);
+        if (s + 2 < NSTAGE) stage(std::integral_constant<int, 2>{}, s + 2);
+        if (s + 3 < NSTAGE) stage(std::integral_constant<int, 3>{}, s + 3);
+        if (s + 4 < NSTAGE) stage(std::integral_constant<int, 4>{}, s + 4);
+        if (s + 5 < NSTAGE) stage(std::integral_constant<int, 5>{}, s + 5);
+    }
+    epilogue(1, (NSTAGE - 1) & 1, C::GPS - 1);
+
+    // store: fp16(r * As) into a wave-private 16x16 block per tile in a ring
+    // slot no wave reads any more ((NSTAGE + 1) % 3: consumed before the last
+    // stage's barrier, or never filled), then 16-byte rows to global memory
+    const float post = INT4 ? 0.0625f : 1.0f;
+    uint16_t* ob = reinterpret_cast<uint16_t*>(smem + ((NSTAGE + 1) % C::NS) * C::STAGE) +
+                   wv * (C::TM * C::TN * 256);
+#pragma unroll
+    for (int x = 0; x < C::TM; x++)
+#pragma unroll
+        for (int y = 0; y < C::TN; y++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                ob[(x * C::TN + y) * 256 + (4 * q + e) * 16 + l16] = f2h((r[x][y][e] * post) * as[x][e]);
+    const bool vec_ok = (N & 7) == 0 && ((uintptr_t)a.C & 15) == 0;
+    // lane -> (tile, row, half): 32 lanes per tile
+#pragma unroll
+    for (int t0 = 0; t0 < C::TM * C::TN; t0 += 2) {
+        const int t = t0 + (lane >> 5);
+        if (t < C::TM * C::TN) {
+            const int x = t / C::TN, y = t % C::TN;
+            const int rr = (lane >> 1) & 15, hh = lane & 1;
+            const uint4 v = *reinterpret_cast<const uint4*>(ob + t * 256 + rr * 16 + hh * 8);
+            const int row = mb + wm * C::WM + x * 16 + rr;
+            const int col = nb + wn * C::WN + y * 16 + hh * 8;
+            if (row < M) {
+                uint16_t* dst = a.C + (size_t)row * N + col;
+                if (vec_ok && col + 8 <= N) {
+                    *reinterpret_cast<uint4*>(dst) = v;
+                } else {
+                    const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+#pragma unroll
+                    for (int i = 0; i < 8; i++)
+                        if (col + i < N) dst[i] = h[i];
+                }
+            }
+        }
+    }
+}
+
+template <class C>
+static size_t lds_bytes() {
+    return (size_t)C::NS * C::STAGE;
+}
+
+template <bool INT4, int WM, int WN, int WGM, int WGN, int KSUB>
+static bool launch_lds(const GemmArgs& a, hipStream_t st) {
+    using C = LdsCfg<INT4, WM, WN, WGM, WGN, KSUB>;
+    if ((a.K / 32) % C::SG != 0) return false;
+    const size_t lds = lds_bytes<C>();
+    if (lds > 160 * 1024) return false;
+    if (lds > 64 * 1024) {
+        static std::once_flag once;
+        std::call_once(once, [] {
+            (void)hipFuncSetAttribute((const void*)gemm_lds_kernel<C, INT4>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        });
+    }
+    const dim3 grid(ceil_div(a.N, C::BN), ceil_div(a.M, C::BM));
+    hipLaunchKernelGGL((gemm_lds_kernel<C, INT4>), grid, dim3(C::NT), lds, st, a);
+    return true;
+}
+
+// Workgroup tiles (wave tile, wave grid).  Each is scored by a rough time
+// model: per CU, max(VALU cycles, DMA cycles) times the workgroups it runs
+// in turn.  VALU: 2 instructions per output and group at ~7 cycles per
+// instruction for one wave per SIMD, ~3.5 for two, ~2.4 for three; DMA: ~20
+// bytes per cycle and CU (both measured on MI355X).
+struct TileChoice {
+    int wm, wn, wgm, wgn;
+};
+static constexpr TileChoice kTiles[] = {
+    {16, 16, 1, 4},   // 16 x 64, 4 waves
+    {16, 16, 2, 2},   // 32 x 32, 4 waves
+    {16, 48, 4, 2},   // 64 x 96, 8 waves
+    {16, 32, 4, 2},   // 64 x 64, 8 waves
+    {32, 32, 2, 4},   // 64 x 128, 8 waves
+    {16, 32, 4, 3},   // 64 x 96, 12 waves
+};
+static int pick_tile(const GemmArgs& a, bool int4) {
+    constexpr double kCUs = 256.0;
+    int best = 0;
+    double best_t = 1e300;
+    for (int i = 0; i < (int)(sizeof(kTiles) / sizeof(kTiles[0])); i++) {
+        const TileChoice& t = kTiles[i];
+        const int nw = t.wgm * t.wgn, bm = t.wm * t.wgm, bn = t.wn * t.wgn;
+        const double wgs = (double)ceil_div(a.M, bm) * ceil_div(a.N, bn);
+        const double rounds = std::ceil(wgs / kCUs);
+        const double waves_per_simd = nw / 4.0;
+        const double cyc_per_instr = waves_per_simd >= 3 ? 2.4 : waves_per_simd >= 2 ? 3.5 : 7.0;
+        const double valu = (double)bm * bn * (a.K / a.gs) * 2.0 / 64.0 / 4.0 * cyc_per_instr;
+        const double dma = (double)(bm + (int4 ? bn / 2.0 : bn)) * a.K / 20.0;
+        const double tt = rounds * std::max(valu, dma);
+        if (tt < best_t * 0.999) {
+            best_t = tt;
+            best = i;
+        }
+    }
+    return best;
+}
+
+template <bool INT4, int KSUB>
+static bool launch_lds_ksub(const GemmArgs& a, hipStream_t st) {
+    switch (pick_tile(a, INT4)) {
+        case 0: return launch_lds<INT4, 16, 16, 1, 4, KSUB>(a, st);
+        case 1: return launch_lds<INT4, 16, 16, 2, 2, KSUB>(a, st);
+        case 2: return launch_lds<INT4, 16, 48, 4, 2, KSUB>(a, st);
+        case 3: return launch_lds<INT4, 16, 32, 4, 2, KSUB>(a, st);
+        case 4: return launch_lds<INT4, 32, 32, 2, 4, KSUB>(a, st);
+        default: return launch_lds<INT4, 16, 32, 4, 3, KSUB>(a, st);
+    }
+}
+
+template <bool INT4>
+static bool launch_lds_any(const GemmArgs& a, hipStream_t st) {
+    switch (a.gs / 32) {
+        case 1: return launch_lds_ksub<INT4, 1>(a, st);
+        case 2: return launch_lds_ksub<INT4, 2>(a, st);
+        case 4: return launch_lds_ksub<INT4, 4>(a, st);
+        default: return false;
+    }
+}
+
 // ------------------------------------------------ activation scratch
 struct GemmScratch {
     void* ptr = nullptr;
@@ -221,7 +588,13 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
         Asc = s;
     }
     GemmArgs a{Aq, Asc, B, Bs, C, (int)M, (int)K, (int)N, (int)gs};
-    // two MFMA tiles per wave when the grid still fills the GPU
+    // the LDS path moves group scales as dwords
+    const bool scales4 = ((uintptr_t)Bs & 3) == 0;
+    if (scales4 && (int4 ? launch_lds_any<true>(a, st) : launch_lds_any<false>(a, st))) {
+        *handled = true;
+        return check_launch("grouped matmul (mfma, lds)");
+    }
+    // register-streamed fallback: two MFMA tiles per wave when the grid still fills the GPU
     const size_t mblk = ceil_div(M, 64);
     const bool wide = mblk * ceil_div(N, 128) >= 512;
     const dim3 grid((unsigned)ceil_div(N, wide ? 128 : 64), (unsigned)mblk);

@@ -181,6 +181,30 @@ __device__ __forceinline__ float poly_exp_weight(float s, float bm) {
     return y * exp2_bits(xi);
 }
 
+// --------------------------------------------------------- LDS DMA (gfx950)
+// global_load_lds_dword(x4): every active lane moves DW bytes from its own
+// global address to LDS at lds_addr + lane * DW.  lds_addr must be uniform over
+// the wave.  Completion is counted by vmcnt.
+template <int DW>
+__device__ __forceinline__ void lds_dma(const void* src, uint32_t lds_addr) {
+    // M0 takes a scalar: the destination is uniform over the wave
+    const uint32_t lds = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr);
+    if constexpr (DW == 16)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(lds)
+                     : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// workgroup barrier that orders LDS only (outstanding DMA keeps flying)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
