@@ -1145,6 +1145,241 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
     }
 }
 
+// ------------------------------------------------ kernel B, decode form
+// Decode form of the product-tile kernel: a workgroup is one chain wave and
+// NP stage waves.  The chain wave owns NH query heads of one KV head and DR
+// 16-dim sub-slices (16-lane row r -> head r % NH, sub-slice r / NH); the
+// heads share the product rows and the DPP row broadcast gives each row its
+// own head's weights.  Stage waves move the tiles (LDS DMA, D - 1 tiles
+// ahead; a single wave issues LDS DMA too slowly to feed a chain) and compute
+// the rows' block corrections.  The chain wave reads tile t + 1 into
+// registers while tile t's chain runs: between barriers it only issues LDS
+// reads and chain steps (~9.5 cycles each on gfx950).
+template <int NH, int DR, int NP>
+struct PairCfg {
+    static constexpr int SW = 16 * DR;                       // dims per workgroup
+    static constexpr int LANES = 16 * NH * DR;               // chain lanes
+    static constexpr int PB = SW * SH_PS * 4;                // product bytes per tile
+    static constexpr int NPC = (PB + 1023) / 1024;           // product DMA instructions per tile
+    static constexpr int W_OFF = PB;
+    static constexpr int SLOT = PB + NH * CD_T * 4;
+    static constexpr int NPT = NPC + 1;                      // DMA instructions per tile (+ weights)
+    static constexpr int PER = NPT / NP;                     // per stage wave and tile
+    static_assert(LANES <= 64 && PB % 16 == 0, "pair layout");
+    static_assert(NPT % NP == 0 && NH <= NP, "stage waves share the DMA evenly");
+};
+
+// s_waitcnt lgkmcnt(0) + s_barrier as compiler-visible instructions, so the
+// compiler's own wait tracking knows every LDS read before it has completed
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
+    __builtin_amdgcn_s_barrier();
+}
+
+template <int D, int NH, int DR, int NP>
+__global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs a_in, int nbmax) {
+    using C = PairCfg<NH, DR, NP>;
+    const AttnArgs a = resolve(a_in);
+    extern __shared__ __align__(16) unsigned char smem[];
+    unsigned char* ring = smem;                                             // [D][SLOT]
+    float* corr_s = reinterpret_cast<float*>(smem + D * C::SLOT);           // [NH][nbmax]
+    float* bsum_s = corr_s + (size_t)NH * nbmax;
+    int* fast_s = reinterpret_cast<int*>(bsum_s + (size_t)NH * nbmax);     // [nbmax]: tile t on the fast path
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const bool is_chain = wv == 0;
+    const int pw = wv - 1;                                    // stage wave index
+    const int d = a.d, da = (d / 8) * 8;
+    const int nsl = (d + C::SW - 1) / C::SW;
+    const int nsl64 = (d + 63) / 64;
+    const int ngh = a.gq / NH;
+    size_t g = blockIdx.x;
+    const int sl = (int)(g % nsl);
+    g /= nsl;
+    const int hg = (int)(g % ngh);
+    g /= ngh;
+    const int kvh = (int)(g % a.Hkv);
+    g /= a.Hkv;
+    const int qp = (int)(g % a.S);
+    const size_t b = g / a.S;
+
+    const int r16 = lane >> 4, lr = lane & 15;
+    const int hj = r16 % NH;                                  // chain lane's head within the group
+    const bool dlane = is_chain && lane < C::LANES;
+    const int dim = sl * C::SW + (r16 / NH) * 16 + lr;
+    const size_t row0 = (b * a.S + qp) * a.Hq + (size_t)kvh * a.gq + hg * NH;
+    const size_t row = row0 + hj;
+
+    size_t rks, rke, rbl;
+    kv_range<true>(a, (size_t)qp, rks, rke, rbl);
+    const int nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
+    size_t kneed = rks;
+    if (rke > rks) {
+        kneed = rks + (size_t)nb * ATT_BLOCK;
+        if (kneed > rbl) kneed = rbl;
+    }
+    const size_t kt_end = kneed < a.cache_len ? kneed : (size_t)a.cache_len;
+    const int nst = kt_end > 0 ? (int)((kt_end + CD_T - 1) / CD_T) : 0;
+    const int nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
+
+    // stage wave pw moves DMA units u = pw + NP i of each tile: units below
+    // NPC are 1 KB product chunks, unit NPC the NH weight rows (16 lanes x
+    // 16 bytes each)
+    const char* psrc = reinterpret_cast<const char*>(a.vsh) +
+                       (((b * a.Hkv + kvh) * nsl64 + (sl * C::SW) / 64) * a.sh_ntile) * (size_t)SH_TILE_B +
+                       (size_t)((sl * C::SW) % 64) * SH_PS * 4 + lane * 16;
+    const float* wsrc = a.w + (row0 + min(lane >> 4, NH - 1)) * a.wstride + lr * 4;
+    auto issue = [&](int t) {
+        const uint32_t slot = ring_lds + (uint32_t)((t % D) * C::SLOT);
+#pragma unroll
+        for (int i = 0; i < C::PER; i++) {
+            const int u = pw + NP * i;
+            if (u < C::NPC) {
+                if (u * 1024 + lane * 16 < C::PB)
+                    lds_dma<16>(psrc + (size_t)t * SH_TILE_B + u * 1024, slot + u * 1024);
+            } else if (lane < 16 * NH) {
+                lds_dma<16>(wsrc + (size_t)t * CD_T, slot + C::W_OFF);
+            }
+        }
+    };
+    // this stage wave's DMA for tile t complete, younger tiles may fly:
+    // issued so far min(last, nst - 1) with last = t_issued
+    auto wait_landed = [&](int t, int last_issued) {
+        const int younger = min(last_issued, nst - 1) - t;
+        if (younger <= 0) wait_dma<0>();
+        else if (younger >= D - 2) wait_dma<(D - 2) * C::PER>();
+        else {
+            switch (younger) {
+                case 5: wait_dma<5 * C::PER>(); break;
+                case 4: wait_dma<4 * C::PER>(); break;
+                case 3: wait_dma<3 * C::PER>(); break;
+                case 2: wait_dma<2 * C::PER>(); break;
+                default: wait_dma<1 * C::PER>(); break;
+            }
+        }
+    };
+    static_assert(D <= 8, "wait counts above cover younger <= 6");
+
+    // ---- prologue: stage waves start the ring and compute the rows' block
+    // corrections and which tiles take the fast path; the chain wave fetches
+    // the first new row
+    float pf_p = 0.0f, pf_w = 0.0f;
+    const bool pf = a.cache_len < rke;
+    if (!is_chain) {
+        for (int t = 0; t < D - 1; t++)
+            if (t < nst) issue(t);
+        if (pw < NH) chain_corr(a, row0 + pw, nb, corr_s + pw * nbmax, bsum_s + pw * nbmax);
+    } else if (pf && dlane) {
+        pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
+        if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
+    }
+    lds_sync();
+    if (!is_chain) {
+        // tile t is fast when both its blocks lie inside the tile and no head
+        // has a zero weight in them (flag: sign of the block sum)
+        if (pw == 0) {
+            for (int t = lane; t < nst; t += 64) {
+                const int b0 = t * (CD_T / ATT_BLOCK);
+                bool f = b0 + 2 <= nb_tile && rks + (size_t)(b0 + 2) * ATT_BLOCK <= rbl;
+                for (int j = 0; j < NH && f; j++)
+                    f = !__builtin_signbit(bsum_s[j * nbmax + b0]) && !__builtin_signbit(bsum_s[j * nbmax + b0 + 1]);
+                fast_s[t] = f ? 1 : 0;
+            }
+        }
+        if (nst > 1) wait_landed(1, D - 2);
+        else if (nst > 0) wait_landed(0, D - 2);
+    }
+    lds_sync();
+    const float* cw = corr_s + hj * nbmax;
+    const float* cb = bsum_s + hj * nbmax;
+
+    float acc = 0.0f, rs = 0.0f;
+    // per tile: 64 products, 4 row-replicated weight registers (the DPP row
+    // broadcast gives every step its weight), the two blocks' {corr, corr,
+    // sum, sum} and the fast-path flag.  Tile t + 1 is read while t chains.
+    float pv[2][64], wq[2][4], mt[2][4];
+    int fl[2];
+    const int prow = (r16 / NH) * 16 + lr;                    // product row within the slot
+    auto read_tile = [&](int t, float* p, float* w, float* m, int& f) {
+        const unsigned char* slot = ring + (t % D) * C::SLOT;
+        const float* pt = reinterpret_cast<const float*>(slot) + prow * SH_PS;
+        const float* wt = reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const float4 v = *reinterpret_cast<const float4*>(pt + 4 * q);
+            p[4 * q] = v.x;
+            p[4 * q + 1] = v.y;
+            p[4 * q + 2] = v.z;
+            p[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) w[q] = wt[16 * q + lr];
+        const int i0 = min(t * (CD_T / ATT_BLOCK), nbmax - 1), i1 = min(t * (CD_T / ATT_BLOCK) + 1, nbmax - 1);
+        m[0] = cw[i0];
+        m[1] = cw[i1];
+        m[2] = cb[i0];
+        m[3] = cb[i1];
+        f = fast_s[t];
+    };
+    auto chain_regs = [&](int t, const float* p, const float* w, const float* m, int f) {
+        const float NEG_INF = -__builtin_inff();
+        if (__builtin_amdgcn_readfirstlane(f)) {
+            // both blocks inside the tile and free of zero weights
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float c = m[h];
+                if (c != NEG_INF) {
+                    acc = acc * c;
+                    rs = rs * c;
+                }
+                chain16(acc, p + 32 * h, w[2 * h], std::make_integer_sequence<int, 16>{});
+                chain16(acc, p + 32 * h + 16, w[2 * h + 1], std::make_integer_sequence<int, 16>{});
+                rs = rs + m[2 + h];
+            }
+        } else if (dlane) {
+            const unsigned char* slot = ring + (t % D) * C::SLOT;
+            const int b0 = t * (CD_T / ATT_BLOCK);
+            chain_tile(reinterpret_cast<const float*>(slot) + prow * SH_PS,
+                       reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, b0,
+                       min(nb_tile, b0 + CD_T / ATT_BLOCK), rks, rbl, cw, cb, acc, rs);
+        }
+    };
+
+    if (is_chain && nst > 0) read_tile(0, pv[0], wq[0], mt[0], fl[0]);
+    // unrolled by two so the chain wave's register buffers are static
+    for (int t = 0; t < nst; t += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int tt = t + u;
+            if (tt < nst) {
+                if (is_chain) {
+                    // next tile (the last re-reads itself: its slot stays intact)
+                    read_tile(min(tt + 1, nst - 1), pv[u ^ 1], wq[u ^ 1], mt[u ^ 1], fl[u ^ 1]);
+                    chain_regs(tt, pv[u], wq[u], mt[u], fl[u]);
+                } else {
+                    // slot of tile tt - 1: its last reader finished before the
+                    // previous barrier
+                    if (tt + D - 1 < nst) issue(tt + D - 1);
+                    if (tt + 2 < nst) wait_landed(tt + 2, tt + D - 1);
+                }
+                lds_sync();
+            }
+        }
+    }
+    if (!dlane) return;
+    const int tl = nst > 0 ? nst - 1 : 0;
+    const unsigned char* slot = ring + (tl % D) * C::SLOT;
+    chain_tail<true>(a, b, kvh, dim, row, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
+                     reinterpret_cast<const float*>(slot) + prow * SH_PS,
+                     reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, pf, pf_p, pf_w, cw, cb, acc, rs);
+    if (dim < d) {
+        uint16_t* ov = a.o + row * (size_t)d;
+        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
+        else ov[dim] = f2h(acc * (1.0f / rs));
+    }
+}
+
 // ------------------------------------------------ per-(device, stream) scratch
 struct AttnScratch {
     void* ptr = nullptr;
@@ -1224,6 +1459,24 @@ static int launch_attention(AttnArgs a, void* stream) {
     if (qpg < 1) qpg = 1;
     const int nbmax = a.nbstride;
     const size_t nsl = (size_t)(a.d + 63) / 64;
+    if (HYBRID && a.vsh && (size_t)a.B * a.S <= 2) {
+        // decode: one chain wave and three stage waves per workgroup, two heads
+        // per chain wave when the query-head group splits evenly
+        constexpr int SD = 8;
+        const bool two = a.gq % 2 == 0;
+        const size_t slot = two ? PairCfg<2, 1, 3>::SLOT : PairCfg<1, 1, 3>::SLOT;
+        const size_t smem = SD * slot + (2 * (size_t)(two ? 2 : 1) + 1) * nbmax * sizeof(float);
+        if (smem <= 64 * 1024) {
+            const size_t groups = (size_t)a.B * a.S * a.Hkv * (a.gq / (two ? 2 : 1)) * ((a.d + 15) / 16);
+            if (two)
+                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 2, 1, 3>), dim3((unsigned)groups), dim3(256), smem,
+                                   as_stream(stream), a, nbmax);
+            else
+                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 1, 1, 3>), dim3((unsigned)groups), dim3(256), smem,
+                                   as_stream(stream), a, nbmax);
+            return check_launch("attention values (decode)");
+        }
+    }
     if (HYBRID && a.vsh && a.gq <= SH_MAX_CHAINS) {
         // product tiles: ring depth 8, or 5 where the rows' block data needs
         // the room

@@ -191,7 +191,7 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(GemmArgs a) {
 // In LDS a row is [pieces][16 B] with piece p stored in slot p ^ (row & 7)
 // (INT4 columns of 4 pieces: p ^ (col & 3)), so the 16 rows one operand read
 // spans land on distinct banks; scales are [col][GPS] fp16.
-template <bool INT4, int WM_, int WN_, int WGM_, int WGN_, int KSUB_>
+template <bool INT4, int WM_, int WN_, int WGM_, int WGN_, int KSUB_, int NS_ = 3>
 struct LdsCfg {
     static constexpr int WM = WM_, WN = WN_, WGM = WGM_, WGN = WGN_, KSUB = KSUB_;
     static constexpr int NW = WGM * WGN, NT = 64 * NW;  // waves, threads
@@ -211,13 +211,20 @@ struct LdsCfg {
     static constexpr int NSI = (SC_U + NT - 1) / NT;    // dword DMA instructions per wave per stage
     static constexpr int STAGE = OPND + NSI * NW * 256; // bytes per ring slot
     static constexpr int VM_STAGE = NI + NSI;           // vmcnt per stage and wave
-    static constexpr int NS = 3;
+    static constexpr int NS = NS_;                      // ring slots
+    static constexpr int UNR = NS % 2 == 0 ? NS : 2 * NS;   // stage loop unroll: slot and scale parity static
     static constexpr int CSTEP_B = INT4 ? 16 : 32;      // B bytes per chunk and column
     static_assert(WM % 16 == 0 && WN % 16 == 0 && NW <= 16, "tile");
     static_assert(GPS % 2 == 0, "accumulator parity is static within a stage");
     static_assert(BM * BN * 2 <= STAGE, "output transpose fits one ring slot");
-    static_assert(VM_STAGE <= 31, "vmcnt range");
+    static_assert(VM_STAGE * (NS - 2) <= 63, "vmcnt range");
+    static_assert(NS == 3 || NS == 4, "ring of three or four slots");
 };
+
+template <int... I, class F>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
 
 template <class C, bool INT4>
 __global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
@@ -370,8 +377,11 @@ __global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
     auto stage = [&](auto slotc, int s) {
         constexpr int SL = decltype(slotc)::value;
         constexpr int SB = SL & 1;   // scale register set of this stage (ring of two)
-        static_assert(SL < 2 * C::NS, "slot index");
-        if (s + 1 < NSTAGE) wait_dma<C::VM_STAGE>();
+        static_assert(SL < C::UNR, "slot index");
+        // stage s landed once at most the younger stages s + 1 .. s + NS - 2 fly
+        const int younger = min(NSTAGE - 1 - s, C::NS - 2);
+        if (younger >= C::NS - 2) wait_dma<C::VM_STAGE * (C::NS - 2)>();
+        else if (younger == 1) wait_dma<C::VM_STAGE>();
         else wait_dma<0>();
         lds_barrier();
         if (s + C::NS - 1 < NSTAGE) issue(s + C::NS - 1, (SL + C::NS - 1) % C::NS);
@@ -400,24 +410,21 @@ __global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
             }
         }
     };
-    // the ring has 3 slots but the scale registers alternate by stage parity:
-    // unroll by 6 so both are compile-time
-    static_assert(C::NS == 3, "stage loop unrolled by the ring depth");
-    for (int s = 0; s < NSTAGE; s += 6) {
-        stage(std::integral_constant<int, 0>{}, s);
-        if (s + 1 < NSTAGE) stage(std::integral_constant<int, 1>{}, s + 1);
-        if (s + 2 < NSTAGE) stage(std::integral_constant<int, 2>{}, s + 2);
-        if (s + 3 < NSTAGE) stage(std::integral_constant<int, 3>{}, s + 3);
-        if (s + 4 < NSTAGE) stage(std::integral_constant<int, 4>{}, s + 4);
-        if (s + 5 < NSTAGE) stage(std::integral_constant<int, 5>{}, s + 5);
-    }
+    // ring slot (s % NS) and scale register set (s % 2) are compile-time
+    // constants in the unrolled body
+    for (int s = 0; s < NSTAGE; s += C::UNR)
+        static_for(std::make_integer_sequence<int, C::UNR>{}, [&](auto ic) {
+            constexpr int I = decltype(ic)::value;
+            if (s + I < NSTAGE) stage(ic, s + I);
+        });
     epilogue(1, (NSTAGE - 1) & 1, C::GPS - 1);
 
     // store: fp16(r * As) into a wave-private 16x16 block per tile in a ring
-    // slot no wave reads any more ((NSTAGE + 1) % 3: consumed before the last
-    // stage's barrier, or never filled), then 16-byte rows to global memory
+    // slot no wave reads any more (that of stage NSTAGE - 2, consumed before
+    // the last stage's barrier, or one never filled), then 16-byte rows to
+    // global memory
     const float post = INT4 ? 0.0625f : 1.0f;
-    uint16_t* ob = reinterpret_cast<uint16_t*>(smem + ((NSTAGE + 1) % C::NS) * C::STAGE) +
+    uint16_t* ob = reinterpret_cast<uint16_t*>(smem + ((NSTAGE + C::NS - 2) % C::NS) * C::STAGE) +
                    wv * (C::TM * C::TN * 256);
 #pragma unroll
     for (int x = 0; x < C::TM; x++)
@@ -476,8 +483,8 @@ static bool launch_lds(const GemmArgs& a, hipStream_t st) {
 }
 
 // Workgroup tiles (wave tile, wave grid).  Each is scored by a rough time
-// model: per CU, max(VALU cycles, DMA cycles) times the workgroups it runs
-// in turn.  VALU: 2 instructions per output and group at ~7 cycles per
+// model: per CU, max(VALU cycles, DMA cycles) plus a quarter of the other,
+// times the workgroups it runs in turn.  VALU: 2 instructions per output and group at ~7 cycles per
 // instruction for one wave per SIMD, ~3.5 for two, ~2.4 for three; DMA: ~20
 // bytes per cycle and CU (both measured on MI355X).
 struct TileChoice {
@@ -504,7 +511,8 @@ static int pick_tile(const GemmArgs& a, bool int4) {
         const double cyc_per_instr = waves_per_simd >= 3 ? 2.4 : waves_per_simd >= 2 ? 3.5 : 7.0;
         const double valu = (double)bm * bn * (a.K / a.gs) * 2.0 / 64.0 / 4.0 * cyc_per_instr;
         const double dma = (double)(bm + (int4 ? bn / 2.0 : bn)) * a.K / 20.0;
-        const double tt = rounds * std::max(valu, dma);
+        // the smaller of the two only partly overlaps the larger
+        const double tt = rounds * (std::max(valu, dma) + 0.25 * std::min(valu, dma));
         if (tt < best_t * 0.999) {
             best_t = tt;
             best = i;

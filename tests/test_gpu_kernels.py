@@ -353,13 +353,16 @@ def _shadow_ref(vc, vs, cap, d):
     return ref
 
 
-@pytest.mark.parametrize("cache,Hq,Hkv,d", [(4095, 16, 8, 128), (700, 4, 2, 64), (63, 8, 1, 128)])
+@pytest.mark.parametrize("cache,Hq,Hkv,d,qmul", [(4095, 16, 8, 128, 1.0), (700, 4, 2, 64, 1.0), (63, 8, 1, 128, 1.0),
+                                                (1000, 4, 4, 128, 1.0), (640, 8, 4, 128, 40.0)])
 @pytest.mark.parametrize("shadow", [True, False])
-def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, shadow):
+def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, qmul, shadow):
     """The decode step's attention: cache length and position from the device
     state, INT8 cache of capacity cache + 37, optionally through the value
-    product tiles; equal to the hybrid attention with one new row."""
-    say("decode_attention", cache, Hq, Hkv, d, "shadow" if shadow else "int8")
+    product tiles; equal to the hybrid attention with one new row.  qmul
+    scales the query: at 40 the scores spread so far that weights underflow
+    to zero, which sends blocks through the zero-skipping path."""
+    say("decode_attention", cache, Hq, Hkv, d, qmul, "shadow" if shadow else "int8")
     rng = np.random.default_rng(cache + d)
     cap = cache + 37
     kf = f16(rng.normal(0, 1, (cap, Hkv, d)))
@@ -368,7 +371,7 @@ def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, shadow):
     vc, vs = orc.quantize_kv(vf)
     kn = f16(rng.normal(0, 1, (1, 1, Hkv, d)))
     vn = f16(rng.normal(0, 1, (1, 1, Hkv, d)))
-    q = f16(rng.normal(0, 1, (1, 1, Hq, d)))
+    q = f16(rng.normal(0, 1, (1, 1, Hq, d)) * qmul)
     scale = 1.0 / math.sqrt(d)
     ref = orc.attention_hybrid(q, kc[None, :cache], vc[None, :cache], ks[None, :cache], vs[None, :cache],
                                kn, vn, scale, pos_off=cache)
