@@ -5,6 +5,7 @@
 // mlp_up (RMSNorm + INT4 gate/up + SiLU*mul), down + residual.  Then the LM
 // head with the fused argmax advances the device step state.  Bit-identical
 // to decode mode 0 (the node-by-node graph).
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -28,7 +29,7 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     mlp_ = DevBuf(F * 2);
     max_steps_ = c.max_seq + 1;
     tokens_ = DevBuf(max_steps_ * 4);
-    const size_t blocks = (c.vocab + 255) / 256;
+    const size_t blocks = (c.vocab + 127) / 128;   // cactus_hip_decode_lm_head's scratch contract
     lm_scratch_ = DevBuf(256 + 8 * blocks);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
     check_hip(cactus_hip_rope_reserve(c.max_seq + 1, hd, c.rope_theta), "rope_reserve");
@@ -121,8 +122,18 @@ void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
         warmed_ = true;
         done = 1;
     }
-    if (done < n) ensure_graph();
-    for (; done < n; done++) check_hip(cactus_hip_graph_launch(graph_, m_.stream()), "graph launch");
+    // CACTUS_DECODE_EAGER=1 enqueues the step's kernels directly instead of
+    // replaying the graph (same kernels and results; for kernel tracers)
+    static const bool eager = [] {
+        const char* e = std::getenv("CACTUS_DECODE_EAGER");
+        return e && e[0] == '1';
+    }();
+    if (eager) {
+        for (; done < n; done++) enqueue();
+    } else {
+        if (done < n) ensure_graph();
+        for (; done < n; done++) check_hip(cactus_hip_graph_launch(graph_, m_.stream()), "graph launch");
+    }
     check_hip(cactus_hip_memcpy_d2h(out, tokens_.ptr, n * 4, m_.stream()), "tokens");
     kv.current_seq_len += n;
     kv.total_seq_len += n;

@@ -264,7 +264,7 @@ int cactus_hip_decode_attention(const uint16_t* q, const int8_t* k_cache, const 
                                 float scale, const uint32_t* state, size_t max_cache,
                                 const float* v_shadow, void* stream);
 /* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
- * and advances state.  scratch: >= 256 + 8 * ceil(N/256) bytes, zeroed once. */
+ * and advances state.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
                               const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
                               uint32_t* tokens_out, size_t max_steps, void* scratch,
