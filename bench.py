@@ -84,6 +84,86 @@ def bench_gemv(steps: int, warmup: int, R: int = 768):
     return {"gbs": gbs, "ms_per_step": ms / steps, "wall_s": wall, "R": R}
 
 
+INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense INT8 MFMA
+
+
+def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: int = 50, rounds: int = 5,
+               eager: bool = False):
+    """One grouped matmul (the reference's compute_matmul_node: FP16
+    activations quantized per row, then the INT8/INT4 grouped matmul; or the
+    matmul alone on pre-quantized activations), timed as a HIP graph of
+    `reps` launches replayed `rounds` times, so host call overhead stays
+    out of the per-call time."""
+    import cactus_amd as cm
+    from _data import f16
+    rng = np.random.default_rng(M + K + N)
+    A16 = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, (M, K))))
+    A8 = cm.DeviceBuffer.from_numpy(rng.integers(-127, 128, (M, K), dtype=np.int8))
+    As = cm.DeviceBuffer.from_numpy(np.abs(rng.normal(0, 0.01, M)).astype(np.float32))
+    if int4:
+        B = cm.DeviceBuffer.from_numpy(rng.integers(0, 256, (N, K // 2), dtype=np.uint8))
+    else:
+        B = cm.DeviceBuffer.from_numpy(rng.integers(-127, 128, (N, K), dtype=np.int8))
+    Bs = cm.DeviceBuffer.from_numpy(f16(np.abs(rng.normal(0, 0.02, (N, K // gs))) / 127.0))
+    C = cm.DeviceBuffer(M * N * 2)
+    st = cm.Stream()
+    name = "cactus_hip_matmul_int4" if int4 else "cactus_hip_matmul_int8"
+    if f16act:
+        def fn():
+            cm.call(name + "_f16act", A16.ptr, B.ptr, Bs.ptr, C.ptr, M, K, N, gs, st.handle)
+    else:
+        def fn():
+            cm.call(name, A8.ptr, As.ptr, B.ptr, Bs.ptr, C.ptr, M, K, N, gs, st.handle)
+    for _ in range(3):
+        fn()   # first call sizes the activation scratch outside the capture
+    st.sync()
+    if eager:
+        # direct launches (kernel tracers); the per-call time then includes
+        # host call overhead
+        e0, e1 = cm.Event(), cm.Event()
+        e0.record(st)
+        for _ in range(reps * rounds):
+            fn()
+        e1.record(st)
+        st.sync()
+        us = e0.elapsed_ms(e1) * 1e3 / (reps * rounds)
+        tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
+        return {"us_per_call": round(us, 2), "tops": round(tops, 1),
+                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4), "timing": "direct launches"}
+    cm.call("cactus_hip_graph_capture_begin", st.handle)
+    for _ in range(reps):
+        fn()
+    ge = ctypes.c_void_p()
+    cm.call("cactus_hip_graph_capture_end", st.handle, ctypes.byref(ge))
+    cm.call("cactus_hip_graph_launch", ge, st.handle)
+    st.sync()
+    e0, e1 = cm.Event(), cm.Event()
+    e0.record(st)
+    for _ in range(rounds):
+        cm.call("cactus_hip_graph_launch", ge, st.handle)
+    e1.record(st)
+    st.sync()
+    cm.call("cactus_hip_graph_destroy", ge)
+    us = e0.elapsed_ms(e1) * 1e3 / (reps * rounds)
+    tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
+    return {"us_per_call": round(us, 2), "tops": round(tops, 1),
+            "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+
+
+def bench_prefill_gemms(eager: bool = False):
+    """Prefill matmul shapes: Qwen3-0.6B MLP gate/up (INT8, M=512) and
+    down-proj (INT4, M=256 prefill and M=1 decode)."""
+    out = {"int8_m512_k1024_n3072_g32": {
+        "workload": "INT8 grouped matmul M=512 K=1024 N=3072 group 32, FP16 activations quantized per row",
+        **bench_gemm(512, 1024, 3072, 32, False, True, eager=eager),
+        "matmul_only": bench_gemm(512, 1024, 3072, 32, False, False, eager=eager)}}
+    out["int4_k3072_n1024_g32"] = {
+        "workload": "INT4 grouped matmul K=3072 N=1024 group 32, FP16 activations quantized per row",
+        "m256": bench_gemm(256, 3072, 1024, 32, True, True, eager=eager),
+        "m1": bench_gemm(1, 3072, 1024, 32, True, True, eager=eager)}
+    return out
+
+
 def measured_traffic():
     """HBM bytes per GEMV launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated),
     as recorded by the rocprofv3 counter runs summarised in
@@ -173,6 +253,9 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
     ap.add_argument("--new-tokens", type=int, default=128)
+    ap.add_argument("--eager", action="store_true",
+                    help="no HIP graphs: matmuls launched directly and the decode step enqueued per token "
+                         "(for kernel tracers; timings then include host launch overhead)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes)")
@@ -182,6 +265,8 @@ def main():
               "(this build has no multi-GPU path)", file=sys.stderr)
         sys.exit(2)
 
+    if args.eager:
+        os.environ["CACTUS_DECODE_EAGER"] = "1"
     import cactus_amd as cm
     cm.call("cactus_hip_init", 0)
     if args.decode_only:
@@ -194,6 +279,7 @@ def main():
         cm.call("cactus_hip_stream_sync", None)
         del src, dst
     g = bench_gemv(args.steps, args.warmup)
+    gemms = bench_prefill_gemms(eager=args.eager)
     dec = None if args.skip_decode else bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)
     cpu = cpu_baseline(args.cpu_seconds)
     out = {
@@ -225,6 +311,7 @@ def main():
             "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
+        "prefill_gemm": gemms,
         "qwen3_0p6b_decode": dec,
     }
     print(json.dumps(out), flush=True)

@@ -20,8 +20,6 @@
 #include "gemv_device.h"
 #include "lm_device.h"
 
-#include <mutex>
-
 namespace cactus_hip {
 
 int attention_hybrid_decode(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* ks,
@@ -801,12 +799,15 @@ int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float e
     p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps;
     if (streamed) {
         const size_t smem = 4 * K + (size_t)LMS_WAVES * LMS_D * LMS_SLOT;
-        CH_REQUIRE(smem <= 160 * 1024, "decode_lm_head: K too large for the streamed kernel");
-        static std::once_flag attr;
-        std::call_once(attr, [] {
-            (void)hipFuncSetAttribute((const void*)dec_lm_head_stream_kernel,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        });
+        // dynamic LDS for the largest K accepted here (4096); the kernel's
+        // static reduction arrays take the rest of the CU's 160 KB
+        constexpr size_t kMaxSmem = 4 * 4096 + (size_t)LMS_WAVES * LMS_D * LMS_SLOT;
+        static const hipError_t attr = hipFuncSetAttribute(
+            (const void*)dec_lm_head_stream_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxSmem);
+        if (attr != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(CACTUS_HIP_ERUNTIME, std::string("decode_lm_head: LDS attribute: ") + hipGetErrorString(attr));
+        }
         hipLaunchKernelGGL(dec_lm_head_stream_kernel, dim3(blocks), dim3(LMS_THREADS), smem, as_stream(stream), p);
         return check_launch("decode_lm_head");
     }

@@ -471,11 +471,12 @@ static bool launch_lds(const GemmArgs& a, hipStream_t st) {
     const size_t lds = lds_bytes<C>();
     if (lds > 160 * 1024) return false;
     if (lds > 64 * 1024) {
-        static std::once_flag once;
-        std::call_once(once, [] {
-            (void)hipFuncSetAttribute((const void*)gemm_lds_kernel<C, INT4>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        });
+        static const hipError_t attr = hipFuncSetAttribute((const void*)gemm_lds_kernel<C, INT4>,
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (attr != hipSuccess) {
+            (void)hipGetLastError();   // leave no error behind; the register-streamed kernel runs instead
+            return false;
+        }
     }
     const dim3 grid(ceil_div(a.N, C::BN), ceil_div(a.M, C::BM));
     hipLaunchKernelGGL((gemm_lds_kernel<C, INT4>), grid, dim3(C::NT), lds, st, a);
