@@ -165,6 +165,212 @@ static size_t gemv_smem(int MR, int K, int rows, int G) {
     return (s + 15) & ~(size_t)15;
 }
 
+// Orders one wave's LDS writes before its later LDS reads (and reads before
+// later writes).  LDS operations of one wavefront execute in program order,
+// so no s_barrier and no counter wait are needed, only compiler ordering.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Wave-streaming grouped GEMV for M <= 4 activation rows.
+//
+// A wave tile is `rows` consecutive weight rows, a contiguous run of
+// rows*cpr 16-byte chunks that one wave loads as CH coalesced 1 KB slots
+// (chunk f = slot*64 + lane).  The four waves of a workgroup share only the
+// activation codes, quantized once in the prologue; after that each wave
+// streams its own tiles (t0+wave, t0+wave+4, ...) with no workgroup barrier:
+// dot products and exact group sums, group sums and the tile's fp16 group
+// scales into the wave's own LDS slice, the loads of its next tile, then the
+// reference epilogue (kernel_gemm.cpp:311-324) by one lane per output while
+// those loads are in flight.
+template <int MR, bool F16ACT, bool INT4, int CH>
+__global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int m0) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int K = a.K, gs = a.gs, G = K / gs;
+    const int rows = a.rows;
+    const size_t bi = blockIdx.y;
+    const int mr = min(MR, a.M - m0);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ntiles_all = (a.N + rows - 1) / rows;
+    const int t0 = blockIdx.x * a.tiles;
+    const int t1 = min(t0 + a.tiles, ntiles_all);
+    if (t0 >= t1) return;  // uniform over the workgroup
+
+    const int cpr = INT4 ? K / 32 : K / 16;  // 16-byte chunks per row
+    const int P = INT4 ? gs / 32 : gs / 16;  // chunks per group (power of 2, <= 64)
+    const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
+    const int acc_words = MR * rows * G;
+    const int wave_bytes = ((acc_words * 4 + 15) & ~15) + ((rows * G * 2 + 15) & ~15);
+
+    int8_t* actq = reinterpret_cast<int8_t*>(smem);  // MR*K
+    unsigned char* wbase = smem + ((MR * K + 15) & ~15) + wid * wave_bytes;
+    int32_t* acc = reinterpret_cast<int32_t*>(wbase);                                 // [MR][rows][G]
+    uint16_t* scl = reinterpret_cast<uint16_t*>(wbase + ((acc_words * 4 + 15) & ~15));  // [rows][G]
+    float* rsc = reinterpret_cast<float*>(smem + ((MR * K + 15) & ~15) + 4 * wave_bytes);  // MR
+    float* red = rsc + MR;                                                                // 4
+
+    const uint8_t* Bbase = a.B + bi * a.sB;
+    const uint16_t* Bsbase = a.Bs + bi * a.sBs;
+
+    // chunk f = i*64 + lane of a tile: row f / cpr, column f % cpr (the same
+    // for every tile; a short last tile only masks chunks off)
+    int crow[CH], ccol[CH];
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int f = i * 64 + lane;
+        crow[i] = f / cpr;
+        ccol[i] = f - crow[i] * cpr;
+    }
+    i32x4 w[CH];
+    uint16_t sv[CH];
+    auto load_tile = [&](int t) {
+        const int n0 = t * rows;
+        const int nr = min(rows, a.N - n0);
+        const i32x4* Bw = reinterpret_cast<const i32x4*>(Bbase + (size_t)n0 * row_bytes);
+        const uint16_t* Sw = Bsbase + (size_t)n0 * G;
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            w[i] = (i32x4){0, 0, 0, 0};
+            if (i * 64 + lane < nr * cpr) w[i] = __builtin_nontemporal_load(Bw + i * 64 + lane);
+        }
+        // rows*G <= 64*CH for every tile shape the launcher picks
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            sv[i] = 0;
+            if (i * 64 + lane < nr * G) sv[i] = Sw[i * 64 + lane];
+        }
+    };
+
+    int t = t0 + wid;
+    if (t < t1) load_tile(t);
+
+    // activation codes (the per-row quantization of the matmul node)
+    const int body = (K / 8) * 8;
+    for (int m = 0; m < mr; m++) {
+        if (F16ACT) {
+            const uint16_t* x = a.A16 + bi * a.sA + (size_t)(m0 + m) * K;
+            const float mx = block_max_abs_f16(x, K, red);
+            const float s = row_scale_from_max(mx);
+            const float inv = 1.0f / s;
+            for (int i = tid; i < K; i += GEMV_THREADS)
+                actq[m * K + act_pos<INT4>(i)] = quant_code(h2f(x[i]), inv, i >= body);
+            if (tid == 0) rsc[m] = s;
+        } else {
+            const int8_t* x = a.A8 + bi * a.sA + (size_t)(m0 + m) * K;
+            for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + act_pos<INT4>(i)] = x[i];
+            if (tid == 0) rsc[m] = a.As[bi * (a.sA / K) + m0 + m];
+        }
+    }
+    __syncthreads();
+    float rsm[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) rsm[m] = m < mr ? rsc[m] : 0.0f;
+
+    for (; t < t1; t += 4) {
+        const int n0 = t * rows;
+        const int nr = min(rows, a.N - n0);
+        const int nch = nr * cpr;
+#pragma unroll
+        for (int i = 0; i < CH; i++)
+            if (i * 64 + lane < nr * G) scl[i * 64 + lane] = sv[i];
+#pragma unroll
+        for (int i = 0; i < CH; i++) {
+            const bool valid = i * 64 + lane < nch;
+            int dot[MR];
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], w[i]) : 0;
+                dot[m] = group_lane_sum(dot[m], P);
+            }
+            if (valid && (lane & (P - 1)) == 0) {
+                const int g = ccol[i] / P;
+#pragma unroll
+                for (int m = 0; m < MR; m++)
+                    if (m < mr) acc[(m * rows + crow[i]) * G + g] = dot[m];
+            }
+        }
+        if (t + 4 < t1) load_tile(t + 4);
+        wave_lds_order();
+        // reference epilogue, one lane per output of this tile
+        for (int o = lane; o < mr * nr; o += 64) {
+            const int m = o / nr, r = o - (o / nr) * nr;
+            const int32_t* ag = acc + (m * rows + r) * G;
+            const uint16_t* sg = scl + r * G;
+            float rs = 0.0f;
+            for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+            float s = rsm[0];
+#pragma unroll
+            for (int mm = 1; mm < MR; mm++)
+                if (m == mm) s = rsm[mm];
+            a.C[bi * a.sC + (size_t)(m0 + m) * a.N + n0 + r] = f2h(rs * s);
+        }
+        wave_lds_order();
+    }
+}
+
+static size_t gemv_wave_smem(int MR, int K, int rows, int G) {
+    const size_t wave = (size_t)((MR * rows * G * 4 + 15) & ~15) + (size_t)((rows * G * 2 + 15) & ~15);
+    return (size_t)((MR * K + 15) & ~15) + 4 * wave + (size_t)(MR + 4) * 4;
+}
+
+template <int MR, bool F16ACT, bool INT4, int CH>
+static int launch_gemv_wave_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st) {
+    const int ntiles = (a.N + a.rows - 1) / a.rows;
+    dim3 grid(ceil_div(ntiles, a.tiles), (unsigned)batch);
+    hipLaunchKernelGGL((gemv_wave_kernel<MR, F16ACT, INT4, CH>), grid, dim3(GEMV_THREADS), smem,
+                       st, a, m0);
+    return check_launch("gemv_wave");
+}
+
+template <int MR, bool F16ACT, bool INT4>
+static int launch_gemv_wave_ch(const GemvArgs& a, size_t batch, int m0, size_t smem, int ch,
+                               hipStream_t st) {
+    switch (ch) {
+        case 1: return launch_gemv_wave_t<MR, F16ACT, INT4, 1>(a, batch, m0, smem, st);
+        case 2: return launch_gemv_wave_t<MR, F16ACT, INT4, 2>(a, batch, m0, smem, st);
+        case 3: return launch_gemv_wave_t<MR, F16ACT, INT4, 3>(a, batch, m0, smem, st);
+        case 4: return launch_gemv_wave_t<MR, F16ACT, INT4, 4>(a, batch, m0, smem, st);
+        case 5: return launch_gemv_wave_t<MR, F16ACT, INT4, 5>(a, batch, m0, smem, st);
+        case 6: return launch_gemv_wave_t<MR, F16ACT, INT4, 6>(a, batch, m0, smem, st);
+        default: return launch_gemv_wave_t<MR, F16ACT, INT4, 8>(a, batch, m0, smem, st);
+    }
+}
+
+// Wave tile shape for the streaming kernel: CH chunks per lane and the rows
+// (whole rows only) that fill them.  Prefers the slot count that wastes the
+// fewest lanes, 5 or 4 chunks per lane at equal waste, then fewer chunks
+// while the problem has too few tiles to give every CU several waves.
+// Returns false when a row does not fit 8 slots (cpr > 512).
+static bool pick_wave_tile(int cpr, size_t N, size_t batch, int* ch_out, int* rows_out) {
+    static const int kCh[] = {5, 4, 6, 8, 3, 2, 1};
+    int best_ch = 0;
+    double best_util = 0.0;
+    for (int ch : kCh) {
+        const int rows = 64 * ch / cpr;
+        if (rows < 1) continue;
+        const double util = (double)rows * cpr / (64.0 * ch);
+        if (util > best_util + 0.02) { best_util = util; best_ch = ch; }
+    }
+    if (!best_ch) return false;
+    int ch = best_ch;
+    // >= 4096 wave tiles in flight (1024 workgroups) when the problem allows
+    while (ch > 1) {
+        const int rows = 64 * ch / cpr;
+        if ((size_t)ceil_div(N, (size_t)rows) * batch >= 4096) break;
+        int next = 0;
+        for (int c = ch - 1; c >= 1; c--)
+            if (64 * c / cpr >= 1) { next = c; break; }
+        if (!next) break;
+        ch = next;
+    }
+    *ch_out = ch;
+    *rows_out = min((size_t)(64 * ch / cpr), N);
+    return true;
+}
+
 template <int MR, bool F16ACT, bool INT4, int CH>
 static int launch_gemv_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st) {
     const int ntiles = (a.N + a.rows - 1) / a.rows;
@@ -191,6 +397,28 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
     const int G = a.K / a.gs;
     const int cpr = INT4 ? a.K / 32 : a.K / 16;
     const int MR = a.M >= 4 ? 4 : (a.M >= 2 ? 2 : 1);
+    int wch = 0, wrows = 0;
+    if (pick_wave_tile(cpr, a.N, batch, &wch, &wrows) &&
+        gemv_wave_smem(MR, a.K, wrows, G) <= 60 * 1024) {
+        // wave tiles per workgroup: 4 (one per wave) up to 4*8, aiming at
+        // about three resident rounds of 2048 workgroups
+        const size_t nt = ceil_div(a.N, (size_t)wrows);
+        size_t per = nt * batch / (4 * 2048 * 3);
+        if (per < 1) per = 1;
+        if (per > 8) per = 8;
+        size_t nb = ceil_div(nt, 4 * per);
+        a.rows = wrows;
+        a.tiles = (int)ceil_div(nt, nb);  // balanced: every workgroup but the last full
+        const size_t smem = gemv_wave_smem(MR, a.K, wrows, G);
+        for (int m0 = 0; m0 < a.M; m0 += MR) {
+            int rc;
+            if (MR == 4) rc = launch_gemv_wave_ch<4, F16ACT, INT4>(a, batch, m0, smem, wch, st);
+            else if (MR == 2) rc = launch_gemv_wave_ch<2, F16ACT, INT4>(a, batch, m0, smem, wch, st);
+            else rc = launch_gemv_wave_ch<1, F16ACT, INT4>(a, batch, m0, smem, wch, st);
+            if (rc) return rc;
+        }
+        return CACTUS_HIP_OK;
+    }
     // a tile is about 4 chunks per thread (measured best: more registers per
     // thread cost occupancy); fewer rows when the whole problem would leave
     // CUs idle (256 CUs, aim for >= 4 workgroups each)

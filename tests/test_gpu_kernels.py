@@ -104,6 +104,9 @@ GEMM_CASES = [
     (40, 512, 96, 128),
     (256, 2048, 1024, 32),  # Qwen3-0.6B o-proj prefill chunk
     (512, 1024, 3072, 32),  # Qwen3-0.6B gate/up prefill GEMM (MFMA, two tiles per wave)
+    (1, 10240, 64, 1024),   # row longer than 8 wave slots: block-tiled GEMV
+    (2, 16, 300, 16),       # one chunk per row and per group
+    (3, 2048, 130, 1024),   # 64-chunk groups, ragged last wave tile
 ]
 
 
@@ -192,6 +195,25 @@ def test_matmul_int8_batched(dev, orc):
     Bs = np.stack([w[1] for w in ws])
     C = dev.empty(R * M * N * 2)
     dev.cm.call("cactus_hip_matmul_int8_f16act_batched", dev.put(A), dev.put(B), dev.put(Bs), C.ptr,
+                M, K, N, gs, R, M * K, N * K, N * (K // gs), M * N, None)
+    got = dev.get(C, np.uint16, (R, M, N))
+    for r in range(R):
+        rq, rs = orc.quantize_activations(xs[r])
+        assert_bits(got[r], orc.matmul_int8(rq, rs, ws[r][0], ws[r][1], gs), f"batch {r}")
+
+
+@pytest.mark.parametrize("M,K,N,gs,R", [(4, 128, 4096, 16, 40), (3, 2048, 1000, 1024, 5), (1, 640, 2048, 32, 1)])
+def test_matmul_int8_batched_shapes(dev, orc, M, K, N, gs, R):
+    """Batched GEMV shapes that pick the wide wave tiles: 40-row tiles whose
+    epilogue loops over 160 outputs (M=4, K=128), 64-chunk groups, and a
+    single problem."""
+    say("matmul_int8_f16act_batched", M, K, N, gs, R)
+    rng = np.random.default_rng(M * K + N + R)
+    xs = [activations(rng, M, K) for _ in range(R)]
+    ws = [grouped_int8_weights(rng, N, K, gs) for _ in range(R)]
+    C = dev.empty(R * M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int8_f16act_batched", dev.put(np.stack(xs)),
+                dev.put(np.stack([w[0] for w in ws])), dev.put(np.stack([w[1] for w in ws])), C.ptr,
                 M, K, N, gs, R, M * K, N * K, N * (K // gs), M * N, None)
     got = dev.get(C, np.uint16, (R, M, N))
     for r in range(R):
