@@ -299,6 +299,203 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
     }
 }
 
+// ------------------------------------------------ kernel A, many query rows
+// Prefill form of the scores.  A lane still owns one key, but a wave scores
+// it against SQ_NQ query vectors (SQ_NQ/gq consecutive query rows times the
+// gq heads of the kv head): the key row is loaded and converted once per 16
+// dims for all of them.  A query vector enters the FMA through DPP
+// row_newbcast from a register that holds 16 of its dims replicated over the
+// four 16-lane rows, so a score step is one VALU op.  The reference's
+// per-score order is kept: accumulator c of query q takes dims 8i+c in
+// increasing i, then ((c0+c4)+(c1+c5)) + ((c2+c6)+(c3+c7)), times scale.
+// The INT8 key value (float)code * scale is formed as
+// fma((float)(code + 128), scale, -128 * scale): the exact product rounded
+// once, the same float as the reference's rounded multiply.  Block sums run
+// in the reference's sequential order in one lane per (query, block), from
+// the wave's weights in LDS.
+constexpr int SQ_NQ = 8;
+
+template <int K>
+__device__ __forceinline__ void sq_step(float (&acc)[SQ_NQ][8], const float (&qv)[SQ_NQ], float k) {
+#pragma unroll
+    for (int q = 0; q < SQ_NQ; q++) fmac_row_bcast<K>(acc[q][K & 7], qv[q], k);
+}
+template <int... K>
+__device__ __forceinline__ void sq_group16(float (&acc)[SQ_NQ][8], const float (&qv)[SQ_NQ], const float* kk,
+                                           std::integer_sequence<int, K...>) {
+    asm volatile("s_nop 1");   // DPP source read after a possible VALU write of qv
+    (sq_step<K>(acc, qv, kk[K]), ...);
+}
+
+template <bool HYBRID, int D>
+__global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
+    const AttnArgs a = resolve(a_in);
+    __shared__ float qsh[SQ_NQ][D];
+    __shared__ float wsh[4][SQ_NQ][64];
+    __shared__ float msh[4][SQ_NQ][2];
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int gq = a.gq, qr = SQ_NQ / gq;
+    const int ngrp = (a.S + qr - 1) / qr;
+    size_t gy = blockIdx.y;                            // (b, row group, kv head)
+    const int kvh = (int)(gy % a.Hkv);
+    gy /= a.Hkv;
+    const int qp0 = (int)(gy % ngrp) * qr;
+    const size_t b = gy / ngrp;
+    const int d = a.d;
+    const int h0 = kvh * gq;
+    for (int i = threadIdx.x; i < SQ_NQ * D; i += 256) {
+        const int v = i / D, dim = i % D;
+        const int qp = qp0 + v / gq;
+        qsh[v][dim] = qp < a.S ? h2f(a.q[((b * a.S + qp) * a.Hq + h0 + v % gq) * (size_t)d + dim]) : 0.0f;
+    }
+    __syncthreads();
+
+    // per query vector: its row's key range (kv_start is 0 on this path)
+    const float NEG_INF = -__builtin_inff();
+    size_t kv_end_max = 0;
+    for (int r = 0; r < qr; r++) {
+        if (qp0 + r >= a.S) break;
+        size_t s0, e, bl;
+        kv_range<HYBRID>(a, (size_t)(qp0 + r), s0, e, bl);
+        if (e > kv_end_max) kv_end_max = e;
+    }
+    const size_t chunk = (size_t)blockIdx.x * 4 + wid;
+    const size_t wbase = chunk * 64;                   // first key of the wave
+    if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
+    const int jl = lane & 31;
+    const size_t bs0 = wbase + (lane & 32);
+    const size_t kp = wbase + lane;
+
+    // ---- dot products of this lane's key with every query vector
+    float acc[SQ_NQ][8];
+#pragma unroll
+    for (int q = 0; q < SQ_NQ; q++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[q][c] = 0.0f;
+    const bool kload = kp < kv_end_max;
+    const bool kint8 = HYBRID && kp < a.cache_len;
+    const int8_t* krow8 = nullptr;
+    const uint16_t* krow16 = nullptr;
+    const float* ksr = nullptr;
+    if (kint8) {
+        krow8 = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
+        ksr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
+    } else {
+        const size_t kpos = HYBRID ? kp - a.cache_len : kp;
+        const size_t klen = HYBRID ? a.new_len : a.Skv;
+        krow16 = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
+    }
+    const int lr = lane & 15;
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) {
+        float kk[16];
+        if (kload && kint8) {
+            const uint4 raw = *reinterpret_cast<const uint4*>(krow8 + 16 * m);
+            const float s = ksr[(16 * m) / a.qgs];
+            const float ns = -128.0f * s;
+            const uint32_t w4[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
+                                    raw.w ^ 0x80808080u};
+#pragma unroll
+            for (int e = 0; e < 16; e++)
+                kk[e] = __builtin_fmaf((float)((w4[e >> 2] >> (8 * (e & 3))) & 0xFFu), s, ns);
+        } else if (kload) {
+            const uint4 r0 = *reinterpret_cast<const uint4*>(krow16 + 16 * m);
+            const uint4 r1 = *reinterpret_cast<const uint4*>(krow16 + 16 * m + 8);
+            const uint32_t h[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                kk[2 * e] = h2f((uint16_t)(h[e] & 0xFFFF));
+                kk[2 * e + 1] = h2f((uint16_t)(h[e] >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; e++) kk[e] = 0.0f;
+        }
+        float qv[SQ_NQ];
+#pragma unroll
+        for (int q = 0; q < SQ_NQ; q++) qv[q] = qsh[q][16 * m + lr];
+        sq_group16(acc, qv, kk, std::make_integer_sequence<int, 16>{});
+    }
+
+    // ---- per query vector: mask, block max, weight, stores
+#pragma unroll
+    for (int q = 0; q < SQ_NQ; q++) {
+        const int qp = qp0 + q / gq;
+        const bool row_ok = qp < a.S;
+        const size_t aq = a.pos_off + qp;
+        size_t s0 = 0, kv_end = 0, blk_limit = 0;
+        if (row_ok) kv_range<HYBRID>(a, (size_t)qp, s0, kv_end, blk_limit);
+        const bool block_live = row_ok && bs0 < kv_end;
+        const size_t be = block_live ? ((bs0 + ATT_BLOCK < blk_limit) ? bs0 + ATT_BLOCK : blk_limit) : bs0;
+        const int bsz = (int)(be - bs0);
+        const bool is_decode = (!HYBRID) && (qp == a.S - 1) && a.S > 1;
+        const bool block_skipped = !HYBRID && !is_decode && a.causal && bs0 > aq;
+        const bool in_block = block_live && jl < bsz && !block_skipped;
+        bool computed = in_block;
+        if (computed && a.causal && kp > aq && (HYBRID || !is_decode)) computed = false;
+        float sc = NEG_INF;
+        if (computed) {
+            const float t0 = acc[q][0] + acc[q][4], t1 = acc[q][1] + acc[q][5];
+            const float t2 = acc[q][2] + acc[q][6], t3 = acc[q][3] + acc[q][7];
+            sc = ((t0 + t1) + (t2 + t3)) * a.scale;
+            if (!HYBRID) {
+                if (a.causal && kp > aq) sc = NEG_INF;
+                else if (a.mask && h2f(a.mask[(b * a.S + qp) * a.Skv + kp]) == 0.0f) sc = NEG_INF;
+            }
+        }
+        float mx = sc;
+#pragma unroll
+        for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+        const int vs4 = HYBRID ? 0 : (bsz / 4) * 4;
+        float w = 0.0f;
+        if (in_block) {
+            if (jl < vs4) w = poly_exp_weight(sc, mx);
+            else w = (sc != NEG_INF) ? cactus_expf(sc - mx) : 0.0f;
+        }
+        const bool wlane = block_live && jl < bsz;
+        const size_t row = (b * a.S + (row_ok ? qp : 0)) * a.Hq + h0 + q % gq;
+        if (wlane) a.w[row * a.wstride + kp] = w;
+        wsh[wid][q][lane] = w;
+        if (jl == 0) msh[wid][q][lane >> 5] = mx;
+    }
+    wave_lds_order();
+    // ---- block sums, one lane per (query vector, block), reference order
+    if (lane < 2 * SQ_NQ) {
+        const int q = lane >> 1, half = lane & 1;
+        const int qp = qp0 + q / gq;
+        const size_t bs = wbase + 32 * half;
+        if (qp < a.S) {
+            const size_t aq = a.pos_off + qp;
+            size_t s0, kv_end, blk_limit;
+            kv_range<HYBRID>(a, (size_t)qp, s0, kv_end, blk_limit);
+            if (bs < kv_end) {
+                const size_t be = (bs + ATT_BLOCK < blk_limit) ? bs + ATT_BLOCK : blk_limit;
+                const int bsz = (int)(be - bs);
+                const bool is_decode = (!HYBRID) && (qp == a.S - 1) && a.S > 1;
+                const bool block_skipped = !HYBRID && !is_decode && a.causal && bs > aq;
+                const float* x = &wsh[wid][q][32 * half];
+                const int v4 = HYBRID ? 0 : (bsz / 4) * 4;
+                float sum = 0.0f;
+                bool has_zero = false;
+                int j = 0;
+                for (; j < v4; j += 4) {
+                    sum = sum + ((x[j] + x[j + 1]) + (x[j + 2] + x[j + 3]));
+                    has_zero |= !(x[j] != 0.0f) || !(x[j + 1] != 0.0f) || !(x[j + 2] != 0.0f) || !(x[j + 3] != 0.0f);
+                }
+                for (; j < bsz; j++) {
+                    sum = sum + x[j];
+                    has_zero |= !(x[j] != 0.0f);
+                }
+                const size_t row = (b * a.S + qp) * a.Hq + h0 + q % gq;
+                const int blk = (int)(bs / ATT_BLOCK);
+                a.bmax[row * a.nbstride + blk] = block_skipped ? NEG_INF : msh[wid][q][half];
+                const float bsv = block_skipped ? 0.0f : sum;
+                a.bsum[row * a.nbstride + blk] = has_zero ? set_sign(bsv) : bsv;
+            }
+        }
+    }
+}
+
 // ----------------------------------------------------------------- kernel B
 // The value accumulation is one fp32 FMA chain per (query, head, dimension)
 // over the keys in order, rescaled at every block whose max is finite
@@ -591,17 +788,6 @@ __device__ __forceinline__ void chain_corr(const AttnArgs& a, size_t row, int nb
         const int last = __shfl(idx, 63, 64);
         if (last >= 0) carry = __shfl(m, last, 64);
     }
-}
-
-// acc = fma(w, p, acc) with w taken from lane k of each 16-lane row of wv
-// (DPP row_newbcast): a row-replicated weight vector feeds 16 chain steps
-// without an LDS broadcast read per step.  One VALU op per step, the same
-// single rounding as fmaf.
-template <int K>
-__device__ __forceinline__ void fmac_row_bcast(float& acc, float wv, float p) {
-    asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
-                 : "+v"(acc)
-                 : "v"(wv), "v"(p), "n"(K));
 }
 
 // 16 chain steps: keys k = 0..15 with products p[k], weights in lanes k of wv
@@ -1380,6 +1566,290 @@ __global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs
     }
 }
 
+// ------------------------------------------------ kernel B, many query rows
+// Prefill form of the value chains.  A workgroup owns RW_CH chains -- RW_CH/gq
+// consecutive query rows times the gq heads of one kv head -- on one 64-dim
+// slice.  Each chain wave runs RW_CPW chains per lane (lane = dimension), so
+// one LDS read of a value row feeds RW_CPW FMAs, and the chains of a lane
+// interleave instead of waiting on each other's FMA latency.  Weights enter
+// the FMA through DPP row_newbcast (a 16-key weight vector replicated per
+// 16-lane row), so a step reads no weight from LDS.  The stage waves fetch
+// the next tile's value rows into registers a whole step ahead and store the
+// reference's fp32 operands (INT8 code * per-key group scale for the cache,
+// fp16 -> fp32 for new rows and the FP16 path) as [dim][key] rows, plus the
+// chains' weights.  Blocks that are partial or hold a zero weight run key by
+// key with the reference's zero skip (kernel_attention.cpp:200-201).
+constexpr int RW_T = 64;                          // keys per tile
+constexpr int RW_PS = RW_T + 4;                   // floats per dim row (bank skew)
+constexpr int RW_CH = 32;                         // chains per workgroup
+constexpr int RW_CPW = 4;                         // chains per lane of a chain wave
+constexpr int RW_NCW = RW_CH / RW_CPW;            // chain waves
+constexpr int RW_NSW = 4;                         // stage waves
+constexpr int RW_THREADS = 64 * (RW_NCW + RW_NSW);
+constexpr int RW_PROD_B = 2 * 64 * RW_PS * 4;
+constexpr int RW_W_B = 2 * RW_CH * RW_T * 4;
+
+template <int K>
+__device__ __forceinline__ void rw_step(float (&acc)[RW_CPW], const float (&wv)[RW_CPW], float p) {
+#pragma unroll
+    for (int c = 0; c < RW_CPW; c++) fmac_row_bcast<K>(acc[c], wv[c], p);
+}
+template <int... K>
+__device__ __forceinline__ void rw_chain16(float (&acc)[RW_CPW], const float* p, const float (&wv)[RW_CPW],
+                                           std::integer_sequence<int, K...>) {
+    asm volatile("s_nop 1");   // DPP source read after a possible VALU write of wv
+    (rw_step<K>(acc, wv, p[K]), ...);
+}
+
+// weight k of a 16-lane row, broadcast over the row (DPP row_newbcast:k)
+template <int K>
+__device__ __forceinline__ float row_bcast(float w) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, w), 0x150 + K, 0xF, 0xF, false));
+}
+// 16 chain steps of one chain, key k taken only where bit k of the
+// wave-uniform mask nz is set
+template <int... K>
+__device__ __forceinline__ void rw_masked16(float& acc, const float* p, float wv, uint32_t nz,
+                                            std::integer_sequence<int, K...>) {
+    ((((nz >> K) & 1u) ? (void)(acc = __builtin_fmaf(p[K], row_bcast<K>(wv), acc)) : (void)0), ...);
+}
+
+template <bool HYBRID>
+__global__ void __launch_bounds__(RW_THREADS) attn_rows_kernel(AttnArgs a_in, int nbmax) {
+    const AttnArgs a = resolve(a_in);
+    extern __shared__ __align__(16) unsigned char smem[];
+    float* prod = reinterpret_cast<float*>(smem);                        // [2][64][RW_PS]
+    float* wts = reinterpret_cast<float*>(smem + RW_PROD_B);             // [2][RW_CH][RW_T]
+    float* corr_s = reinterpret_cast<float*>(smem + RW_PROD_B + RW_W_B); // [RW_CH][nbmax]
+    float* bsum_s = corr_s + (size_t)RW_CH * nbmax;                      // [RW_CH][nbmax]
+    const float NEG_INF = -__builtin_inff();
+
+    const int d = a.d, da = (d / 8) * 8, gq = a.gq;
+    const int qr = RW_CH / gq;                     // query rows of the workgroup
+    const int nsl = (d + 63) / 64;
+    size_t g = blockIdx.x;
+    const int sl = (int)(g % nsl);
+    g /= nsl;
+    const int kvh = (int)(g % a.Hkv);
+    g /= a.Hkv;
+    const int ngrp = (a.S + qr - 1) / qr;
+    const int qp0 = (int)(g % ngrp) * qr;
+    const size_t b = g / ngrp;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+
+    // keys of the group: every row starts at the same key (no sliding
+    // window on this path); the last row reaches furthest
+    size_t ks, ke_f, bl_f;
+    kv_range<HYBRID>(a, (size_t)qp0, ks, ke_f, bl_f);
+    const int qlast = min(qp0 + qr, a.S) - 1;
+    size_t ks_l, ke_l, bl_l;
+    kv_range<HYBRID>(a, (size_t)qlast, ks_l, ke_l, bl_l);
+    size_t kneed = ks;
+    if (ke_l > ks) {
+        kneed = ks + ((ke_l - ks + ATT_BLOCK - 1) / ATT_BLOCK) * ATT_BLOCK;
+        if (kneed > bl_l) kneed = bl_l;
+    }
+    const int nst = (int)((kneed - ks + RW_T - 1) / RW_T);
+    const bool is_chain = wv < RW_NCW;
+
+    // ---- stage waves: item (dq, kq) = 4 dims x 4 keys of a tile
+    const int pl = (int)threadIdx.x - RW_NCW * 64;
+    const int dq = pl & 15, kq = pl >> 4;
+    const int dim0 = sl * 64 + dq * 4;
+    uint32_t r8[4];
+    uint2 r16[4];
+    float rsc[4];
+    float4 wr[2];
+    auto load_raw = [&](int t) {
+        const size_t tb = ks + (size_t)t * RW_T;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const size_t kp = tb + kq * 4 + e;
+            r8[e] = 0;
+            r16[e] = make_uint2(0, 0);
+            rsc[e] = 0.0f;
+            if (kp >= kneed || dim0 >= da) continue;
+            if (HYBRID && kp < a.cache_len) {
+                const size_t off = (b * a.cache_len + kp) * a.Hkv + kvh;
+                r8[e] = *reinterpret_cast<const uint32_t*>(a.vc + off * d + dim0);
+                rsc[e] = a.vs[off * a.nqg + dim0 / a.qgs];
+            } else {
+                const size_t vpos = HYBRID ? kp - a.cache_len : kp;
+                const size_t vlen = HYBRID ? a.new_len : a.Skv;
+                r16[e] = *reinterpret_cast<const uint2*>(a.v + ((b * vlen + vpos) * a.Hkv + kvh) * (size_t)d + dim0);
+            }
+        }
+        // weights of the chains for this tile: 32 rows x 64 keys, 8 per thread
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = pl + 256 * j;
+            const int c = i >> 4, j4 = (i & 15) * 4;
+            const int qp = qp0 + c / gq;
+            wr[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const size_t col = (size_t)t * RW_T + j4;
+            if (qp < a.S && col + 4 <= a.wstride) {
+                const size_t row = (b * a.S + qp) * a.Hq + kvh * gq + (c % gq);
+                wr[j] = *reinterpret_cast<const float4*>(a.w + row * a.wstride + col);
+            }
+        }
+    };
+    auto store_tile = [&](int t) {
+        const size_t tb = ks + (size_t)t * RW_T;
+        float* pb = prod + (t & 1) * 64 * RW_PS;
+        float pr[4][4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const size_t kp = tb + kq * 4 + e;
+            if (HYBRID && kp < a.cache_len) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) pr[e][c] = (float)(int8_t)((r8[e] >> (8 * c)) & 0xFF) * rsc[e];
+            } else {
+                pr[e][0] = h2f((uint16_t)(r16[e].x & 0xFFFF));
+                pr[e][1] = h2f((uint16_t)(r16[e].x >> 16));
+                pr[e][2] = h2f((uint16_t)(r16[e].y & 0xFFFF));
+                pr[e][3] = h2f((uint16_t)(r16[e].y >> 16));
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            *reinterpret_cast<float4*>(pb + (dq * 4 + c) * RW_PS + kq * 4) =
+                make_float4(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+        float* wb = wts + (t & 1) * RW_CH * RW_T;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int i = pl + 256 * j;
+            *reinterpret_cast<float4*>(wb + (i >> 4) * RW_T + (i & 15) * 4) = wr[j];
+        }
+    };
+
+    // ---- chain waves: chains c0..c0+3 of the workgroup
+    const int c0 = wv * RW_CPW;
+    size_t crow[RW_CPW];
+    size_t crbl[RW_CPW];
+    int cnb[RW_CPW];
+#pragma unroll
+    for (int c = 0; c < RW_CPW; c++) {
+        const int ch = c0 + c;
+        const int qp = qp0 + ch / gq;
+        crow[c] = 0;
+        crbl[c] = 0;
+        cnb[c] = 0;
+        if (is_chain && qp < a.S) {
+            size_t rks, rke, rbl;
+            kv_range<HYBRID>(a, (size_t)qp, rks, rke, rbl);
+            crow[c] = (b * a.S + qp) * a.Hq + kvh * gq + ch % gq;
+            crbl[c] = rbl;
+            cnb[c] = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
+            chain_corr(a, crow[c], cnb[c], corr_s + (size_t)ch * nbmax, bsum_s + (size_t)ch * nbmax);
+        }
+    }
+    if (!is_chain && nst > 0) {
+        load_raw(0);
+        store_tile(0);
+        if (nst > 1) load_raw(1);
+    }
+
+    float acc[RW_CPW], rs[RW_CPW];
+#pragma unroll
+    for (int c = 0; c < RW_CPW; c++) {
+        acc[c] = 0.0f;
+        rs[c] = 0.0f;
+    }
+    const int lr = lane & 15;
+    for (int t = 0; t < nst; t++) {
+        __syncthreads();
+        if (!is_chain) {
+            // buffer (t+1)&1 last held tile t-1, finished before this barrier
+            if (t + 1 < nst) {
+                store_tile(t + 1);
+                if (t + 2 < nst) load_raw(t + 2);
+            }
+            continue;
+        }
+        const float* pt = prod + (t & 1) * 64 * RW_PS + lane * RW_PS;
+        const float* wt = wts + (t & 1) * RW_CH * RW_T + (size_t)c0 * RW_T;
+#pragma unroll
+        for (int h = 0; h < RW_T / ATT_BLOCK; h++) {
+            const int blk = t * (RW_T / ATT_BLOCK) + h;
+            const int jo = h * ATT_BLOCK;
+            const size_t bs0 = ks + (size_t)blk * ATT_BLOCK;
+            bool all_fast = true;
+            float bse[RW_CPW];
+            int bsz[RW_CPW];
+#pragma unroll
+            for (int c = 0; c < RW_CPW; c++) {
+                bse[c] = 0.0f;
+                bsz[c] = 0;
+                if (blk < cnb[c]) {
+                    const float cr = corr_s[(size_t)(c0 + c) * nbmax + blk];
+                    bse[c] = bsum_s[(size_t)(c0 + c) * nbmax + blk];
+                    if (cr != NEG_INF) {
+                        acc[c] = acc[c] * cr;
+                        rs[c] = rs[c] * cr;
+                    }
+                    bsz[c] = (int)((bs0 + ATT_BLOCK < crbl[c] ? bs0 + ATT_BLOCK : crbl[c]) - bs0);
+                    if (bsz[c] != ATT_BLOCK || __builtin_signbit(bse[c])) all_fast = false;
+                } else {
+                    all_fast = false;
+                }
+            }
+            if (blk >= cnb[0] && blk >= cnb[1] && blk >= cnb[2] && blk >= cnb[3]) continue;
+            float pv[ATT_BLOCK];
+#pragma unroll
+            for (int q = 0; q < ATT_BLOCK / 4; q++) {
+                const float4 v = *reinterpret_cast<const float4*>(pt + jo + 4 * q);
+                pv[4 * q] = v.x;
+                pv[4 * q + 1] = v.y;
+                pv[4 * q + 2] = v.z;
+                pv[4 * q + 3] = v.w;
+            }
+            if (all_fast) {
+#pragma unroll
+                for (int hh = 0; hh < 2; hh++) {
+                    float wvv[RW_CPW];
+#pragma unroll
+                    for (int c = 0; c < RW_CPW; c++) wvv[c] = wt[c * RW_T + jo + 16 * hh + lr];
+                    rw_chain16(acc, pv + 16 * hh, wvv, std::make_integer_sequence<int, 16>{});
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < RW_CPW; c++) {
+                    if (blk >= cnb[c]) continue;
+                    // keys of a partial block's end, and zero weights, are
+                    // skipped: an FMA with a zero weight could turn an
+                    // accumulator of -0 into +0
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const int lim = bsz[c] - 16 * hh;
+                        if (lim <= 0) break;
+                        const float wvv = wt[c * RW_T + jo + 16 * hh + lr];
+                        uint32_t nz = (uint32_t)__ballot(wvv != 0.0f) & 0xFFFFu;   // lanes 0-15: keys
+                        if (lim < 16) nz &= (1u << lim) - 1u;
+                        rw_masked16(acc[c], pv + 16 * hh, wvv, nz, std::make_integer_sequence<int, 16>{});
+                    }
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < RW_CPW; c++)
+                if (blk < cnb[c]) rs[c] = rs[c] + __builtin_fabsf(bse[c]);
+        }
+    }
+    if (!is_chain) return;
+    const int dim = sl * 64 + lane;
+    if (dim >= d) return;
+#pragma unroll
+    for (int c = 0; c < RW_CPW; c++) {
+        if (qp0 + (c0 + c) / gq >= a.S) continue;
+        uint16_t* ov = a.o + crow[c] * (size_t)d;
+        if (!(rs[c] > 0.0f) || dim >= da) ov[dim] = 0;
+        else ov[dim] = f2h(acc[c] * (1.0f / rs[c]));
+    }
+}
+
+static size_t rows_smem(int nbmax) { return (size_t)RW_PROD_B + RW_W_B + 2 * (size_t)RW_CH * nbmax * sizeof(float); }
+
 // ------------------------------------------------ per-(device, stream) scratch
 struct AttnScratch {
     void* ptr = nullptr;
@@ -1440,7 +1910,21 @@ static int launch_attention(AttnArgs a, void* stream) {
     a.bmax = reinterpret_cast<float*>(static_cast<char*>(scratch) + wbytes);
     a.bsum = a.bmax + rows * a.nbstride;
     const size_t chunks = (maxr + 63) / 64;
-    if (chunks > 0) {
+    const bool windowed = !HYBRID && a.window > 0 && a.window < a.Skv;
+    // prefill scores: several query rows per wave (16-dim DPP groups, one
+    // scale per 16 dims, 16-byte key rows)
+    const bool k16 = HYBRID ? ((uintptr_t)a.kc % 16 == 0 && (uintptr_t)a.ks % 4 == 0 && a.qgs % 16 == 0) : true;
+    if (chunks > 0 && !windowed && (size_t)a.B * a.S > 2 && (a.d == 64 || a.d == 128) && a.gq <= SQ_NQ &&
+        SQ_NQ % a.gq == 0 && k16 && (uintptr_t)a.k % 16 == 0) {
+        const int qr = SQ_NQ / a.gq;
+        dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * ((a.S + qr - 1) / qr) * a.Hkv));
+        if (a.d == 64)
+            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 64>), ga, dim3(256), 0, as_stream(stream), a);
+        else
+            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 128>), ga, dim3(256), 0, as_stream(stream), a);
+        rc = check_launch("attention scores (rows)");
+        if (rc) return rc;
+    } else if (chunks > 0) {
         dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * a.S * a.Hkv));
         if (a.d <= 64)
             hipLaunchKernelGGL((attn_scores_kernel<HYBRID, 64>), ga, dim3(256), 0, as_stream(stream), a);
@@ -1453,7 +1937,6 @@ static int launch_attention(AttnArgs a, void* stream) {
     }
     // chain kernel: rows sharing a kv head are grouped so that their value
     // tiles are staged once; a sliding window gives every row its own start
-    const bool windowed = !HYBRID && a.window > 0 && a.window < a.Skv;
     int qpg = windowed ? 1 : ATT_MAX_GQ / a.gq;
     if (qpg > a.S) qpg = a.S;
     if (qpg < 1) qpg = 1;
@@ -1475,6 +1958,27 @@ static int launch_attention(AttnArgs a, void* stream) {
                 hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 1, 1, 3>), dim3((unsigned)groups), dim3(256), smem,
                                    as_stream(stream), a, nbmax);
             return check_launch("attention values (decode)");
+        }
+    }
+    {
+        // prefill: many query rows per workgroup, several chains per lane
+        const bool aligned = (HYBRID ? (uintptr_t)a.vc % 4 == 0 && (uintptr_t)a.vs % 4 == 0 : true) &&
+                             (uintptr_t)a.v % 8 == 0;
+        if (!windowed && (size_t)a.B * a.S > 2 && a.gq <= ATT_MAX_GQ && RW_CH % a.gq == 0 && a.d % 4 == 0 &&
+            aligned && rows_smem(nbmax) <= 160 * 1024) {
+            static hipError_t attr[2] = {
+                hipFuncSetAttribute((const void*)attn_rows_kernel<false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024),
+                hipFuncSetAttribute((const void*)attn_rows_kernel<true>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024)};
+            if (attr[HYBRID] == hipSuccess) {
+                const int qr = RW_CH / a.gq;
+                const size_t groups = (size_t)a.B * (((size_t)a.S + qr - 1) / qr) * a.Hkv * nsl;
+                hipLaunchKernelGGL(attn_rows_kernel<HYBRID>, dim3((unsigned)groups), dim3(RW_THREADS),
+                                   rows_smem(nbmax), as_stream(stream), a, nbmax);
+                return check_launch("attention values (rows)");
+            }
+            (void)hipGetLastError();  // clear the sticky attribute error before the forms below
         }
     }
     if (HYBRID && a.vsh && a.gq <= SH_MAX_CHAINS) {

@@ -165,15 +165,6 @@ static size_t gemv_smem(int MR, int K, int rows, int G) {
     return (s + 15) & ~(size_t)15;
 }
 
-// Orders one wave's LDS writes before its later LDS reads (and reads before
-// later writes).  LDS operations of one wavefront execute in program order,
-// so no s_barrier and no counter wait are needed, only compiler ordering.
-__device__ __forceinline__ void wave_lds_order() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 // Wave-streaming grouped GEMV for M <= 4 activation rows.
 //
 // A wave tile is `rows` consecutive weight rows, a contiguous run of

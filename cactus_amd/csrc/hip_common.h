@@ -205,6 +205,26 @@ __device__ __forceinline__ void wait_dma() {
 // workgroup barrier that orders LDS only (outstanding DMA keeps flying)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Orders one wave's LDS writes before its later LDS reads (and reads before
+// later writes).  LDS operations of one wavefront execute in program order,
+// so no s_barrier and no counter wait are needed, only compiler ordering.
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// acc = fma(w, p, acc) with w taken from lane k of each 16-lane row of wv
+// (DPP row_newbcast): a row-replicated operand vector feeds 16 steps without
+// an LDS broadcast read per step.  One VALU op per step, the same
+// single rounding as fmaf.
+template <int K>
+__device__ __forceinline__ void fmac_row_bcast(float& acc, float wv, float p) {
+    asm volatile("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+                 : "+v"(acc)
+                 : "v"(wv), "v"(p), "n"(K));
+}
+
 // ---------------------------------------------------------- wave reductions
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

@@ -364,9 +364,22 @@ def test_attention_f16_mask_noncausal(dev, orc):
     (1, 100, 1, 8, 1, 128),        # 8 query heads per kv head
     (40, 1000, 40, 16, 8, 128),    # new rows spanning two blocks, cache not block aligned
     (2, 100, 2, 4, 2, 256),        # head_dim 256
+    (128, 1500, 128, 16, 8, 128),  # prefill chunk deep into the context
+    (50, 300, 50, 8, 1, 128),      # 8 query heads per kv head, prefill
+    (33, 64, 33, 4, 4, 64),        # one query head per kv head, prefill
 ])
 def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
-    say("attention_hybrid", S, cache, new, Hq, Hkv, d)
+    _attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d, 1.0)
+
+
+def test_attention_hybrid_peaked(dev, orc):
+    """Queries scaled by 40: scores spread so far that weights underflow to
+    zero inside full blocks, which the value chains must skip key by key."""
+    _attention_hybrid(dev, orc, 48, 500, 48, 16, 8, 128, 40.0)
+
+
+def _attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d, qmul):
+    say("attention_hybrid", S, cache, new, Hq, Hkv, d, qmul)
     rng = np.random.default_rng(cache + new + d)
     kf = f16(rng.normal(0, 1, (max(cache, 1), Hkv, d)))
     vf = f16(rng.normal(0, 1, (max(cache, 1), Hkv, d)))
@@ -375,7 +388,7 @@ def test_attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d):
     kc, vc, ks, vs = kc[:cache], vc[:cache], ks[:cache], vs[:cache]
     kn = f16(rng.normal(0, 1, (1, new, Hkv, d)))
     vn = f16(rng.normal(0, 1, (1, new, Hkv, d)))
-    q = f16(rng.normal(0, 1, (1, S, Hq, d)))
+    q = f16(rng.normal(0, 1, (1, S, Hq, d)) * qmul)
     scale = 1.0 / math.sqrt(d)
     ref = orc.attention_hybrid(q, kc[None] if cache else None, vc[None] if cache else None,
                                ks[None] if cache else None, vs[None] if cache else None, kn, vn,
