@@ -1335,12 +1335,13 @@ __global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shado
 // Decode form of the product-tile kernel: a workgroup is one chain wave and
 // NP stage waves.  The chain wave owns NH query heads of one KV head and DR
 // 16-dim sub-slices (16-lane row r -> head r % NH, sub-slice r / NH); the
-// heads share the product rows and the DPP row broadcast gives each row its
-// own head's weights.  Stage waves move the tiles (LDS DMA, D - 1 tiles
-// ahead; a single wave issues LDS DMA too slowly to feed a chain) and compute
-// the rows' block corrections.  The chain wave reads tile t + 1 into
-// registers while tile t's chain runs: between barriers it only issues LDS
-// reads and chain steps (~9.5 cycles each on gfx950).
+// heads share the product rows and each row reads its own head's weights.
+// Stage waves move the tiles (LDS DMA, D - 1 tiles ahead; one wave issues
+// LDS DMA at ~4.5 bytes per cycle, so six of them keep a chain fed) and
+// compute the rows' block corrections.  The chain wave holds half a tile in
+// registers and reads the next half while this one chains: between
+// barriers it only issues LDS reads and plain FMAs (a dependent FMA with a
+// DPP-broadcast operand costs about twice as much here).
 template <int NH, int DR, int NP>
 struct PairCfg {
     static constexpr int SW = 16 * DR;                       // dims per workgroup
@@ -1481,77 +1482,81 @@ __global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs
     const float* cb = bsum_s + hj * nbmax;
 
     float acc = 0.0f, rs = 0.0f;
-    // per tile: 64 products, 4 row-replicated weight registers (the DPP row
-    // broadcast gives every step its weight), the two blocks' {corr, corr,
-    // sum, sum} and the fast-path flag.  Tile t + 1 is read while t chains.
-    float pv[2][64], wq[2][4], mt[2][4];
-    int fl[2];
+    // A fast tile chains as plain FMAs over two halves (one 32-key block
+    // each) held in registers: the block's 32 products of this lane's
+    // dimension, its head's 32 weights (a 16-lane row reads one head's
+    // weight row, so two heads share a wave) and the block's {corr, sum}.
+    // The next half is read while this one chains.  A tile whose blocks are
+    // partial or hold a zero weight runs key by key from LDS.
+    float pv[2][32], hw[2][32], mt[2][2];
     const int prow = (r16 / NH) * 16 + lr;                    // product row within the slot
-    auto read_tile = [&](int t, float* p, float* w, float* m, int& f) {
+    auto read_half = [&](int t, int h, float* p, float* w, float* m) {
         const unsigned char* slot = ring + (t % D) * C::SLOT;
-        const float* pt = reinterpret_cast<const float*>(slot) + prow * SH_PS;
-        const float* wt = reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T;
+        const float* pt = reinterpret_cast<const float*>(slot) + prow * SH_PS + 32 * h;
+        const float* wt = reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T + 32 * h;
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
+        for (int q = 0; q < 8; q++) {
             const float4 v = *reinterpret_cast<const float4*>(pt + 4 * q);
+            const float4 x = *reinterpret_cast<const float4*>(wt + 4 * q);
             p[4 * q] = v.x;
             p[4 * q + 1] = v.y;
             p[4 * q + 2] = v.z;
             p[4 * q + 3] = v.w;
+            w[4 * q] = x.x;
+            w[4 * q + 1] = x.y;
+            w[4 * q + 2] = x.z;
+            w[4 * q + 3] = x.w;
         }
-#pragma unroll
-        for (int q = 0; q < 4; q++) w[q] = wt[16 * q + lr];
-        const int i0 = min(t * (CD_T / ATT_BLOCK), nbmax - 1), i1 = min(t * (CD_T / ATT_BLOCK) + 1, nbmax - 1);
-        m[0] = cw[i0];
-        m[1] = cw[i1];
-        m[2] = cb[i0];
-        m[3] = cb[i1];
-        f = fast_s[t];
+        const int i = min(t * (CD_T / ATT_BLOCK) + h, nbmax - 1);
+        m[0] = cw[i];
+        m[1] = cb[i];
     };
-    auto chain_regs = [&](int t, const float* p, const float* w, const float* m, int f) {
+    auto chain_half = [&](const float* p, const float* w, const float* m) {
         const float NEG_INF = -__builtin_inff();
-        if (__builtin_amdgcn_readfirstlane(f)) {
-            // both blocks inside the tile and free of zero weights
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const float c = m[h];
-                if (c != NEG_INF) {
-                    acc = acc * c;
-                    rs = rs * c;
-                }
-                chain16(acc, p + 32 * h, w[2 * h], std::make_integer_sequence<int, 16>{});
-                chain16(acc, p + 32 * h + 16, w[2 * h + 1], std::make_integer_sequence<int, 16>{});
-                rs = rs + m[2 + h];
-            }
-        } else if (dlane) {
-            const unsigned char* slot = ring + (t % D) * C::SLOT;
-            const int b0 = t * (CD_T / ATT_BLOCK);
-            chain_tile(reinterpret_cast<const float*>(slot) + prow * SH_PS,
-                       reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, b0,
-                       min(nb_tile, b0 + CD_T / ATT_BLOCK), rks, rbl, cw, cb, acc, rs);
+        if (m[0] != NEG_INF) {
+            acc = acc * m[0];
+            rs = rs * m[0];
         }
+#pragma unroll
+        for (int k = 0; k < ATT_BLOCK; k++) acc = __builtin_fmaf(p[k], w[k], acc);
+        rs = rs + m[1];
     };
 
-    if (is_chain && nst > 0) read_tile(0, pv[0], wq[0], mt[0], fl[0]);
-    // unrolled by two so the chain wave's register buffers are static
-    for (int t = 0; t < nst; t += 2) {
-#pragma unroll
-        for (int u = 0; u < 2; u++) {
-            const int tt = t + u;
-            if (tt < nst) {
-                if (is_chain) {
-                    // next tile (the last re-reads itself: its slot stays intact)
-                    read_tile(min(tt + 1, nst - 1), pv[u ^ 1], wq[u ^ 1], mt[u ^ 1], fl[u ^ 1]);
-                    chain_regs(tt, pv[u], wq[u], mt[u], fl[u]);
-                } else {
-                    // slot of tile tt - 1: its last reader finished before the
-                    // previous barrier
-                    if (tt + D - 1 < nst) issue(tt + D - 1);
-                    if (tt + 2 < nst) wait_landed(tt + 2, tt + D - 1);
+    int fl = 0;
+    if (is_chain && nst > 0) {
+        read_half(0, 0, pv[0], hw[0], mt[0]);
+        fl = fast_s[0];
+    }
+    for (int tt = 0; tt < nst; tt++) {
+        if (is_chain) {
+            // tiles tt and tt + 1 have landed (the stage waves waited for
+            // tt + 1 before the previous barrier); the last tile re-reads
+            // itself, its slot stays intact
+            const int tn = min(tt + 1, nst - 1);
+            const int fn = fast_s[tn];
+            read_half(tt, 1, pv[1], hw[1], mt[1]);
+            if (__builtin_amdgcn_readfirstlane(fl)) {
+                chain_half(pv[0], hw[0], mt[0]);
+                read_half(tn, 0, pv[0], hw[0], mt[0]);
+                chain_half(pv[1], hw[1], mt[1]);
+            } else {
+                if (dlane) {
+                    const unsigned char* slot = ring + (tt % D) * C::SLOT;
+                    const int b0 = tt * (CD_T / ATT_BLOCK);
+                    chain_tile(reinterpret_cast<const float*>(slot) + prow * SH_PS,
+                               reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, b0,
+                               min(nb_tile, b0 + CD_T / ATT_BLOCK), rks, rbl, cw, cb, acc, rs);
                 }
-                lds_sync();
+                read_half(tn, 0, pv[0], hw[0], mt[0]);
             }
+            fl = fn;
+        } else {
+            // slot of tile tt - 1: its last reader finished before the
+            // previous barrier
+            if (tt + D - 1 < nst) issue(tt + D - 1);
+            if (tt + 2 < nst) wait_landed(tt + 2, tt + D - 1);
         }
+        lds_sync();
     }
     if (!dlane) return;
     const int tl = nst > 0 ? nst - 1 : 0;
@@ -1943,19 +1948,19 @@ static int launch_attention(AttnArgs a, void* stream) {
     const int nbmax = a.nbstride;
     const size_t nsl = (size_t)(a.d + 63) / 64;
     if (HYBRID && a.vsh && (size_t)a.B * a.S <= 2) {
-        // decode: one chain wave and three stage waves per workgroup, two heads
+        // decode: one chain wave and six stage waves per workgroup, two heads
         // per chain wave when the query-head group splits evenly
         constexpr int SD = 8;
         const bool two = a.gq % 2 == 0;
-        const size_t slot = two ? PairCfg<2, 1, 3>::SLOT : PairCfg<1, 1, 3>::SLOT;
+        const size_t slot = two ? PairCfg<2, 1, 6>::SLOT : PairCfg<1, 1, 6>::SLOT;
         const size_t smem = SD * slot + (2 * (size_t)(two ? 2 : 1) + 1) * nbmax * sizeof(float);
         if (smem <= 64 * 1024) {
             const size_t groups = (size_t)a.B * a.S * a.Hkv * (a.gq / (two ? 2 : 1)) * ((a.d + 15) / 16);
             if (two)
-                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 2, 1, 3>), dim3((unsigned)groups), dim3(256), smem,
+                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 2, 1, 6>), dim3((unsigned)groups), dim3(448), smem,
                                    as_stream(stream), a, nbmax);
             else
-                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 1, 1, 3>), dim3((unsigned)groups), dim3(256), smem,
+                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 1, 1, 6>), dim3((unsigned)groups), dim3(448), smem,
                                    as_stream(stream), a, nbmax);
             return check_launch("attention values (decode)");
         }
