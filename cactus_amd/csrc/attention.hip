@@ -315,26 +315,31 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
 // the wave's weights in LDS.
 constexpr int SQ_NQ = 8;
 
-template <int K>
-__device__ __forceinline__ void sq_step(float (&acc)[SQ_NQ][8], const float (&qv)[SQ_NQ], float k) {
+template <int NQ, int K>
+__device__ __forceinline__ void sq_step(float (&acc)[NQ][8], const float (&qv)[NQ], float k) {
 #pragma unroll
-    for (int q = 0; q < SQ_NQ; q++) fmac_row_bcast<K>(acc[q][K & 7], qv[q], k);
+    for (int q = 0; q < NQ; q++) fmac_row_bcast<K>(acc[q][K & 7], qv[q], k);
 }
-template <int... K>
-__device__ __forceinline__ void sq_group16(float (&acc)[SQ_NQ][8], const float (&qv)[SQ_NQ], const float* kk,
+template <int NQ, int... K>
+__device__ __forceinline__ void sq_group16(float (&acc)[NQ][8], const float (&qv)[NQ], const float* kk,
                                            std::integer_sequence<int, K...>) {
     asm volatile("s_nop 1");   // DPP source read after a possible VALU write of qv
-    (sq_step<K>(acc, qv, kk[K]), ...);
+    (sq_step<NQ, K>(acc, qv, kk[K]), ...);
 }
 
-template <bool HYBRID, int D>
-__global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
+// NQ query vectors per wave, NW waves (64-key chunks) per workgroup.  The
+// prefill form is NQ = 8, NW = 4; the decode form (one query row) is
+// NQ = gq, NW = 1 with the lane's whole INT8 key row loaded before the
+// query, so the two memory round trips overlap.
+template <bool HYBRID, int D, int NQ, int NW>
+__global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in) {
+    constexpr bool PRE = NQ <= 2;                      // key row preloaded
     const AttnArgs a = resolve(a_in);
-    __shared__ float qsh[SQ_NQ][D];
-    __shared__ float wsh[4][SQ_NQ][64];
-    __shared__ float msh[4][SQ_NQ][2];
+    __shared__ float qsh[NQ][D];
+    __shared__ float wsh[NW][NQ][64];
+    __shared__ float msh[NW][NQ][2];
     const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-    const int gq = a.gq, qr = SQ_NQ / gq;
+    const int gq = a.gq, qr = NQ / gq;
     const int ngrp = (a.S + qr - 1) / qr;
     size_t gy = blockIdx.y;                            // (b, row group, kv head)
     const int kvh = (int)(gy % a.Hkv);
@@ -343,13 +348,6 @@ __global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
     const size_t b = gy / ngrp;
     const int d = a.d;
     const int h0 = kvh * gq;
-    for (int i = threadIdx.x; i < SQ_NQ * D; i += 256) {
-        const int v = i / D, dim = i % D;
-        const int qp = qp0 + v / gq;
-        qsh[v][dim] = qp < a.S ? h2f(a.q[((b * a.S + qp) * a.Hq + h0 + v % gq) * (size_t)d + dim]) : 0.0f;
-    }
-    __syncthreads();
-
     // per query vector: its row's key range (kv_start is 0 on this path)
     const float NEG_INF = -__builtin_inff();
     size_t kv_end_max = 0;
@@ -359,19 +357,11 @@ __global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
         kv_range<HYBRID>(a, (size_t)(qp0 + r), s0, e, bl);
         if (e > kv_end_max) kv_end_max = e;
     }
-    const size_t chunk = (size_t)blockIdx.x * 4 + wid;
+    const size_t chunk = (size_t)blockIdx.x * NW + wid;
     const size_t wbase = chunk * 64;                   // first key of the wave
-    if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
     const int jl = lane & 31;
     const size_t bs0 = wbase + (lane & 32);
     const size_t kp = wbase + lane;
-
-    // ---- dot products of this lane's key with every query vector
-    float acc[SQ_NQ][8];
-#pragma unroll
-    for (int q = 0; q < SQ_NQ; q++)
-#pragma unroll
-        for (int c = 0; c < 8; c++) acc[q][c] = 0.0f;
     const bool kload = kp < kv_end_max;
     const bool kint8 = HYBRID && kp < a.cache_len;
     const int8_t* krow8 = nullptr;
@@ -385,13 +375,36 @@ __global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
         const size_t klen = HYBRID ? a.new_len : a.Skv;
         krow16 = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
     }
+    uint4 pre[PRE ? D / 16 : 1];
+    float pres = 0.0f;
+    if constexpr (PRE) {
+        if (kload && kint8) {
+#pragma unroll
+            for (int m = 0; m < D / 16; m++) pre[m] = *reinterpret_cast<const uint4*>(krow8 + 16 * m);
+            pres = ksr[0];
+        }
+    }
+    for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
+        const int v = i / D, dim = i % D;
+        const int qp = qp0 + v / gq;
+        qsh[v][dim] = qp < a.S ? h2f(a.q[((b * a.S + qp) * a.Hq + h0 + v % gq) * (size_t)d + dim]) : 0.0f;
+    }
+    __syncthreads();
+    if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
+
+    // ---- dot products of this lane's key with every query vector
+    float acc[NQ][8];
+#pragma unroll
+    for (int q = 0; q < NQ; q++)
+#pragma unroll
+        for (int c = 0; c < 8; c++) acc[q][c] = 0.0f;
     const int lr = lane & 15;
 #pragma unroll
     for (int m = 0; m < D / 16; m++) {
         float kk[16];
         if (kload && kint8) {
-            const uint4 raw = *reinterpret_cast<const uint4*>(krow8 + 16 * m);
-            const float s = ksr[(16 * m) / a.qgs];
+            const uint4 raw = PRE ? pre[PRE ? m : 0] : *reinterpret_cast<const uint4*>(krow8 + 16 * m);
+            const float s = (PRE && a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs];
             const float ns = -128.0f * s;
             const uint32_t w4[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
                                     raw.w ^ 0x80808080u};
@@ -411,15 +424,15 @@ __global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
 #pragma unroll
             for (int e = 0; e < 16; e++) kk[e] = 0.0f;
         }
-        float qv[SQ_NQ];
+        float qv[NQ];
 #pragma unroll
-        for (int q = 0; q < SQ_NQ; q++) qv[q] = qsh[q][16 * m + lr];
-        sq_group16(acc, qv, kk, std::make_integer_sequence<int, 16>{});
+        for (int q = 0; q < NQ; q++) qv[q] = qsh[q][16 * m + lr];
+        sq_group16<NQ>(acc, qv, kk, std::make_integer_sequence<int, 16>{});
     }
 
     // ---- per query vector: mask, block max, weight, stores
 #pragma unroll
-    for (int q = 0; q < SQ_NQ; q++) {
+    for (int q = 0; q < NQ; q++) {
         const int qp = qp0 + q / gq;
         const bool row_ok = qp < a.S;
         const size_t aq = a.pos_off + qp;
@@ -460,7 +473,7 @@ __global__ void __launch_bounds__(256) attn_scores_rows_kernel(AttnArgs a_in) {
     }
     wave_lds_order();
     // ---- block sums, one lane per (query vector, block), reference order
-    if (lane < 2 * SQ_NQ) {
+    if (lane < 2 * NQ) {
         const int q = lane >> 1, half = lane & 1;
         const int qp = qp0 + q / gq;
         const size_t bs = wbase + 32 * half;
@@ -1919,15 +1932,29 @@ static int launch_attention(AttnArgs a, void* stream) {
     // prefill scores: several query rows per wave (16-dim DPP groups, one
     // scale per 16 dims, 16-byte key rows)
     const bool k16 = HYBRID ? ((uintptr_t)a.kc % 16 == 0 && (uintptr_t)a.ks % 4 == 0 && a.qgs % 16 == 0) : true;
-    if (chunks > 0 && !windowed && (size_t)a.B * a.S > 2 && (a.d == 64 || a.d == 128) && a.gq <= SQ_NQ &&
-        SQ_NQ % a.gq == 0 && k16 && (uintptr_t)a.k % 16 == 0) {
+    const bool rows_ok = chunks > 0 && !windowed && (a.d == 64 || a.d == 128) && a.gq <= SQ_NQ &&
+                         SQ_NQ % a.gq == 0 && k16 && (uintptr_t)a.k % 16 == 0;
+    if (rows_ok && (size_t)a.B * a.S > 2) {
         const int qr = SQ_NQ / a.gq;
         dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * ((a.S + qr - 1) / qr) * a.Hkv));
         if (a.d == 64)
-            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 64>), ga, dim3(256), 0, as_stream(stream), a);
+            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 64, SQ_NQ, 4>), ga, dim3(256), 0, as_stream(stream), a);
         else
-            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 128>), ga, dim3(256), 0, as_stream(stream), a);
+            hipLaunchKernelGGL((attn_scores_rows_kernel<HYBRID, 128, SQ_NQ, 4>), ga, dim3(256), 0, as_stream(stream), a);
         rc = check_launch("attention scores (rows)");
+        if (rc) return rc;
+    } else if (rows_ok && (a.gq == 1 || a.gq == 2)) {
+        // decode: one query row, its gq heads per wave, one wave per 64 keys
+        dim3 ga((unsigned)chunks, (unsigned)((size_t)a.B * a.S * a.Hkv));
+        auto go = [&](auto kern) { hipLaunchKernelGGL(kern, ga, dim3(64), 0, as_stream(stream), a); };
+        if (a.d == 64) {
+            if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 64, 1, 1>);
+            else go(attn_scores_rows_kernel<HYBRID, 64, 2, 1>);
+        } else {
+            if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 128, 1, 1>);
+            else go(attn_scores_rows_kernel<HYBRID, 128, 2, 1>);
+        }
+        rc = check_launch("attention scores (decode)");
         if (rc) return rc;
     } else if (chunks > 0) {
         dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * a.S * a.Hkv));
