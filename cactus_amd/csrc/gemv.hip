@@ -1,12 +1,15 @@
 // gemv.hip -- grouped INT8 / packed-INT4 matmul for small M (decode GEMV).
 //
-// Weights are streamed as a flat run of 16-byte chunks: one workgroup owns
-// `rows` consecutive weight rows ([rows][K] int8, or [rows][K/2] packed INT4),
-// so its loads are fully coalesced whatever K is.  Each chunk is dotted with
-// the int8 activation codes held in LDS (v_dot4_i32_i8); the lanes that share
-// one quantization group are summed exactly in int32 with cross-lane shuffles
-// and the group sum goes to LDS.  One thread per output then runs the
-// reference epilogue (kernel_gemm.cpp:311-324):
+// Weights are streamed as a flat run of 16-byte chunks: consecutive weight
+// rows ([rows][K] int8, or [rows][K/2] packed INT4) are one contiguous run,
+// so the loads are fully coalesced whatever K is.  The main kernel
+// (gemv_wave_kernel) gives each wave its own tiles of whole rows and needs
+// no workgroup barrier after the prologue; the block-tiled kernel
+// (gemv_grouped_kernel) serves rows longer than a wave tile.  Each chunk is
+// dotted with the int8 activation codes held in LDS (v_dot4_i32_i8); the
+// lanes that share one quantization group are summed exactly in int32 with
+// cross-lane shuffles and the group sum goes to LDS.  One lane per output
+// then runs the reference epilogue (kernel_gemm.cpp:311-324):
 //     r = fma((float)acc_g, (float)B_scale[n][g], r)   for g = 0..G-1
 //     C = fp16(r * A_scale[m])
 // With an FP16 activation input the per-row quantization of
