@@ -21,6 +21,7 @@
 //     key, in increasing position, exactly as the reference.  The output is
 //     fp16(acc * (1/sum)) on the 8-aligned prefix of head_dim.
 #include "hip_common.h"
+#include "decode_device.h"
 
 #include <map>
 #include <utility>
@@ -61,6 +62,18 @@ struct AttnArgs {
     // fp32 value-product tiles of the INT8 cache (kv_shadow.hip), or null
     const float* vsh;
     size_t sh_ntile;
+    // decode step with the head preparation fused into the scores (null
+    // q_raw: q and the new key row come prepared in q and k): raw q / k / v
+    // rows of the step, head RMSNorm weights, RoPE tables, and the cache
+    // rows the new key and value are appended to
+    struct {
+        const uint16_t* q_raw; const uint16_t* k_raw; const uint16_t* v_raw;
+        const uint16_t* q_norm; const uint16_t* k_norm;
+        const uint16_t* cos_t; const uint16_t* sin_t;
+        float eps;
+        uint32_t table_pos;
+        int8_t* kc; int8_t* vc; float* ks; float* vs; float* vsh;
+    } prep;
 };
 
 __device__ __forceinline__ AttnArgs resolve(const AttnArgs& in) {
@@ -384,10 +397,62 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             pres = ksr[0];
         }
     }
-    for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
-        const int v = i / D, dim = i % D;
-        const int qp = qp0 + v / gq;
-        qsh[v][dim] = qp < a.S ? h2f(a.q[((b * a.S + qp) * a.Hq + h0 + v % gq) * (size_t)d + dim]) : 0.0f;
+    // decode form with the head preparation fused in (one wave, one row):
+    // q of the group's heads and, in the chunk holding it, the new key row
+    // get the reference's head RMSNorm and RoPE here (the step's attn_prep
+    // arithmetic, kernel_attention.cpp:484-676); that chunk also appends the
+    // new key and value to the INT8 cache (and the value's product tiles)
+    __shared__ uint16_t prow[2][PRE ? D : 1];
+    __shared__ uint16_t krot[PRE ? D : 1];
+    if constexpr (PRE && NW == 1) {
+        if (a.prep.q_raw) {
+            const bool appender = blockIdx.x == gridDim.x - 1;
+            if (!appender && wbase >= kv_end_max) return;   // one wave: no barrier waits for it
+            const int end8 = (d / 8) * 8, half = d / 2;
+            const uint32_t pos = (uint32_t)a.pos_off;
+            const bool tab_ok = pos < a.prep.table_pos;
+            const uint16_t* ct = a.prep.cos_t + (size_t)(tab_ok ? pos : 0) * half;
+            const uint16_t* stb = a.prep.sin_t + (size_t)(tab_ok ? pos : 0) * half;
+            auto head = [&](const uint16_t* src, const uint16_t* nw, auto out) {
+                for (int i = lane; i < d; i += 64) prow[0][i] = src[i];
+                wave_lds_order();
+                float inv;
+                uint16_t hinv;
+                rms_stats_wave(prow[0], d, a.prep.eps, inv, hinv);
+                for (int i = lane; i < d; i += 64) prow[1][i] = rms_apply(prow[0][i], nw[i], i, end8, inv, hinv);
+                wave_lds_order();
+                rope_row(prow[1], d, ct, stb, out);
+                wave_lds_order();
+            };
+            if (appender) {
+                // the extra workgroup of the kv head appends the step's key
+                // and value to the cache (read by later steps only)
+                head(a.prep.k_raw + (size_t)kvh * d, a.prep.k_norm, [&](int i, uint16_t o) { krot[i] = o; });
+                if (tab_ok && a.cache_len < a.max_cache) {
+                    const int ng = (d + 127) / 128;
+                    const size_t crow = (size_t)a.cache_len * a.Hkv + kvh;
+                    kv_append_row(krot, a.prep.kc + crow * d, a.prep.ks + crow * ng, d);
+                    kv_append_row(a.prep.v_raw + (size_t)kvh * d, a.prep.vc + crow * d, a.prep.vs + crow * ng, d,
+                                  a.prep.vsh, a.sh_ntile, a.cache_len, kvh);
+                }
+                return;
+            }
+#pragma unroll
+            for (int v = 0; v < NQ; v++)
+                head(a.prep.q_raw + (size_t)(h0 + v) * d, a.prep.q_norm,
+                     [&](int i, uint16_t o) { qsh[v][i] = tab_ok ? h2f(o) : 0.0f; });
+            if (wbase <= a.cache_len && a.cache_len < wbase + 64) {
+                head(a.prep.k_raw + (size_t)kvh * d, a.prep.k_norm, [&](int i, uint16_t o) { krot[i] = o; });
+                if (kp == a.cache_len) krow16 = krot;
+            }
+        }
+    }
+    if (!(PRE && NW == 1) || !a.prep.q_raw) {
+        for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
+            const int v = i / D, dim = i % D;
+            const int qp = qp0 + v / gq;
+            qsh[v][dim] = qp < a.S ? h2f(a.q[((b * a.S + qp) * a.Hq + h0 + v % gq) * (size_t)d + dim]) : 0.0f;
+        }
     }
     __syncthreads();
     if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
@@ -1934,6 +1999,9 @@ static int launch_attention(AttnArgs a, void* stream) {
     const bool k16 = HYBRID ? ((uintptr_t)a.kc % 16 == 0 && (uintptr_t)a.ks % 4 == 0 && a.qgs % 16 == 0) : true;
     const bool rows_ok = chunks > 0 && !windowed && (a.d == 64 || a.d == 128) && a.gq <= SQ_NQ &&
                          SQ_NQ % a.gq == 0 && k16 && (uintptr_t)a.k % 16 == 0;
+    CH_REQUIRE(!a.prep.q_raw || (rows_ok && (size_t)a.B * a.S <= 2 && (a.gq == 1 || a.gq == 2)),
+               "decode attention with fused head preparation: needs head_dim 64 or 128, 1 or 2 query heads "
+               "per KV head and 16-byte aligned rows");
     if (rows_ok && (size_t)a.B * a.S > 2) {
         const int qr = SQ_NQ / a.gq;
         dim3 ga((unsigned)((chunks + 3) / 4), (unsigned)((size_t)a.B * ((a.S + qr - 1) / qr) * a.Hkv));
@@ -1945,7 +2013,9 @@ static int launch_attention(AttnArgs a, void* stream) {
         if (rc) return rc;
     } else if (rows_ok && (a.gq == 1 || a.gq == 2)) {
         // decode: one query row, its gq heads per wave, one wave per 64 keys
-        dim3 ga((unsigned)chunks, (unsigned)((size_t)a.B * a.S * a.Hkv));
+        // (with the fused head preparation, one more workgroup per kv head
+        // appends the step's key and value)
+        dim3 ga((unsigned)(chunks + (a.prep.q_raw ? 1 : 0)), (unsigned)((size_t)a.B * a.S * a.Hkv));
         auto go = [&](auto kern) { hipLaunchKernelGGL(kern, ga, dim3(64), 0, as_stream(stream), a); };
         if (a.d == 64) {
             if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 64, 1, 1>);
@@ -2113,6 +2183,27 @@ int attention_hybrid_decode(const uint16_t* q, const int8_t* kc, const int8_t* v
     a.causal = 1; a.scale = scale; a.qgs = 128; a.nqg = (d + 127) / 128;
     a.dyn = state; a.max_cache = max_cache;
     a.vsh = v_shadow; a.sh_ntile = shadow_tiles;
+    CH_REQUIRE(!v_shadow || shadow_tiles * CD_T >= max_cache, "decode attention: product tiles too short");
+    return launch_attention<true>(a, stream);
+}
+
+int attention_hybrid_decode_prep(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                 const uint16_t* cos_t, const uint16_t* sin_t, uint32_t table_pos,
+                                 int8_t* kc, int8_t* vc, float* ks, float* vs, float* v_shadow,
+                                 uint16_t* o, int Hq, int Hkv, int d, float scale, const uint32_t* state,
+                                 size_t max_cache, size_t shadow_tiles, void* stream) {
+    AttnArgs a{};
+    a.q = q_raw; a.k = k_raw; a.v = v_raw; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.o = o;
+    a.B = 1; a.S = 1; a.Hq = Hq; a.Hkv = Hkv; a.gq = Hq / Hkv; a.d = d;
+    a.new_len = 1; a.cache_len = max_cache; a.Skv = max_cache + 1; a.pos_off = max_cache;
+    a.causal = 1; a.scale = scale; a.qgs = 128; a.nqg = (d + 127) / 128;
+    a.dyn = state; a.max_cache = max_cache;
+    a.vsh = v_shadow; a.sh_ntile = shadow_tiles;
+    a.prep.q_raw = q_raw; a.prep.k_raw = k_raw; a.prep.v_raw = v_raw;
+    a.prep.q_norm = q_norm; a.prep.k_norm = k_norm; a.prep.cos_t = cos_t; a.prep.sin_t = sin_t;
+    a.prep.eps = eps; a.prep.table_pos = table_pos;
+    a.prep.kc = kc; a.prep.vc = vc; a.prep.ks = ks; a.prep.vs = vs; a.prep.vsh = v_shadow;
     CH_REQUIRE(!v_shadow || shadow_tiles * CD_T >= max_cache, "decode attention: product tiles too short");
     return launch_attention<true>(a, stream);
 }

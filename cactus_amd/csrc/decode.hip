@@ -19,6 +19,7 @@
 //               the step state (engine_model.cpp:221-297)
 #include "gemv_device.h"
 #include "lm_device.h"
+#include "decode_device.h"
 
 namespace cactus_hip {
 
@@ -26,54 +27,12 @@ int attention_hybrid_decode(const uint16_t* q, const int8_t* kc, const int8_t* v
                             const float* vs, const uint16_t* k_new, const uint16_t* v_new,
                             uint16_t* o, int Hq, int Hkv, int d, float scale, const uint32_t* state,
                             size_t max_cache, const float* v_shadow, size_t shadow_tiles, void* stream);
-
-// ----------------------------------------------------------------- RMSNorm
-// 1/rms of an fp16 row held in LDS, in the reference's order (16 fp32 FMA
-// chains, kernel_attention.cpp:500-538).  Called by one whole wave; every
-// lane returns inv and fp16(inv).
-__device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float eps, float& inv,
-                                               uint16_t& hinv) {
-    const int lane = threadIdx.x & 63;
-    float chain = 0.0f;
-    const int n16 = n / 16, end8 = (n / 8) * 8;
-    if (lane < 16) {
-        int i = 0;
-        // 16 reads in flight per batch, then the chain steps
-        for (; i + 16 <= n16; i += 16) {
-            float v[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++) v[j] = h2f(xs[(i + j) * 16 + lane]);
-#pragma unroll
-            for (int j = 0; j < 16; j++) chain = __builtin_fmaf(v[j], v[j], chain);
-        }
-        for (; i < n16; i++) {
-            const float v = h2f(xs[i * 16 + lane]);
-            chain = __builtin_fmaf(v, v, chain);
-        }
-        if (lane < 8 && n16 * 16 + 8 <= n) {
-            const float a = h2f(xs[n16 * 16 + lane]);
-            chain = __builtin_fmaf(a, a, chain);
-        }
-    }
-    const float c4 = __shfl(chain, (lane + 4) & 63, 64);
-    const float c8 = __shfl(chain, (lane + 8) & 63, 64);
-    const float c12 = __shfl(chain, (lane + 12) & 63, 64);
-    const float t = ((chain + c4) + c8) + c12;
-    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
-    float ss = (t0 + t1) + (t2 + t3);
-    for (int k = end8; k < n; k++) {
-        const float a = h2f(xs[k]);
-        ss = __builtin_fmaf(a, a, ss);
-    }
-    const float rms = __builtin_sqrtf(ss / (float)n + eps);
-    inv = 1.0f / rms;
-    hinv = f2h(inv);
-}
-
-__device__ __forceinline__ uint16_t rms_apply(uint16_t x, uint16_t w, int i, int end8, float inv,
-                                              uint16_t hinv) {
-    return i < end8 ? hmul(hmul(x, hinv), w) : f2h((h2f(x) * inv) * h2f(w));
-}
+int attention_hybrid_decode_prep(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                 const uint16_t* cos_t, const uint16_t* sin_t, uint32_t table_pos,
+                                 int8_t* kc, int8_t* vc, float* ks, float* vs, float* v_shadow,
+                                 uint16_t* o, int Hq, int Hkv, int d, float scale, const uint32_t* state,
+                                 size_t max_cache, size_t shadow_tiles, void* stream);
 
 // ----------------------------------------------------------------- embed
 __global__ void dec_embed_kernel(const uint16_t* __restrict__ table, const uint32_t* __restrict__ st,
@@ -333,36 +292,6 @@ struct PrepArgs {
     size_t sh_ntile;
 };
 
-// quantize_group_fp16_to_int8 per 128-dim group (kernel_quants.cpp:223-264);
-// with `sh`, also the row's fp32 products (float)code * scale into the
-// product tiles (kv_shadow.hip layout, key `key`, kv head `h`)
-__device__ __forceinline__ void kv_append_row(const uint16_t* src, int8_t* dst, float* scales, int d,
-                                              float* sh = nullptr, size_t ntile = 0, size_t key = 0, int h = 0) {
-    const int lane = threadIdx.x & 63;
-    const int nsl = (d + 63) / 64, da = (d / 8) * 8;
-    for (int g0 = 0, g = 0; g0 < d; g0 += 128, g++) {
-        const int cnt = min(128, d - g0);
-        float m = 0.0f;
-        for (int i = lane; i < cnt; i += 64) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(src[g0 + i])));
-        m = wave_max(m);
-        const float s = row_scale_from_max(m);
-        const float inv = 1.0f / s;
-        const int body = (cnt / 8) * 8;
-        for (int i = lane; i < cnt; i += 64) {
-            const float v = h2f(src[g0 + i]) * inv;
-            const int32_t c = i < body ? cvt_rne_sat(v) : (int32_t)__builtin_roundf(v);
-            const int8_t code = (int8_t)sat8(c);
-            dst[g0 + i] = code;
-            if (sh) {
-                const int dim = g0 + i;
-                const float p = dim < da ? (float)code * s : 0.0f;
-                sh[(((size_t)h * nsl + dim / 64) * ntile + key / 64) * (64 * 68) + (dim % 64) * 68 + key % 64] = p;
-            }
-        }
-        if (lane == 0) scales[g] = s;
-    }
-}
-
 __global__ void __launch_bounds__(64) dec_attn_prep_kernel(PrepArgs a) {
     __shared__ uint16_t xs[256];
     __shared__ uint16_t ys[256];
@@ -383,26 +312,12 @@ __global__ void __launch_bounds__(64) dec_attn_prep_kernel(PrepArgs a) {
     rms_stats_wave(xs, d, a.eps, inv, hinv);
     for (int i = lane; i < d; i += 64) ys[i] = rms_apply(xs[i], nw[i], i, end8, inv, hinv);
     __syncthreads();
-    // RoPE (kernel_attention.cpp:640-671) at absolute position `pos`
-    const uint16_t* ct = a.cos_t + (size_t)pos * half;
-    const uint16_t* stb = a.sin_t + (size_t)pos * half;
-    const int vh = (half / 8) * 8;
-    for (int i = lane; i < half; i += 64) {
-        const uint16_t x1 = ys[i], x2 = ys[i + half], c = ct[i], s = stb[i];
-        uint16_t o1, o2;
-        if (i < vh) {
-            o1 = hfma(x2 ^ 0x8000u, s, hmul(x1, c));
-            o2 = hfma(x1, s, hmul(x2, c));
-        } else {
-            const float fa = h2f(x1), fb = h2f(x2), cf = h2f(c), sf = h2f(s);
-            o1 = f2h(fa * cf - fb * sf);
-            o2 = f2h(fb * cf + fa * sf);
-        }
-        out[i] = o1;
-        out[i + half] = o2;
-        xs[i] = o1;          // keep the roped row for the cache append
-        xs[i + half] = o2;
-    }
+    // RoPE at absolute position `pos`; the roped row stays in xs for the
+    // cache append
+    rope_row(ys, d, a.cos_t + (size_t)pos * half, a.sin_t + (size_t)pos * half, [&](int i, uint16_t v) {
+        out[i] = v;
+        xs[i] = v;
+    });
     __syncthreads();
     if (!is_q && clen < a.max_cache) {
         const int ng = (d + 127) / 128;
@@ -780,6 +695,25 @@ int cactus_hip_decode_attention(const uint16_t* q, const int8_t* k_cache, const 
     return attention_hybrid_decode(q, k_cache, v_cache, k_scales, v_scales, k_new, v_new, o,
                                    (int)num_q_heads, (int)num_kv_heads, (int)head_dim, scale, state,
                                    max_cache, v_shadow, (max_cache + 63) / 64, stream);
+}
+
+int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                     const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                     size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float theta,
+                                     const uint32_t* state, int8_t* k_cache, int8_t* v_cache,
+                                     float* k_scales, float* v_scales, size_t max_cache, float* v_shadow,
+                                     float scale, uint16_t* o, void* stream) {
+    CH_REQUIRE(q_raw && k_raw && v_raw && q_norm && k_norm && state && k_cache && v_cache && k_scales &&
+               v_scales && o, "decode_prep_attention: null pointer");
+    CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "decode_prep_attention: bad head counts");
+    CH_REQUIRE(head_dim == 64 || head_dim == 128, "decode_prep_attention: head_dim must be 64 or 128");
+    const RopeTable* t = nullptr;
+    int rc = rope_table(max_cache + 1, head_dim, theta, &t);
+    if (rc) return rc;
+    return attention_hybrid_decode_prep(q_raw, k_raw, v_raw, q_norm, k_norm, eps, t->cos_d, t->sin_d,
+                                        (uint32_t)t->npos, k_cache, v_cache, k_scales, v_scales, v_shadow, o,
+                                        (int)num_q_heads, (int)num_kv_heads, (int)head_dim, scale, state,
+                                        max_cache, (max_cache + 63) / 64, stream);
 }
 
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,

@@ -1,0 +1,112 @@
+// decode_device.h -- per-row pieces of the Qwen3 decode step shared by the
+// fused decode kernels and the decode attention: the reference's RMSNorm
+// statistics and scaling, the head RoPE, and the INT8 KV-cache append.
+#pragma once
+#include "quant_device.h"
+
+namespace cactus_hip {
+
+// ----------------------------------------------------------------- RMSNorm
+// 1/rms of an fp16 row held in LDS, in the reference's order (16 fp32 FMA
+// chains, kernel_attention.cpp:500-538).  Called by one whole wave; every
+// lane returns inv and fp16(inv).
+__device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float eps, float& inv,
+                                               uint16_t& hinv) {
+    const int lane = threadIdx.x & 63;
+    float chain = 0.0f;
+    const int n16 = n / 16, end8 = (n / 8) * 8;
+    if (lane < 16) {
+        int i = 0;
+        // 16 reads in flight per batch, then the chain steps
+        for (; i + 16 <= n16; i += 16) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = h2f(xs[(i + j) * 16 + lane]);
+#pragma unroll
+            for (int j = 0; j < 16; j++) chain = __builtin_fmaf(v[j], v[j], chain);
+        }
+        for (; i < n16; i++) {
+            const float v = h2f(xs[i * 16 + lane]);
+            chain = __builtin_fmaf(v, v, chain);
+        }
+        if (lane < 8 && n16 * 16 + 8 <= n) {
+            const float a = h2f(xs[n16 * 16 + lane]);
+            chain = __builtin_fmaf(a, a, chain);
+        }
+    }
+    const float c4 = __shfl(chain, (lane + 4) & 63, 64);
+    const float c8 = __shfl(chain, (lane + 8) & 63, 64);
+    const float c12 = __shfl(chain, (lane + 12) & 63, 64);
+    const float t = ((chain + c4) + c8) + c12;
+    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    float ss = (t0 + t1) + (t2 + t3);
+    for (int k = end8; k < n; k++) {
+        const float a = h2f(xs[k]);
+        ss = __builtin_fmaf(a, a, ss);
+    }
+    const float rms = __builtin_sqrtf(ss / (float)n + eps);
+    inv = 1.0f / rms;
+    hinv = f2h(inv);
+}
+
+__device__ __forceinline__ uint16_t rms_apply(uint16_t x, uint16_t w, int i, int end8, float inv,
+                                              uint16_t hinv) {
+    return i < end8 ? hmul(hmul(x, hinv), w) : f2h((h2f(x) * inv) * h2f(w));
+}
+
+// RoPE of one head row held in LDS (kernel_attention.cpp:640-671) at the
+// tables' row for the position: pairs (i, i + d/2); the 8-aligned part of
+// the half row in fp16 arithmetic, the tail in fp32.  Writes the rotated
+// fp16 values through out(i, value).  One whole wave.
+template <class Out>
+__device__ __forceinline__ void rope_row(const uint16_t* ys, int d, const uint16_t* ct, const uint16_t* stb,
+                                         Out out) {
+    const int lane = threadIdx.x & 63;
+    const int half = d / 2, vh = (half / 8) * 8;
+    for (int i = lane; i < half; i += 64) {
+        const uint16_t x1 = ys[i], x2 = ys[i + half], c = ct[i], s = stb[i];
+        uint16_t o1, o2;
+        if (i < vh) {
+            o1 = hfma(x2 ^ 0x8000u, s, hmul(x1, c));
+            o2 = hfma(x1, s, hmul(x2, c));
+        } else {
+            const float fa = h2f(x1), fb = h2f(x2), cf = h2f(c), sf = h2f(s);
+            o1 = f2h(fa * cf - fb * sf);
+            o2 = f2h(fb * cf + fa * sf);
+        }
+        out(i, o1);
+        out(i + half, o2);
+    }
+}
+
+// quantize_group_fp16_to_int8 per 128-dim group (kernel_quants.cpp:223-264);
+// with `sh`, also the row's fp32 products (float)code * scale into the
+// product tiles (kv_shadow.hip layout, key `key`, kv head `h`)
+__device__ __forceinline__ void kv_append_row(const uint16_t* src, int8_t* dst, float* scales, int d,
+                                              float* sh = nullptr, size_t ntile = 0, size_t key = 0, int h = 0) {
+    const int lane = threadIdx.x & 63;
+    const int nsl = (d + 63) / 64, da = (d / 8) * 8;
+    for (int g0 = 0, g = 0; g0 < d; g0 += 128, g++) {
+        const int cnt = min(128, d - g0);
+        float m = 0.0f;
+        for (int i = lane; i < cnt; i += 64) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(src[g0 + i])));
+        m = wave_max(m);
+        const float s = row_scale_from_max(m);
+        const float inv = 1.0f / s;
+        const int body = (cnt / 8) * 8;
+        for (int i = lane; i < cnt; i += 64) {
+            const float v = h2f(src[g0 + i]) * inv;
+            const int32_t c = i < body ? cvt_rne_sat(v) : (int32_t)__builtin_roundf(v);
+            const int8_t code = (int8_t)sat8(c);
+            dst[g0 + i] = code;
+            if (sh) {
+                const int dim = g0 + i;
+                const float p = dim < da ? (float)code * s : 0.0f;
+                sh[(((size_t)h * nsl + dim / 64) * ntile + key / 64) * (64 * 68) + (dim % 64) * 68 + key % 64] = p;
+            }
+        }
+        if (lane == 0) scales[g] = s;
+    }
+}
+
+}  // namespace cactus_hip

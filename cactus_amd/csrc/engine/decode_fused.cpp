@@ -1,8 +1,10 @@
 // decode_fused.cpp -- fused decode path of QwenModel (decode mode 1).
 //
 // Per layer: qkv (RMSNorm + INT8 GEMV x3), attn_prep (q/k RMSNorm, RoPE,
-// INT8 KV append), attention (scores + value chains), o-proj + residual,
-// mlp_up (RMSNorm + INT4 gate/up + SiLU*mul), down + residual.  Then the LM
+// INT8 KV append) and attention (scores + value chains) -- for head_dim 64
+// or 128 with one or two query heads per KV head, the prep runs inside the
+// score kernel --, o-proj + residual, mlp_up (RMSNorm + INT4 gate/up +
+// SiLU*mul), down + residual.  Then the LM
 // head with the fused argmax advances the device step state.  Bit-identical
 // to decode mode 0 (the node-by-node graph).
 #include <cstdlib>
@@ -49,6 +51,10 @@ void FusedDecoder::enqueue() {
     uint16_t* h = h_.as<uint16_t>();
     KVCache& kv = m_.cache();
     auto u16 = [](const DevBuf& b) { return b.as<uint16_t>(); };
+    // head preparation inside the attention's score kernel where the shape
+    // allows (one kernel fewer per layer)
+    const size_t gqa = c.heads / c.kv_heads;
+    const bool fused_prep = (hd == 64 || hd == 128) && (gqa == 1 || gqa == 2);
     check_hip(cactus_hip_decode_embed(u16(m_.embedding()), state, h, H, c.vocab, st), "decode_embed");
     for (uint32_t l = 0; l < c.num_layers; l++) {
         const QwenLayer& L = m_.layer(l);
@@ -57,17 +63,28 @@ void FusedDecoder::enqueue() {
                                         k_raw_.as<uint16_t>(), nkv, L.v_w.as<int8_t>(), u16(L.v_s),
                                         v_raw_.as<uint16_t>(), nkv, st),
                   "decode_qkv");
-        check_hip(cactus_hip_decode_attn_prep(q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(),
-                                              u16(L.q_norm), u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd,
-                                              c.rope_theta, state, q_rot_.as<uint16_t>(), k_rot_.as<uint16_t>(),
-                                              kv.keys_mut(l), kv.values_mut(l), kv.key_scales_mut(l),
-                                              kv.value_scales_mut(l), kv.max_seq_len, kv.value_products(l), st),
-                  "decode_attn_prep");
-        check_hip(cactus_hip_decode_attention(q_rot_.as<uint16_t>(), kv.keys(l), kv.values(l), kv.key_scales(l),
-                                              kv.value_scales(l), k_rot_.as<uint16_t>(), v_raw_.as<uint16_t>(),
-                                              attn_.as<uint16_t>(), c.heads, c.kv_heads, hd, m_.attention_scale(),
-                                              state, kv.max_seq_len, kv.value_products(l), st),
-                  "decode_attention");
+        if (fused_prep) {
+            check_hip(cactus_hip_decode_prep_attention(
+                          q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(), u16(L.q_norm),
+                          u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd, c.rope_theta, state, kv.keys_mut(l),
+                          kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l), kv.max_seq_len,
+                          kv.value_products(l), m_.attention_scale(), attn_.as<uint16_t>(), st),
+                      "decode_prep_attention");
+        } else {
+            check_hip(cactus_hip_decode_attn_prep(q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(),
+                                                  v_raw_.as<uint16_t>(), u16(L.q_norm), u16(L.k_norm), c.eps,
+                                                  c.heads, c.kv_heads, hd, c.rope_theta, state,
+                                                  q_rot_.as<uint16_t>(), k_rot_.as<uint16_t>(), kv.keys_mut(l),
+                                                  kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l),
+                                                  kv.max_seq_len, kv.value_products(l), st),
+                      "decode_attn_prep");
+            check_hip(cactus_hip_decode_attention(q_rot_.as<uint16_t>(), kv.keys(l), kv.values(l),
+                                                  kv.key_scales(l), kv.value_scales(l), k_rot_.as<uint16_t>(),
+                                                  v_raw_.as<uint16_t>(), attn_.as<uint16_t>(), c.heads,
+                                                  c.kv_heads, hd, m_.attention_scale(), state, kv.max_seq_len,
+                                                  kv.value_products(l), st),
+                      "decode_attention");
+        }
         check_hip(cactus_hip_decode_matmul_residual(attn_.as<uint16_t>(), nq, gs, L.o_w.ptr, u16(L.o_s), H, 0, h,
                                                     st),
                   "decode_o_proj");

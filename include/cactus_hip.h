@@ -263,6 +263,17 @@ int cactus_hip_decode_attention(const uint16_t* q, const int8_t* k_cache, const 
                                 size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
                                 float scale, const uint32_t* state, size_t max_cache,
                                 const float* v_shadow, void* stream);
+/* cactus_hip_decode_attn_prep followed by cactus_hip_decode_attention (k_new =
+ * the prepared key, v_new = v_raw) with the head preparation done inside
+ * the attention's score kernel: one kernel fewer per layer.  head_dim 64 or
+ * 128, one or two query heads per KV head. */
+int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_raw,
+                                     const uint16_t* v_raw, const uint16_t* q_norm,
+                                     const uint16_t* k_norm, float eps, size_t num_q_heads,
+                                     size_t num_kv_heads, size_t head_dim, float theta,
+                                     const uint32_t* state, int8_t* k_cache, int8_t* v_cache,
+                                     float* k_scales, float* v_scales, size_t max_cache,
+                                     float* v_shadow, float scale, uint16_t* o, void* stream);
 /* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
  * and advances state.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,

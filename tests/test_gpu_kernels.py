@@ -42,6 +42,13 @@ class Dev:
         self.cm.call("cactus_hip_stream_sync", None)
         return buf.to_numpy(dtype, shape)
 
+    def get_ptr(self, ptr, dtype, shape):
+        """Copy of a buffer made by put (a raw device pointer)."""
+        out = np.empty(shape, dtype)
+        self.cm.call("cactus_hip_stream_sync", None)
+        self.cm.call("cactus_hip_memcpy_d2h", out.ctypes.data, ptr, out.nbytes, None)
+        return out
+
 
 @pytest.fixture
 def dev(hip_ready):
@@ -455,6 +462,78 @@ def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, qmul, shadow):
     dev.cm.call("cactus_hip_decode_attention", dev.put(q), dev.put(kc), vcp, dev.put(ks), vsp, dev.put(kn),
                 dev.put(vn), o.ptr, Hq, Hkv, d, ctypes.c_float(scale), dev.put(state), cap, shp, None)
     assert_bits(dev.get(o, np.uint16, q.shape), ref, "decode attention")
+
+
+@pytest.mark.parametrize("cache,Hq,Hkv,d", [(4095, 16, 8, 128), (700, 4, 4, 64), (127, 4, 2, 128)])
+@pytest.mark.parametrize("shadow", [True, False])
+def test_decode_prep_attention_fused(dev, orc, cache, Hq, Hkv, d, shadow):
+    """The head preparation fused into the attention's score kernel equals
+    cactus_hip_decode_attn_prep followed by cactus_hip_decode_attention:
+    the same output bits and the same appended cache row (codes, scales and
+    product tiles); the output is also the oracle's hybrid attention on the
+    prepared q and key."""
+    say("decode_prep_attention", cache, Hq, Hkv, d, "shadow" if shadow else "int8")
+    rng = np.random.default_rng(cache * 7 + d)
+    cap = cache + 21
+    kc, ks = orc.quantize_kv(f16(rng.normal(0, 1, (cap, Hkv, d))))
+    vc, vs = orc.quantize_kv(f16(rng.normal(0, 1, (cap, Hkv, d))))
+    q_raw = f16(rng.normal(0, 1, (Hq, d)))
+    k_raw = f16(rng.normal(0, 1, (Hkv, d)))
+    v_raw = f16(rng.normal(0, 1, (Hkv, d)))
+    qn = f16(rng.normal(1, 0.2, d))
+    kn = f16(rng.normal(1, 0.2, d))
+    eps, theta, scale = 1e-6, 1e6, 1.0 / math.sqrt(d)
+    state = dev.put(np.array([0, cache, cache, 0], np.uint32))
+
+    def caches():
+        bufs = [dev.put(kc), dev.put(vc), dev.put(ks), dev.put(vs)]
+        sh = None
+        if shadow:
+            nbytes = ctypes.c_size_t()
+            dev.cm.call("cactus_hip_kv_shadow_bytes", cap, Hkv, d, ctypes.byref(nbytes))
+            sh = dev.empty(nbytes.value)
+            dev.cm.call("cactus_hip_kv_shadow_update", bufs[1], bufs[3], sh.ptr, 0, cache, Hkv, d, 128, cap, None)
+        return bufs, sh
+
+    args = lambda: (dev.put(q_raw), dev.put(k_raw), dev.put(v_raw), dev.put(qn), dev.put(kn))
+    # separate kernels
+    (kcA, vcA, ksA, vsA), shA = caches()
+    qa, ka, va, qna, kna = args()
+    q_out, k_out, oA = dev.empty(q_raw.nbytes), dev.empty(k_raw.nbytes), dev.empty(q_raw.nbytes)
+    dev.cm.call("cactus_hip_decode_attn_prep", qa, ka, va, qna, kna, ctypes.c_float(eps), Hq, Hkv, d,
+                ctypes.c_float(theta), state, q_out.ptr, k_out.ptr, kcA, vcA, ksA, vsA, cap,
+                shA.ptr if shadow else None, None)
+    dev.cm.call("cactus_hip_decode_attention", q_out.ptr, kcA, vcA, ksA, vsA, k_out.ptr, va, oA.ptr, Hq, Hkv, d,
+                ctypes.c_float(scale), state, cap, shA.ptr if shadow else None, None)
+    # fused
+    (kcB, vcB, ksB, vsB), shB = caches()
+    qb, kb, vb, qnb, knb = args()
+    oB = dev.empty(q_raw.nbytes)
+    dev.cm.call("cactus_hip_decode_prep_attention", qb, kb, vb, qnb, knb, ctypes.c_float(eps), Hq, Hkv, d,
+                ctypes.c_float(theta), state, kcB, vcB, ksB, vsB, cap, shB.ptr if shadow else None,
+                ctypes.c_float(scale), oB.ptr, None)
+    got_a = dev.get(oA, np.uint16, (Hq, d))
+    got_b = dev.get(oB, np.uint16, (Hq, d))
+    assert_bits(got_b, got_a, "fused output")
+    for name, x, y, dt, shp in (("k codes", kcA, kcB, np.int8, (cap, Hkv, d)), ("v codes", vcA, vcB, np.int8, (cap, Hkv, d)),
+                                ("k scales", ksA, ksB, np.float32, (cap, Hkv, 1)),
+                                ("v scales", vsA, vsB, np.float32, (cap, Hkv, 1))):
+        a_, b_ = dev.get_ptr(x, dt, shp), dev.get_ptr(y, dt, shp)
+        assert (a_[cache] == b_[cache]).all(), name + " of the appended row"
+        assert (a_[:cache] == b_[:cache]).all(), name + " before the appended row"
+    if shadow:
+        # written entries only: keys 0..cache (padding and later keys are
+        # never written, so two fresh buffers differ there)
+        ts = (Hkv, (d + 63) // 64, (cap + 63) // 64, 64, 68)
+        keys = np.arange(cache + 1)
+        ta = dev.get(shA, np.float32, ts)[:, :, keys // 64, :, keys % 64]
+        tb = dev.get(shB, np.float32, ts)[:, :, keys // 64, :, keys % 64]
+        assert (ta.view(np.uint32) == tb.view(np.uint32)).all(), "product tiles"
+    qp = dev.get(q_out, np.uint16, (Hq, d)).reshape(1, 1, Hq, d)
+    kp = dev.get(k_out, np.uint16, (Hkv, d)).reshape(1, 1, Hkv, d)
+    ref = orc.attention_hybrid(qp, kc[None, :cache], vc[None, :cache], ks[None, :cache], vs[None, :cache], kp,
+                               v_raw.reshape(1, 1, Hkv, d), scale, pos_off=cache)
+    assert_bits(got_b.reshape(1, 1, Hq, d), ref, "fused output vs oracle")
 
 
 # ------------------------------------------------------------------ a7
