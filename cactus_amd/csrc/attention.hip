@@ -402,32 +402,82 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     // get the reference's head RMSNorm and RoPE here (the step's attn_prep
     // arithmetic, kernel_attention.cpp:484-676); that chunk also appends the
     // new key and value to the INT8 cache (and the value's product tiles)
-    __shared__ uint16_t prow[2][PRE ? D : 1];
+    __shared__ uint16_t prow[PRE ? NQ + 1 : 1][PRE ? D : 1];
+    __shared__ uint16_t pys[PRE ? NQ + 1 : 1][PRE ? D : 1];
     __shared__ uint16_t krot[PRE ? D : 1];
     if constexpr (PRE && NW == 1) {
         if (a.prep.q_raw) {
             const bool appender = blockIdx.x == gridDim.x - 1;
             if (!appender && wbase >= kv_end_max) return;   // one wave: no barrier waits for it
-            const int end8 = (d / 8) * 8, half = d / 2;
+            const int end8 = (d / 8) * 8, half = d / 2, vh = (half / 8) * 8;
             const uint32_t pos = (uint32_t)a.pos_off;
             const bool tab_ok = pos < a.prep.table_pos;
-            const uint16_t* ct = a.prep.cos_t + (size_t)(tab_ok ? pos : 0) * half;
-            const uint16_t* stb = a.prep.sin_t + (size_t)(tab_ok ? pos : 0) * half;
-            auto head = [&](const uint16_t* src, const uint16_t* nw, auto out) {
-                for (int i = lane; i < d; i += 64) prow[0][i] = src[i];
-                wave_lds_order();
-                float inv;
-                uint16_t hinv;
-                rms_stats_wave(prow[0], d, a.prep.eps, inv, hinv);
-                for (int i = lane; i < d; i += 64) prow[1][i] = rms_apply(prow[0][i], nw[i], i, end8, inv, hinv);
-                wave_lds_order();
-                rope_row(prow[1], d, ct, stb, out);
-                wave_lds_order();
-            };
+            const bool has_k = appender || (wbase <= a.cache_len && a.cache_len < wbase + 64);
+            const int nq = appender ? 0 : NQ;            // q rows of this workgroup
+            // every operand of the rows' RMSNorm and RoPE is loaded up front
+            constexpr int EPL = D / 64;                   // elements per lane of a row
+            uint16_t raw[NQ + 1][EPL], nwq[EPL], nwk[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; e++) {
+                const int i = lane + 64 * e;
+#pragma unroll
+                for (int r = 0; r < NQ; r++) raw[r][e] = nq ? a.prep.q_raw[(size_t)(h0 + r) * d + i] : (uint16_t)0;
+                raw[NQ][e] = has_k ? a.prep.k_raw[(size_t)kvh * d + i] : (uint16_t)0;
+                nwq[e] = a.prep.q_norm[i];
+                nwk[e] = a.prep.k_norm[i];
+            }
+            const size_t trow = (size_t)(tab_ok ? pos : 0) * half;
+            const uint16_t cv = lane < half ? a.prep.cos_t[trow + lane] : (uint16_t)0;
+            const uint16_t sv = lane < half ? a.prep.sin_t[trow + lane] : (uint16_t)0;
+            // rows r < nq: q heads h0 + r; row NQ: the new key
+#pragma unroll
+            for (int r = 0; r <= NQ; r++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++) prow[r][lane + 64 * e] = raw[r][e];
+            wave_lds_order();
+            float inv[NQ + 1];
+            uint16_t hinv[NQ + 1];
+#pragma unroll
+            for (int r = 0; r <= NQ; r++) {
+                inv[r] = 0.0f;
+                hinv[r] = 0;
+                if ((r < nq) || (r == NQ && has_k)) rms_stats_wave(prow[r], d, a.prep.eps, inv[r], hinv[r]);
+            }
+#pragma unroll
+            for (int r = 0; r <= NQ; r++)
+#pragma unroll
+                for (int e = 0; e < EPL; e++) {
+                    const int i = lane + 64 * e;
+                    pys[r][i] = rms_apply(raw[r][e], r < NQ ? nwq[e] : nwk[e], i, end8, inv[r], hinv[r]);
+                }
+            wave_lds_order();
+            // RoPE (kernel_attention.cpp:640-671): pair (i, i + d/2), lane i
+#pragma unroll
+            for (int r = 0; r <= NQ; r++) {
+                if (lane < half && ((r < nq) || (r == NQ && has_k))) {
+                    const uint16_t x1 = pys[r][lane], x2 = pys[r][lane + half];
+                    uint16_t o1, o2;
+                    if (lane < vh) {
+                        o1 = hfma(x2 ^ 0x8000u, sv, hmul(x1, cv));
+                        o2 = hfma(x1, sv, hmul(x2, cv));
+                    } else {
+                        const float fa = h2f(x1), fb = h2f(x2), cf = h2f(cv), sf = h2f(sv);
+                        o1 = f2h(fa * cf - fb * sf);
+                        o2 = f2h(fb * cf + fa * sf);
+                    }
+                    if (r < NQ) {
+                        qsh[r][lane] = tab_ok ? h2f(o1) : 0.0f;
+                        qsh[r][lane + half] = tab_ok ? h2f(o2) : 0.0f;
+                    } else {
+                        krot[lane] = o1;
+                        krot[lane + half] = o2;
+                    }
+                }
+            }
+            wave_lds_order();
             if (appender) {
                 // the extra workgroup of the kv head appends the step's key
                 // and value to the cache (read by later steps only)
-                head(a.prep.k_raw + (size_t)kvh * d, a.prep.k_norm, [&](int i, uint16_t o) { krot[i] = o; });
                 if (tab_ok && a.cache_len < a.max_cache) {
                     const int ng = (d + 127) / 128;
                     const size_t crow = (size_t)a.cache_len * a.Hkv + kvh;
@@ -437,14 +487,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
                 }
                 return;
             }
-#pragma unroll
-            for (int v = 0; v < NQ; v++)
-                head(a.prep.q_raw + (size_t)(h0 + v) * d, a.prep.q_norm,
-                     [&](int i, uint16_t o) { qsh[v][i] = tab_ok ? h2f(o) : 0.0f; });
-            if (wbase <= a.cache_len && a.cache_len < wbase + 64) {
-                head(a.prep.k_raw + (size_t)kvh * d, a.prep.k_norm, [&](int i, uint16_t o) { krot[i] = o; });
-                if (kp == a.cache_len) krow16 = krot;
-            }
+            if (has_k && kp == a.cache_len) krow16 = krot;
         }
     }
     if (!(PRE && NW == 1) || !a.prep.q_raw) {
