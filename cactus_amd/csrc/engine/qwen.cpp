@@ -172,14 +172,24 @@ void QwenModel::reset() {
     graph_->soft_reset();
 }
 
+// Input of matmuls that share it: at prefill sizes its per-row INT8
+// quantization (graph_ops_nn.cpp:35-66, the same codes and scales every
+// matmul node would compute for itself) runs once as a node of its own;
+// a decode-sized GEMV quantizes inside its kernel at no extra launch.
+size_t QwenModel::shared_matmul_input(size_t x) {
+    CactusGraph& g = *graph_;
+    return g.get_output_buffer(x).shape[0] >= 32 ? g.quantize_activations(x) : x;
+}
+
 // model_qwen.cpp:51-106
 size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
     const size_t hd = cfg_.head_dim, nh = cfg_.heads, nkv = cfg_.kv_heads;
-    size_t q = g.matmul(x, L.n_q, true);
-    size_t k = g.matmul(x, L.n_k, true);
-    size_t v = g.matmul(x, L.n_v, true);
+    const size_t xq = shared_matmul_input(x);
+    size_t q = g.matmul(xq, L.n_q, true);
+    size_t k = g.matmul(xq, L.n_k, true);
+    size_t v = g.matmul(xq, L.n_v, true);
     const size_t S = g.get_output_buffer(q).shape[0];
     q = g.reshape(q, {S * nh, hd});
     q = g.rms_norm(q, L.n_q_norm, cfg_.eps);
@@ -211,8 +221,9 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
 size_t QwenModel::build_mlp(size_t x, uint32_t l) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
-    size_t gate = g.matmul(x, L.n_gate, true);
-    size_t up = g.matmul(x, L.n_up, true);
+    const size_t xq = shared_matmul_input(x);
+    size_t gate = g.matmul(xq, L.n_gate, true);
+    size_t up = g.matmul(xq, L.n_up, true);
     size_t act = g.silu(gate);
     size_t m = g.multiply(act, up);
     return g.matmul(m, L.n_down, true);
