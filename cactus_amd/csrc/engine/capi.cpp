@@ -4,12 +4,15 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <string>
 #include <thread>
 #include <vector>
 
+#include "cact_file.h"
 #include "cactus_hip.h"
 #include "engine.h"
+#include "loader.h"
 
 namespace cactus {
 
@@ -160,6 +163,33 @@ static void make_random(const cactus_qwen_config& c, uint64_t seed, HostWeights&
     }
 }
 
+static void fill_info(const CactHeader& h, cactus_cact_info* info) {
+    if (!info) return;
+    std::memset(info, 0, sizeof(*info));
+    info->version = h.version;
+    info->flags = h.flags;
+    info->alignment = h.alignment;
+    info->ndim = h.ndim;
+    for (int i = 0; i < 4; i++) info->shape[i] = h.dims[i];
+    info->precision = h.precision;
+    info->group_size = h.group_size;
+    info->num_groups = h.num_groups;
+    info->data_bytes = h.data_bytes;
+    info->scales_bytes = h.scales_bytes;
+    info->scales_offset = h.scales_offset;
+    info->data_offset = h.data_offset;
+}
+
+// A graph of the file API with a stream of its own.
+struct GraphHandle {
+    void* stream = nullptr;
+    std::unique_ptr<CactusGraph> g;
+    ~GraphHandle() {
+        g.reset();
+        if (stream) cactus_hip_stream_destroy(stream);
+    }
+};
+
 static void validate(const cactus_qwen_config* c) {
     if (!c) throw std::runtime_error("null config");
     if (!c->num_layers || !c->hidden || !c->ffn || !c->heads || !c->kv_heads || !c->head_dim ||
@@ -307,6 +337,134 @@ int cactus_qwen_read_weights(void* model, cactus_qwen_layer_weights* lw, uint16_
             rd(w.gate_w, L.gate_w); rd(w.gate_s, L.gate_s); rd(w.up_w, L.up_w); rd(w.up_s, L.up_s);
             rd(w.down_w, L.down_w); rd(w.down_s, L.down_s);
         }
+    });
+}
+
+// ---------------------------------------------------------------- tensor files
+int cactus_cact_read_info(const char* path, cactus_cact_info* info) {
+    return guarded([&] {
+        if (!path || !info) throw std::runtime_error("null argument");
+        CactFile f(path);
+        fill_info(f.header(), info);
+    });
+}
+
+int cactus_cact_save(const char* path, const uint64_t* shape, uint32_t ndim, uint32_t precision,
+                     const void* data, uint64_t data_bytes, const uint16_t* scales, uint32_t group_size,
+                     uint32_t num_groups) {
+    return guarded([&] {
+        if (!path || (ndim && !shape) || (data_bytes && !data)) throw std::runtime_error("null argument");
+        if (precision > static_cast<uint32_t>(Precision::INT4)) throw std::runtime_error("unknown precision");
+        std::vector<size_t> sh(shape, shape + ndim);
+        save_cact(path, sh, static_cast<Precision>(precision), data, data_bytes, scales, group_size, num_groups);
+    });
+}
+
+int cactus_cact_load_device(const char* path, cactus_cact_info* info, void** data, void** scales) {
+    return guarded([&] {
+        if (!path || !data) throw std::runtime_error("null argument");
+        CactFile f(path);
+        void* st = nullptr;
+        check_hip(cactus_hip_stream_create(&st), "stream_create");
+        DeviceTensor t;
+        try {
+            t = upload_cact(f, st);
+        } catch (...) {
+            cactus_hip_stream_destroy(st);
+            throw;
+        }
+        cactus_hip_stream_destroy(st);
+        fill_info(f.header(), info);
+        *data = t.data;
+        if (scales) *scales = t.scales;
+        else if (t.scales) cactus_hip_free(t.scales);
+    });
+}
+
+int cactus_qwen_read_config(const char* folder, cactus_qwen_config* cfg) {
+    return guarded([&] {
+        if (!folder || !cfg) throw std::runtime_error("null argument");
+        *cfg = read_qwen_config(folder);
+    });
+}
+
+int cactus_qwen_create_from_folder(const char* folder, size_t context_size, void** model) {
+    return guarded([&] {
+        if (!folder || !model) throw std::runtime_error("null argument");
+        *model = load_qwen_folder(folder, context_size);
+    });
+}
+
+int cactus_graph_create(void** graph) {
+    return guarded([&] {
+        if (!graph) throw std::runtime_error("null argument");
+        auto h = std::make_unique<GraphHandle>();
+        check_hip(cactus_hip_stream_create(&h->stream), "stream_create");
+        h->g = std::make_unique<CactusGraph>(h->stream);
+        *graph = h.release();
+    });
+}
+
+int cactus_graph_destroy(void* graph) {
+    return guarded([&] { delete static_cast<GraphHandle*>(graph); });
+}
+
+int cactus_graph_load_weights(void* graph, const char* path, size_t* node) {
+    return guarded([&] {
+        if (!graph || !path || !node) throw std::runtime_error("null argument");
+        *node = static_cast<GraphHandle*>(graph)->g->load_weights(path);
+    });
+}
+
+int cactus_graph_mmap_embeddings(void* graph, const char* path, size_t* node) {
+    return guarded([&] {
+        if (!graph || !path || !node) throw std::runtime_error("null argument");
+        *node = static_cast<GraphHandle*>(graph)->g->mmap_embeddings(path);
+    });
+}
+
+int cactus_graph_save_node(void* graph, size_t node, const char* path) {
+    return guarded([&] {
+        if (!graph || !path) throw std::runtime_error("null argument");
+        static_cast<GraphHandle*>(graph)->g->save_node(node, path);
+    });
+}
+
+int cactus_graph_node_info(void* graph, size_t node, cactus_graph_node_desc* desc) {
+    return guarded([&] {
+        if (!graph || !desc) throw std::runtime_error("null argument");
+        const BufferDesc& b = static_cast<GraphHandle*>(graph)->g->get_output_buffer(node);
+        std::memset(desc, 0, sizeof(*desc));
+        if (b.shape.size() > 4) throw std::runtime_error("node has more than 4 dimensions");
+        desc->ndim = (uint32_t)b.shape.size();
+        for (size_t i = 0; i < b.shape.size(); i++) desc->shape[i] = b.shape[i];
+        desc->precision = b.is_packed_int4() ? static_cast<uint32_t>(Precision::INT4) : static_cast<uint32_t>(b.precision);
+        desc->data_bytes = b.is_packed_int4() ? b.packed_int4_size : b.byte_size;
+        desc->group_size = (uint32_t)b.group_size;
+        desc->num_groups = (uint32_t)b.num_groups;
+    });
+}
+
+int cactus_graph_read_node(void* graph, size_t node, void* data, uint64_t capacity, uint16_t* scales,
+                           uint64_t scales_capacity) {
+    return guarded([&] {
+        if (!graph) throw std::runtime_error("null argument");
+        GraphHandle* h = static_cast<GraphHandle*>(graph);
+        const BufferDesc& b = h->g->get_output_buffer(node);
+        const bool packed = b.is_packed_int4();
+        const void* src = packed ? b.packed_int4 : b.data;
+        const size_t n = packed ? b.packed_int4_size : b.byte_size;
+        if (!src) throw std::runtime_error("node has no data");
+        if (data) {
+            if (capacity < n) throw std::runtime_error("data capacity too small");
+            check_hip(cactus_hip_memcpy_d2h(data, src, n, h->stream), "read_node");
+        }
+        if (scales && b.scales && b.num_groups) {
+            const size_t sb = (b.shape.empty() ? 1 : b.shape[0]) * b.num_groups * 2;
+            if (scales_capacity < sb) throw std::runtime_error("scales capacity too small");
+            check_hip(cactus_hip_memcpy_d2h(scales, b.scales, sb, h->stream), "read_node scales");
+        }
+        check_hip(cactus_hip_stream_sync(h->stream), "read_node sync");
     });
 }
 

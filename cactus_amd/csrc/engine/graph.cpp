@@ -12,7 +12,9 @@
 #include <cstring>
 #include <numeric>
 
+#include "cact_file.h"
 #include "cactus_hip.h"
+#include "loader.h"
 
 namespace cactus {
 
@@ -278,6 +280,71 @@ void* CactusGraph::get_output(size_t id) {
     return m.data();
 }
 
+// ------------------------------------------------------------------ tensor files
+size_t CactusGraph::load_weights(const std::string& filename) {
+    auto it = weight_cache_.find(filename);
+    if (it != weight_cache_.end()) return it->second;
+    CactFile f(filename);
+    const CactHeader& h = f.header();
+    const bool int4 = h.precision == static_cast<uint32_t>(Precision::INT4);
+    const Precision eff = int4 ? Precision::INT8 : static_cast<Precision>(h.precision);
+    const size_t elems = numel(h.shape);
+    if (int4 && elems % 2) throw std::runtime_error(filename + ": INT4 tensor with an odd element count");
+    const size_t want = int4 ? elems / 2 : elems * precision_size(eff);
+    if (h.data_bytes != want)
+        throw std::runtime_error(filename + ": " + std::to_string(h.data_bytes) + " data bytes for " +
+                                 std::to_string(elems) + " elements");
+    DeviceTensor t = upload_cact(f, stream_);
+    owned_weights_.push_back(t.data);
+    if (t.scales) owned_weights_.push_back(t.scales);
+    const size_t id = input(h.shape, eff);
+    set_external_input(id, t.data, eff);
+    if (int4) {
+        set_packed_int4(id, t.data, h.data_bytes);
+        node(id).out.byte_size = h.data_bytes;
+    }
+    if (h.scales_bytes && h.group_size && h.num_groups) set_grouped_scales(id, h.group_size, h.num_groups, t.scales);
+    weight_cache_[filename] = id;
+    return id;
+}
+
+size_t CactusGraph::mmap_embeddings(const std::string& filename) {
+    {
+        CactFile f(filename);
+        if (f.shape().size() != 2)
+            throw std::runtime_error("Memory-mapped embeddings must be 2D [vocab_size, embedding_dim]");
+    }
+    return load_weights(filename);
+}
+
+void CactusGraph::save_node(size_t id, const std::string& filename) {
+    execute();
+    const BufferDesc& b = node(id).out;
+    const bool packed = b.is_packed_int4();
+    const void* src = packed ? b.packed_int4 : b.data;
+    const size_t n = packed ? b.packed_int4_size : b.byte_size;
+    if (!src) throw std::runtime_error("save_node: node has no data");
+    std::vector<unsigned char> host(n);
+    if (n) check_hip(cactus_hip_memcpy_d2h(host.data(), src, n, stream_), "save_node");
+    std::vector<uint16_t> sc;
+    const bool scaled = (b.precision == Precision::INT8) && b.group_size && b.num_groups && b.scales;
+    if (scaled) {
+        const size_t rows = b.shape.empty() ? 1 : b.shape[0];
+        sc.resize(rows * b.num_groups);
+        check_hip(cactus_hip_memcpy_d2h(sc.data(), b.scales, sc.size() * 2, stream_), "save_node scales");
+    }
+    check_hip(cactus_hip_stream_sync(stream_), "save_node sync");
+    save_cact(filename, b.shape, packed ? Precision::INT4 : b.precision, host.data(), n,
+              scaled ? sc.data() : nullptr, scaled ? b.group_size : 0, scaled ? b.num_groups : 0);
+}
+
+void CactusGraph::free_weights() {
+    cactus_hip_stream_sync(stream_);
+    for (void* p : owned_weights_) cactus_hip_free(p);
+    owned_weights_.clear();
+    weight_cache_.clear();
+}
+
 // ------------------------------------------------------------------ execution
 void CactusGraph::allocate(GraphNode& n) {
     if (n.op == OpType::INPUT) {
@@ -524,6 +591,7 @@ void CactusGraph::hard_reset() {
     host_mirror_.clear();
     next_id_ = 0;
     pool_.clear();
+    free_weights();
 }
 
 }  // namespace cactus

@@ -138,6 +138,17 @@ public:
     void* get_output(size_t node);                      // host mirror (synchronous)
     const BufferDesc& get_output_buffer(size_t node) const;
 
+    // --- tensor files (graph_io.cpp:25-101, :228-320): a CACT file becomes an
+    // INPUT node over a device copy the graph owns.  INT4 stays packed, the
+    // node keeping its shape in elements with precision INT8 (graph.h:526-528).
+    // Cached by file name; soft_reset keeps them, hard_reset frees them.
+    size_t load_weights(const std::string& filename);
+    size_t mmap_weights(const std::string& filename) { return load_weights(filename); }
+    size_t mmap_embeddings(const std::string& filename);   // 2D [vocab][dim] only
+    // GraphFile::save_node (graph_io.cpp:145-222): executes the graph, then
+    // writes the node's data (and INT8 group scales) with alignment 32
+    void save_node(size_t node, const std::string& filename);
+
     // --- execution
     void execute();
     void soft_reset();   // drop all non-INPUT nodes (weights stay)
@@ -167,6 +178,10 @@ private:
     void* quant_scales_ = nullptr;
     size_t quant_cap_ = 0, quant_rows_cap_ = 0;
     int* embed_err_ = nullptr;
+    // device copies of loaded tensor files
+    std::unordered_map<std::string, size_t> weight_cache_;
+    std::vector<void*> owned_weights_;
+    void free_weights();
 };
 
 void check_hip(int rc, const char* what);

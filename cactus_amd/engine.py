@@ -75,6 +75,24 @@ class Qwen:
                                                     ctypes.byref(h)))
         self.h = h.value
 
+    @classmethod
+    def from_folder(cls, folder, context_size: int) -> "Qwen":
+        """Model::init(model_folder, context_size) over a folder of CACT
+        tensor files and config.txt (cactus_qwen_create_from_folder)."""
+        self = cls.__new__(cls)
+        self.lib = engine()
+        self.h = None
+        c = QwenConfig()
+        path = str(folder).encode()
+        self._check(self.lib.cactus_qwen_read_config(path, ctypes.byref(c)))
+        c.max_seq = context_size
+        h = ctypes.c_void_p()
+        self._check(self.lib.cactus_qwen_create_from_folder(path, context_size, ctypes.byref(h)))
+        self.c = c
+        self.cfg = {name: getattr(c, name) for name, _ in QwenConfig._fields_}
+        self.h = h.value
+        return self
+
     def _check(self, rc):
         if rc != 0:
             raise NativeError(rc, self.lib.cactus_engine_last_error().decode(errors="replace"))

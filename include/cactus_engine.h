@@ -92,6 +92,70 @@ int cactus_qwen_read_kv(void* model, size_t layer, int8_t* k, int8_t* v, float* 
 int cactus_qwen_read_weights(void* model, cactus_qwen_layer_weights* layers_out_buffers,
                              uint16_t* embedding, uint16_t* output_norm);
 
+/* ---- CACT tensor files (cactus/graph/graph_io.cpp) -------------------------
+ * One tensor per file: an 80-byte little-endian header (magic "CACT",
+ * version, flags, alignment, ndim, dims[4] as u64, precision, data bytes,
+ * scales bytes, group size, group count), fp16 group scales [rows][groups]
+ * at align(80, alignment), data at align(end of scales, alignment).
+ * Precision: 0 INT8, 1 FP16, 2 FP32, 3 INT4 (two codes per byte, low nibble
+ * = even column) -- graph.h:99-104. */
+typedef struct {
+    uint32_t version, flags, alignment, ndim;
+    uint64_t shape[4];
+    uint32_t precision, group_size, num_groups;
+    uint64_t data_bytes, scales_bytes, scales_offset, data_offset;
+} cactus_cact_info;
+
+/* MappedFile::parse_header (graph_io.cpp:497-566); host only.  Fails on a
+ * short file, a wrong magic, scales or data past the end of the file, or an
+ * unknown precision. */
+int cactus_cact_read_info(const char* path, cactus_cact_info* info);
+/* GraphFile::save_node's layout (graph_io.cpp:145-222), alignment 32, from
+ * host buffers; scales may be NULL (then group_size and num_groups are
+ * written as 0).  Host only. */
+int cactus_cact_save(const char* path, const uint64_t* shape, uint32_t ndim, uint32_t precision,
+                     const void* data, uint64_t data_bytes, const uint16_t* scales, uint32_t group_size,
+                     uint32_t num_groups);
+/* GraphFile::load_into_graph (graph_io.cpp:228-320) to device memory: the
+ * data (INT4 stays packed) and the scales (NULL when the file has none),
+ * each from cactus_hip_malloc; release them with cactus_hip_free.  With
+ * scales == NULL the scales are not kept. */
+int cactus_cact_load_device(const char* path, cactus_cact_info* info, void** data, void** scales);
+
+/* Config::from_json over folder/config.txt (engine_model.cpp:403-520):
+ * key=value lines, '#' comments; keys not present keep the reference's
+ * defaults (engine.h:42-58).  group_size is read from
+ * layer_0_attn_q.weights; max_seq is 0.  Fails for model types other than
+ * Qwen, untied output weights and mixture-of-experts configs. */
+int cactus_qwen_read_config(const char* folder, cactus_qwen_config* cfg);
+/* Model::init(model_folder, context_size) (engine_model.cpp:47-160) over the
+ * reference's file names (model_qwen.cpp:17-42, token_embeddings.weights):
+ * FP16 embeddings and norms, grouped INT8 attention projections, packed INT4
+ * MLP, one group size.  Any other precision, shape or group layout is an
+ * error naming the file. */
+int cactus_qwen_create_from_folder(const char* folder, size_t context_size, void** model);
+
+/* A device graph for the file API (CactusGraph::load_weights / mmap_weights /
+ * mmap_embeddings, graph_io.cpp:25-101; GraphFile::save_node). */
+typedef struct {
+    uint32_t ndim;
+    uint64_t shape[4];
+    uint32_t precision;      /* 3 for packed INT4 nodes */
+    uint64_t data_bytes;
+    uint32_t group_size, num_groups;
+} cactus_graph_node_desc;
+
+int cactus_graph_create(void** graph);
+int cactus_graph_destroy(void* graph);
+int cactus_graph_load_weights(void* graph, const char* path, size_t* node);
+int cactus_graph_mmap_embeddings(void* graph, const char* path, size_t* node);
+int cactus_graph_save_node(void* graph, size_t node, const char* path);
+int cactus_graph_node_info(void* graph, size_t node, cactus_graph_node_desc* desc);
+/* Copies a node's data (packed bytes for INT4) and, when asked, its group
+ * scales to host memory. */
+int cactus_graph_read_node(void* graph, size_t node, void* data, uint64_t capacity, uint16_t* scales,
+                           uint64_t scales_capacity);
+
 #ifdef __cplusplus
 }
 #endif
