@@ -236,6 +236,14 @@ int cactus_qwen_set_decode_mode(void* model, int mode) {
     return guarded([&] { static_cast<QwenModel*>(model)->set_decode_mode(mode); });
 }
 
+int cactus_qwen_set_kv_window(void* model, size_t window, size_t sink) {
+    return guarded([&] { static_cast<QwenModel*>(model)->set_kv_window(window, sink); });
+}
+
+int cactus_qwen_total_len(void* model, size_t* len) {
+    return guarded([&] { *len = static_cast<QwenModel*>(model)->cache().total_seq_len; });
+}
+
 int cactus_qwen_prefill(void* model, const uint32_t* tokens, size_t n) {
     return guarded([&] {
         static_cast<QwenModel*>(model)->prefill(std::vector<uint32_t>(tokens, tokens + n));

@@ -7,8 +7,10 @@
 // SiLU*mul), down + residual.  Then the LM
 // head with the fused argmax advances the device step state.  Bit-identical
 // to decode mode 0 (the node-by-node graph).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <string>
 #include <stdexcept>
 
 #include "cactus_hip.h"
@@ -34,8 +36,32 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     const size_t blocks = (c.vocab + 127) / 128;   // cactus_hip_decode_lm_head's scratch contract
     lm_scratch_ = DevBuf(256 + 8 * blocks);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
-    check_hip(cactus_hip_rope_reserve(c.max_seq + 1, hd, c.rope_theta), "rope_reserve");
+    rope_pos_ = (size_t)c.max_seq + 1;
+    check_hip(cactus_hip_rope_reserve(rope_pos_, hd, c.rope_theta), "rope_reserve");
     check_hip(cactus_hip_stream_sync(m.stream()), "sync");
+}
+
+void FusedDecoder::reserve(size_t positions, size_t steps) {
+    const cactus_qwen_config& c = m_.config();
+    bool grown = false;
+    if (positions + 1 > rope_pos_ || steps > max_steps_) {
+        // nothing queued may still read the buffers being replaced
+        check_hip(cactus_hip_stream_sync(m_.stream()), "sync");
+    }
+    if (positions + 1 > rope_pos_) {
+        rope_pos_ = std::max(positions + 1, 2 * rope_pos_);
+        check_hip(cactus_hip_rope_reserve(rope_pos_, c.head_dim, c.rope_theta), "rope_reserve");
+        grown = true;
+    }
+    if (steps > max_steps_) {
+        max_steps_ = std::max(steps, 2 * max_steps_);
+        tokens_ = DevBuf(max_steps_ * 4);
+        grown = true;
+    }
+    if (grown && graph_) {
+        cactus_hip_graph_destroy(graph_);
+        graph_ = nullptr;
+    }
 }
 
 FusedDecoder::~FusedDecoder() {
@@ -67,7 +93,7 @@ void FusedDecoder::enqueue() {
             check_hip(cactus_hip_decode_prep_attention(
                           q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(), u16(L.q_norm),
                           u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd, c.rope_theta, state, kv.keys_mut(l),
-                          kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l), kv.max_seq_len,
+                          kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l), kv.slots,
                           kv.value_products(l), m_.attention_scale(), attn_.as<uint16_t>(), st),
                       "decode_prep_attention");
         } else {
@@ -76,12 +102,12 @@ void FusedDecoder::enqueue() {
                                                   c.heads, c.kv_heads, hd, c.rope_theta, state,
                                                   q_rot_.as<uint16_t>(), k_rot_.as<uint16_t>(), kv.keys_mut(l),
                                                   kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l),
-                                                  kv.max_seq_len, kv.value_products(l), st),
+                                                  kv.slots, kv.value_products(l), st),
                       "decode_attn_prep");
             check_hip(cactus_hip_decode_attention(q_rot_.as<uint16_t>(), kv.keys(l), kv.values(l),
                                                   kv.key_scales(l), kv.value_scales(l), k_rot_.as<uint16_t>(),
                                                   v_raw_.as<uint16_t>(), attn_.as<uint16_t>(), c.heads,
-                                                  c.kv_heads, hd, m_.attention_scale(), state, kv.max_seq_len,
+                                                  c.kv_heads, hd, m_.attention_scale(), state, kv.slots,
                                                   kv.value_products(l), st),
                       "decode_attention");
         }
@@ -125,35 +151,41 @@ void FusedDecoder::ensure_graph() {
 void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
     if (n == 0) return;
     KVCache& kv = m_.cache();
-    if (kv.current_seq_len + n > kv.max_seq_len)
-        throw std::runtime_error("KV cache capacity exceeded (sliding window not built)");
+    if (kv.window_size == 0 && kv.current_seq_len + n > kv.max_seq_len)
+        throw std::runtime_error("KV cache capacity exceeded (" + std::to_string(kv.current_seq_len + n) + " > " +
+                                 std::to_string(kv.max_seq_len) + " tokens; set a window or a larger context)");
+    reserve(kv.total_seq_len + n, n);
     set_state(token);
     // the fused step keeps neither the final hidden state nor the logits
     m_.last_hidden_ = SIZE_MAX;
     m_.last_logits_ = SIZE_MAX;
-    size_t done = 0;
-    if (!warmed_) {
-        // the first step runs eagerly: it allocates the library's scratch
-        // buffers outside of any capture; later steps replay the graph
-        enqueue();
-        warmed_ = true;
-        done = 1;
-    }
     // CACTUS_DECODE_EAGER=1 enqueues the step's kernels directly instead of
     // replaying the graph (same kernels and results; for kernel tracers)
     static const bool eager = [] {
         const char* e = std::getenv("CACTUS_DECODE_EAGER");
         return e && e[0] == '1';
     }();
-    if (eager) {
-        for (; done < n; done++) enqueue();
-    } else {
-        if (done < n) ensure_graph();
-        for (; done < n; done++) check_hip(cactus_hip_graph_launch(graph_, m_.stream()), "graph launch");
+    for (size_t done = 0; done < n; done++) {
+        // into a full window the step attends over the whole window plus its
+        // own token and appends at slot `window`; the slide follows
+        // (engine_cache.cpp:268-327 for seq_len 1)
+        const bool slides = kv.step_slides();
+        if (!warmed_ || eager) {
+            // the first step runs eagerly: it allocates the library's
+            // scratch buffers outside of any capture
+            enqueue();
+            warmed_ = true;
+        } else {
+            ensure_graph();
+            check_hip(cactus_hip_graph_launch(graph_, m_.stream()), "graph launch");
+        }
+        if (slides) kv.slide_after_step(state_.as<uint32_t>(), m_.stream());
+        else kv.current_seq_len += 1;
+        kv.total_seq_len += 1;
+        if (slides) kv.resident = kv.window_size;
+        else kv.resident = std::max(kv.resident, kv.current_seq_len);
     }
     check_hip(cactus_hip_memcpy_d2h(out, tokens_.ptr, n * 4, m_.stream()), "tokens");
-    kv.current_seq_len += n;
-    kv.total_seq_len += n;
 }
 
 uint32_t FusedDecoder::step(uint32_t token) {

@@ -28,17 +28,30 @@ struct DevBuf {
 };
 
 // INT8 KV cache, one per-token/per-kv-head scale per 128 dims
-// (KV_QUANT_GROUP_SIZE, kernel.h:18; engine_cache.cpp:234-267).  Append-only:
-// capacity must cover the sequence (the sliding window is not built).
+// (KV_QUANT_GROUP_SIZE, kernel.h:18; engine/engine_cache.cpp), with the
+// reference's sliding window and attention sinks.  Storage holds max_seq
+// tokens per layer (the context size); a window, when set, is at most that.
 class KVCache {
 public:
     static constexpr size_t GROUP = 128;
     void init(size_t layers, size_t max_seq, size_t kv_heads, size_t head_dim);
+    // KVCache::set_window_size (engine_cache.cpp:25-46): window 0 = none;
+    // the first `window` slots become codes 0, scales 1.0
+    void set_window(size_t window, size_t sink, void* stream);
     void reset() { current_seq_len = 0; total_seq_len = 0; }
     bool is_empty() const { return current_seq_len == 0; }
-    // quantize `seq` new fp16 tokens [seq][kv_heads][head_dim] of one layer
-    void append(size_t layer, const void* k_fp16, const void* v_fp16, size_t seq, void* stream);
-    void commit(size_t seq) { current_seq_len += seq; total_seq_len += seq; }
+    // KVCache::update_from_graph (engine_cache.cpp:103-330): k[l], v[l] are
+    // the fp16 rows [seq][kv_heads][head_dim] of layer l's new tokens.
+    // Throws where the reference's update is undefined (a sliding step
+    // longer than window - sink) or the storage would overflow.
+    void update(const std::vector<const void*>& k, const std::vector<const void*>& v, size_t seq, void* stream);
+    // After a one-token decode step into a full window (the fused path):
+    // the step attended over all `window` cached tokens plus its own and
+    // appended at slot `window` (the spare slot); tokens [sink + 1, window + 1)
+    // move down by one in every layer and the device step state's cache
+    // length returns to `window` -- the content update_from_graph leaves.
+    void slide_after_step(uint32_t* state, void* stream);
+    bool step_slides() const { return window_size > 0 && current_seq_len + 1 > window_size; }
     const int8_t* keys(size_t l) const { return k_[l].as<int8_t>(); }
     const int8_t* values(size_t l) const { return v_[l].as<int8_t>(); }
     const float* key_scales(size_t l) const { return ks_[l].as<float>(); }
@@ -53,9 +66,15 @@ public:
 
     size_t current_seq_len = 0, total_seq_len = 0;
     size_t max_seq_len = 0, num_layers = 0, num_kv_heads = 0, head_dim = 0;
+    size_t slots = 0;      // storage tokens per layer: max_seq_len + 1 (the fused step's spare slot)
+    size_t window_size = 0, sink_size = 0;
+    size_t resident = 0;   // tokens the reference's per-layer vectors would hold
 
 private:
+    void put(size_t l, const void* k, const void* v, size_t row0, size_t n, size_t at, void* stream);
+    void shift(size_t dst, size_t src, size_t count, uint32_t* state, uint32_t len, void* stream);
     std::vector<DevBuf> k_, v_, ks_, vs_, vsh_;
+    DevBuf table_, temp_;   // device layer records and move buffer of cactus_hip_kv_window_shift
 };
 
 struct QwenLayer {
@@ -79,6 +98,7 @@ public:
     // n greedy steps from `token` (decode mode 1 keeps them on the device)
     void decode_many(uint32_t token, size_t n, uint32_t* out);
     void set_decode_mode(int mode);
+    void set_kv_window(size_t window, size_t sink);
     int decode_mode() const { return decode_mode_; }
 
     const cactus_qwen_config& config() const { return cfg_; }

@@ -21,10 +21,14 @@ private:
     void enqueue();            // all launches of one step on the model stream
     void set_state(uint32_t token);
     void ensure_graph();
+    // RoPE positions and token slots for a run; a captured graph that would
+    // read past them is dropped and captured again
+    void reserve(size_t positions, size_t steps);
 
     QwenModel& m_;
     DevBuf state_, h_, q_raw_, k_raw_, v_raw_, q_rot_, k_rot_, attn_, mlp_, tokens_, lm_scratch_;
     size_t max_steps_ = 0;
+    size_t rope_pos_ = 0;      // positions the RoPE tables hold
     void* graph_ = nullptr;
     bool warmed_ = false;
 };

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cctype>
+#include <cstdlib>
 #include <fstream>
 #include <memory>
 #include <stdexcept>
@@ -210,8 +211,24 @@ QwenModel* load_qwen_folder(const std::string& folder, size_t context_size) {
         w.down_s = dn.scales();
     }
     // the constructor uploads and synchronizes before the maps close
-    return new QwenModel(c, lw.data(), static_cast<const uint16_t*>(emb.data()),
-                         static_cast<const uint16_t*>(out_norm.data()));
+    std::unique_ptr<QwenModel> m(new QwenModel(c, lw.data(), static_cast<const uint16_t*>(emb.data()),
+                                               static_cast<const uint16_t*>(out_norm.data())));
+    // engine_model.cpp:136-146: window min(context, 512), 4 sinks, both
+    // overridable from the environment
+    size_t window = std::min(context_size, (size_t)512), sink = 4;
+    auto env = [](const char* name, size_t& v) {
+        const char* e = std::getenv(name);
+        if (!e) return;
+        try {
+            v = std::stoul(e);
+        } catch (const std::exception&) {
+            throw std::runtime_error(std::string(name) + ": not a number: " + e);
+        }
+    };
+    env("CACTUS_KV_WINDOW_SIZE", window);
+    env("CACTUS_KV_SINK_SIZE", sink);
+    m->set_kv_window(window, sink);
+    return m.release();
 }
 
 }  // namespace cactus

@@ -41,37 +41,128 @@ void KVCache::init(size_t layers, size_t max_seq, size_t kv_heads, size_t hd) {
     max_seq_len = max_seq;
     num_kv_heads = kv_heads;
     head_dim = hd;
-    const size_t codes = max_seq * kv_heads * hd;
-    const size_t scales = max_seq * kv_heads * groups() * sizeof(float);
+    slots = max_seq + 1;
+    const size_t codes = slots * kv_heads * hd;
+    const size_t scales = slots * kv_heads * groups() * sizeof(float);
     size_t shadow = 0;
-    check_hip(cactus_hip_kv_shadow_bytes(max_seq, kv_heads, hd, &shadow), "kv shadow size");
+    check_hip(cactus_hip_kv_shadow_bytes(slots, kv_heads, hd, &shadow), "kv shadow size");
     k_.clear(); v_.clear(); ks_.clear(); vs_.clear(); vsh_.clear();
+    std::vector<cactus_hip_kv_layer> recs(layers);
     for (size_t l = 0; l < layers; l++) {
         k_.emplace_back(codes);
         v_.emplace_back(codes);
         ks_.emplace_back(scales);
         vs_.emplace_back(scales);
         vsh_.emplace_back(shadow);
+        recs[l] = {keys_mut(l), values_mut(l), key_scales_mut(l), value_scales_mut(l), value_products(l)};
     }
+    table_ = DevBuf(layers * sizeof(cactus_hip_kv_layer));
+    table_.upload(recs.data(), table_.bytes, nullptr);
+    check_hip(cactus_hip_stream_sync(nullptr), "kv table upload");
+    window_size = sink_size = resident = 0;
     reset();
 }
 
-void KVCache::append(size_t l, const void* kf, const void* vf, size_t seq, void* stream) {
-    if (current_seq_len + seq > max_seq_len)
-        throw std::runtime_error("KV cache capacity exceeded (sliding window not built)");
-    const size_t off = current_seq_len * num_kv_heads * head_dim;
-    const size_t soff = current_seq_len * num_kv_heads * groups();
-    check_hip(cactus_hip_quantize_kv_fp16_to_int8(static_cast<const uint16_t*>(kf), keys_mut(l) + off,
-                                                  key_scales_mut(l) + soff, seq, num_kv_heads, head_dim,
-                                                  GROUP, stream),
-              "kv append (keys)");
-    check_hip(cactus_hip_quantize_kv_fp16_to_int8(static_cast<const uint16_t*>(vf), values_mut(l) + off,
-                                                  value_scales_mut(l) + soff, seq, num_kv_heads, head_dim,
-                                                  GROUP, stream),
-              "kv append (values)");
-    check_hip(cactus_hip_kv_shadow_update(values(l), value_scales(l), value_products(l), current_seq_len, seq,
-                                          num_kv_heads, head_dim, GROUP, max_seq_len, stream),
-              "kv append (value products)");
+// engine_cache.cpp:25-46
+void KVCache::set_window(size_t window, size_t sink, void* stream) {
+    if (window > max_seq_len)
+        throw std::runtime_error("KV window " + std::to_string(window) + " exceeds the cache capacity " +
+                                 std::to_string(max_seq_len));
+    if (window && sink >= window) throw std::runtime_error("KV sink size must be smaller than the window");
+    window_size = window;
+    sink_size = sink;
+    if (!window) return;
+    const std::vector<float> ones(window * num_kv_heads * groups(), 1.0f);
+    size_t shadow = 0;
+    check_hip(cactus_hip_kv_shadow_bytes(slots, num_kv_heads, head_dim, &shadow), "kv shadow size");
+    for (size_t l = 0; l < num_layers; l++) {
+        check_hip(cactus_hip_memset(keys_mut(l), 0, window * num_kv_heads * head_dim, stream), "kv window");
+        check_hip(cactus_hip_memset(values_mut(l), 0, window * num_kv_heads * head_dim, stream), "kv window");
+        check_hip(cactus_hip_memcpy_h2d(key_scales_mut(l), ones.data(), ones.size() * 4, stream), "kv window");
+        check_hip(cactus_hip_memcpy_h2d(value_scales_mut(l), ones.data(), ones.size() * 4, stream), "kv window");
+        check_hip(cactus_hip_memset(value_products(l), 0, shadow, stream), "kv window");   // products of zeros
+    }
+    size_t tb = 0;
+    check_hip(cactus_hip_kv_shift_temp_bytes(num_layers, window + 1, num_kv_heads, head_dim, &tb), "kv temp size");
+    if (temp_.bytes < tb) temp_ = DevBuf(tb);
+    check_hip(cactus_hip_stream_sync(stream), "kv window sync");
+    resident = window;
+}
+
+// quantize rows [row0, row0 + n) of one layer's new K/V into slots [at, at + n)
+void KVCache::put(size_t l, const void* kf, const void* vf, size_t row0, size_t n, size_t at, void* stream) {
+    if (n == 0) return;
+    const size_t row = num_kv_heads * head_dim, srow = num_kv_heads * groups();
+    const uint16_t* k = static_cast<const uint16_t*>(kf) + row0 * row;
+    const uint16_t* v = static_cast<const uint16_t*>(vf) + row0 * row;
+    check_hip(cactus_hip_quantize_kv_fp16_to_int8(k, keys_mut(l) + at * row, key_scales_mut(l) + at * srow, n,
+                                                  num_kv_heads, head_dim, GROUP, stream),
+              "kv update (keys)");
+    check_hip(cactus_hip_quantize_kv_fp16_to_int8(v, values_mut(l) + at * row, value_scales_mut(l) + at * srow, n,
+                                                  num_kv_heads, head_dim, GROUP, stream),
+              "kv update (values)");
+    check_hip(cactus_hip_kv_shadow_update(values(l), value_scales(l), value_products(l), at, n, num_kv_heads,
+                                          head_dim, GROUP, slots, stream),
+              "kv update (value products)");
+}
+
+void KVCache::shift(size_t dst, size_t src, size_t count, uint32_t* state, uint32_t len, void* stream) {
+    check_hip(cactus_hip_kv_window_shift(table_.as<cactus_hip_kv_layer>(), num_layers, num_kv_heads, head_dim,
+                                         slots, dst, src, count, temp_.ptr, temp_.bytes, state, len, stream),
+              "kv window shift");
+}
+
+// engine_cache.cpp:103-330.  All layers take the same branch; the reference
+// shifts and appends layer by layer, here every layer shifts first (one
+// launch pair), then each appends -- the layers are independent.
+void KVCache::update(const std::vector<const void*>& k, const std::vector<const void*>& v, size_t seq,
+                     void* stream) {
+    if (seq == 0) return;
+    const size_t old = current_seq_len, nt = old + seq, W = window_size, S = sink_size;
+    const bool sliding = W > 0 && nt > W;
+    if (!sliding && nt > max_seq_len)
+        throw std::runtime_error("KV cache capacity exceeded (" + std::to_string(nt) + " > " +
+                                 std::to_string(max_seq_len) + " tokens; set a window or a larger context)");
+    if (old == 0) {
+        // the K/V nodes hold all new_total rows (:131-232)
+        if (!sliding) {
+            for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, nt, 0, stream);
+            resident = nt;
+        } else {
+            // sinks are written only when the storage was not window-sized
+            const bool first = resident != W;
+            const size_t skip = nt - W;
+            for (size_t l = 0; l < num_layers; l++) {
+                if (first) put(l, k[l], v[l], 0, S, 0, stream);
+                put(l, k[l], v[l], S + skip, W - S, S, stream);
+            }
+            resident = W;
+        }
+    } else if (!sliding) {
+        for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, seq, old, stream);
+        resident = nt;   // std::vector::resize to the new total (:238-240)
+    } else {
+        // window full: keep the sinks, slide the rest (:268-327); the
+        // reference's size_t arithmetic wraps for a step longer than W - S
+        if (seq > W - S)
+            throw std::runtime_error("KV update of " + std::to_string(seq) + " tokens into a full window of " +
+                                     std::to_string(W) + " with " + std::to_string(S) +
+                                     " sinks (the step must not exceed window - sink)");
+        const size_t tts = W - S - seq;
+        if (tts > 0 && old > S && old - tts > S) shift(S, old - tts, tts, nullptr, 0, stream);
+        for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, seq, W - seq, stream);
+        resident = W;
+    }
+    current_seq_len = sliding ? W : nt;
+    total_seq_len += seq;
+}
+
+void KVCache::slide_after_step(uint32_t* state, void* stream) {
+    const size_t W = window_size, S = sink_size;
+    if (W == 0 || current_seq_len != W) throw std::runtime_error("slide_after_step: the window is not full");
+    // update_from_graph with seq 1 moves [S + 1, W) to [S, W - 1) and appends
+    // at W - 1; the step already appended at W, so W - S tokens move
+    shift(S, S + 1, W - S, state, (uint32_t)W, stream);
 }
 
 // ------------------------------------------------------------------ QwenModel
@@ -259,10 +350,18 @@ size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
 
 // engine_model.cpp:317-321 -> engine_cache.cpp:234-267 (append branch)
 void QwenModel::update_kv_cache(size_t seq) {
-    for (uint32_t l = 0; l < cfg_.num_layers; l++)
-        cache_.append(l, graph_->get_output_buffer(k_nodes_[l]).data,
-                      graph_->get_output_buffer(v_nodes_[l]).data, seq, stream_);
-    cache_.commit(seq);
+    std::vector<const void*> k(cfg_.num_layers), v(cfg_.num_layers);
+    for (uint32_t l = 0; l < cfg_.num_layers; l++) {
+        k[l] = graph_->get_output_buffer(k_nodes_[l]).data;
+        v[l] = graph_->get_output_buffer(v_nodes_[l]).data;
+    }
+    cache_.update(k, v, seq, stream_);
+}
+
+// KVCache::set_window_size through the model (engine_model.cpp:136-146)
+void QwenModel::set_kv_window(size_t window, size_t sink) {
+    check_hip(cactus_hip_stream_sync(stream_), "sync");
+    cache_.set_window(window, sink, stream_);
 }
 
 // engine_model.cpp:170-219

@@ -35,6 +35,81 @@ __global__ void kv_shadow_kernel(const int8_t* __restrict__ vc, const float* __r
     }
 }
 
+// ---------------------------------------------------------------- window shift
+// Moving cached tokens [src, src + count) to [dst, dst + count) in every
+// layer (the sliding window's memmove, engine_cache.cpp:268-306).  The
+// ranges may overlap, so the move goes through `temp` in two launches: the
+// first copies the source tokens out, the second writes them to their new
+// slots and recomputes their value products with kv_shadow_kernel's
+// expression.  Grid (count, layers); a workgroup moves one token of one
+// layer: Hkv*d code bytes and Hkv*ng scales for keys and for values.
+struct KvLayer {
+    int8_t* k;
+    int8_t* v;
+    float* ks;
+    float* vs;
+    float* sh;
+};
+
+__global__ void kv_shift_out_kernel(const KvLayer* __restrict__ layers, unsigned char* __restrict__ temp,
+                                    size_t src, int Hkv, int d, size_t count) {
+    const KvLayer L = layers[blockIdx.y];
+    const size_t i = blockIdx.x;
+    const int nqg = (d + 127) / 128;
+    const size_t cb = (size_t)Hkv * d, sb = (size_t)Hkv * nqg;
+    unsigned char* t = temp + ((size_t)blockIdx.y * count + i) * (2 * cb + 2 * sb * 4);
+    const size_t tok = src + i;
+    for (size_t j = threadIdx.x; j < cb; j += blockDim.x) {
+        t[j] = (unsigned char)L.k[tok * cb + j];
+        t[cb + j] = (unsigned char)L.v[tok * cb + j];
+    }
+    float* ts = reinterpret_cast<float*>(t + 2 * cb);
+    for (size_t j = threadIdx.x; j < sb; j += blockDim.x) {
+        ts[j] = L.ks[tok * sb + j];
+        ts[sb + j] = L.vs[tok * sb + j];
+    }
+}
+
+__global__ void kv_shift_in_kernel(const KvLayer* __restrict__ layers, const unsigned char* __restrict__ temp,
+                                   size_t dst, int Hkv, int d, size_t count, size_t ntile, uint32_t* state,
+                                   uint32_t cache_len) {
+    const KvLayer L = layers[blockIdx.y];
+    const size_t i = blockIdx.x;
+    const int nqg = (d + 127) / 128;
+    const size_t cb = (size_t)Hkv * d, sb = (size_t)Hkv * nqg;
+    const unsigned char* t = temp + ((size_t)blockIdx.y * count + i) * (2 * cb + 2 * sb * 4);
+    const float* ts = reinterpret_cast<const float*>(t + 2 * cb);
+    const size_t key = dst + i;
+    for (size_t j = threadIdx.x; j < cb; j += blockDim.x) {
+        L.k[key * cb + j] = (int8_t)t[j];
+        L.v[key * cb + j] = (int8_t)t[cb + j];
+    }
+    for (size_t j = threadIdx.x; j < sb; j += blockDim.x) {
+        L.ks[key * sb + j] = ts[j];
+        L.vs[key * sb + j] = ts[sb + j];
+    }
+    if (L.sh) {
+        // products from the moved codes and scales (same expression and
+        // layout as kv_shadow_kernel)
+        const int da = (d / 8) * 8, nsl = (d + 63) / 64;
+        const size_t tt = key / KS_T;
+        const int jj = (int)(key % KS_T);
+        for (int x = threadIdx.x; x < Hkv * nsl * 64; x += blockDim.x) {
+            const int kvh = x / (nsl * 64), dim = x % (nsl * 64);
+            float p = 0.0f;
+            if (dim < da)
+                p = (float)(int8_t)t[cb + (size_t)kvh * d + dim] * ts[sb + (size_t)kvh * nqg + ((dim / 8) * 8) / 128];
+            const int sl = dim / 64, dl = dim % 64;
+            L.sh[(((size_t)kvh * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = p;
+        }
+    }
+    if (state && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) state[2] = cache_len;
+}
+
+__global__ void kv_set_len_kernel(uint32_t* state, uint32_t cache_len) {
+    if (threadIdx.x == 0) state[2] = cache_len;
+}
+
 }  // namespace cactus_hip
 
 using namespace cactus_hip;
@@ -62,6 +137,49 @@ int cactus_hip_kv_shadow_update(const int8_t* v_cache, const float* v_scales, fl
                        as_stream(stream), v_cache, v_scales, shadow, start, (int)kv_heads, (int)head_dim,
                        (int)quant_group_size, ntile);
     return check_launch("kv_shadow_update");
+}
+
+static size_t kv_shift_token_bytes(size_t kv_heads, size_t head_dim) {
+    const size_t nqg = (head_dim + 127) / 128;
+    return 2 * kv_heads * head_dim + 2 * kv_heads * nqg * sizeof(float);
+}
+
+int cactus_hip_kv_shift_temp_bytes(size_t nlayers, size_t count, size_t kv_heads, size_t head_dim,
+                                   size_t* bytes) {
+    CH_REQUIRE(bytes, "kv_shift_temp_bytes: null");
+    *bytes = nlayers * count * kv_shift_token_bytes(kv_heads, head_dim);
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_kv_window_shift(const cactus_hip_kv_layer* layers, size_t nlayers, size_t kv_heads,
+                               size_t head_dim, size_t max_seq, size_t dst, size_t src, size_t count,
+                               void* temp, size_t temp_bytes, uint32_t* state, uint32_t cache_len,
+                               void* stream) {
+    static_assert(sizeof(cactus_hip_kv_layer) == sizeof(KvLayer), "layer record layout");
+    CH_REQUIRE(layers || count == 0, "kv_window_shift: null layer table");
+    CH_REQUIRE(head_dim % 8 == 0 && head_dim <= 256 && kv_heads > 0 && kv_heads * head_dim <= (1u << 20),
+               "kv_window_shift: head_dim must be a multiple of 8 (<= 256)");
+    CH_REQUIRE(nlayers < 65536 && count < (1u << 31), "kv_window_shift: bad sizes");
+    CH_REQUIRE(dst <= src, "kv_window_shift: tokens move towards the start only");
+    CH_REQUIRE(src + count <= max_seq && dst + count <= max_seq, "kv_window_shift: tokens beyond the cache");
+    if (count == 0 || nlayers == 0) {
+        if (!state) return CACTUS_HIP_OK;
+        hipLaunchKernelGGL(kv_set_len_kernel, dim3(1), dim3(64), 0, as_stream(stream), state, cache_len);
+        return check_launch("kv_window_shift");
+    }
+    CH_REQUIRE(temp && temp_bytes >= nlayers * count * kv_shift_token_bytes(kv_heads, head_dim),
+               "kv_window_shift: temp buffer too small (cactus_hip_kv_shift_temp_bytes)");
+    const size_t ntile = (max_seq + KS_T - 1) / KS_T;
+    const KvLayer* L = reinterpret_cast<const KvLayer*>(layers);
+    const dim3 grid((unsigned)count, (unsigned)nlayers);
+    hipLaunchKernelGGL(kv_shift_out_kernel, grid, dim3(256), 0, as_stream(stream), L,
+                       static_cast<unsigned char*>(temp), src, (int)kv_heads, (int)head_dim, count);
+    int rc = check_launch("kv_window_shift (out)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(kv_shift_in_kernel, grid, dim3(256), 0, as_stream(stream), L,
+                       static_cast<const unsigned char*>(temp), dst, (int)kv_heads, (int)head_dim, count, ntile,
+                       state, cache_len);
+    return check_launch("kv_window_shift (in)");
 }
 
 }  // extern "C"

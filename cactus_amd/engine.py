@@ -103,6 +103,16 @@ class Qwen:
     def reset(self):
         self._check(self.lib.cactus_qwen_reset(self.h))
 
+    def set_kv_window(self, window: int, sink: int):
+        """KVCache::set_window_size: keep the first `sink` and the latest
+        window - sink tokens (0 = no window)."""
+        self._check(self.lib.cactus_qwen_set_kv_window(self.h, window, sink))
+
+    def total_len(self) -> int:
+        n = ctypes.c_size_t()
+        self._check(self.lib.cactus_qwen_total_len(self.h, ctypes.byref(n)))
+        return n.value
+
     def prefill(self, tokens):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
         self._check(self.lib.cactus_qwen_prefill(self.h, t.ctypes.data, t.size))

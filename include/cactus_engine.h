@@ -28,7 +28,7 @@ typedef struct {
     uint32_t num_layers, hidden, ffn, heads, kv_heads, head_dim, vocab;
     uint32_t group_size;     /* quantization group of the INT8 / INT4 weights */
     float eps, rope_theta;
-    uint32_t max_seq;        /* KV-cache capacity in tokens (no eviction) */
+    uint32_t max_seq;        /* KV-cache capacity in tokens (the context size) */
     uint32_t prefill_chunk;  /* Model::get_prefill_chunk_size() = 256 */
 } cactus_qwen_config;
 
@@ -73,6 +73,22 @@ int cactus_qwen_reset(void* model);
  * the reference's structure), 1 = fused per-layer kernels replayed as one
  * HIP graph per token.  Both are bit-identical. */
 int cactus_qwen_set_decode_mode(void* model, int mode);
+/* KVCache::set_window_size (engine/engine_cache.cpp:25-46): keep at most
+ * `window` cached tokens -- the first `sink` of the sequence and the most
+ * recent window - sink (update_from_graph, :103-330) -- while positions keep
+ * counting (RoPE and the attention's causal offset use the total length).
+ * window 0 = no window (the cache must then hold the whole sequence).  The
+ * first `window` slots are reset to codes 0, scales 1.0, as in the
+ * reference; call it before the first token.  Models from
+ * cactus_qwen_create / _create_random start without a window;
+ * cactus_qwen_create_from_folder applies Model::init's default
+ * (min(context, 512), 4 sinks, CACTUS_KV_WINDOW_SIZE / CACTUS_KV_SINK_SIZE,
+ * engine_model.cpp:136-146).  A step that would add more than
+ * window - sink tokens to a full window is an error (the reference's
+ * arithmetic wraps there). */
+int cactus_qwen_set_kv_window(void* model, size_t window, size_t sink);
+/* total_seq_len: tokens processed since the last reset */
+int cactus_qwen_total_len(void* model, size_t* len);
 int cactus_qwen_prefill(void* model, const uint32_t* tokens, size_t n);
 int cactus_qwen_decode(void* model, uint32_t token, uint32_t* next_token);
 /* FFI flow: prefill prompt[:-1], decode prompt[-1], then feed back

@@ -219,6 +219,31 @@ int cactus_hip_kv_shadow_update(const int8_t* v_cache, const float* v_scales, fl
                                 size_t start, size_t count, size_t kv_heads, size_t head_dim,
                                 size_t quant_group_size, size_t max_seq, void* stream);
 
+/* The sliding window's memmove (KVCache::update_from_graph,
+ * engine/engine_cache.cpp:268-306, std::memmove on host vectors there) on the
+ * device, for every layer at once: cached tokens [src, src + count) move to
+ * [dst, dst + count) (dst <= src; the ranges may overlap) -- key and value
+ * codes and scales -- and the value-product tiles of the moved tokens are
+ * recomputed (records with shadow == NULL skip them).  `layers` is a DEVICE
+ * array of nlayers records; caches are [max_seq][kv_heads][head_dim] codes
+ * and [max_seq][kv_heads][ceil(head_dim/128)] scales.  `temp` is device
+ * memory of cactus_hip_kv_shift_temp_bytes(nlayers, count, ...) bytes.
+ * With state != NULL, state[2] (the decode step's cache length) is set to
+ * cache_len after the move (also when count == 0). */
+typedef struct {
+    int8_t* k;
+    int8_t* v;
+    float* k_scales;
+    float* v_scales;
+    float* shadow;
+} cactus_hip_kv_layer;
+int cactus_hip_kv_shift_temp_bytes(size_t nlayers, size_t count, size_t kv_heads, size_t head_dim,
+                                   size_t* bytes);
+int cactus_hip_kv_window_shift(const cactus_hip_kv_layer* layers, size_t nlayers, size_t kv_heads,
+                               size_t head_dim, size_t max_seq, size_t dst, size_t src, size_t count,
+                               void* temp, size_t temp_bytes, uint32_t* state, uint32_t cache_len,
+                               void* stream);
+
 /* ------------------------------------------------ fused decode step
  * Each entry point computes a run of consecutive graph nodes of
  * QwenModel::forward (models/model_qwen.cpp:51-172) for ONE token with the

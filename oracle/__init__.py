@@ -62,6 +62,15 @@ _SIGS = {
     "orc_qwen_last_hidden": (P, [P, P]),
     "orc_qwen_cache_len": (SZ, [P]),
     "orc_qwen_kv": (None, [P, SZ, P, P, P, P]),
+    "orc_qwen_set_window": (I, [P, SZ, SZ]),
+    "orc_kv_create": (P, [SZ, SZ, SZ, SZ]),
+    "orc_kv_destroy": (None, [P]),
+    "orc_kv_set_window": (I, [P, SZ, SZ]),
+    "orc_kv_reset": (None, [P]),
+    "orc_kv_update": (I, [P, P, P, SZ]),
+    "orc_kv_len": (SZ, [P]),
+    "orc_kv_total": (SZ, [P]),
+    "orc_kv_layer": (None, [P, SZ, P, P, P, P]),
 }
 
 
@@ -223,6 +232,61 @@ class _Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in QWEN_LAYER_FIELDS]
 
 
+def _kv_arrays(ptrs, n, kvh, hd, ng):
+    def arr(p, dt, shape):
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(dt)), (int(np.prod(shape)),)).reshape(
+            shape).copy()
+    return (arr(ptrs[0], ctypes.c_int8, (n, kvh, hd)), arr(ptrs[1], ctypes.c_int8, (n, kvh, hd)),
+            arr(ptrs[2], ctypes.c_float, (n, kvh, ng)), arr(ptrs[3], ctypes.c_float, (n, kvh, ng)))
+
+
+class OracleKV:
+    """orc_kv_* (kv_oracle.c): the engine's INT8 KV cache with sliding window
+    and sinks (engine_cache.cpp)."""
+
+    def __init__(self, layers, max_seq, kv_heads, head_dim):
+        self.layers, self.kvh, self.hd = layers, kv_heads, head_dim
+        self.h = lib().orc_kv_create(layers, max_seq, kv_heads, head_dim)
+
+    def set_window(self, window, sink):
+        assert lib().orc_kv_set_window(self.h, window, sink) == 0
+
+    def reset(self):
+        lib().orc_kv_reset(self.h)
+
+    def update(self, k_layers, v_layers) -> int:
+        """k_layers / v_layers: per layer fp16 bits [seq][kv_heads][head_dim]."""
+        ks = [np.ascontiguousarray(k, dtype=np.uint16) for k in k_layers]
+        vs = [np.ascontiguousarray(v, dtype=np.uint16) for v in v_layers]
+        kp = (ctypes.c_void_p * self.layers)(*[k.ctypes.data for k in ks])
+        vp = (ctypes.c_void_p * self.layers)(*[v.ctypes.data for v in vs])
+        return int(lib().orc_kv_update(self.h, kp, vp, ks[0].shape[0]))
+
+    def len(self):
+        return int(lib().orc_kv_len(self.h))
+
+    def total(self):
+        return int(lib().orc_kv_total(self.h))
+
+    def layer(self, l, n=None):
+        """(codes k, codes v, scales k, scales v) of the first n tokens (default: len)."""
+        n = self.len() if n is None else n
+        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        lib().orc_kv_layer(self.h, l, *[ctypes.byref(p) for p in ptrs])
+        return _kv_arrays(ptrs, n, self.kvh, self.hd, (self.hd + 127) // 128)
+
+    def close(self):
+        if self.h:
+            lib().orc_kv_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class OracleQwen:
     """orc_qwen_* (qwen_oracle.c): the reference's Qwen3 block and engine flow."""
 
@@ -242,6 +306,9 @@ class OracleQwen:
 
     def reset(self):
         lib().orc_qwen_reset(self.h)
+
+    def set_window(self, window: int, sink: int):
+        assert lib().orc_qwen_set_window(self.h, window, sink) == 0
 
     def prefill(self, tokens, chunk=256):
         t = np.ascontiguousarray(tokens, dtype=np.uint32)
@@ -277,10 +344,7 @@ class OracleQwen:
         ng = (hd + 127) // 128
         ptrs = [ctypes.c_void_p() for _ in range(4)]
         lib().orc_qwen_kv(self.h, layer, *[ctypes.byref(p) for p in ptrs])
-        arr = lambda p, dt, shape: np.ctypeslib.as_array(
-            ctypes.cast(p, ctypes.POINTER(dt)), (int(np.prod(shape)),)).reshape(shape).copy()
-        return (arr(ptrs[0], ctypes.c_int8, (n, kvh, hd)), arr(ptrs[1], ctypes.c_int8, (n, kvh, hd)),
-                arr(ptrs[2], ctypes.c_float, (n, kvh, ng)), arr(ptrs[3], ctypes.c_float, (n, kvh, ng)))
+        return _kv_arrays(ptrs, n, kvh, hd, ng)
 
     def close(self):
         if self.h:

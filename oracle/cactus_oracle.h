@@ -110,7 +110,7 @@ typedef struct {
     uint32_t num_layers, hidden, ffn, heads, kv_heads, head_dim, vocab;
     uint32_t group_size;       /* weight quant group (attention INT8 and MLP INT4) */
     float eps, rope_theta;
-    uint32_t max_seq;          /* KV capacity in tokens (no eviction) */
+    uint32_t max_seq;          /* KV cache tokens allocated up front (grows on demand) */
 } orc_qwen_config;
 
 typedef struct {
@@ -143,6 +143,25 @@ size_t    orc_qwen_cache_len(const orc_qwen* m);
 /* KV cache read-back for one layer: pointers into the oracle's own cache */
 void      orc_qwen_kv(const orc_qwen* m, size_t layer, const int8_t** k, const int8_t** v,
                       const float** ks, const float** vs);
+/* KVCache::set_window_size on the model's cache (engine_model.cpp:136-146) */
+int       orc_qwen_set_window(orc_qwen* m, size_t window, size_t sink);
+
+/* ---- f2: INT8 KV cache with sliding window and sinks (kv_oracle.c) ------- */
+typedef struct orc_kv orc_kv;
+orc_kv* orc_kv_create(size_t layers, size_t max_seq, size_t kv_heads, size_t head_dim);
+void    orc_kv_destroy(orc_kv* c);
+/* KVCache::set_window_size (engine_cache.cpp:25-46): window 0 = no window */
+int     orc_kv_set_window(orc_kv* c, size_t window, size_t sink);
+void    orc_kv_reset(orc_kv* c);
+/* KVCache::update_from_graph (engine_cache.cpp:103-330) with the K and V
+ * rows of `seq` new tokens per layer ([seq][kv_heads][head_dim] fp16); -1
+ * where the reference's update is undefined (see kv_oracle.c) */
+int     orc_kv_update(orc_kv* c, const uint16_t* const* k_layers, const uint16_t* const* v_layers,
+                      size_t seq);
+size_t  orc_kv_len(const orc_kv* c);     /* current_seq_len */
+size_t  orc_kv_total(const orc_kv* c);   /* total_seq_len */
+void    orc_kv_layer(const orc_kv* c, size_t layer, const int8_t** k, const int8_t** v,
+                     const float** ks, const float** vs);
 
 #ifdef __cplusplus
 }

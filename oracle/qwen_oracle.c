@@ -7,11 +7,12 @@
  *   forward                       models/model_qwen.cpp:51-172
  *   Model::prefill                engine/engine_model.cpp:170-219
  *   Model::decode (greedy)        engine/engine_model.cpp:221-297
- *   KVCache append (INT8)         engine/engine_cache.cpp:234-267
+ *   KVCache update (INT8)         engine/engine_cache.cpp:103-330 (kv_oracle.c)
  *
  * The graph's reshape nodes are copies in the reference and views here;
- * neither changes a value.  Sliding-window eviction is not modelled: the
- * cache capacity must hold the whole sequence.
+ * neither changes a value.  Positions (RoPE and the attention's causal
+ * offset) are total_seq_len, the cache length current_seq_len
+ * (model_qwen.cpp:85-99, :141-145); with a sliding window the two differ.
  */
 #include "cactus_oracle.h"
 
@@ -28,8 +29,7 @@ struct orc_qwen {
     const uint16_t* out_norm;
     float attn_scale;
     /* KV cache, INT8 per token/head/128-dim group */
-    int8_t** kc; int8_t** vc; float** ks; float** vs;
-    size_t cache_len, total_len;
+    orc_kv* kv;
     /* final hidden state of the last forward */
     uint16_t* last_hidden; size_t last_rows;
 };
@@ -44,39 +44,25 @@ orc_qwen* orc_qwen_create(const orc_qwen_config* cfg, const orc_qwen_layer* laye
     m->out_norm = output_norm;
     /* engine_model.cpp:125-129 */
     m->attn_scale = 1.0f / sqrtf((float)cfg->head_dim);
-    const size_t L = cfg->num_layers;
-    const size_t per_tok = (size_t)cfg->kv_heads * cfg->head_dim;
-    const size_t ng = (cfg->head_dim + KV_GROUP - 1) / KV_GROUP;
-    m->kc = (int8_t**)calloc(L, sizeof(void*));
-    m->vc = (int8_t**)calloc(L, sizeof(void*));
-    m->ks = (float**)calloc(L, sizeof(void*));
-    m->vs = (float**)calloc(L, sizeof(void*));
-    for (size_t l = 0; l < L; l++) {
-        m->kc[l] = (int8_t*)calloc((size_t)cfg->max_seq * per_tok, 1);
-        m->vc[l] = (int8_t*)calloc((size_t)cfg->max_seq * per_tok, 1);
-        m->ks[l] = (float*)calloc((size_t)cfg->max_seq * cfg->kv_heads * ng, sizeof(float));
-        m->vs[l] = (float*)calloc((size_t)cfg->max_seq * cfg->kv_heads * ng, sizeof(float));
-    }
+    m->kv = orc_kv_create(cfg->num_layers, cfg->max_seq, cfg->kv_heads, cfg->head_dim);
     return m;
 }
 
 void orc_qwen_destroy(orc_qwen* m) {
     if (!m) return;
-    for (size_t l = 0; l < m->cfg.num_layers; l++) {
-        free(m->kc[l]); free(m->vc[l]); free(m->ks[l]); free(m->vs[l]);
-    }
-    free(m->kc); free(m->vc); free(m->ks); free(m->vs);
+    orc_kv_destroy(m->kv);
     free(m->layers);
     free(m->last_hidden);
     free(m);
 }
 
-void orc_qwen_reset(orc_qwen* m) { m->cache_len = 0; m->total_len = 0; }
-size_t orc_qwen_cache_len(const orc_qwen* m) { return m->cache_len; }
+void orc_qwen_reset(orc_qwen* m) { orc_kv_reset(m->kv); }
+size_t orc_qwen_cache_len(const orc_qwen* m) { return orc_kv_len(m->kv); }
+int orc_qwen_set_window(orc_qwen* m, size_t window, size_t sink) { return orc_kv_set_window(m->kv, window, sink); }
 
 void orc_qwen_kv(const orc_qwen* m, size_t l, const int8_t** k, const int8_t** v,
                  const float** ks, const float** vs) {
-    *k = m->kc[l]; *v = m->vc[l]; *ks = m->ks[l]; *vs = m->vs[l];
+    orc_kv_layer(m->kv, l, k, v, ks, vs);
 }
 
 const uint16_t* orc_qwen_last_hidden(const orc_qwen* m, size_t* rows) {
@@ -104,9 +90,8 @@ static int qwen_forward(orc_qwen* m, const uint32_t* tok, size_t S) {
     const size_t H = c->hidden, F = c->ffn, hd = c->head_dim;
     const size_t nq = (size_t)c->heads * hd, nkv = (size_t)c->kv_heads * hd;
     const size_t gs = c->group_size;
-    const size_t pos = m->total_len;
-    const size_t ng = (hd + KV_GROUP - 1) / KV_GROUP;
-    if (m->cache_len + S > c->max_seq) return -1;
+    const size_t pos = orc_kv_total(m->kv);
+    const size_t cache_len = orc_kv_len(m->kv);
 
     size_t maxK = H > F ? H : F;
     if (nq > maxK) maxK = nq;
@@ -121,8 +106,8 @@ static int qwen_forward(orc_qwen* m, const uint32_t* tok, size_t S) {
     int8_t* qbuf = (int8_t*)malloc(S * maxK);
     float* sbuf = (float*)malloc(sizeof(float) * S);
     float* ids = (float*)malloc(sizeof(float) * S);
-    uint16_t** kl = (uint16_t**)malloc(sizeof(void*) * c->num_layers);
-    uint16_t** vl = (uint16_t**)malloc(sizeof(void*) * c->num_layers);
+    uint16_t** kl = (uint16_t**)calloc(c->num_layers, sizeof(void*));
+    uint16_t** vl = (uint16_t**)calloc(c->num_layers, sizeof(void*));
 
     for (size_t i = 0; i < S; i++) ids[i] = (float)tok[i];
     int rc = orc_embedding_f16(m->embedding, ids, h, S, H, c->vocab);
@@ -141,13 +126,16 @@ static int qwen_forward(orc_qwen* m, const uint32_t* tok, size_t S) {
         orc_rope_f16(q2, q, 1, S, c->heads, hd, pos, c->rope_theta);
         orc_rope_f16(k2, k, 1, S, c->kv_heads, hd, pos, c->rope_theta);
         free(k2);
-        if (m->cache_len == 0)
+        if (cache_len == 0) {
             orc_attention_f16(q, k, v, at, 1, S, S, c->heads, c->kv_heads, hd, m->attn_scale,
                               NULL, pos, 0, 1);
-        else
-            orc_attention_hybrid_int8_fp16(q, m->kc[l], m->vc[l], m->ks[l], m->vs[l], k, v, at,
-                                           1, S, m->cache_len, S, c->heads, c->kv_heads, hd,
-                                           m->attn_scale, pos, 1, KV_GROUP);
+        } else {
+            const int8_t *kc, *vc;
+            const float *ks, *vs;
+            orc_kv_layer(m->kv, l, &kc, &vc, &ks, &vs);
+            orc_attention_hybrid_int8_fp16(q, kc, vc, ks, vs, k, v, at, 1, S, cache_len, S, c->heads,
+                                           c->kv_heads, hd, m->attn_scale, pos, 1, KV_GROUP);
+        }
         kl[l] = k; vl[l] = v;
         mm_int8(at, S, nq, L->o_w, L->o_s, H, gs, t, qbuf, sbuf);
         orc_add_f16(h, t, h, S * H);
@@ -164,18 +152,12 @@ static int qwen_forward(orc_qwen* m, const uint32_t* tok, size_t S) {
         m->last_hidden = (uint16_t*)malloc(2 * S * H);
         m->last_rows = S;
         orc_rms_norm_f16(h, m->out_norm, m->last_hidden, S, H, c->eps);
-        /* KV append after the graph executes (engine_model.cpp:317-321) */
-        for (size_t l = 0; l < c->num_layers; l++) {
-            orc_quantize_kv_fp16_to_int8(kl[l], m->kc[l] + m->cache_len * nkv,
-                                         m->ks[l] + m->cache_len * c->kv_heads * ng,
-                                         S, c->kv_heads, hd, KV_GROUP);
-            orc_quantize_kv_fp16_to_int8(vl[l], m->vc[l] + m->cache_len * nkv,
-                                         m->vs[l] + m->cache_len * c->kv_heads * ng,
-                                         S, c->kv_heads, hd, KV_GROUP);
-            free(kl[l]); free(vl[l]);
-        }
-        m->cache_len += S;
-        m->total_len += S;
+        /* KV update after the graph executes (engine_model.cpp:317-321) */
+        rc = orc_kv_update(m->kv, (const uint16_t* const*)kl, (const uint16_t* const*)vl, S);
+    }
+    for (size_t l = 0; l < c->num_layers; l++) {
+        free(kl[l]);
+        free(vl[l]);
     }
     free(h); free(x); free(q); free(q2); free(at); free(t); free(g); free(u);
     free(qbuf); free(sbuf); free(ids); free(kl); free(vl);
