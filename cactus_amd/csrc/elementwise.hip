@@ -1,5 +1,5 @@
 // elementwise.hip -- RMSNorm (a8), RoPE (a9), softmax (a10), SiLU (a11),
-// fp16 add/multiply (a12), embedding gather (a13) and the greedy sampler (a14).
+// fp16 add/multiply (a12) and the embedding gather (a13).
 #include "hip_common.h"
 
 #include <cmath>
@@ -240,44 +240,6 @@ __global__ void embedding_kernel(const uint16_t* __restrict__ table, const float
     for (int j = threadIdx.x; j < hidden; j += blockDim.x) o[j] = src[j];
 }
 
-// ---------------------------------------------------------------- greedy sample
-// First index of the maximum of (float)logit (kernel_nn.cpp:451-466): each
-// thread scans an increasing index range keeping a strict '>' winner; the
-// combine takes the larger value and, on equal values, the smaller index.
-__global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* __restrict__ L, size_t V,
-                                                      uint32_t* out) {
-    __shared__ float bv_s[1024];
-    __shared__ uint32_t bi_s[1024];
-    const int tid = threadIdx.x;
-    const size_t per = (V + 1023) / 1024;
-    const size_t s0 = tid * per;
-    const size_t s1 = (s0 + per < V) ? s0 + per : V;
-    float bv = -__builtin_inff();
-    uint32_t bi = 0xFFFFFFFFu;
-    for (size_t i = s0; i < s1; i++) {
-        const float v = h2f(L[i]);
-        if (bi == 0xFFFFFFFFu || v > bv) { bv = v; bi = (uint32_t)i; }
-    }
-    bv_s[tid] = bv;
-    bi_s[tid] = bi;
-    __syncthreads();
-    for (int w = 512; w > 0; w >>= 1) {
-        if (tid < w) {
-            const float ov = bv_s[tid + w];
-            const uint32_t oi = bi_s[tid + w];
-            const float mv = bv_s[tid];
-            const uint32_t mi = bi_s[tid];
-            bool take;
-            if (oi == 0xFFFFFFFFu) take = false;
-            else if (mi == 0xFFFFFFFFu) take = true;
-            else take = (ov > mv) || (ov == mv && oi < mi);
-            if (take) { bv_s[tid] = ov; bi_s[tid] = oi; }
-        }
-        __syncthreads();
-    }
-    if (tid == 0) *out = (bi_s[0] == 0xFFFFFFFFu) ? 0u : bi_s[0];
-}
-
 static unsigned grid_for(size_t n, unsigned block) {
     size_t g = (n + block - 1) / block;
     if (g < 1) g = 1;
@@ -378,19 +340,6 @@ int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* 
     hipLaunchKernelGGL(embedding_kernel, dim3((unsigned)num_ids), dim3(256), 0, as_stream(stream),
                        table, ids, out, num_ids, (int)hidden, vocab, error_flag);
     return check_launch("embedding");
-}
-
-int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, float temperature,
-                          float top_p, size_t top_k, size_t random_seed, void* stream) {
-    (void)random_seed;
-    CH_REQUIRE(out, "sample: null output");
-    if (!(temperature == 0.0f && top_p <= 0.0f && top_k == 0))
-        return fail(CACTUS_HIP_EUNSUPPORTED,
-                    "sample: only greedy decoding (temperature=0, top_p<=0, top_k=0) is built");
-    CH_REQUIRE(vocab == 0 || logits, "sample: null logits");
-    if (vocab == 0) return cactus_hip_memset(out, 0, 4, stream);
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
-    return check_launch("sample");
 }
 
 }  // extern "C"

@@ -240,6 +240,10 @@ int cactus_qwen_set_kv_window(void* model, size_t window, size_t sink) {
     return guarded([&] { static_cast<QwenModel*>(model)->set_kv_window(window, sink); });
 }
 
+int cactus_qwen_set_sampling(void* model, float temperature, float top_p, size_t top_k, size_t random_seed) {
+    return guarded([&] { static_cast<QwenModel*>(model)->set_sampling(temperature, top_p, top_k, random_seed); });
+}
+
 int cactus_qwen_total_len(void* model, size_t* len) {
     return guarded([&] { *len = static_cast<QwenModel*>(model)->cache().total_seq_len; });
 }
@@ -299,10 +303,25 @@ int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t*
 int cactus_qwen_last_logits(void* model, uint16_t* out) {
     return guarded([&] {
         QwenModel* m = static_cast<QwenModel*>(model);
-        if (m->last_logits_node() == SIZE_MAX || m->decode_mode() != 0)
-            throw std::runtime_error("logits are kept by decode mode 0 only");
+        if (m->last_logits_node() == SIZE_MAX)
+            throw std::runtime_error("logits are kept by the node-graph decode only (mode 0 or non-greedy)");
         const BufferDesc& b = m->graph().get_output_buffer(m->last_logits_node());
         check_hip(cactus_hip_memcpy_d2h(out, b.data, b.byte_size, m->stream()), "last_logits");
+    });
+}
+
+int cactus_qwen_last_entropy(void* model, float* entropy) {
+    return guarded([&] {
+        QwenModel* m = static_cast<QwenModel*>(model);
+        if (!entropy) throw std::runtime_error("null argument");
+        if (m->last_logits_node() == SIZE_MAX)
+            throw std::runtime_error("no logits kept: the greedy fused decode (mode 1) keeps none");
+        const BufferDesc& b = m->graph().get_output_buffer(m->last_logits_node());
+        DevBuf e(4);
+        check_hip(cactus_hip_logits_entropy_f16(static_cast<const uint16_t*>(b.data), b.shape.back(), e.as<float>(),
+                                                m->stream()),
+                  "entropy");
+        check_hip(cactus_hip_memcpy_d2h(entropy, e.ptr, 4, m->stream()), "entropy");
     });
 }
 

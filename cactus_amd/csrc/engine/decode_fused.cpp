@@ -207,7 +207,7 @@ void QwenModel::set_decode_mode(int mode) {
 }
 
 void QwenModel::decode_many(uint32_t token, size_t n, uint32_t* out) {
-    if (decode_mode_ == 1 && fused_) {
+    if (decode_mode_ == 1 && fused_ && greedy()) {
         fused_->run(token, n, out);
         return;
     }

@@ -99,6 +99,10 @@ public:
     void decode_many(uint32_t token, size_t n, uint32_t* out);
     void set_decode_mode(int mode);
     void set_kv_window(size_t window, size_t sink);
+    // Model::decode's temperature / top_p / top_k (engine_model.cpp:221-250);
+    // all zero = greedy.  seed 0 = the reference's clock seed per step
+    void set_sampling(float temperature, float top_p, size_t top_k, size_t seed);
+    bool greedy() const { return temperature_ == 0.0f && top_p_ <= 0.0f && top_k_ == 0; }
     int decode_mode() const { return decode_mode_; }
 
     const cactus_qwen_config& config() const { return cfg_; }
@@ -131,6 +135,8 @@ private:
     std::vector<size_t> k_nodes_, v_nodes_;
     size_t last_hidden_ = SIZE_MAX, last_logits_ = SIZE_MAX;
     int decode_mode_ = 0;
+    float temperature_ = 0.0f, top_p_ = 0.0f;
+    size_t top_k_ = 0, seed_ = 0;
     std::unique_ptr<FusedDecoder> fused_;
     friend class FusedDecoder;
 };

@@ -9,6 +9,7 @@
 #include "graph.h"
 
 #include <algorithm>
+#include <chrono>
 #include <cstring>
 #include <numeric>
 
@@ -226,11 +227,14 @@ size_t CactusGraph::reshape(size_t input, const std::vector<size_t>& new_shape) 
     return add_node(OpType::RESHAPE, {input}, new_shape, node(input).out.precision, p);
 }
 
-size_t CactusGraph::sample(size_t logits, float temperature, float top_p, size_t top_k) {
+size_t CactusGraph::sample(size_t logits, float temperature, float top_p, size_t top_k, size_t random_seed) {
     OpParams p;
     p.temperature = temperature;
     p.top_p = top_p;
     p.top_k = top_k;
+    p.random_seed = random_seed
+                        ? random_seed
+                        : (size_t)std::chrono::high_resolution_clock::now().time_since_epoch().count();
     return add_node(OpType::SAMPLE, {logits}, {1}, Precision::FP32, p);
 }
 
@@ -525,7 +529,7 @@ void CactusGraph::compute(GraphNode& n) {
             const size_t V = l.shape[1];
             const uint16_t* last = u16(l.data) + (l.shape[0] - 1) * V;
             check_hip(cactus_hip_sample_f16(last, static_cast<uint32_t*>(n.out.data), V, n.params.temperature,
-                                            n.params.top_p, n.params.top_k, 0, st),
+                                            n.params.top_p, n.params.top_k, n.params.random_seed, st),
                       "sample");
             return;
         }

@@ -81,6 +81,7 @@ struct OpParams {
     float temperature = 0.0f;
     float top_p = 0.0f;
     size_t top_k = 0;
+    size_t random_seed = 0;   // graph_builder.cpp:408: the build time in clock ticks
     size_t index_value = 0;
     // ATTENTION_INT8_HYBRID (graph_builder.cpp:301-316)
     const int8_t* cached_keys_int8 = nullptr;
@@ -127,7 +128,9 @@ public:
     size_t embedding(size_t table, size_t indices);
     size_t index(size_t input, size_t index_value, int dim);
     size_t reshape(size_t input, const std::vector<size_t>& new_shape);
-    size_t sample(size_t logits, float temperature = 0.6f, float top_p = 0.95f, size_t top_k = 20);
+    // random_seed 0: the reference's seed, the clock at build time
+    size_t sample(size_t logits, float temperature = 0.6f, float top_p = 0.95f, size_t top_k = 20,
+                  size_t random_seed = 0);
 
     // --- data
     void set_input(size_t node, const void* host_data, Precision precision);

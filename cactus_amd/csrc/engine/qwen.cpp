@@ -384,8 +384,18 @@ void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
 }
 
 // engine_model.cpp:221-297, greedy
+void QwenModel::set_sampling(float temperature, float top_p, size_t top_k, size_t seed) {
+    if (!(temperature >= 0.0f)) throw std::runtime_error("temperature must be >= 0");
+    temperature_ = temperature;
+    top_p_ = top_p;
+    top_k_ = top_k;
+    seed_ = seed;
+}
+
 uint32_t QwenModel::decode(uint32_t token) {
-    if (decode_mode_ == 1 && fused_) {
+    // the fused step ends in the greedy LM head; other settings run the
+    // node graph's sample node (its draw is made on the host per step)
+    if (decode_mode_ == 1 && fused_ && greedy()) {
         return fused_decode(*this, *fused_, token);
     }
     CactusGraph& g = *graph_;
@@ -394,7 +404,7 @@ uint32_t QwenModel::decode(uint32_t token) {
     size_t last = g.index(fin, 0, 0);
     last = g.reshape(last, {1, cfg_.hidden});
     last_logits_ = g.matmul(last, n_embedding_, true);
-    size_t tok = g.sample(last_logits_, 0.0f, 0.0f, 0);
+    size_t tok = g.sample(last_logits_, temperature_, top_p_, top_k_, seed_);
     g.execute();
     update_kv_cache(1);
     uint32_t id = 0;

@@ -1,0 +1,433 @@
+// sample.hip -- the FP16 sampler (a14 greedy, and the full sampler of
+// kernel_nn.cpp:446-651): temperature, repetition penalty over the last 128
+// sampled tokens, top-k, top-p and the draw, in one workgroup.
+//
+// Phases (one 1024-thread workgroup, vocabulary in a scratch copy):
+//   1. f = fp16(logit * fp16(1/T)) (or the raw logits); thread 0 applies the
+//      repetition penalty entry by entry in history order (duplicates apply
+//      again, as in the reference's loop);
+//   2. top-k: the k-th largest value by a two-pass radix select over
+//      order-preserving 16-bit keys (high byte, then low byte, LDS
+//      histograms); values below it become -inf;
+//   3. top-p: the survivors (top_k <= 4096 plus ties, at most SP_CAND) are sorted descending by a
+//      bitonic sort in LDS (ties: ascending token, see the oracle), thread 0
+//      forms the probabilities and the running sum in that order and every
+//      position from the first j > 0 whose sum exceeds top_p is removed;
+//   4. the final probabilities over the survivors in token order: parallel
+//      expf, an order-preserving compaction, then thread 0 sums, normalises
+//      and walks the running sum to the first value >= u, and appends the
+//      token to the device-resident history.
+// The sequential float sums run by one thread over the survivors only
+// (probabilities of removed tokens are exactly 0 and add nothing), so with
+// top-k they are short; without any filter they cover the vocabulary.
+#include "hip_common.h"
+
+#include <map>
+#include <mutex>
+#include <random>
+
+namespace cactus_hip {
+
+constexpr int SP_T = 1024;
+constexpr int SP_TOPK = 4096;          // largest top_k with top-p
+constexpr int SP_CAND = 16384;         // top-p candidates sorted in LDS (top_k plus ties)
+constexpr int SP_HIST = 128;           // kernel_nn.cpp:517
+constexpr uint16_t SP_NEG_INF = 0xFC00u;
+
+// ---------------------------------------------------------------- greedy
+// First index of the maximum of (float)logit (kernel_nn.cpp:451-466): each
+// thread scans an increasing index range keeping a strict '>' winner; the
+// combine takes the larger value and, on equal values, the smaller index.
+__global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* __restrict__ L, size_t V,
+                                                      uint32_t* out) {
+    __shared__ float bv_s[1024];
+    __shared__ uint32_t bi_s[1024];
+    const int tid = threadIdx.x;
+    const size_t per = (V + 1023) / 1024;
+    const size_t s0 = tid * per;
+    const size_t s1 = (s0 + per < V) ? s0 + per : V;
+    float bv = -__builtin_inff();
+    uint32_t bi = 0xFFFFFFFFu;
+    for (size_t i = s0; i < s1; i++) {
+        const float v = h2f(L[i]);
+        if (bi == 0xFFFFFFFFu || v > bv) { bv = v; bi = (uint32_t)i; }
+    }
+    bv_s[tid] = bv;
+    bi_s[tid] = bi;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (tid < w) {
+            const float ov = bv_s[tid + w];
+            const uint32_t oi = bi_s[tid + w];
+            const float mv = bv_s[tid];
+            const uint32_t mi = bi_s[tid];
+            bool take;
+            if (oi == 0xFFFFFFFFu) take = false;
+            else if (mi == 0xFFFFFFFFu) take = true;
+            else take = (ov > mv) || (ov == mv && oi < mi);
+            if (take) { bv_s[tid] = ov; bi_s[tid] = oi; }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) *out = (bi_s[0] == 0xFFFFFFFFu) ? 0u : bi_s[0];
+}
+
+// ---------------------------------------------------------------- full sampler
+struct SampleArgs {
+    const uint16_t* logits;
+    uint32_t* out;
+    uint16_t* f;        // [V] filtered logits
+    float* pv;          // [V] unnormalised probabilities of the survivors
+    uint32_t* surv;     // [V] survivor tokens in order
+    uint32_t* hist;     // [1 + SP_HIST]: count, tokens
+    size_t V, top_k;
+    float top_p, u;
+    uint16_t inv_t;     // fp16(1/T)
+    uint16_t pen_inv, pen;
+    int scale;          // temperature > 0
+};
+
+// order-preserving key of an fp16 value (non-NaN; -0 folded onto +0)
+__device__ __forceinline__ uint32_t okey(uint16_t h) {
+    if (h == 0x8000u) h = 0;
+    return (h & 0x8000u) ? (~(uint32_t)h & 0xFFFFu) : ((uint32_t)h | 0x8000u);
+}
+__device__ __forceinline__ uint16_t ukey(uint32_t k) {
+    return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
+}
+
+__global__ void __launch_bounds__(SP_T) sample_kernel(SampleArgs a) {
+    extern __shared__ unsigned long long cand[];   // [SP_CAND], dynamic: 128 KB
+    __shared__ uint32_t hbin[256];
+    __shared__ uint32_t scan[SP_T];
+    __shared__ float red[SP_T / 64];
+    __shared__ uint32_t sh_u32[4];
+    const int tid = threadIdx.x;
+    const size_t V = a.V;
+
+    // 1. temperature, then the repetition penalty (kernel_nn.cpp:501-529)
+    for (size_t i = tid; i < V; i += SP_T) a.f[i] = a.scale ? hmul(a.logits[i], a.inv_t) : a.logits[i];
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t n = a.hist[0];
+        for (uint32_t j = 0; j < n; j++) {
+            const uint32_t t = a.hist[1 + j];
+            if (t < V) a.f[t] = h2f(a.f[t]) > 0.0f ? hmul(a.f[t], a.pen_inv) : hmul(a.f[t], a.pen);
+        }
+    }
+    __syncthreads();
+
+    // 2. top-k (:531-548): the k-th largest value, two radix passes
+    if (a.top_k > 0 && a.top_k < V) {
+        uint32_t prefix = 0, need = (uint32_t)a.top_k;
+        for (int pass = 0; pass < 2; pass++) {
+            if (tid < 256) hbin[tid] = 0;
+            __syncthreads();
+            for (size_t i = tid; i < V; i += SP_T) {
+                const uint32_t k = okey(a.f[i]);
+                if (pass == 0) atomicAdd(&hbin[k >> 8], 1u);
+                else if ((k >> 8) == prefix) atomicAdd(&hbin[k & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t cum = 0;
+                int b = 255;
+                for (; b > 0; b--) {
+                    if (cum + hbin[b] >= need) break;
+                    cum += hbin[b];
+                }
+                sh_u32[0] = (uint32_t)b;
+                sh_u32[1] = need - cum;
+            }
+            __syncthreads();
+            prefix = pass == 0 ? sh_u32[0] : ((prefix << 8) | sh_u32[0]);
+            need = sh_u32[1];
+            __syncthreads();
+        }
+        const uint32_t kth = prefix;
+        for (size_t i = tid; i < V; i += SP_T)
+            if (okey(a.f[i]) < kth) a.f[i] = SP_NEG_INF;
+        __syncthreads();
+    }
+
+    // 3. top-p (:550-590) over the survivors, sorted descending
+    if (a.top_p > 0.0f && a.top_p < 1.0f) {
+        if (tid == 0) sh_u32[2] = 0;
+        __syncthreads();
+        for (size_t i = tid; i < V; i += SP_T) {
+            if (a.f[i] == SP_NEG_INF) continue;
+            const uint32_t slot = atomicAdd(&sh_u32[2], 1u);
+            if (slot < (uint32_t)SP_CAND)
+                cand[slot] = ((unsigned long long)(0xFFFFu - okey(a.f[i])) << 32) | (unsigned long long)i;
+        }
+        __syncthreads();
+        const uint32_t n = sh_u32[2];
+        if (n > (uint32_t)SP_CAND) {
+            // more tied survivors than the sort holds: refused, loudly
+            if (tid == 0) *a.out = 0xFFFFFFFFu;
+            return;
+        }
+        uint32_t n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (uint32_t j = n + tid; j < n2; j += SP_T) cand[j] = ~0ull;
+        __syncthreads();
+        for (uint32_t size = 2; size <= n2; size <<= 1) {
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t i = tid; i < n2; i += SP_T) {
+                    const uint32_t j = i ^ stride;
+                    if (j > i) {
+                        const bool up = (i & size) == 0;
+                        const unsigned long long x = cand[i], y = cand[j];
+                        if ((x > y) == up) {
+                            cand[i] = y;
+                            cand[j] = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        if (tid == 0) {
+            uint32_t cut = n;
+            if (n > 0) {
+                const float mx = h2f(ukey(0xFFFFu - (uint32_t)(cand[0] >> 32)));
+                float sum = 0.0f;
+                for (uint32_t j = 0; j < n; j++) sum += cactus_expf(h2f(ukey(0xFFFFu - (uint32_t)(cand[j] >> 32))) - mx);
+                float cum = 0.0f;
+                for (uint32_t j = 0; j < n; j++) {
+                    cum += cactus_expf(h2f(ukey(0xFFFFu - (uint32_t)(cand[j] >> 32))) - mx) / sum;
+                    if (cum > a.top_p && j > 0) {
+                        cut = j;
+                        break;
+                    }
+                }
+            }
+            sh_u32[3] = cut;
+        }
+        __syncthreads();
+        for (uint32_t j = sh_u32[3] + tid; j < n; j += SP_T) a.f[(uint32_t)cand[j]] = SP_NEG_INF;
+        __syncthreads();
+    }
+
+    // 4. the draw over the survivors in token order (:592-651)
+    float m = -__builtin_inff();
+    for (size_t i = tid; i < V; i += SP_T) m = __builtin_fmaxf(m, h2f(a.f[i]));
+    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 64));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int w = 1; w < SP_T / 64; w++) mx = __builtin_fmaxf(mx, red[w]);
+    if (mx == -__builtin_inff()) {
+        if (tid == 0) *a.out = 0;
+        return;
+    }
+    const size_t per = (V + SP_T - 1) / SP_T;
+    const size_t c0 = (size_t)tid * per, c1 = c0 + per < V ? c0 + per : V;
+    uint32_t cnt = 0;
+    for (size_t i = c0; i < c1; i++) cnt += a.f[i] != SP_NEG_INF;
+    scan[tid] = cnt;
+    __syncthreads();
+    for (int o = 1; o < SP_T; o <<= 1) {   // inclusive scan
+        const uint32_t v = tid >= o ? scan[tid - o] : 0u;
+        __syncthreads();
+        scan[tid] += v;
+        __syncthreads();
+    }
+    uint32_t off = scan[tid] - cnt;
+    for (size_t i = c0; i < c1; i++) {
+        if (a.f[i] == SP_NEG_INF) continue;
+        a.surv[off] = (uint32_t)i;
+        a.pv[off] = cactus_expf(h2f(a.f[i]) - mx);
+        off++;
+    }
+    __syncthreads();
+    if (tid != 0) return;
+    const uint32_t S = scan[SP_T - 1];
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < S; j++) sum += a.pv[j];
+    if (sum == 0.0f) {
+        *a.out = 0;
+        return;
+    }
+    uint32_t tok = 0;
+    bool found = false;
+    if (a.u <= 0.0f) {
+        found = true;   // the running sum is >= u already at token 0
+    } else {
+        float cum = 0.0f;
+        for (uint32_t j = 0; j < S && !found; j++) {
+            cum += a.pv[j] / sum;
+            if (cum >= a.u) { tok = a.surv[j]; found = true; }
+        }
+        for (uint32_t j = S; j > 0 && !found; j--)
+            if (a.pv[j - 1] / sum > 0.0f) { tok = a.surv[j - 1]; found = true; }
+    }
+    // history (:633-650)
+    uint32_t n = a.hist[0];
+    if (n == (uint32_t)SP_HIST) {
+        for (uint32_t j = 1; j < (uint32_t)SP_HIST; j++) a.hist[j] = a.hist[j + 1];
+        n = SP_HIST - 1;
+    }
+    a.hist[1 + n] = tok;
+    a.hist[0] = n + 1;
+    *a.out = tok;
+}
+
+// ---------------------------------------------------------------- entropy
+// Model::decode's out_entropy (engine_model.cpp:255-290): max, then the sum
+// of exp in double and the entropy sum in double, each a tree over the
+// workgroup (the reference sums sequentially; the double partial sums
+// differ in the last bits, far below the float result's precision).
+__global__ void __launch_bounds__(1024) entropy_kernel(const uint16_t* __restrict__ L, size_t V, float* out) {
+    __shared__ double rd[1024];
+    __shared__ float rf[1024];
+    const int tid = threadIdx.x;
+    float m = -__builtin_inff();
+    for (size_t i = tid; i < V; i += 1024) m = __builtin_fmaxf(m, h2f(L[i]));
+    rf[tid] = m;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (tid < w) rf[tid] = __builtin_fmaxf(rf[tid], rf[tid + w]);
+        __syncthreads();
+    }
+    const float mx = rf[0];
+    double se = 0.0;
+    for (size_t i = tid; i < V; i += 1024) se += exp((double)(h2f(L[i]) - mx));
+    rd[tid] = se;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (tid < w) rd[tid] += rd[tid + w];
+        __syncthreads();
+    }
+    const double lse = (double)mx + log(rd[0]);
+    __syncthreads();
+    double ent = 0.0;
+    for (size_t i = tid; i < V; i += 1024) {
+        const double lp = (double)h2f(L[i]) - lse;
+        const double p = exp(lp);
+        if (p > 1e-10) ent -= p * lp;
+    }
+    rd[tid] = ent;
+    __syncthreads();
+    for (int w = 512; w > 0; w >>= 1) {
+        if (tid < w) rd[tid] += rd[tid + w];
+        __syncthreads();
+    }
+    if (tid == 0) *out = (float)(rd[0] / log((double)V));
+}
+
+// per-device scratch (grown) and token history (zeroed once)
+struct SampleState {
+    uint16_t* f = nullptr;
+    float* pv = nullptr;
+    uint32_t* surv = nullptr;
+    size_t cap = 0;
+    uint32_t* hist = nullptr;
+};
+static std::mutex g_sample_mu;
+static std::map<int, SampleState> g_sample;
+
+static int sample_state(size_t V, SampleState** out) {
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_sample_mu);
+    SampleState& s = g_sample[dev];
+    if (!s.hist) {
+        CH_HIP(hipMalloc(&s.hist, (1 + SP_HIST) * sizeof(uint32_t)));
+        CH_HIP(hipMemset(s.hist, 0, (1 + SP_HIST) * sizeof(uint32_t)));
+    }
+    if (s.cap < V) {
+        // buffers of earlier calls may still be read by queued kernels
+        CH_HIP(hipDeviceSynchronize());
+        if (s.f) CH_HIP(hipFree(s.f));
+        if (s.pv) CH_HIP(hipFree(s.pv));
+        if (s.surv) CH_HIP(hipFree(s.surv));
+        s.f = nullptr; s.pv = nullptr; s.surv = nullptr; s.cap = 0;
+        CH_HIP(hipMalloc(&s.f, V * sizeof(uint16_t)));
+        CH_HIP(hipMalloc(&s.pv, V * sizeof(float)));
+        CH_HIP(hipMalloc(&s.surv, V * sizeof(uint32_t)));
+        s.cap = V;
+    }
+    *out = &s;
+    return CACTUS_HIP_OK;
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+extern "C" {
+
+int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, float temperature,
+                          float top_p, size_t top_k, size_t random_seed, void* stream) {
+    CH_REQUIRE(out, "sample: null output");
+    CH_REQUIRE(vocab == 0 || logits, "sample: null logits");
+    if (vocab == 0) return cactus_hip_memset(out, 0, 4, stream);
+    if (temperature == 0.0f && top_p <= 0.0f && top_k == 0) {
+        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
+        return check_launch("sample");
+    }
+    CH_REQUIRE(vocab < (1ull << 31), "sample: vocabulary too large");
+    CH_REQUIRE(temperature >= 0.0f && temperature == temperature, "sample: temperature must be >= 0");
+    if (top_p > 0.0f && top_p < 1.0f && (top_k == 0 || top_k > (size_t)SP_TOPK))
+        return fail(CACTUS_HIP_EUNSUPPORTED,
+                    "sample: top-p is built over at most 4096 top-k survivors (1 <= top_k <= 4096)");
+    SampleState* s = nullptr;
+    int rc = sample_state(vocab, &s);
+    if (rc) return rc;
+    // the reference's draw (kernel_nn.cpp:609-612): mt19937 seeded with the
+    // 32-bit seed (a random one for seed 0), first output through libc++'s
+    // generate_canonical<float, 24>
+    const uint32_t seed = random_seed ? (uint32_t)random_seed : std::random_device{}();
+    std::mt19937 gen(seed);
+    const uint32_t x = (uint32_t)gen();
+    SampleArgs a{};
+    a.logits = logits;
+    a.out = out;
+    a.f = s->f;
+    a.pv = s->pv;
+    a.surv = s->surv;
+    a.hist = s->hist;
+    a.V = vocab;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.u = (float)x / 4294967296.0f;
+    a.scale = temperature > 0.0f;
+    a.inv_t = a.scale ? host_f2h(1.0f / temperature) : (uint16_t)0;
+    a.pen_inv = host_f2h(1.0f / 1.1f);
+    a.pen = host_f2h(1.1f);
+    const size_t lds = SP_CAND * sizeof(unsigned long long);
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)sample_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    CH_REQUIRE(attr == hipSuccess, "sample: cannot reserve the candidate LDS");
+    hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SP_T), lds, as_stream(stream), a);
+    return check_launch("sample");
+}
+
+int cactus_hip_logits_entropy_f16(const uint16_t* logits, size_t vocab, float* out, void* stream) {
+    CH_REQUIRE(logits && out && vocab > 0, "logits_entropy: null pointer or empty vocabulary");
+    hipLaunchKernelGGL(entropy_kernel, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
+    return check_launch("logits_entropy");
+}
+
+int cactus_hip_sample_history(uint32_t* tokens, size_t* count, void* stream) {
+    CH_REQUIRE(tokens && count, "sample_history: null argument");
+    SampleState* s = nullptr;
+    int rc = sample_state(0, &s);
+    if (rc) return rc;
+    uint32_t h[1 + SP_HIST];
+    CH_HIP(hipMemcpyAsync(h, s->hist, sizeof(h), hipMemcpyDeviceToHost, as_stream(stream)));
+    CH_HIP(hipStreamSynchronize(as_stream(stream)));
+    *count = h[0];
+    for (uint32_t j = 0; j < h[0] && j < (uint32_t)SP_HIST; j++) tokens[j] = h[1 + j];
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_sample_history_reset(void* stream) {
+    SampleState* s = nullptr;
+    int rc = sample_state(0, &s);
+    if (rc) return rc;
+    return cactus_hip_memset(s->hist, 0, (1 + SP_HIST) * sizeof(uint32_t), stream);
+}
+
+}  // extern "C"

@@ -108,6 +108,11 @@ class Qwen:
         window - sink tokens (0 = no window)."""
         self._check(self.lib.cactus_qwen_set_kv_window(self.h, window, sink))
 
+    def set_sampling(self, temperature: float, top_p: float, top_k: int, seed: int = 0):
+        """Model::decode's temperature / top_p / top_k; all zero = greedy."""
+        self._check(self.lib.cactus_qwen_set_sampling(self.h, ctypes.c_float(temperature), ctypes.c_float(top_p),
+                                                      top_k, seed))
+
     def total_len(self) -> int:
         n = ctypes.c_size_t()
         self._check(self.lib.cactus_qwen_total_len(self.h, ctypes.byref(n)))
@@ -141,6 +146,11 @@ class Qwen:
         out = np.zeros(self.cfg["vocab"], np.uint16)
         self._check(self.lib.cactus_qwen_last_logits(self.h, out.ctypes.data))
         return out
+
+    def last_entropy(self) -> float:
+        e = ctypes.c_float()
+        self._check(self.lib.cactus_qwen_last_entropy(self.h, ctypes.byref(e)))
+        return e.value
 
     def cache_len(self) -> int:
         n = ctypes.c_size_t()

@@ -87,6 +87,12 @@ int cactus_qwen_set_decode_mode(void* model, int mode);
  * window - sink tokens to a full window is an error (the reference's
  * arithmetic wraps there). */
 int cactus_qwen_set_kv_window(void* model, size_t window, size_t sink);
+/* Model::decode's sampling settings (engine_model.cpp:221-250 ->
+ * cactus_hip_sample_f16): all zero = greedy (the default).  Non-greedy steps
+ * run the node graph's sample node in either decode mode; random_seed 0
+ * draws the reference's seed (the clock) per step, a nonzero seed is used
+ * for every step. */
+int cactus_qwen_set_sampling(void* model, float temperature, float top_p, size_t top_k, size_t random_seed);
 /* total_seq_len: tokens processed since the last reset */
 int cactus_qwen_total_len(void* model, size_t* len);
 int cactus_qwen_prefill(void* model, const uint32_t* tokens, size_t n);
@@ -100,6 +106,11 @@ int cactus_qwen_generate(void* model, const uint32_t* prompt, size_t n, size_t m
 int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t* rows);
 /* Logits of the last decode step, fp16 [vocab] (decode mode 0 only). */
 int cactus_qwen_last_logits(void* model, uint16_t* out);
+/* Model::decode's out_entropy (engine_model.cpp:255-290) for the last
+ * decode step's logits: normalised softmax entropy in [0, 1], the
+ * confidence signal of the reference's cloud handoff.  Needs a step that
+ * kept its logits (decode mode 0, or non-greedy sampling). */
+int cactus_qwen_last_entropy(void* model, float* entropy);
 int cactus_qwen_cache_len(void* model, size_t* len);
 /* Copies layer `layer` of the INT8 KV cache (first cache_len tokens). */
 int cactus_qwen_read_kv(void* model, size_t layer, int8_t* k, int8_t* v, float* k_scales,

@@ -199,12 +199,32 @@ int cactus_hip_transpose_2d_f16(const uint16_t* src, uint16_t* dst, size_t rows,
 int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* out,
                              size_t num_ids, size_t hidden, size_t vocab, int* error_flag,
                              void* stream);
-/* cactus_sample_f16 (kernel/kernel.h:127, kernel_nn.cpp:446-466): only the
- * greedy branch (temperature == 0, top_p <= 0, top_k == 0) is built; other
- * settings return CACTUS_HIP_EUNSUPPORTED.  Writes one uint32 to *out. */
+/* cactus_sample_f16 (kernel/kernel.h:127, kernel_nn.cpp:446-651): greedy
+ * (temperature == 0, top_p <= 0, top_k == 0: first index of the maximum) or
+ * the full sampler: fp16 temperature scaling, the repetition penalty 1.1 over
+ * the last 128 tokens this sampler returned (a history kept per device, like
+ * the reference's process-wide one), top-k (ties at the k-th value kept),
+ * top-p (the position whose running sum first exceeds top_p, after the
+ * first, and everything after it removed), and the draw u from
+ * std::mt19937(random_seed) (a random seed for 0) through libc++'s
+ * generate_canonical<float, 24>.  The reference's logit bias never reaches
+ * its result and has no argument here; the f16 sampler has no min-p.
+ * 0 < top_p < 1 needs 1 <= top_k <= 4096 (else CACTUS_HIP_EUNSUPPORTED); if
+ * ties leave more than 16384 top-k survivors, *out is set to 0xFFFFFFFF.
+ * Writes one uint32 to *out (device memory), stream-ordered. */
 int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
                           float temperature, float top_p, size_t top_k, size_t random_seed,
                           void* stream);
+/* Model::decode's out_entropy (engine/engine_model.cpp:255-290): the
+ * softmax entropy of fp16 logits [vocab] in double, divided by log(vocab),
+ * written as one float to *out (device memory).  Floating point: within a
+ * few float ulp of the reference's sequential double sums. */
+int cactus_hip_logits_entropy_f16(const uint16_t* logits, size_t vocab, float* out, void* stream);
+/* No reference counterpart (the reference's history is a static vector in
+ * kernel_nn.cpp:516): read back this device's sampler history (oldest
+ * first, at most 128 entries; synchronises the stream) or clear it. */
+int cactus_hip_sample_history(uint32_t* tokens, size_t* count, void* stream);
+int cactus_hip_sample_history_reset(void* stream);
 
 /* ------------------------------------------------ value product tiles
  * No reference counterpart: an fp32 mirror of the INT8 value cache holding

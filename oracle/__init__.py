@@ -63,6 +63,10 @@ _SIGS = {
     "orc_qwen_cache_len": (SZ, [P]),
     "orc_qwen_kv": (None, [P, SZ, P, P, P, P]),
     "orc_qwen_set_window": (I, [P, SZ, SZ]),
+    "orc_mt19937_nth": (ctypes.c_uint32, [ctypes.c_uint32, SZ]),
+    "orc_sample_uniform": (F, [ctypes.c_uint32]),
+    "orc_logits_entropy_f16": (F, [P, SZ]),
+    "orc_sample_f16": (ctypes.c_uint32, [P, SZ, F, F, SZ, F, P, P]),
     "orc_kv_create": (P, [SZ, SZ, SZ, SZ]),
     "orc_kv_destroy": (None, [P]),
     "orc_kv_set_window": (I, [P, SZ, SZ]),
@@ -230,6 +234,36 @@ class _Cfg(ctypes.Structure):
 
 class _Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in QWEN_LAYER_FIELDS]
+
+
+def mt19937_nth(seed: int, n: int) -> int:
+    return int(lib().orc_mt19937_nth(seed, n))
+
+
+def logits_entropy(logits) -> float:
+    x = np.ascontiguousarray(logits, dtype=np.uint16)
+    return float(lib().orc_logits_entropy_f16(x.ctypes.data, x.size))
+
+
+def sample_uniform(seed: int) -> float:
+    return float(lib().orc_sample_uniform(seed))
+
+
+class OracleSampler:
+    """cactus_sample_f16 with its process-wide token history held here."""
+
+    def __init__(self):
+        self.hist = np.zeros(128, np.uint32)
+        self.n = ctypes.c_size_t(0)
+
+    def history(self):
+        return self.hist[:self.n.value].copy()
+
+    def sample(self, logits, temperature, top_p, top_k, seed):
+        x = np.ascontiguousarray(logits, dtype=np.uint16)
+        u = sample_uniform(seed)
+        return int(lib().orc_sample_f16(x.ctypes.data, x.size, temperature, top_p, top_k, u,
+                                        self.hist.ctypes.data, ctypes.byref(self.n)))
 
 
 def _kv_arrays(ptrs, n, kvh, hd, ng):

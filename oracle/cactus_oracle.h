@@ -105,6 +105,21 @@ int      orc_embedding_f16(const uint16_t* table, const float* ids, uint16_t* ou
                            size_t num_ids, size_t hidden, size_t vocab);
 uint32_t orc_argmax_f16(const uint16_t* logits, size_t vocab);
 
+/* ---- f3: non-greedy FP16 sampler (sample_oracle.c) ----------------------- */
+#define ORC_SAMPLE_HISTORY 128
+/* the n-th output (n >= 1) of std::mt19937 seeded with `seed` */
+uint32_t orc_mt19937_nth(uint32_t seed, size_t n);
+/* uniform_real_distribution<float>(0, 1) over the first mt19937(seed) draw */
+float    orc_sample_uniform(uint32_t seed);
+/* cactus_sample_f16 (kernel_nn.cpp:446-651) with the draw `u` given and the
+ * token history explicit (hist holds up to ORC_SAMPLE_HISTORY entries,
+ * *hist_n of them used; updated like the reference's static history) */
+uint32_t orc_sample_f16(const uint16_t* logits, size_t vocab, float temperature, float top_p,
+                        size_t top_k, float u, uint32_t* hist, size_t* hist_n);
+
+/* Model::decode's normalised entropy of the logits (engine_model.cpp:255-290) */
+float    orc_logits_entropy_f16(const uint16_t* logits, size_t vocab);
+
 /* ---- a15: Qwen3-architecture forward ------------------------------------ */
 typedef struct {
     uint32_t num_layers, hidden, ffn, heads, kv_heads, head_dim, vocab;
