@@ -220,6 +220,26 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
  * written as one float to *out (device memory).  Floating point: within a
  * few float ulp of the reference's sequential double sums. */
 int cactus_hip_logits_entropy_f16(const uint16_t* logits, size_t vocab, float* out, void* stream);
+/* ---- ops of other model families (kernel.h, graph_ops_nn.cpp) ----------
+ * cactus_gelu_f16 (kernel_nn.cpp:46-92): the 8-element body uses
+ * fast_tanh_f32x4 (kernel_utils.h:143-163), the n % 8 tail tanhf. */
+int cactus_hip_gelu_f16(const uint16_t* in, uint16_t* out, size_t n, void* stream);
+/* cactus_gelu_f16_erf (kernel_nn.cpp:94-150) */
+int cactus_hip_gelu_erf_f16(const uint16_t* in, uint16_t* out, size_t n, void* stream);
+/* compute_layernorm_node, FP16 input / weight / bias / output
+ * (graph_ops_nn.cpp:373-457): rows of `features` values */
+int cactus_hip_layer_norm_f16(const uint16_t* x, const uint16_t* weight, const uint16_t* bias, uint16_t* y,
+                              size_t rows, size_t features, float eps, void* stream);
+/* cactus_conv1d_causal_depthwise_f16 (kernel_conv.cpp:15-110): input and
+ * output [N][L][C], weight [C][K], y[t] = sum_k w[K-1-k] x[t - k*dilation] */
+int cactus_hip_conv1d_causal_depthwise_f16(const uint16_t* input, const uint16_t* weight, uint16_t* output,
+                                           size_t N, size_t L, size_t C, size_t K, size_t dilation,
+                                           void* stream);
+/* cactus_conv1d_f16_k3 (kernel_conv.cpp:112-236): input [N][C_in][L], weight
+ * [C_out][C_in][3], output [N][C_out][(L-1)/stride + 1], zero padding 1 */
+int cactus_hip_conv1d_f16_k3(const uint16_t* input, const uint16_t* weight, uint16_t* output, size_t N,
+                             size_t L, size_t C_in, size_t C_out, size_t stride, void* stream);
+
 /* No reference counterpart (the reference's history is a static vector in
  * kernel_nn.cpp:516): read back this device's sampler history (oldest
  * first, at most 128 entries; synchronises the stream) or clear it. */

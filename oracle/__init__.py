@@ -67,6 +67,12 @@ _SIGS = {
     "orc_sample_uniform": (F, [ctypes.c_uint32]),
     "orc_logits_entropy_f16": (F, [P, SZ]),
     "orc_sample_f16": (ctypes.c_uint32, [P, SZ, F, F, SZ, F, P, P]),
+    "orc_fast_tanh": (F, [F]),
+    "orc_gelu_f16": (None, [P, P, SZ]),
+    "orc_gelu_erf_f16": (None, [P, P, SZ]),
+    "orc_layer_norm_f16": (None, [P, P, P, P, SZ, SZ, F]),
+    "orc_conv1d_causal_depthwise_f16": (None, [P, P, P, SZ, SZ, SZ, SZ, SZ]),
+    "orc_conv1d_f16_k3": (None, [P, P, P, SZ, SZ, SZ, SZ, SZ]),
     "orc_kv_create": (P, [SZ, SZ, SZ, SZ]),
     "orc_kv_destroy": (None, [P]),
     "orc_kv_set_window": (I, [P, SZ, SZ]),
@@ -234,6 +240,47 @@ class _Cfg(ctypes.Structure):
 
 class _Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in QWEN_LAYER_FIELDS]
+
+
+def fast_tanh(x: float) -> float:
+    return float(lib().orc_fast_tanh(x))
+
+
+def gelu(x16):
+    y = np.empty_like(x16)
+    lib().orc_gelu_f16(ptr(x16), ptr(y), x16.size)
+    return y
+
+
+def gelu_erf(x16):
+    y = np.empty_like(x16)
+    lib().orc_gelu_erf_f16(ptr(x16), ptr(y), x16.size)
+    return y
+
+
+def layer_norm(x16, w16, b16, eps):
+    rows, F = x16.shape
+    y = np.empty_like(x16)
+    lib().orc_layer_norm_f16(ptr(x16), ptr(w16), ptr(b16), ptr(y), rows, F, eps)
+    return y
+
+
+def conv1d_causal_depthwise(x16, w16, dilation):
+    """x [N][L][C], w [C][K] -> y [N][L][C]"""
+    N, L, C = x16.shape
+    K = w16.shape[1]
+    y = np.empty_like(x16)
+    lib().orc_conv1d_causal_depthwise_f16(ptr(x16), ptr(w16), ptr(y), N, L, C, K, dilation)
+    return y
+
+
+def conv1d_k3(x16, w16, stride):
+    """x [N][C_in][L], w [C_out][C_in][3] -> y [N][C_out][(L-1)/stride + 1]"""
+    N, Cin, L = x16.shape
+    Cout = w16.shape[0]
+    y = np.empty((N, Cout, (L - 1) // stride + 1), np.uint16)
+    lib().orc_conv1d_f16_k3(ptr(x16), ptr(w16), ptr(y), N, L, Cin, Cout, stride)
+    return y
 
 
 def mt19937_nth(seed: int, n: int) -> int:

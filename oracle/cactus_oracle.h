@@ -120,6 +120,17 @@ uint32_t orc_sample_f16(const uint16_t* logits, size_t vocab, float temperature,
 /* Model::decode's normalised entropy of the logits (engine_model.cpp:255-290) */
 float    orc_logits_entropy_f16(const uint16_t* logits, size_t vocab);
 
+/* ---- f4: ops of other model families (family_oracle.c) ------------------ */
+float orc_fast_tanh(float x);                                  /* kernel_utils.h:143-163 */
+void  orc_gelu_f16(const uint16_t* in, uint16_t* out, size_t n);
+void  orc_gelu_erf_f16(const uint16_t* in, uint16_t* out, size_t n);
+void  orc_layer_norm_f16(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
+                         size_t rows, size_t features, float eps);
+void  orc_conv1d_causal_depthwise_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t N,
+                                      size_t L, size_t C, size_t K, size_t dilation);
+void  orc_conv1d_f16_k3(const uint16_t* x, const uint16_t* w, uint16_t* y, size_t N, size_t L,
+                        size_t C_in, size_t C_out, size_t stride);
+
 /* ---- a15: Qwen3-architecture forward ------------------------------------ */
 typedef struct {
     uint32_t num_layers, hidden, ffn, heads, kv_heads, head_dim, vocab;
