@@ -631,6 +631,12 @@ def test_sample_greedy(dev, orc):
     dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.0), ctypes.c_float(0.0), 0, 0,
                 None)
     assert dev.get(out, np.uint32, 1)[0] == orc.argmax(logits) == 77
-    rc = dev.cm.hip().cactus_hip_sample_f16(lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 20,
+    # the full sampler (tests/test_sampler.py covers it in depth); top-p
+    # without a top-k is refused
+    dev.cm.call("cactus_hip_sample_history_reset", None)
+    dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 20, 1, None)
+    assert dev.get(out, np.uint32, 1)[0] == orc.OracleSampler().sample(logits, 0.7, 0.9, 20, 1)
+    dev.cm.call("cactus_hip_sample_history_reset", None)
+    rc = dev.cm.hip().cactus_hip_sample_f16(lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 0,
                                             1, None)
-    assert rc == -2  # CACTUS_HIP_EUNSUPPORTED: only greedy decoding is built
+    assert rc == -2  # CACTUS_HIP_EUNSUPPORTED
