@@ -36,7 +36,9 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     const size_t blocks = (c.vocab + 127) / 128;   // cactus_hip_decode_lm_head's scratch contract
     lm_scratch_ = DevBuf(256 + 8 * blocks);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
-    rope_pos_ = (size_t)c.max_seq + 1;
+    // the decode entry points ask for max_cache + 1 positions, max_cache
+    // being the cache's slot count (context + 1)
+    rope_pos_ = m.cache().slots + 1;
     check_hip(cactus_hip_rope_reserve(rope_pos_, hd, c.rope_theta), "rope_reserve");
     check_hip(cactus_hip_stream_sync(m.stream()), "sync");
 }
