@@ -119,6 +119,7 @@ public:
 private:
     size_t forward(const std::vector<uint32_t>& tokens);
     size_t shared_matmul_input(size_t x);
+    size_t norm_for_matmuls(size_t h, size_t weight);
     size_t build_attention(size_t x, uint32_t l, size_t pos);
     size_t build_mlp(size_t x, uint32_t l);
     size_t build_block(size_t h, uint32_t l, size_t pos);

@@ -143,6 +143,12 @@ size_t CactusGraph::rms_norm(size_t input, size_t weight, float epsilon) {
     return add_node(OpType::RMS_NORM, {input, weight}, node(input).out.shape, Precision::FP16, p);
 }
 
+size_t CactusGraph::rms_norm_quantize(size_t input, size_t weight, float epsilon) {
+    OpParams p;
+    p.epsilon = epsilon;
+    return add_node(OpType::RMS_NORM_QUANTIZE, {input, weight}, node(input).out.shape, Precision::INT8, p);
+}
+
 size_t CactusGraph::rope(size_t input, float theta, size_t position_offset) {
     OpParams p;
     p.theta = theta;
@@ -376,7 +382,7 @@ void CactusGraph::allocate(GraphNode& n) {
         n.out.data = pool_.acquire(n.out.byte_size);
         n.out.pooled_bytes = n.out.byte_size;
     }
-    if (n.op == OpType::QUANTIZE_ACTIVATIONS && !n.out.activation_scales) {
+    if (has_row_scales(n.op) && !n.out.activation_scales) {
         const auto& s = n.out.shape;
         const size_t rows = n.out.total_size / s.back();
         n.out.activation_scales = pool_.acquire(rows * sizeof(float));
@@ -461,6 +467,15 @@ void CactusGraph::compute(GraphNode& n) {
             check_hip(cactus_hip_rms_norm_f16(u16(x.data), u16(in(1).data), out16, x.shape[0], x.shape[1],
                                               n.params.epsilon, st),
                       "rms_norm");
+            return;
+        }
+        case OpType::RMS_NORM_QUANTIZE: {
+            const BufferDesc& x = in(0);
+            if (x.shape.size() != 2) throw std::runtime_error("RMS normalization requires 2D input tensor");
+            check_hip(cactus_hip_rms_norm_quantize_f16(u16(x.data), u16(in(1).data), static_cast<int8_t*>(n.out.data),
+                                                       static_cast<float*>(n.out.activation_scales), x.shape[0],
+                                                       x.shape[1], n.params.epsilon, st),
+                      "rms_norm_quantize");
             return;
         }
         case OpType::ROPE: {  // graph_ops_nn.cpp:253-277
@@ -555,7 +570,7 @@ void CactusGraph::release_outputs() {
             n->out.data = nullptr;
             n->out.pooled_bytes = 0;
         }
-        if (n->op == OpType::QUANTIZE_ACTIVATIONS && n->out.activation_scales) {
+        if (has_row_scales(n->op) && n->out.activation_scales) {
             const size_t rows = n->out.total_size / n->out.shape.back();
             pool_.release(n->out.activation_scales, rows * sizeof(float));
             n->out.activation_scales = nullptr;
@@ -577,7 +592,7 @@ void CactusGraph::soft_reset() {
             keep.push_back(std::move(n));
         } else if (n->out.pooled_bytes && !n->out.external) {
             pool_.release(n->out.data, n->out.pooled_bytes);
-            if (n->op == OpType::QUANTIZE_ACTIVATIONS && n->out.activation_scales)
+            if (has_row_scales(n->op) && n->out.activation_scales)
                 pool_.release(n->out.activation_scales, n->out.total_size / n->out.shape.back() * sizeof(float));
         }
     }

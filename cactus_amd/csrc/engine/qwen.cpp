@@ -269,7 +269,17 @@ void QwenModel::reset() {
 // a decode-sized GEMV quantizes inside its kernel at no extra launch.
 size_t QwenModel::shared_matmul_input(size_t x) {
     CactusGraph& g = *graph_;
-    return g.get_output_buffer(x).shape[0] >= 32 ? g.quantize_activations(x) : x;
+    const BufferDesc& b = g.get_output_buffer(x);
+    if (b.precision == Precision::INT8) return x;   // already codes with row scales
+    return b.shape[0] >= 32 ? g.quantize_activations(x) : x;
+}
+
+// The RMSNorm in front of q/k/v and of gate/up feeds only those matmuls: at
+// prefill sizes it is one node with their row quantization.
+size_t QwenModel::norm_for_matmuls(size_t h, size_t weight) {
+    CactusGraph& g = *graph_;
+    if (g.get_output_buffer(h).shape[0] >= 32) return g.rms_norm_quantize(h, weight, cfg_.eps);
+    return g.rms_norm(h, weight, cfg_.eps);
 }
 
 // model_qwen.cpp:51-106
@@ -324,10 +334,10 @@ size_t QwenModel::build_mlp(size_t x, uint32_t l) {
 size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
-    size_t x = g.rms_norm(h, L.n_input_norm, cfg_.eps);
+    size_t x = norm_for_matmuls(h, L.n_input_norm);
     size_t att = build_attention(x, l, pos);
     size_t h1 = g.add(h, att);
-    size_t x2 = g.rms_norm(h1, L.n_post_norm, cfg_.eps);
+    size_t x2 = norm_for_matmuls(h1, L.n_post_norm);
     size_t mlp = build_mlp(x2, l);
     return g.add(h1, mlp);
 }

@@ -1,5 +1,6 @@
 // quant.hip -- activation quantization (a1), KV-cache quantization (a7) and
 // INT4 unpacking.
+#include "decode_device.h"
 #include "quant_device.h"
 
 namespace cactus_hip {
@@ -44,6 +45,53 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
     int8_t* qr = q + row * (size_t)K;
     for (int i = threadIdx.x; i < K; i += blockDim.x) qr[i] = quant_code(h2f(xr[i]), inv, i >= body);
     if (threadIdx.x == 0) scales[row] = s;
+}
+
+// RMSNorm (kernel_attention.cpp:484-563) followed by the per-row
+// activation quantization of the matmul that consumes it
+// (graph_ops_nn.cpp:35-66): the normalized fp16 row stays in LDS, its max
+// gives the row scale, the codes are written directly.  The same results as
+// cactus_hip_rms_norm_f16 then cactus_hip_quantize_activations, one launch.
+__global__ void __launch_bounds__(256) rms_quant_rows_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             int8_t* __restrict__ q, float* __restrict__ scales,
+                                                             int K, float eps) {
+    extern __shared__ uint16_t xs[];   // the row, then its normalized values
+    __shared__ float red[4];
+    __shared__ float st[2];
+    const int tid = threadIdx.x;
+    const size_t row = blockIdx.x;
+    const uint16_t* xr = x + row * (size_t)K;
+    for (int i = tid; i < K; i += 256) xs[i] = xr[i];
+    __syncthreads();
+    if (tid < 64) {
+        float inv;
+        uint16_t hinv;
+        rms_stats_wave(xs, K, eps, inv, hinv);
+        if (tid == 0) {
+            st[0] = inv;
+            st[1] = __builtin_bit_cast(float, (uint32_t)hinv);
+        }
+    }
+    __syncthreads();
+    const float inv = st[0];
+    const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, st[1]);
+    const int end8 = (K / 8) * 8;
+    float m = 0.0f;
+    for (int i = tid; i < K; i += 256) {
+        const uint16_t y = rms_apply(xs[i], w[i], i, end8, inv, hinv);
+        xs[i] = y;
+        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(y)));
+    }
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float s = row_scale_from_max(mx);
+    const float inv_s = 1.0f / s;
+    int8_t* qr = q + row * (size_t)K;
+    for (int i = tid; i < K; i += 256) qr[i] = quant_code(h2f(xs[i]), inv_s, i >= end8);
+    if (tid == 0) scales[row] = s;
 }
 
 // cactus_quantize_kv_fp16_to_int8: one wave per (token, head, group).
@@ -124,6 +172,16 @@ int cactus_hip_quantize_activations(const uint16_t* x, int8_t* q, float* scales,
     hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)M), dim3(256), 0, as_stream(stream), x,
                        q, scales, (int)K);
     return check_launch("quantize_activations");
+}
+
+int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, int8_t* q, float* scales,
+                                     size_t M, size_t K, float eps, void* stream) {
+    if (M == 0 || K == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && weight && q && scales, "rms_norm_quantize: null pointer");
+    CH_REQUIRE(K <= 32768 && M < (1u << 31), "rms_norm_quantize: rows of at most 32768 values");
+    hipLaunchKernelGGL(rms_quant_rows_kernel, dim3((unsigned)M), dim3(256), K * sizeof(uint16_t),
+                       as_stream(stream), x, weight, q, scales, (int)K, eps);
+    return check_launch("rms_norm_quantize");
 }
 
 int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,

@@ -155,6 +155,13 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
                                           int is_causal, size_t quant_group_size, void* stream);
 
 /* ------------------------------------------------ a7: KV quantization */
+/* No single reference function: an RMSNorm node (cactus_rms_norm_f16,
+ * kernel_attention.cpp:484-563) whose output only feeds matmuls, fused with
+ * those matmuls' per-row activation quantization (graph_ops_nn.cpp:35-66):
+ * codes [M][K] and row scales [M], identical to cactus_hip_rms_norm_f16
+ * followed by cactus_hip_quantize_activations.  K <= 32768. */
+int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, int8_t* q, float* scales,
+                                     size_t M, size_t K, float eps, void* stream);
 /* cactus_quantize_kv_fp16_to_int8 (kernel/kernel.h:150, kernel_quants.cpp:223-293)
  * src [S][Hkv][d] fp16 -> dst int8 same shape, scales [S][Hkv][ceil(d/g)] f32. */
 int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,

@@ -640,3 +640,19 @@ def test_sample_greedy(dev, orc):
     rc = dev.cm.hip().cactus_hip_sample_f16(lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 0,
                                             1, None)
     assert rc == -2  # CACTUS_HIP_EUNSUPPORTED
+
+
+@pytest.mark.parametrize("M,K", [(256, 1024), (33, 1001), (1, 3072), (512, 2048), (40, 16)])
+def test_rms_norm_quantize_fused(dev, orc, M, K):
+    """The fused RMSNorm + row quantization equals cactus_hip_rms_norm_f16
+    followed by cactus_hip_quantize_activations, and the oracle's pair."""
+    say("rms_norm_quantize", M, K)
+    rng = np.random.default_rng(M + K)
+    x = f16(rng.normal(0, 1.5, (M, K)))
+    w = f16(1 + rng.normal(0, 0.05, K))
+    xp, wp = dev.put(x), dev.put(w)
+    q, s = dev.empty(M * K), dev.empty(M * 4)
+    dev.cm.call("cactus_hip_rms_norm_quantize_f16", xp, wp, q.ptr, s.ptr, M, K, ctypes.c_float(1e-6), None)
+    rq, rs = orc.quantize_activations(orc.rms_norm(x, w, 1e-6))
+    assert_bits(dev.get(s, np.float32, M).view(np.uint32), rs.view(np.uint32), "scales")
+    assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
