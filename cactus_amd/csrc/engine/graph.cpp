@@ -149,6 +149,12 @@ size_t CactusGraph::rms_norm_quantize(size_t input, size_t weight, float epsilon
     return add_node(OpType::RMS_NORM_QUANTIZE, {input, weight}, node(input).out.shape, Precision::INT8, p);
 }
 
+size_t CactusGraph::silu_mul_quantize(size_t gate, size_t up) {
+    if (node(gate).out.total_size != node(up).out.total_size)
+        throw std::runtime_error("multiply: broadcasting is not built (shapes must match)");
+    return add_node(OpType::SILU_MUL_QUANTIZE, {gate, up}, node(gate).out.shape, Precision::INT8);
+}
+
 size_t CactusGraph::rope(size_t input, float theta, size_t position_offset) {
     OpParams p;
     p.theta = theta;
@@ -476,6 +482,14 @@ void CactusGraph::compute(GraphNode& n) {
                                                        static_cast<float*>(n.out.activation_scales), x.shape[0],
                                                        x.shape[1], n.params.epsilon, st),
                       "rms_norm_quantize");
+            return;
+        }
+        case OpType::SILU_MUL_QUANTIZE: {
+            const BufferDesc& gt = in(0);
+            const size_t K = gt.shape.back(), M = gt.total_size / K;
+            check_hip(cactus_hip_silu_mul_quantize_f16(u16(gt.data), u16(in(1).data), static_cast<int8_t*>(n.out.data),
+                                                       static_cast<float*>(n.out.activation_scales), M, K, st),
+                      "silu_mul_quantize");
             return;
         }
         case OpType::ROPE: {  // graph_ops_nn.cpp:253-277

@@ -24,11 +24,13 @@ enum class OpType {
     INPUT, MATMUL, RMS_NORM, ROPE, SOFTMAX, ATTENTION, ATTENTION_INT8_HYBRID,
     SILU, ADD, MULTIPLY, EMBEDDING, INDEX, RESHAPE, SAMPLE, QUANTIZE_ACTIVATIONS,
     RMS_NORM_QUANTIZE,   // RMS_NORM feeding only matmuls, fused with their row quantization
+    SILU_MUL_QUANTIZE,   // silu(gate) * up feeding only a matmul, fused with its row quantization
 };
 
 // nodes whose output is INT8 codes with per-row activation scales
 inline bool has_row_scales(OpType op) {
-    return op == OpType::QUANTIZE_ACTIVATIONS || op == OpType::RMS_NORM_QUANTIZE;
+    return op == OpType::QUANTIZE_ACTIVATIONS || op == OpType::RMS_NORM_QUANTIZE ||
+           op == OpType::SILU_MUL_QUANTIZE;
 }
 
 size_t precision_size(Precision p);
@@ -121,6 +123,8 @@ public:
     size_t rms_norm(size_t input, size_t weight, float epsilon = 1e-5f);
     // rms_norm + quantize_activations in one node (same codes and scales)
     size_t rms_norm_quantize(size_t input, size_t weight, float epsilon = 1e-5f);
+    // multiply(silu(gate), up) + quantize_activations in one node
+    size_t silu_mul_quantize(size_t gate, size_t up);
     size_t rope(size_t input, float theta, size_t position_offset = 0);
     size_t softmax(size_t input, int axis = -1);
     size_t attention(size_t q, size_t k, size_t v, float scale, size_t position_offset = 0,

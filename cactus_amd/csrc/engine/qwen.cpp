@@ -325,6 +325,9 @@ size_t QwenModel::build_mlp(size_t x, uint32_t l) {
     const size_t xq = shared_matmul_input(x);
     size_t gate = g.matmul(xq, L.n_gate, true);
     size_t up = g.matmul(xq, L.n_up, true);
+    // at prefill sizes the SwiGLU product is one node with the down
+    // projection's row quantization
+    if (g.get_output_buffer(gate).shape[0] >= 32) return g.matmul(g.silu_mul_quantize(gate, up), L.n_down, true);
     size_t act = g.silu(gate);
     size_t m = g.multiply(act, up);
     return g.matmul(m, L.n_down, true);

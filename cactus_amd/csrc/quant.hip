@@ -94,6 +94,41 @@ __global__ void __launch_bounds__(256) rms_quant_rows_kernel(const uint16_t* __r
     if (tid == 0) scales[row] = s;
 }
 
+// SiLU (kernel_nn.cpp:12-44: fast_exp in the vector body, expf in the n % 8
+// tail of the whole tensor), the SwiGLU multiply (kernel_blas.cpp:291-316)
+// and the row quantization of the down projection that consumes the
+// product: one launch, the same codes and scales as the three nodes.
+__global__ void __launch_bounds__(256) silu_mul_quant_rows_kernel(const uint16_t* __restrict__ gate,
+                                                                  const uint16_t* __restrict__ up,
+                                                                  int8_t* __restrict__ q,
+                                                                  float* __restrict__ scales, int K,
+                                                                  size_t body) {
+    extern __shared__ uint16_t ms[];   // the row of silu(gate) * up
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const size_t row = blockIdx.x, base = row * (size_t)K;
+    float m = 0.0f;
+    for (int i = tid; i < K; i += 256) {
+        const size_t gi = base + i;
+        const float x = h2f(gate[gi]);
+        const float e = gi < body ? fast_exp(-x) : cactus_expf(-x);
+        const float sig = 1.0f / (1.0f + e);
+        const uint16_t v = hmul(f2h(x * sig), up[gi]);
+        ms[i] = v;
+        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(v)));
+    }
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float s = row_scale_from_max(mx);
+    const float inv_s = 1.0f / s;
+    const int end8 = (K / 8) * 8;
+    int8_t* qr = q + base;
+    for (int i = tid; i < K; i += 256) qr[i] = quant_code(h2f(ms[i]), inv_s, i >= end8);
+    if (tid == 0) scales[row] = s;
+}
+
 // cactus_quantize_kv_fp16_to_int8: one wave per (token, head, group).
 // Body codes: sat8(rne(x * inv)) without a clamp; the count%8 tail of a
 // group uses roundf (kernel_quants.cpp:223-264).
@@ -182,6 +217,17 @@ int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, 
     hipLaunchKernelGGL(rms_quant_rows_kernel, dim3((unsigned)M), dim3(256), K * sizeof(uint16_t),
                        as_stream(stream), x, weight, q, scales, (int)K, eps);
     return check_launch("rms_norm_quantize");
+}
+
+int cactus_hip_silu_mul_quantize_f16(const uint16_t* gate, const uint16_t* up, int8_t* q, float* scales,
+                                     size_t M, size_t K, void* stream) {
+    if (M == 0 || K == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(gate && up && q && scales, "silu_mul_quantize: null pointer");
+    CH_REQUIRE(K <= 32768 && M < (1u << 31), "silu_mul_quantize: rows of at most 32768 values");
+    const size_t body = ((M * K) / 8) * 8;
+    hipLaunchKernelGGL(silu_mul_quant_rows_kernel, dim3((unsigned)M), dim3(256), K * sizeof(uint16_t),
+                       as_stream(stream), gate, up, q, scales, (int)K, body);
+    return check_launch("silu_mul_quantize");
 }
 
 int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,

@@ -162,6 +162,13 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
  * followed by cactus_hip_quantize_activations.  K <= 32768. */
 int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, int8_t* q, float* scales,
                                      size_t M, size_t K, float eps, void* stream);
+/* No single reference function: the SwiGLU nodes silu(gate) * up
+ * (cactus_silu_f16, kernel_nn.cpp:12-44; cactus_multiply_f16,
+ * kernel_blas.cpp:291-316) fused with the row quantization of the matmul
+ * they feed: codes [M][K] and row scales [M], identical to the three nodes
+ * (the silu tail rule counts over the whole [M][K] tensor).  K <= 32768. */
+int cactus_hip_silu_mul_quantize_f16(const uint16_t* gate, const uint16_t* up, int8_t* q, float* scales,
+                                     size_t M, size_t K, void* stream);
 /* cactus_quantize_kv_fp16_to_int8 (kernel/kernel.h:150, kernel_quants.cpp:223-293)
  * src [S][Hkv][d] fp16 -> dst int8 same shape, scales [S][Hkv][ceil(d/g)] f32. */
 int cactus_hip_quantize_kv_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,

@@ -656,3 +656,20 @@ def test_rms_norm_quantize_fused(dev, orc, M, K):
     rq, rs = orc.quantize_activations(orc.rms_norm(x, w, 1e-6))
     assert_bits(dev.get(s, np.float32, M).view(np.uint32), rs.view(np.uint32), "scales")
     assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
+
+
+@pytest.mark.parametrize("M,K", [(256, 3072), (33, 1001), (64, 12), (1, 3072)])
+def test_silu_mul_quantize_fused(dev, orc, M, K):
+    """silu(gate) * up with the row quantization in one launch equals the
+    oracle's silu, multiply and quantize_activations (ragged M*K puts the
+    silu expf tail in the last row)."""
+    say("silu_mul_quantize", M, K)
+    rng = np.random.default_rng(M * 3 + K)
+    gate = f16(rng.normal(0, 2, (M, K)))
+    up = f16(rng.normal(0, 1, (M, K)))
+    q, s = dev.empty(M * K), dev.empty(M * 4)
+    dev.cm.call("cactus_hip_silu_mul_quantize_f16", dev.put(gate), dev.put(up), q.ptr, s.ptr, M, K, None)
+    prod = orc.multiply(orc.silu(gate.reshape(-1)), up.reshape(-1)).reshape(M, K)
+    rq, rs = orc.quantize_activations(prod)
+    assert_bits(dev.get(s, np.float32, M).view(np.uint32), rs.view(np.uint32), "scales")
+    assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
