@@ -1,5 +1,6 @@
 // elementwise.hip -- RMSNorm (a8), RoPE (a9), softmax (a10), SiLU (a11),
 // fp16 add/multiply (a12) and the embedding gather (a13).
+#include "decode_device.h"
 #include "hip_common.h"
 
 #include <cmath>
@@ -181,6 +182,37 @@ __global__ void __launch_bounds__(256) softmax_kernel(const uint16_t* __restrict
 }
 
 // ---------------------------------------------------------------- SiLU, add, mul
+// The per-head RMSNorm of q and k (the q_norm / k_norm nodes,
+// kernel_attention.cpp:484-563) followed by RoPE (:565-676) at the rows'
+// positions: one wave per (token, head) row, the row and its normalized
+// values in LDS.  The same results as cactus_hip_rms_norm_f16 then
+// cactus_hip_rope_f16.
+__global__ void __launch_bounds__(256) rms_rope_rows_kernel(const uint16_t* __restrict__ X,
+                                                            const uint16_t* __restrict__ W,
+                                                            uint16_t* __restrict__ Y, const uint16_t* __restrict__ ct,
+                                                            const uint16_t* __restrict__ stb, size_t rows, int S,
+                                                            int H, int d, size_t start_pos, float eps) {
+    __shared__ uint16_t buf[4][2][256];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * 4 + wv;
+    if (r >= rows) return;   // the whole wave: no workgroup barrier below
+    const int s = (int)((r / H) % S);   // row = (b * S + s) * H + h
+    uint16_t* xs = buf[wv][0];
+    uint16_t* ys = buf[wv][1];
+    const uint16_t* xr = X + r * d;
+    for (int i = lane; i < d; i += 64) xs[i] = xr[i];
+    wave_lds_order();
+    float inv;
+    uint16_t hinv;
+    rms_stats_wave(xs, d, eps, inv, hinv);
+    const int end8 = (d / 8) * 8;
+    for (int i = lane; i < d; i += 64) ys[i] = rms_apply(xs[i], W[i], i, end8, inv, hinv);
+    wave_lds_order();
+    const size_t toff = (start_pos + s) * (size_t)(d / 2);
+    uint16_t* yr = Y + r * d;
+    rope_row(ys, d, ct + toff, stb + toff, [&](int i, uint16_t v) { yr[i] = v; });
+}
+
 __global__ void silu_kernel(const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, size_t n) {
     const size_t body = (n / 8) * 8;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -286,6 +318,23 @@ int cactus_hip_rope_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq
                        y, t->cos_d, t->sin_d, pairs, (int)seq_len, (int)num_heads, (int)head_dim,
                        start_pos);
     return check_launch("rope");
+}
+
+int cactus_hip_rms_norm_rope_f16(const uint16_t* x, const uint16_t* weight, uint16_t* y, size_t batch,
+                                 size_t seq_len, size_t num_heads, size_t head_dim, size_t start_pos, float theta,
+                                 float eps, void* stream) {
+    const size_t rows = batch * seq_len * num_heads;
+    if (rows == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(x && weight && y, "rms_norm_rope: null pointer");
+    CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, "rms_norm_rope: head_dim must be even, <= 256");
+    CH_REQUIRE(rows / 4 < (1u << 31), "rms_norm_rope: too many rows");
+    const RopeTable* t = nullptr;
+    int rc = rope_table(seq_len + start_pos, head_dim, theta, &t);
+    if (rc) return rc;
+    hipLaunchKernelGGL(rms_rope_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, as_stream(stream), x,
+                       weight, y, t->cos_d, t->sin_d, rows, (int)seq_len, (int)num_heads, (int)head_dim, start_pos,
+                       eps);
+    return check_launch("rms_norm_rope");
 }
 
 int cactus_hip_softmax_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq_len,

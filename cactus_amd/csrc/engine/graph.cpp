@@ -155,6 +155,15 @@ size_t CactusGraph::silu_mul_quantize(size_t gate, size_t up) {
     return add_node(OpType::SILU_MUL_QUANTIZE, {gate, up}, node(gate).out.shape, Precision::INT8);
 }
 
+size_t CactusGraph::rms_norm_rope(size_t input, size_t weight, float epsilon, float theta, size_t position_offset) {
+    if (node(input).out.shape.size() < 4) throw std::runtime_error("RoPE operation requires 4D tensor");
+    OpParams p;
+    p.epsilon = epsilon;
+    p.theta = theta;
+    p.position_offset = position_offset;
+    return add_node(OpType::RMS_NORM_ROPE, {input, weight}, node(input).out.shape, Precision::FP16, p);
+}
+
 size_t CactusGraph::rope(size_t input, float theta, size_t position_offset) {
     OpParams p;
     p.theta = theta;
@@ -490,6 +499,13 @@ void CactusGraph::compute(GraphNode& n) {
             check_hip(cactus_hip_silu_mul_quantize_f16(u16(gt.data), u16(in(1).data), static_cast<int8_t*>(n.out.data),
                                                        static_cast<float*>(n.out.activation_scales), M, K, st),
                       "silu_mul_quantize");
+            return;
+        }
+        case OpType::RMS_NORM_ROPE: {
+            const auto& sh = in(0).shape;
+            check_hip(cactus_hip_rms_norm_rope_f16(u16(in(0).data), u16(in(1).data), out16, sh[0], sh[1], sh[2], sh[3],
+                                                   n.params.position_offset, n.params.theta, n.params.epsilon, st),
+                      "rms_norm_rope");
             return;
         }
         case OpType::ROPE: {  // graph_ops_nn.cpp:253-277

@@ -292,18 +292,19 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
     size_t k = g.matmul(xq, L.n_k, true);
     size_t v = g.matmul(xq, L.n_v, true);
     const size_t S = g.get_output_buffer(q).shape[0];
-    q = g.reshape(q, {S * nh, hd});
-    q = g.rms_norm(q, L.n_q_norm, cfg_.eps);
-    q = g.reshape(q, {S, nh * hd});
-    k = g.reshape(k, {S * nkv, hd});
-    k = g.rms_norm(k, L.n_k_norm, cfg_.eps);
-    k = g.reshape(k, {S, nkv * hd});
-    size_t q4 = g.reshape(q, {1, S, nh, hd});
-    size_t k4 = g.reshape(k, {1, S, nkv, hd});
+    size_t q4, k4;
     size_t v4 = g.reshape(v, {1, S, nkv, hd});
     if (cfg_.rope_theta > 0) {
-        q4 = g.rope(q4, cfg_.rope_theta, pos);
-        k4 = g.rope(k4, cfg_.rope_theta, pos);
+        // the head RMSNorm and RoPE of q and of k, one node each
+        q4 = g.rms_norm_rope(g.reshape(q, {1, S, nh, hd}), L.n_q_norm, cfg_.eps, cfg_.rope_theta, pos);
+        k4 = g.rms_norm_rope(g.reshape(k, {1, S, nkv, hd}), L.n_k_norm, cfg_.eps, cfg_.rope_theta, pos);
+    } else {
+        q = g.reshape(q, {S * nh, hd});
+        q = g.rms_norm(q, L.n_q_norm, cfg_.eps);
+        k = g.reshape(k, {S * nkv, hd});
+        k = g.rms_norm(k, L.n_k_norm, cfg_.eps);
+        q4 = g.reshape(q, {1, S, nh, hd});
+        k4 = g.reshape(k, {1, S, nkv, hd});
     }
     k_nodes_[l] = k4;
     v_nodes_[l] = v4;

@@ -162,6 +162,13 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
  * followed by cactus_hip_quantize_activations.  K <= 32768. */
 int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, int8_t* q, float* scales,
                                      size_t M, size_t K, float eps, void* stream);
+/* No single reference function: the per-head RMSNorm of q or k (the
+ * q_norm / k_norm nodes, model_qwen.cpp:63-70, cactus_rms_norm_f16 over rows
+ * of head_dim) followed by their RoPE (cactus_rope_f16, model_qwen.cpp:78-81)
+ * on x [batch][seq][heads][head_dim]; identical to the two nodes. */
+int cactus_hip_rms_norm_rope_f16(const uint16_t* x, const uint16_t* weight, uint16_t* y, size_t batch,
+                                 size_t seq_len, size_t num_heads, size_t head_dim, size_t start_pos, float theta,
+                                 float eps, void* stream);
 /* No single reference function: the SwiGLU nodes silu(gate) * up
  * (cactus_silu_f16, kernel_nn.cpp:12-44; cactus_multiply_f16,
  * kernel_blas.cpp:291-316) fused with the row quantization of the matmul

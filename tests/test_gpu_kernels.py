@@ -673,3 +673,17 @@ def test_silu_mul_quantize_fused(dev, orc, M, K):
     rq, rs = orc.quantize_activations(prod)
     assert_bits(dev.get(s, np.float32, M).view(np.uint32), rs.view(np.uint32), "scales")
     assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
+
+
+@pytest.mark.parametrize("S,H,d,pos", [(256, 16, 128, 3840), (1, 8, 128, 4095), (7, 4, 64, 0), (5, 2, 12, 9)])
+def test_rms_norm_rope_fused(dev, orc, S, H, d, pos):
+    """The head RMSNorm then RoPE in one launch equals the oracle's pair."""
+    say("rms_norm_rope", S, H, d, pos)
+    rng = np.random.default_rng(S + H + d + pos)
+    x = f16(rng.normal(0, 1.5, (1, S, H, d)))
+    w = f16(1 + rng.normal(0, 0.05, d))
+    y = dev.empty(x.nbytes)
+    dev.cm.call("cactus_hip_rms_norm_rope_f16", dev.put(x), dev.put(w), y.ptr, 1, S, H, d, pos,
+                ctypes.c_float(1e6), ctypes.c_float(1e-6), None)
+    ref = orc.rope(orc.rms_norm(x.reshape(S * H, d), w, 1e-6).reshape(1, S, H, d), pos, 1e6)
+    assert_bits(dev.get(y, np.uint16, x.shape), ref, "rms_norm_rope")
