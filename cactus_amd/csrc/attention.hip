@@ -507,30 +507,80 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
 #pragma unroll
         for (int c = 0; c < 8; c++) acc[q][c] = 0.0f;
     const int lr = lane & 15;
+    // prefill form: the next 16 dims of the key (codes and scale, or fp16
+    // values) are loaded while the current 16 feed the FMAs, so a step's
+    // global round trip overlaps the previous step's 128 FMAs
+    // The loads take no branch: a lane past the last key reads the row of
+    // the wave's last live key instead (its values are never used), an INT8
+    // row is read through both pointers, an fp16 row as two halves.
+    uint4 nx0[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    uint4 nx1[2] = {make_uint4(0, 0, 0, 0), make_uint4(0, 0, 0, 0)};
+    float nxs[2] = {0.0f, 0.0f};   // two buffers, alternating by step
+    const bool one_scale = a.qgs >= D;
+    float s_row = 0.0f;
+    const uint8_t* ld0 = nullptr;
+    const uint8_t* ld1 = nullptr;
+    int ldstep = 0;
+    if constexpr (!PRE) {
+        if (kload && kint8 && one_scale) s_row = ksr[0];
+        const size_t kpl = kload ? kp : kv_end_max - 1;   // kv_end_max > wbase here
+        if (HYBRID && kpl < a.cache_len) {
+            ld0 = reinterpret_cast<const uint8_t*>(a.kc + ((b * a.cache_len + kpl) * a.Hkv + kvh) * (size_t)d);
+            ld1 = ld0;
+            ldstep = 16;
+        } else {
+            const size_t kpos = HYBRID ? kpl - a.cache_len : kpl;
+            const size_t klen = HYBRID ? a.new_len : a.Skv;
+            ld0 = reinterpret_cast<const uint8_t*>(a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d);
+            ld1 = ld0 + 16;
+            ldstep = 32;
+        }
+    }
+    auto fetch = [&](int m) {
+        if constexpr (!PRE) {
+            nx0[m & 1] = *reinterpret_cast<const uint4*>(ld0 + (size_t)ldstep * m);
+            nx1[m & 1] = *reinterpret_cast<const uint4*>(ld1 + (size_t)ldstep * m);
+            if (!one_scale) nxs[m & 1] = (kload && kint8) ? ksr[(16 * m) / a.qgs] : 0.0f;
+        }
+    };
+    fetch(0);
 #pragma unroll
     for (int m = 0; m < D / 16; m++) {
+        if (m + 1 < D / 16) fetch(m + 1);
+        const uint4 cur0 = nx0[m & 1], cur1 = nx1[m & 1];
+        const float cur_s = nxs[m & 1];
         float kk[16];
-        if (kload && kint8) {
-            const uint4 raw = PRE ? pre[PRE ? m : 0] : *reinterpret_cast<const uint4*>(krow8 + 16 * m);
-            const float s = (PRE && a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs];
+        auto conv_i8 = [&](const uint4 raw, const float s) {
             const float ns = -128.0f * s;
             const uint32_t w4[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
                                     raw.w ^ 0x80808080u};
 #pragma unroll
             for (int e = 0; e < 16; e++)
                 kk[e] = __builtin_fmaf((float)((w4[e >> 2] >> (8 * (e & 3))) & 0xFFu), s, ns);
-        } else if (kload) {
-            const uint4 r0 = *reinterpret_cast<const uint4*>(krow16 + 16 * m);
-            const uint4 r1 = *reinterpret_cast<const uint4*>(krow16 + 16 * m + 8);
+        };
+        auto conv_f16 = [&](const uint4 r0, const uint4 r1) {
             const uint32_t h[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 kk[2 * e] = h2f((uint16_t)(h[e] & 0xFFFF));
                 kk[2 * e + 1] = h2f((uint16_t)(h[e] >> 16));
             }
-        } else {
+        };
+        if constexpr (PRE) {
+            if (kload && kint8) {
+                conv_i8(pre[m], (a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs]);
+            } else if (kload) {
+                conv_f16(*reinterpret_cast<const uint4*>(krow16 + 16 * m),
+                         *reinterpret_cast<const uint4*>(krow16 + 16 * m + 8));
+            } else {
 #pragma unroll
-            for (int e = 0; e < 16; e++) kk[e] = 0.0f;
+                for (int e = 0; e < 16; e++) kk[e] = 0.0f;
+            }
+        } else {
+            // a lane past the last key converts the row it loaded; its
+            // scores are never used (not computed, or masked to -inf)
+            if (ldstep == 16) conv_i8(cur0, one_scale ? s_row : cur_s);
+            else conv_f16(cur0, cur1);
         }
         float qv[NQ];
 #pragma unroll
