@@ -246,7 +246,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=200)   # ~33 ms of GEMV launches: steady clocks
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--decode-mode", type=int, default=1,
                     help="1: fused decode step replayed as one HIP graph (default); 0: node-by-node graph")
