@@ -248,8 +248,14 @@ size_t CactusGraph::reshape(size_t input, const std::vector<size_t>& new_shape) 
     return add_node(OpType::RESHAPE, {input}, new_shape, node(input).out.precision, p);
 }
 
-size_t CactusGraph::sample(size_t logits, float temperature, float top_p, size_t top_k, size_t random_seed) {
+size_t CactusGraph::sample(size_t logits, float temperature, float top_p, size_t top_k, size_t random_seed,
+                           const std::vector<std::pair<uint32_t, float>>& logit_bias) {
+    if (node(logits).out.shape.empty()) throw std::runtime_error("Sample requires non-empty logits tensor");
     OpParams p;
+    for (const auto& e : logit_bias) {
+        p.bias_indices.push_back(e.first);
+        p.bias_values.push_back(e.second);
+    }
     p.temperature = temperature;
     p.top_p = top_p;
     p.top_k = top_k;
@@ -572,6 +578,17 @@ void CactusGraph::compute(GraphNode& n) {
             const BufferDesc& l = in(0);
             if (l.shape.size() != 2) throw std::runtime_error("Sample expects 2D logits tensor [seq_len, vocab_size]");
             const size_t V = l.shape[1];
+            if (l.precision == Precision::FP32) {
+                const float* last = static_cast<const float*>(l.data) + (l.shape[0] - 1) * V;
+                const auto& bv = n.params.bias_values;
+                check_hip(cactus_hip_sample_f32(last, static_cast<uint32_t*>(n.out.data), V, n.params.temperature,
+                                                n.params.top_p, n.params.top_k, n.params.random_seed,
+                                                bv.empty() ? nullptr : bv.data(),
+                                                bv.empty() ? nullptr : n.params.bias_indices.data(), bv.size(),
+                                                st),
+                          "sample");
+                return;
+            }
             const uint16_t* last = u16(l.data) + (l.shape[0] - 1) * V;
             check_hip(cactus_hip_sample_f16(last, static_cast<uint32_t*>(n.out.data), V, n.params.temperature,
                                             n.params.top_p, n.params.top_k, n.params.random_seed, st),

@@ -91,6 +91,8 @@ struct OpParams {
     float top_p = 0.0f;
     size_t top_k = 0;
     size_t random_seed = 0;   // graph_builder.cpp:408: the build time in clock ticks
+    std::vector<float> bias_values;       // logit bias (graph_builder.cpp:411-418)
+    std::vector<uint32_t> bias_indices;
     size_t index_value = 0;
     // ATTENTION_INT8_HYBRID (graph_builder.cpp:301-316)
     const int8_t* cached_keys_int8 = nullptr;
@@ -144,8 +146,9 @@ public:
     size_t index(size_t input, size_t index_value, int dim);
     size_t reshape(size_t input, const std::vector<size_t>& new_shape);
     // random_seed 0: the reference's seed, the clock at build time
+    // logit_bias reaches only FP32 logits: the FP16 sampler discards it
     size_t sample(size_t logits, float temperature = 0.6f, float top_p = 0.95f, size_t top_k = 20,
-                  size_t random_seed = 0);
+                  size_t random_seed = 0, const std::vector<std::pair<uint32_t, float>>& logit_bias = {});
 
     // --- data
     void set_input(size_t node, const void* host_data, Precision precision);

@@ -1,6 +1,7 @@
 // sample.hip -- the FP16 sampler (a14 greedy, and the full sampler of
 // kernel_nn.cpp:446-651): temperature, repetition penalty over the last 128
-// sampled tokens, top-k, top-p and the draw, in one workgroup.
+// sampled tokens, top-k, top-p and the draw, in one workgroup; and the FP32
+// sampler (kernel_nn.cpp:253-444, the one with the logit bias and min-p).
 //
 // Phases (one 1024-thread workgroup, vocabulary in a scratch copy):
 //   1. f = fp16(logit * fp16(1/T)) (or the raw logits); thread 0 applies the
@@ -35,11 +36,15 @@ constexpr int SP_HIST = 128;           // kernel_nn.cpp:517
 constexpr uint16_t SP_NEG_INF = 0xFC00u;
 
 // ---------------------------------------------------------------- greedy
-// First index of the maximum of (float)logit (kernel_nn.cpp:451-466): each
-// thread scans an increasing index range keeping a strict '>' winner; the
-// combine takes the larger value and, on equal values, the smaller index.
-__global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* __restrict__ L, size_t V,
-                                                      uint32_t* out) {
+// First index of the maximum of (float)logit (kernel_nn.cpp:451-466, and
+// :258-273 for FP32 logits): each thread scans an increasing index range
+// keeping a strict '>' winner; the combine takes the larger value and, on
+// equal values, the smaller index.
+__device__ __forceinline__ float logit_f(uint16_t h) { return h2f(h); }
+__device__ __forceinline__ float logit_f(float x) { return x; }
+
+template <typename T>
+__global__ void __launch_bounds__(1024) argmax_kernel(const T* __restrict__ L, size_t V, uint32_t* out) {
     __shared__ float bv_s[1024];
     __shared__ uint32_t bi_s[1024];
     const int tid = threadIdx.x;
@@ -49,7 +54,7 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const uint16_t* __restrict
     float bv = -__builtin_inff();
     uint32_t bi = 0xFFFFFFFFu;
     for (size_t i = s0; i < s1; i++) {
-        const float v = h2f(L[i]);
+        const float v = logit_f(L[i]);
         if (bi == 0xFFFFFFFFu || v > bv) { bv = v; bi = (uint32_t)i; }
     }
     bv_s[tid] = bv;
@@ -273,6 +278,252 @@ __global__ void __launch_bounds__(SP_T) sample_kernel(SampleArgs a) {
     *a.out = tok;
 }
 
+// ---------------------------------------------------------------- FP32 sampler
+// cactus_sample_f32 (kernel_nn.cpp:253-444) in one workgroup: the bias
+// entries in order, the division by T, top-k by a four-pass radix select over
+// order-preserving 32-bit keys, min-p 0.15 (probabilities over the survivors
+// in token order: parallel expf, the sum by one thread in token order, the
+// division and the threshold in parallel), top-p as in the FP16 sampler and
+// the draw.  Both infinities count as removed (std::isinf).  No history.
+constexpr int SP_BIAS = 128;           // logit-bias entries carried in the kernel arguments
+
+struct SampleF32Args {
+    const float* logits;
+    uint32_t* out;
+    float* f;           // [V] filtered logits
+    float* pv;          // [V] unnormalised probabilities of the survivors
+    uint32_t* surv;     // [V] survivor tokens in order
+    size_t V, top_k;
+    float top_p, u, temperature;
+    int scale;          // temperature > 0
+    int bias_n;
+    float bias_v[SP_BIAS];
+    uint32_t bias_i[SP_BIAS];
+};
+
+__device__ __forceinline__ uint32_t okey32(float x) {
+    uint32_t u = __float_as_uint(x);
+    if (u == 0x80000000u) u = 0;   // -0 == +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ bool is_inf(float x) { return x == __builtin_inff() || x == -__builtin_inff(); }
+
+// workgroup max of f over [0, V) (every thread gets it)
+__device__ float wg_max(const float* f, size_t V, float* red) {
+    const int tid = threadIdx.x;
+    float m = -__builtin_inff();
+    for (size_t i = tid; i < V; i += SP_T) m = __builtin_fmaxf(m, f[i]);
+    for (int o = 32; o > 0; o >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, o, 64));
+    __syncthreads();
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    float mx = red[0];
+    for (int w = 1; w < SP_T / 64; w++) mx = __builtin_fmaxf(mx, red[w]);
+    return mx;
+}
+
+// the finite entries of f in token order: surv[j] = token, pv[j] =
+// expf(f - mx); returns their count (every thread)
+__device__ uint32_t wg_compact(const float* f, size_t V, float mx, uint32_t* surv, float* pv, uint32_t* scan) {
+    const int tid = threadIdx.x;
+    const size_t per = (V + SP_T - 1) / SP_T;
+    const size_t c0 = (size_t)tid * per, c1 = c0 + per < V ? c0 + per : V;
+    uint32_t cnt = 0;
+    for (size_t i = c0; i < c1; i++) cnt += !is_inf(f[i]);
+    __syncthreads();
+    scan[tid] = cnt;
+    __syncthreads();
+    for (int o = 1; o < SP_T; o <<= 1) {   // inclusive scan
+        const uint32_t v = tid >= o ? scan[tid - o] : 0u;
+        __syncthreads();
+        scan[tid] += v;
+        __syncthreads();
+    }
+    uint32_t off = scan[tid] - cnt;
+    for (size_t i = c0; i < c1; i++) {
+        if (is_inf(f[i])) continue;
+        surv[off] = (uint32_t)i;
+        pv[off] = cactus_expf(f[i] - mx);
+        off++;
+    }
+    const uint32_t S = scan[SP_T - 1];
+    __syncthreads();
+    return S;
+}
+
+__global__ void __launch_bounds__(SP_T) sample_f32_kernel(SampleF32Args a) {
+    extern __shared__ unsigned long long cand[];   // [SP_CAND], dynamic: 128 KB
+    __shared__ uint32_t hbin[256];
+    __shared__ uint32_t scan[SP_T];
+    __shared__ float red[SP_T / 64];
+    __shared__ float shf[2];
+    __shared__ uint32_t sh_u32[4];
+    const int tid = threadIdx.x;
+    const size_t V = a.V;
+
+    // 1. copy, bias (:280-288, in entry order), temperature (:290-294)
+    for (size_t i = tid; i < V; i += SP_T) a.f[i] = a.logits[i];
+    __syncthreads();
+    if (tid == 0)
+        for (int j = 0; j < a.bias_n; j++)
+            if (a.bias_i[j] < V) a.f[a.bias_i[j]] += a.bias_v[j];
+    __syncthreads();
+    if (a.scale)
+        for (size_t i = tid; i < V; i += SP_T) a.f[i] = a.f[i] / a.temperature;
+    __syncthreads();
+
+    // 2. top-k (:296-313): the k-th largest value, four radix passes
+    if (a.top_k > 0 && a.top_k < V) {
+        uint32_t prefix = 0, need = (uint32_t)a.top_k;
+        for (int pass = 0; pass < 4; pass++) {
+            const int sh = 24 - 8 * pass;
+            if (tid < 256) hbin[tid] = 0;
+            __syncthreads();
+            for (size_t i = tid; i < V; i += SP_T) {
+                const uint32_t k = okey32(a.f[i]);
+                if (pass == 0 || (k >> (sh + 8)) == prefix) atomicAdd(&hbin[(k >> sh) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t cum = 0;
+                int b = 255;
+                for (; b > 0; b--) {
+                    if (cum + hbin[b] >= need) break;
+                    cum += hbin[b];
+                }
+                sh_u32[0] = (uint32_t)b;
+                sh_u32[1] = need - cum;
+            }
+            __syncthreads();
+            prefix = (prefix << 8) | sh_u32[0];
+            need = sh_u32[1];
+            __syncthreads();
+        }
+        const uint32_t kth = prefix;
+        for (size_t i = tid; i < V; i += SP_T)
+            if (okey32(a.f[i]) < kth) a.f[i] = -__builtin_inff();
+        __syncthreads();
+    }
+
+    // 3. min-p 0.15 (:316-346)
+    {
+        const float mx = wg_max(a.f, V, red);
+        if (!is_inf(mx)) {
+            const uint32_t S = wg_compact(a.f, V, mx, a.surv, a.pv, scan);
+            if (tid == 0) {
+                float sum = 0.0f;
+                for (uint32_t j = 0; j < S; j++) sum += a.pv[j];
+                shf[0] = sum;
+            }
+            __syncthreads();
+            const float sum = shf[0];
+            if (sum > 0.0f) {
+                float mp = 0.0f;
+                for (uint32_t j = tid; j < S; j += SP_T) mp = __builtin_fmaxf(mp, a.pv[j] / sum);
+                for (int o = 32; o > 0; o >>= 1) mp = __builtin_fmaxf(mp, __shfl_xor(mp, o, 64));
+                if ((tid & 63) == 0) red[tid >> 6] = mp;
+                __syncthreads();
+                float maxp = red[0];
+                for (int w = 1; w < SP_T / 64; w++) maxp = __builtin_fmaxf(maxp, red[w]);
+                const float thr = maxp * 0.15f;
+                // removed entries (probability 0) stay -inf; survivors below
+                // the threshold join them
+                for (uint32_t j = tid; j < S; j += SP_T)
+                    if (a.pv[j] / sum < thr) a.f[a.surv[j]] = -__builtin_inff();
+            }
+            __syncthreads();
+        }
+    }
+
+    // 4. top-p (:348-392) over the finite entries, sorted descending
+    if (a.top_p > 0.0f && a.top_p < 1.0f) {
+        if (tid == 0) sh_u32[2] = 0;
+        __syncthreads();
+        for (size_t i = tid; i < V; i += SP_T) {
+            if (is_inf(a.f[i])) continue;
+            const uint32_t slot = atomicAdd(&sh_u32[2], 1u);
+            if (slot < (uint32_t)SP_CAND)
+                cand[slot] = ((unsigned long long)(~okey32(a.f[i])) << 32) | (unsigned long long)i;
+        }
+        __syncthreads();
+        const uint32_t n = sh_u32[2];
+        if (n > (uint32_t)SP_CAND) {
+            // more survivors than the sort holds: refused, loudly
+            if (tid == 0) *a.out = 0xFFFFFFFFu;
+            return;
+        }
+        uint32_t n2 = 1;
+        while (n2 < n) n2 <<= 1;
+        for (uint32_t j = n + tid; j < n2; j += SP_T) cand[j] = ~0ull;
+        __syncthreads();
+        for (uint32_t size = 2; size <= n2; size <<= 1) {
+            for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+                for (uint32_t i = tid; i < n2; i += SP_T) {
+                    const uint32_t j = i ^ stride;
+                    if (j > i) {
+                        const bool up = (i & size) == 0;
+                        const unsigned long long x = cand[i], y = cand[j];
+                        if ((x > y) == up) {
+                            cand[i] = y;
+                            cand[j] = x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        if (tid == 0) {
+            uint32_t cut = n;
+            if (n > 0) {
+                const float mx = a.f[(uint32_t)cand[0]];
+                float sum = 0.0f;
+                for (uint32_t j = 0; j < n; j++) sum += cactus_expf(a.f[(uint32_t)cand[j]] - mx);
+                float cum = 0.0f;
+                for (uint32_t j = 0; j < n; j++) {
+                    cum += cactus_expf(a.f[(uint32_t)cand[j]] - mx) / sum;
+                    if (cum > a.top_p) {
+                        cut = j > 0 ? j : 1;   // position 0 always stays (:381-384)
+                        break;
+                    }
+                }
+            }
+            sh_u32[3] = cut;
+        }
+        __syncthreads();
+        for (uint32_t j = sh_u32[3] + tid; j < n; j += SP_T) a.f[(uint32_t)cand[j]] = -__builtin_inff();
+        __syncthreads();
+    }
+
+    // 5. the draw over the finite entries in token order (:394-444)
+    const float mx = wg_max(a.f, V, red);
+    if (is_inf(mx)) {
+        if (tid == 0) *a.out = 0;
+        return;
+    }
+    const uint32_t S = wg_compact(a.f, V, mx, a.surv, a.pv, scan);
+    if (tid != 0) return;
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < S; j++) sum += a.pv[j];
+    if (sum == 0.0f) {
+        *a.out = 0;
+        return;
+    }
+    uint32_t tok = 0;
+    bool found = false;
+    if (a.u <= 0.0f) {
+        found = true;   // the running sum is >= u already at token 0
+    } else {
+        float cum = 0.0f;
+        for (uint32_t j = 0; j < S && !found; j++) {
+            cum += a.pv[j] / sum;
+            if (cum >= a.u) { tok = a.surv[j]; found = true; }
+        }
+        for (uint32_t j = S; j > 0 && !found; j--)
+            if (a.pv[j - 1] / sum > 0.0f) { tok = a.surv[j - 1]; found = true; }
+    }
+    *a.out = tok;
+}
+
 // ---------------------------------------------------------------- entropy
 // Model::decode's out_entropy (engine_model.cpp:255-290): max, then the sum
 // of exp in double and the entropy sum in double, each a tree over the
@@ -319,6 +570,7 @@ __global__ void __launch_bounds__(1024) entropy_kernel(const uint16_t* __restric
 // per-device scratch (grown) and token history (zeroed once)
 struct SampleState {
     uint16_t* f = nullptr;
+    float* f32 = nullptr;
     float* pv = nullptr;
     uint32_t* surv = nullptr;
     size_t cap = 0;
@@ -342,10 +594,12 @@ static int sample_state(size_t V, SampleState** out) {
         if (s.f) CH_HIP(hipFree(s.f));
         if (s.pv) CH_HIP(hipFree(s.pv));
         if (s.surv) CH_HIP(hipFree(s.surv));
-        s.f = nullptr; s.pv = nullptr; s.surv = nullptr; s.cap = 0;
+        if (s.f32) CH_HIP(hipFree(s.f32));
+        s.f = nullptr; s.pv = nullptr; s.surv = nullptr; s.f32 = nullptr; s.cap = 0;
         CH_HIP(hipMalloc(&s.f, V * sizeof(uint16_t)));
         CH_HIP(hipMalloc(&s.pv, V * sizeof(float)));
         CH_HIP(hipMalloc(&s.surv, V * sizeof(uint32_t)));
+        CH_HIP(hipMalloc(&s.f32, V * sizeof(float)));
         s.cap = V;
     }
     *out = &s;
@@ -364,7 +618,7 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, f
     CH_REQUIRE(vocab == 0 || logits, "sample: null logits");
     if (vocab == 0) return cactus_hip_memset(out, 0, 4, stream);
     if (temperature == 0.0f && top_p <= 0.0f && top_k == 0) {
-        hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
+        hipLaunchKernelGGL(argmax_kernel<uint16_t>, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
         return check_launch("sample");
     }
     CH_REQUIRE(vocab < (1ull << 31), "sample: vocabulary too large");
@@ -402,6 +656,52 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, f
     CH_REQUIRE(attr == hipSuccess, "sample: cannot reserve the candidate LDS");
     hipLaunchKernelGGL(sample_kernel, dim3(1), dim3(SP_T), lds, as_stream(stream), a);
     return check_launch("sample");
+}
+
+int cactus_hip_sample_f32(const float* logits, uint32_t* out, size_t vocab, float temperature, float top_p,
+                          size_t top_k, size_t random_seed, const float* bias_values, const uint32_t* bias_indices,
+                          size_t bias_count, void* stream) {
+    CH_REQUIRE(out, "sample_f32: null output");
+    CH_REQUIRE(vocab == 0 || logits, "sample_f32: null logits");
+    if (vocab == 0) return cactus_hip_memset(out, 0, 4, stream);
+    if (temperature == 0.0f && top_p <= 0.0f && top_k == 0) {
+        hipLaunchKernelGGL(argmax_kernel<float>, dim3(1), dim3(1024), 0, as_stream(stream), logits, vocab, out);
+        return check_launch("sample_f32");
+    }
+    CH_REQUIRE(vocab < (1ull << 31), "sample_f32: vocabulary too large");
+    CH_REQUIRE(temperature >= 0.0f && temperature == temperature, "sample_f32: temperature must be >= 0");
+    const bool biased = bias_values && bias_indices && bias_count > 0;
+    if (biased && bias_count > (size_t)SP_BIAS)
+        return fail(CACTUS_HIP_EUNSUPPORTED, "sample_f32: at most 128 logit-bias entries");
+    SampleState* s = nullptr;
+    int rc = sample_state(vocab, &s);
+    if (rc) return rc;
+    const uint32_t seed = random_seed ? (uint32_t)random_seed : std::random_device{}();
+    std::mt19937 gen(seed);
+    const uint32_t x = (uint32_t)gen();
+    SampleF32Args a{};
+    a.logits = logits;
+    a.out = out;
+    a.f = s->f32;
+    a.pv = s->pv;
+    a.surv = s->surv;
+    a.V = vocab;
+    a.top_k = top_k;
+    a.top_p = top_p;
+    a.u = (float)x / 4294967296.0f;
+    a.temperature = temperature;
+    a.scale = temperature > 0.0f;
+    a.bias_n = biased ? (int)bias_count : 0;
+    for (int j = 0; j < a.bias_n; j++) {
+        a.bias_v[j] = bias_values[j];
+        a.bias_i[j] = bias_indices[j];
+    }
+    const size_t lds = SP_CAND * sizeof(unsigned long long);
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void*)sample_f32_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    CH_REQUIRE(attr == hipSuccess, "sample_f32: cannot reserve the candidate LDS");
+    hipLaunchKernelGGL(sample_f32_kernel, dim3(1), dim3(SP_T), lds, as_stream(stream), a);
+    return check_launch("sample_f32");
 }
 
 int cactus_hip_logits_entropy_f16(const uint16_t* logits, size_t vocab, float* out, void* stream) {

@@ -236,6 +236,19 @@ int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* 
 int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
                           float temperature, float top_p, size_t top_k, size_t random_seed,
                           void* stream);
+/* cactus_sample_f32 (kernel/kernel.h:130, kernel_nn.cpp:253-444): greedy
+ * (temperature == 0, top_p <= 0, top_k == 0: first index of the maximum) or
+ * the full FP32 sampler: the logit bias added entry by entry in order
+ * (bias_values / bias_indices in host memory, at most 128 entries, else
+ * CACTUS_HIP_EUNSUPPORTED), division by the temperature, top-k (ties at the
+ * k-th value kept), min-p 0.15, top-p and the draw u from
+ * std::mt19937(random_seed) (a random seed for 0) through libc++'s
+ * generate_canonical<float, 24>.  No repetition penalty and no history.  If
+ * more than 16384 entries reach top-p, *out is set to 0xFFFFFFFF.  Writes
+ * one uint32 to *out (device memory), stream-ordered. */
+int cactus_hip_sample_f32(const float* logits, uint32_t* out, size_t vocab, float temperature, float top_p,
+                          size_t top_k, size_t random_seed, const float* bias_values,
+                          const uint32_t* bias_indices, size_t bias_count, void* stream);
 /* Model::decode's out_entropy (engine/engine_model.cpp:255-290): the
  * softmax entropy of fp16 logits [vocab] in double, divided by log(vocab),
  * written as one float to *out (device memory).  Floating point: within a

@@ -67,6 +67,7 @@ _SIGS = {
     "orc_sample_uniform": (F, [ctypes.c_uint32]),
     "orc_logits_entropy_f16": (F, [P, SZ]),
     "orc_sample_f16": (ctypes.c_uint32, [P, SZ, F, F, SZ, F, P, P]),
+    "orc_sample_f32": (ctypes.c_uint32, [P, SZ, F, F, SZ, P, P, SZ, F]),
     "orc_fast_tanh": (F, [F]),
     "orc_gelu_f16": (None, [P, P, SZ]),
     "orc_gelu_erf_f16": (None, [P, P, SZ]),
@@ -294,6 +295,18 @@ def logits_entropy(logits) -> float:
 
 def sample_uniform(seed: int) -> float:
     return float(lib().orc_sample_uniform(seed))
+
+
+def sample_f32(logits, temperature, top_p, top_k, seed, bias=None):
+    """cactus_sample_f32 with the draw of mt19937(seed); bias: {token: value}
+    or a list of (token, value) pairs applied in order."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    pairs = list(bias.items()) if isinstance(bias, dict) else list(bias or [])
+    bi = np.array([t for t, _ in pairs], np.uint32)
+    bv = np.array([v for _, v in pairs], np.float32)
+    return int(lib().orc_sample_f32(x.ctypes.data, x.size, temperature, top_p, top_k,
+                                    bv.ctypes.data if pairs else None, bi.ctypes.data if pairs else None,
+                                    len(pairs), sample_uniform(seed)))
 
 
 class OracleSampler:

@@ -117,6 +117,11 @@ float    orc_sample_uniform(uint32_t seed);
 uint32_t orc_sample_f16(const uint16_t* logits, size_t vocab, float temperature, float top_p,
                         size_t top_k, float u, uint32_t* hist, size_t* hist_n);
 
+/* cactus_sample_f32 (kernel_nn.cpp:253-444) with the draw `u` given: bias
+ * added, temperature divided, top-k, min-p 0.15, top-p, draw; no history */
+uint32_t orc_sample_f32(const float* logits, size_t vocab, float temperature, float top_p, size_t top_k,
+                        const float* bias_values, const uint32_t* bias_indices, size_t bias_count, float u);
+
 /* Model::decode's normalised entropy of the logits (engine_model.cpp:255-290) */
 float    orc_logits_entropy_f16(const uint16_t* logits, size_t vocab);
 

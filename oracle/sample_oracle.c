@@ -3,6 +3,7 @@
  * sampler and its random draw (test infrastructure; see cactus_oracle.h):
  *
  *   cactus_sample_f16                 kernel/kernel_nn.cpp:446-651
+ *   cactus_sample_f32                 kernel/kernel_nn.cpp:253-444
  *   std::mt19937 + uniform_real_distribution<float>(0, 1), first draw
  *                                     kernel/kernel_nn.cpp:609-612
  *
@@ -200,4 +201,150 @@ float orc_logits_entropy_f16(const uint16_t* logits, size_t V) {
         if (p > 1e-10) ent -= p * lp;
     }
     return (float)(ent / log((double)V));
+}
+
+/* cactus_sample_f32 (kernel_nn.cpp:253-444).  Unlike the f16 sampler: the
+ * logit bias is added (entry by entry, in order, :280-288) and kept; the
+ * temperature divides (:290-294); a min-p step with min_p = 0.15 runs
+ * between top-k and top-p (:316-346); there is no repetition penalty and no
+ * history.  Both infinities count as removed (std::isinf).  expf is the
+ * libm boundary of the f16 sampler.  Ties in the top-p sort keep ascending
+ * token order (parity unpinned where equal logits straddle the cut). */
+static int isinf_f(float x) { return x == INFINITY || x == -INFINITY; }
+
+typedef struct {
+    float v;
+    uint32_t i;
+} cand32;
+
+static int cand32_desc(const void* a, const void* b) {
+    const cand32* x = (const cand32*)a;
+    const cand32* y = (const cand32*)b;
+    if (x->v > y->v) return -1;
+    if (x->v < y->v) return 1;
+    return x->i < y->i ? -1 : (x->i > y->i ? 1 : 0);
+}
+
+uint32_t orc_sample_f32(const float* logits, size_t V, float temperature, float top_p, size_t top_k,
+                        const float* bias_values, const uint32_t* bias_indices, size_t bias_count, float u) {
+    if (temperature == 0.0f && top_p <= 0.0f && top_k == 0) {
+        if (V == 0) return 0;
+        size_t best = 0;
+        float bv = logits[0];
+        for (size_t i = 1; i < V; i++)
+            if (logits[i] > bv) { bv = logits[i]; best = i; }
+        return (uint32_t)best;
+    }
+    float* f = (float*)malloc((V ? V : 1) * sizeof(float));
+    memcpy(f, logits, V * sizeof(float));
+    if (bias_values && bias_indices)
+        for (size_t j = 0; j < bias_count; j++)
+            if (bias_indices[j] < V) f[bias_indices[j]] += bias_values[j];
+    if (temperature > 0)
+        for (size_t i = 0; i < V; i++) f[i] /= temperature;
+    /* :296-313 -- top_k >= vocab keeps everything */
+    if (top_k > 0 && top_k < V) {
+        cand32* c = (cand32*)malloc(V * sizeof(cand32));
+        for (size_t i = 0; i < V; i++) { c[i].v = f[i]; c[i].i = (uint32_t)i; }
+        qsort(c, V, sizeof(cand32), cand32_desc);
+        const float kth = c[top_k - 1].v;
+        free(c);
+        for (size_t i = 0; i < V; i++)
+            if (f[i] < kth) f[i] = -INFINITY;
+    }
+    /* :316-346 */
+    {
+        const float min_p = 0.15f;
+        float mx = V ? f[0] : 0.0f;
+        for (size_t i = 1; i < V; i++)
+            if (f[i] > mx) mx = f[i];
+        if (V && !isinf_f(mx)) {
+            float* tp = (float*)malloc(V * sizeof(float));
+            float sum = 0.0f;
+            for (size_t i = 0; i < V; i++) {
+                if (!isinf_f(f[i])) {
+                    tp[i] = orc_expf(f[i] - mx);
+                    sum += tp[i];
+                } else {
+                    tp[i] = 0.0f;
+                }
+            }
+            if (sum > 0.0f) {
+                float mp = 0.0f;
+                for (size_t i = 0; i < V; i++) {
+                    tp[i] /= sum;
+                    if (i == 0 || tp[i] > mp) mp = tp[i];
+                }
+                const float thr = mp * min_p;
+                for (size_t i = 0; i < V; i++)
+                    if (tp[i] < thr) f[i] = -INFINITY;
+            }
+            free(tp);
+        }
+    }
+    /* :348-392 */
+    if (top_p > 0.0f && top_p < 1.0f) {
+        cand32* c = (cand32*)malloc((V ? V : 1) * sizeof(cand32));
+        size_t n = 0;
+        for (size_t i = 0; i < V; i++)
+            if (!isinf_f(f[i])) { c[n].v = f[i]; c[n].i = (uint32_t)i; n++; }
+        qsort(c, n, sizeof(cand32), cand32_desc);
+        if (n > 0) {
+            const float mx = c[0].v;
+            float* p = (float*)malloc(n * sizeof(float));
+            float sum = 0.0f;
+            for (size_t j = 0; j < n; j++) {
+                p[j] = orc_expf(c[j].v - mx);
+                sum += p[j];
+            }
+            for (size_t j = 0; j < n; j++) p[j] /= sum;
+            /* remove from the first position whose running sum exceeds
+             * top_p on, but never position 0 (:373-386) */
+            float cum = 0.0f;
+            size_t cut = n;
+            for (size_t j = 0; j < n; j++) {
+                cum += p[j];
+                if (cum > top_p) { cut = j; break; }
+            }
+            if (cut == 0) cut = 1;
+            for (size_t j = cut; j < n; j++) f[c[j].i] = -INFINITY;
+            free(p);
+        }
+        free(c);
+    }
+    /* :394-444 */
+    float mx = V ? f[0] : 0.0f;
+    for (size_t i = 1; i < V; i++)
+        if (f[i] > mx) mx = f[i];
+    if (V == 0 || isinf_f(mx)) {
+        free(f);
+        return 0;
+    }
+    float* p = (float*)malloc(V * sizeof(float));
+    float sum = 0.0f;
+    for (size_t i = 0; i < V; i++) {
+        if (isinf_f(f[i])) {
+            p[i] = 0.0f;
+        } else {
+            p[i] = orc_expf(f[i] - mx);
+            sum += p[i];
+        }
+    }
+    free(f);
+    if (sum == 0.0f) {
+        free(p);
+        return 0;
+    }
+    for (size_t i = 0; i < V; i++) p[i] /= sum;
+    float cum = 0.0f;
+    uint32_t tok = 0;
+    int found = 0;
+    for (size_t i = 0; i < V && !found; i++) {
+        cum += p[i];
+        if (cum >= u) { tok = (uint32_t)i; found = 1; }
+    }
+    for (size_t i = V; i > 0 && !found; i--)
+        if (p[i - 1] > 0.0f) { tok = (uint32_t)(i - 1); found = 1; }
+    free(p);
+    return tok;
 }
