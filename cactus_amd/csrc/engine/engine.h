@@ -120,8 +120,10 @@ private:
     size_t forward(const std::vector<uint32_t>& tokens);
     size_t shared_matmul_input(size_t x);
     size_t norm_for_matmuls(size_t h, size_t weight);
-    size_t build_attention(size_t x, uint32_t l, size_t pos);
-    size_t build_mlp(size_t x, uint32_t l);
+    static constexpr size_t NO_RESIDUAL = ~(size_t)0;
+    // residual: a node added to the last matmul's output (fused), or NO_RESIDUAL
+    size_t build_attention(size_t x, uint32_t l, size_t pos, size_t residual = NO_RESIDUAL);
+    size_t build_mlp(size_t x, uint32_t l, size_t residual = NO_RESIDUAL);
     size_t build_block(size_t h, uint32_t l, size_t pos);
     void update_kv_cache(size_t seq);
 

@@ -155,6 +155,15 @@ size_t CactusGraph::silu_mul_quantize(size_t gate, size_t up) {
     return add_node(OpType::SILU_MUL_QUANTIZE, {gate, up}, node(gate).out.shape, Precision::INT8);
 }
 
+size_t CactusGraph::matmul_add(size_t a, size_t b, size_t residual) {
+    const size_t mm = matmul(a, b, true);
+    GraphNode& m = node(mm);
+    if (node(residual).out.shape != m.out.shape) throw std::runtime_error("matmul_add: residual shape mismatch");
+    m.op = OpType::MATMUL_ADD;
+    m.inputs.push_back(residual);
+    return mm;
+}
+
 size_t CactusGraph::rms_norm_rope(size_t input, size_t weight, float epsilon, float theta, size_t position_offset) {
     if (node(input).out.shape.size() < 4) throw std::runtime_error("RoPE operation requires 4D tensor");
     OpParams p;
@@ -427,6 +436,36 @@ void CactusGraph::compute(GraphNode& n) {
             check_hip(cactus_hip_quantize_activations(u16(x.data), static_cast<int8_t*>(n.out.data),
                                                       static_cast<float*>(n.out.activation_scales), M, K, st),
                       "quantize_activations");
+            return;
+        }
+        case OpType::MATMUL_ADD: {
+            const BufferDesc& a = in(0);
+            const BufferDesc& b = in(1);
+            const uint16_t* r = u16(in(2).data);
+            const size_t K = a.shape.back();
+            const size_t M = a.total_size / K;
+            const size_t N = n.out.shape.back();
+            const bool preq = a.precision == Precision::INT8 && a.activation_scales;
+            if (!(b.is_packed_int4() || b.is_grouped_int8()) || (!preq && a.precision != Precision::FP16))
+                throw std::runtime_error("matmul_add: needs grouped INT8/INT4 weights and INT8 or FP16 activations");
+            const uint16_t* bs = u16(b.scales);
+            int rc;
+            if (b.is_packed_int4()) {
+                const uint8_t* bp = static_cast<const uint8_t*>(b.packed_int4);
+                rc = preq ? cactus_hip_matmul_int4_add(static_cast<const int8_t*>(a.data),
+                                                      static_cast<const float*>(a.activation_scales), bp, bs, r,
+                                                      out16, M, K, N, b.group_size, st)
+                          : cactus_hip_matmul_int4_f16act_add(u16(a.data), bp, bs, r, out16, M, K, N, b.group_size,
+                                                              st);
+            } else {
+                const int8_t* bw = static_cast<const int8_t*>(b.data);
+                rc = preq ? cactus_hip_matmul_int8_add(static_cast<const int8_t*>(a.data),
+                                                      static_cast<const float*>(a.activation_scales), bw, bs, r,
+                                                      out16, M, K, N, b.group_size, st)
+                          : cactus_hip_matmul_int8_f16act_add(u16(a.data), bw, bs, r, out16, M, K, N, b.group_size,
+                                                              st);
+            }
+            check_hip(rc, "matmul_add");
             return;
         }
         case OpType::MATMUL: {  // graph_ops_nn.cpp:129-231

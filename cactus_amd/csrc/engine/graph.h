@@ -26,6 +26,7 @@ enum class OpType {
     RMS_NORM_QUANTIZE,   // RMS_NORM feeding only matmuls, fused with their row quantization
     SILU_MUL_QUANTIZE,   // silu(gate) * up feeding only a matmul, fused with its row quantization
     RMS_NORM_ROPE,       // per-head RMSNorm of q or k followed by their RoPE
+    MATMUL_ADD,          // grouped matmul followed by the residual add
 };
 
 // nodes whose output is INT8 codes with per-row activation scales
@@ -130,6 +131,8 @@ public:
     size_t silu_mul_quantize(size_t gate, size_t up);
     // rms_norm over head rows of a [B][S][H][d] tensor, then rope
     size_t rms_norm_rope(size_t input, size_t weight, float epsilon, float theta, size_t position_offset);
+    // add(residual, matmul(a, b)) for pretransposed grouped INT8/INT4 weights
+    size_t matmul_add(size_t a, size_t b, size_t residual);
     size_t rope(size_t input, float theta, size_t position_offset = 0);
     size_t softmax(size_t input, int axis = -1);
     size_t attention(size_t q, size_t k, size_t v, float scale, size_t position_offset = 0,

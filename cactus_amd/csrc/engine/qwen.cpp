@@ -283,7 +283,7 @@ size_t QwenModel::norm_for_matmuls(size_t h, size_t weight) {
 }
 
 // model_qwen.cpp:51-106
-size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
+size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos, size_t residual) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
     const size_t hd = cfg_.head_dim, nh = cfg_.heads, nkv = cfg_.kv_heads;
@@ -316,11 +316,12 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos) {
     else
         att = g.attention(q4, k4, v4, attn_scale_, pos);
     att = g.reshape(att, {S, hd * nh});
+    if (residual != NO_RESIDUAL) return g.matmul_add(att, L.n_o, residual);
     return g.matmul(att, L.n_o, true);
 }
 
 // model_qwen.cpp:109-117
-size_t QwenModel::build_mlp(size_t x, uint32_t l) {
+size_t QwenModel::build_mlp(size_t x, uint32_t l, size_t residual) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
     const size_t xq = shared_matmul_input(x);
@@ -328,9 +329,14 @@ size_t QwenModel::build_mlp(size_t x, uint32_t l) {
     size_t up = g.matmul(xq, L.n_up, true);
     // at prefill sizes the SwiGLU product is one node with the down
     // projection's row quantization
-    if (g.get_output_buffer(gate).shape[0] >= 32) return g.matmul(g.silu_mul_quantize(gate, up), L.n_down, true);
+    if (g.get_output_buffer(gate).shape[0] >= 32) {
+        const size_t q = g.silu_mul_quantize(gate, up);
+        if (residual != NO_RESIDUAL) return g.matmul_add(q, L.n_down, residual);
+        return g.matmul(q, L.n_down, true);
+    }
     size_t act = g.silu(gate);
     size_t m = g.multiply(act, up);
+    if (residual != NO_RESIDUAL) return g.matmul_add(m, L.n_down, residual);
     return g.matmul(m, L.n_down, true);
 }
 
@@ -339,11 +345,13 @@ size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
     CactusGraph& g = *graph_;
     const QwenLayer& L = layers_[l];
     size_t x = norm_for_matmuls(h, L.n_input_norm);
-    size_t att = build_attention(x, l, pos);
-    size_t h1 = g.add(h, att);
+    // at prefill sizes the residual adds ride on the o-proj and down matmuls
+    const bool fuse = g.get_output_buffer(h).shape[0] >= 32;
+    size_t h1 = build_attention(x, l, pos, fuse ? h : NO_RESIDUAL);
+    if (!fuse) h1 = g.add(h, h1);
     size_t x2 = norm_for_matmuls(h1, L.n_post_norm);
-    size_t mlp = build_mlp(x2, l);
-    return g.add(h1, mlp);
+    size_t out = build_mlp(x2, l, fuse ? h1 : NO_RESIDUAL);
+    return fuse ? out : g.add(h1, out);
 }
 
 // model_qwen.cpp:132-172 (use_cache = true)

@@ -58,6 +58,7 @@ struct GemmArgs {
     const uint16_t* Bs;   // [N][K/gs] fp16
     uint16_t* C;          // [M][N] fp16
     int M, K, N, gs;
+    const uint16_t* R = nullptr;   // [M][N] fp16 residual added to C (the add node), or null
 };
 
 // Workgroup: 4 waves, 64 rows x 64*NW columns; wave (wv >> 1, wv & 1) owns
@@ -166,7 +167,10 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
         for (int s = 0; s < NW; s++) {
             const int col = n0 + s * 32 + li;
-            if (col < N) a.C[(size_t)row * N + col] = f2h(r[s][e] * as);
+            if (col < N) {
+                const uint16_t c = f2h(r[s][e] * as);
+                a.C[(size_t)row * N + col] = a.R ? hadd(c, a.R[(size_t)row * N + col]) : c;
+            }
         }
     }
 }
@@ -441,18 +445,28 @@ __global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
         if (t < C::TM * C::TN) {
             const int x = t / C::TN, y = t % C::TN;
             const int rr = (lane >> 1) & 15, hh = lane & 1;
-            const uint4 v = *reinterpret_cast<const uint4*>(ob + t * 256 + rr * 16 + hh * 8);
+            uint4 v = *reinterpret_cast<const uint4*>(ob + t * 256 + rr * 16 + hh * 8);
             const int row = mb + wm * C::WM + x * 16 + rr;
             const int col = nb + wn * C::WN + y * 16 + hh * 8;
             if (row < M) {
                 uint16_t* dst = a.C + (size_t)row * N + col;
-                if (vec_ok && col + 8 <= N) {
+                const uint16_t* res = a.R ? a.R + (size_t)row * N + col : nullptr;
+                const bool vec = vec_ok && col + 8 <= N && (!res || ((uintptr_t)a.R & 15) == 0);
+                if (vec) {
+                    if (res) {
+                        // the residual add node, fused: fp16(fp16(acc) + r)
+                        const uint4 rv = *reinterpret_cast<const uint4*>(res);
+                        uint16_t* h = reinterpret_cast<uint16_t*>(&v);
+                        const uint16_t* rh = reinterpret_cast<const uint16_t*>(&rv);
+#pragma unroll
+                        for (int i = 0; i < 8; i++) h[i] = hadd(h[i], rh[i]);
+                    }
                     *reinterpret_cast<uint4*>(dst) = v;
                 } else {
                     const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
 #pragma unroll
                     for (int i = 0; i < 8; i++)
-                        if (col + i < N) dst[i] = h[i];
+                        if (col + i < N) dst[i] = res ? hadd(h[i], res[i]) : h[i];
                 }
             }
         }
@@ -575,7 +589,7 @@ constexpr size_t GEMM_MIN_M = 32;
 // Returns *handled = false when the shape is left to the GEMV path.
 int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
                       const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
-                      bool int4, hipStream_t st, bool* handled) {
+                      bool int4, hipStream_t st, bool* handled, const uint16_t* R) {
     *handled = false;
     if (M < GEMM_MIN_M || gs % 32 != 0 || N < 32) return CACTUS_HIP_OK;
     if (((uintptr_t)B & 15) != 0) return CACTUS_HIP_OK;
@@ -596,7 +610,7 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
         Aq = q;
         Asc = s;
     }
-    GemmArgs a{Aq, Asc, B, Bs, C, (int)M, (int)K, (int)N, (int)gs};
+    GemmArgs a{Aq, Asc, B, Bs, C, (int)M, (int)K, (int)N, (int)gs, R};
     // the LDS path moves group scales as dwords
     const bool scales4 = ((uintptr_t)Bs & 3) == 0;
     if (scales4 && (int4 ? launch_lds_any<true>(a, st) : launch_lds_any<false>(a, st))) {

@@ -462,25 +462,40 @@ using namespace cactus_hip;
 namespace cactus_hip {
 int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
                       const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
-                      bool int4, hipStream_t st, bool* handled);
+                      bool int4, hipStream_t st, bool* handled,
+                      const uint16_t* R = nullptr);
+
+// C[i] = fp16(C[i] + R[i]): the residual add node after a small-M matmul
+__global__ void add_residual_kernel(uint16_t* C, const uint16_t* R, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        C[i] = hadd(C[i], R[i]);
+}
 
 static int grouped_dispatch(const uint16_t* A16, const int8_t* A8, const float* As,
                             const uint8_t* B, const uint16_t* Bs, uint16_t* C, size_t M, size_t K,
-                            size_t N, size_t gs, bool int4, hipStream_t st) {
+                            size_t N, size_t gs, bool int4, hipStream_t st, const uint16_t* R = nullptr) {
     if (M == 0 || K == 0 || N == 0) return CACTUS_HIP_OK;
     int rc = check_grouped_shape(M, K, N, gs, int4);
     if (rc) return rc;
     CH_REQUIRE(B && Bs && C && (A16 || (A8 && As)), "grouped matmul: null pointer");
     CH_REQUIRE(((uintptr_t)B & 15) == 0, "grouped matmul: weights must be 16-byte aligned");
     bool handled = false;
-    rc = gemm_grouped_mfma(A16, A8, As, B, Bs, C, M, K, N, gs, int4, st, &handled);
+    rc = gemm_grouped_mfma(A16, A8, As, B, Bs, C, M, K, N, gs, int4, st, &handled, R);
     if (rc || handled) return rc;
     GemvArgs a{};
     a.A16 = A16; a.A8 = A8; a.As = As; a.B = B; a.Bs = Bs; a.C = C;
     a.M = (int)M; a.K = (int)K; a.N = (int)N; a.gs = (int)gs;
     a.sA = M * K; a.sB = 0; a.sBs = 0; a.sC = 0;
-    if (A16) return int4 ? launch_gemv<true, true>(a, 1, st) : launch_gemv<true, false>(a, 1, st);
-    return int4 ? launch_gemv<false, true>(a, 1, st) : launch_gemv<false, false>(a, 1, st);
+    if (A16) rc = int4 ? launch_gemv<true, true>(a, 1, st) : launch_gemv<true, false>(a, 1, st);
+    else rc = int4 ? launch_gemv<false, true>(a, 1, st) : launch_gemv<false, false>(a, 1, st);
+    // small M: the residual add runs as its own kernel, in place on C
+    if (rc == 0 && R) {
+        const size_t n = M * N;
+        const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 65535);
+        hipLaunchKernelGGL(add_residual_kernel, dim3(blocks), dim3(256), 0, st, C, R, n);
+        rc = check_launch("matmul_add (residual)");
+    }
+    return rc;
 }
 }  // namespace cactus_hip
 
@@ -512,6 +527,38 @@ int cactus_hip_matmul_int4_f16act(const uint16_t* A, const uint8_t* B_packed,
                                   size_t N, size_t group_size, void* stream) {
     return grouped_dispatch(A, nullptr, nullptr, B_packed, B_scales, C, M, K, N, group_size, true,
                             as_stream(stream));
+}
+
+int cactus_hip_matmul_int8_add(const int8_t* A, const float* A_scales, const int8_t* B, const uint16_t* B_scales,
+                               const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                               size_t group_size, void* stream) {
+    CH_REQUIRE(residual || M * K * N == 0, "matmul_add: null residual");
+    return grouped_dispatch(nullptr, A, A_scales, reinterpret_cast<const uint8_t*>(B), B_scales, C, M, K, N,
+                            group_size, false, as_stream(stream), residual);
+}
+
+int cactus_hip_matmul_int4_add(const int8_t* A, const float* A_scales, const uint8_t* B_packed,
+                               const uint16_t* B_scales, const uint16_t* residual, uint16_t* C, size_t M, size_t K,
+                               size_t N, size_t group_size, void* stream) {
+    CH_REQUIRE(residual || M * K * N == 0, "matmul_add: null residual");
+    return grouped_dispatch(nullptr, A, A_scales, B_packed, B_scales, C, M, K, N, group_size, true,
+                            as_stream(stream), residual);
+}
+
+int cactus_hip_matmul_int8_f16act_add(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                      const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                                      size_t group_size, void* stream) {
+    CH_REQUIRE(residual || M * K * N == 0, "matmul_add: null residual");
+    return grouped_dispatch(A, nullptr, nullptr, reinterpret_cast<const uint8_t*>(B), B_scales, C, M, K, N,
+                            group_size, false, as_stream(stream), residual);
+}
+
+int cactus_hip_matmul_int4_f16act_add(const uint16_t* A, const uint8_t* B_packed, const uint16_t* B_scales,
+                                      const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                                      size_t group_size, void* stream) {
+    CH_REQUIRE(residual || M * K * N == 0, "matmul_add: null residual");
+    return grouped_dispatch(A, nullptr, nullptr, B_packed, B_scales, C, M, K, N, group_size, true,
+                            as_stream(stream), residual);
 }
 
 int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,

@@ -101,6 +101,23 @@ int cactus_hip_matmul_int8_f16act(const uint16_t* A, const int8_t* B, const uint
 int cactus_hip_matmul_int4_f16act(const uint16_t* A, const uint8_t* B_packed,
                                   const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
                                   size_t N, size_t group_size, void* stream);
+/* No single reference function: a grouped matmul (cactus_matmul_int8 /
+ * cactus_matmul_int4, or their FP16-activation forms) followed by the
+ * residual add node (model_qwen.cpp:123 and :126, cactus_add_f16):
+ * C = fp16(fp16(A x B) + residual), identical to the two nodes.  residual
+ * is [M][N] fp16 and may not alias C. */
+int cactus_hip_matmul_int8_add(const int8_t* A, const float* A_scales, const int8_t* B, const uint16_t* B_scales,
+                               const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                               size_t group_size, void* stream);
+int cactus_hip_matmul_int4_add(const int8_t* A, const float* A_scales, const uint8_t* B_packed,
+                               const uint16_t* B_scales, const uint16_t* residual, uint16_t* C, size_t M, size_t K,
+                               size_t N, size_t group_size, void* stream);
+int cactus_hip_matmul_int8_f16act_add(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                      const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                                      size_t group_size, void* stream);
+int cactus_hip_matmul_int4_f16act_add(const uint16_t* A, const uint8_t* B_packed, const uint16_t* B_scales,
+                                      const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
+                                      size_t group_size, void* stream);
 /* Strided-batched form of cactus_hip_matmul_int8_f16act: `batch` independent
  * problems, problem i at A + i*stride_a, B + i*stride_b, B_scales +
  * i*stride_bs, C + i*stride_c (strides in elements).  No reference

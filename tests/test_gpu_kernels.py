@@ -687,3 +687,38 @@ def test_rms_norm_rope_fused(dev, orc, S, H, d, pos):
                 ctypes.c_float(1e6), ctypes.c_float(1e-6), None)
     ref = orc.rope(orc.rms_norm(x.reshape(S * H, d), w, 1e-6).reshape(1, S, H, d), pos, 1e6)
     assert_bits(dev.get(y, np.uint16, x.shape), ref, "rms_norm_rope")
+
+
+@pytest.mark.parametrize("M,K,N,gs,int4,shift", [(256, 1024, 1024, 32, False, 0), (256, 3072, 1024, 32, True, 0),
+                                                 (256, 1024, 1024, 32, False, 1), (40, 1024, 640, 64, True, 0),
+                                                 (5, 1024, 1024, 32, False, 0), (3, 3072, 1024, 32, True, 0)])
+def test_matmul_add_fused(dev, orc, M, K, N, gs, int4, shift):
+    """The grouped matmul with the residual add fused equals the matmul
+    followed by an fp16 add, for pre-quantized and FP16 activations: the
+    LDS MFMA path (and with a residual 2 bytes off 16-byte alignment:
+    shift 1), the register-streamed path (M 40, 2-byte-aligned scales) and
+    the small-M GEMV path."""
+    say("matmul_add", M, K, N, gs, int4, shift)
+    rng = np.random.default_rng(M + K + N + int4)
+    x = activations(rng, M, K)
+    if int4:
+        _, B, Bs = grouped_int4_weights(rng, N, K, gs)
+    else:
+        B, Bs = grouped_int8_weights(rng, N, K, gs)
+    rq, rs = orc.quantize_activations(x)
+    mm = orc.matmul_int4(rq, rs, B, Bs, gs) if int4 else orc.matmul_int8(rq, rs, B, Bs, gs)
+    res = f16(rng.normal(0, 4, (M, N)))
+    want = (mm.view(np.float16) + res.view(np.float16)).astype(np.float16).view(np.uint16)
+    Bp = dev.put(B)
+    if M == 40:   # scales at a 2-byte offset: the LDS path declines
+        Bsp = dev.put(np.concatenate([np.zeros(1, np.uint16), Bs.ravel()])) + 2
+    else:
+        Bsp = dev.put(Bs)
+    Rp = dev.put(np.concatenate([np.zeros(shift, np.uint16), res.ravel()])) + 2 * shift
+    kind = "int4" if int4 else "int8"
+    C = dev.empty(M * N * 2)
+    dev.cm.call(f"cactus_hip_matmul_{kind}_add", dev.put(rq), dev.put(rs), Bp, Bsp, Rp, C.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C, np.uint16, (M, N)), want, f"matmul_{kind}_add")
+    C2 = dev.empty(M * N * 2)
+    dev.cm.call(f"cactus_hip_matmul_{kind}_f16act_add", dev.put(x), Bp, Bsp, Rp, C2.ptr, M, K, N, gs, None)
+    assert_bits(dev.get(C2, np.uint16, (M, N)), want, f"matmul_{kind}_f16act_add")
