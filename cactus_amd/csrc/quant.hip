@@ -103,19 +103,56 @@ __global__ void __launch_bounds__(256) silu_mul_quant_rows_kernel(const uint16_t
                                                                   int8_t* __restrict__ q,
                                                                   float* __restrict__ scales, int K,
                                                                   size_t body) {
-    extern __shared__ uint16_t ms[];   // the row of silu(gate) * up
+    extern __shared__ __align__(16) uint16_t ms[];   // the row of silu(gate) * up
     __shared__ float red[4];
     const int tid = threadIdx.x;
     const size_t row = blockIdx.x, base = row * (size_t)K;
-    float m = 0.0f;
-    for (int i = tid; i < K; i += 256) {
-        const size_t gi = base + i;
-        const float x = h2f(gate[gi]);
+    auto value = [&](uint16_t g, uint16_t u, size_t gi) {
+        const float x = h2f(g);
         const float e = gi < body ? fast_exp(-x) : cactus_expf(-x);
         const float sig = 1.0f / (1.0f + e);
-        const uint16_t v = hmul(f2h(x * sig), up[gi]);
-        ms[i] = v;
-        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(v)));
+        return hmul(f2h(x * sig), u);
+    };
+    float m = 0.0f;
+    // 16-byte rows (K % 8 == 0, aligned pointers): each thread's 8-value
+    // chunks are loaded up front, four at a time, then computed
+    const bool vec = (K & 7) == 0 && (((uintptr_t)gate | (uintptr_t)up | (uintptr_t)q) & 15) == 0;
+    if (vec) {
+        const int nc = K >> 3;
+        for (int c0 = tid; c0 < nc; c0 += 4 * 256) {
+            uint4 gv[4], uv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int c = c0 + 256 * j;
+                if (c < nc) {
+                    gv[j] = *reinterpret_cast<const uint4*>(gate + base + 8 * (size_t)c);
+                    uv[j] = *reinterpret_cast<const uint4*>(up + base + 8 * (size_t)c);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int c = c0 + 256 * j;
+                if (c < nc) {
+                    const uint16_t* g8 = reinterpret_cast<const uint16_t*>(&gv[j]);
+                    const uint16_t* u8 = reinterpret_cast<const uint16_t*>(&uv[j]);
+                    uint4 ov;
+                    uint16_t* o8 = reinterpret_cast<uint16_t*>(&ov);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        o8[e] = value(g8[e], u8[e], base + 8 * (size_t)c + e);
+                        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(o8[e])));
+                    }
+                    *reinterpret_cast<uint4*>(ms + 8 * c) = ov;
+                }
+            }
+        }
+    } else {
+        for (int i = tid; i < K; i += 256) {
+            const size_t gi = base + i;
+            const uint16_t v = value(gate[gi], up[gi], gi);
+            ms[i] = v;
+            m = __builtin_fmaxf(m, __builtin_fabsf(h2f(v)));
+        }
     }
     m = wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
@@ -125,7 +162,22 @@ __global__ void __launch_bounds__(256) silu_mul_quant_rows_kernel(const uint16_t
     const float inv_s = 1.0f / s;
     const int end8 = (K / 8) * 8;
     int8_t* qr = q + base;
-    for (int i = tid; i < K; i += 256) qr[i] = quant_code(h2f(ms[i]), inv_s, i >= end8);
+    if (vec) {
+        // K % 8 == 0: every code is a body code; 8 per thread and store
+        for (int c = tid; c < (K >> 3); c += 256) {
+            const uint4 v = *reinterpret_cast<const uint4*>(ms + 8 * c);
+            const uint16_t* h = reinterpret_cast<const uint16_t*>(&v);
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                lo |= (uint32_t)(uint8_t)quant_code(h2f(h[e]), inv_s, false) << (8 * e);
+                hi |= (uint32_t)(uint8_t)quant_code(h2f(h[4 + e]), inv_s, false) << (8 * e);
+            }
+            *reinterpret_cast<uint2*>(qr + 8 * c) = make_uint2(lo, hi);
+        }
+    } else {
+        for (int i = tid; i < K; i += 256) qr[i] = quant_code(h2f(ms[i]), inv_s, i >= end8);
+    }
     if (tid == 0) scales[row] = s;
 }
 
