@@ -339,6 +339,7 @@ struct LmDecArgs {
     uint32_t* st;            // token, pos, cache_len, step
     uint32_t* tokens_out;    // [max_steps] or null
     uint32_t max_steps;
+    uint16_t* logits_out;    // fp16 [N] or null
 };
 
 // LM head + greedy argmax, streamed: each wave owns 64 vocabulary rows (one
@@ -430,7 +431,9 @@ __global__ void __launch_bounds__(LMS_THREADS) dec_lm_head_stream_kernel(LmDecAr
     float best = -__builtin_inff();
     uint32_t best_i = 0xFFFFFFFFu;
     if (my_row < N) {
-        best = h2f(f16_hsum(acc));
+        const uint16_t logit = f16_hsum(acc);   // fp16 bits
+        if (p.logits_out) p.logits_out[my_row] = logit;
+        best = h2f(logit);
         best_i = (uint32_t)my_row;
     }
     __shared__ float bv_s[LMS_THREADS];
@@ -540,7 +543,9 @@ __global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
     float best = -__builtin_inff();
     uint32_t best_i = 0xFFFFFFFFu;
     if (my_row < p.N) {
-        best = h2f(f16_hsum(acc));
+        const uint16_t logit = f16_hsum(acc);   // fp16 bits
+        if (p.logits_out) p.logits_out[my_row] = logit;
+        best = h2f(logit);
         best_i = (uint32_t)my_row;
     }
     __shared__ float bv_s[LM_THREADS];
@@ -718,8 +723,8 @@ int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_ra
 
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
                               const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
-                              uint32_t* tokens_out, size_t max_steps, void* scratch,
-                              size_t scratch_bytes, void* stream) {
+                              uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,
+                              void* scratch, size_t scratch_bytes, void* stream) {
     CH_REQUIRE(h && norm_w && embedding && state && scratch, "decode_lm_head: null pointer");
     CH_REQUIRE(K % 8 == 0 && K <= 4096 && ((uintptr_t)embedding & 15) == 0, "decode_lm_head: bad K");
     const bool streamed = K % LMS_KC == 0;
@@ -730,7 +735,7 @@ int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float e
     p.counter = static_cast<uint32_t*>(scratch);
     p.part_val = reinterpret_cast<float*>(static_cast<char*>(scratch) + 256);
     p.part_idx = reinterpret_cast<uint32_t*>(p.part_val + blocks);
-    p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps;
+    p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps; p.logits_out = logits_out;
     if (streamed) {
         const size_t smem = 4 * K + (size_t)LMS_WAVES * LMS_D * LMS_SLOT;
         // dynamic LDS for the largest K accepted here (4096); the kernel's

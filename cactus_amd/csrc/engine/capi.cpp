@@ -96,6 +96,18 @@ struct HostWeights {
     std::vector<cactus_qwen_layer_weights> layers;
 };
 
+// Two scales differ from the other tensors' 0.02.  With every tensor at 0.02
+// the attention's context average becomes a component shared by all positions
+// that grows layer over layer, and with tied embeddings a residual stream
+// still dominated by the input row's embedding predicts that same token: a
+// greedy decode then repeats one id forever.  A wider down-projection scale
+// makes the MLP's token-dependent output dominate the residual stream and
+// smaller embeddings keep the input row from predicting itself, so greedy
+// decode walks through distinct ids (128 of 128 at the 28-layer, 4096-token
+// shape; every id of the 2-layer test shapes' short decodes).
+static constexpr double kDownScaleSd = 0.1;
+static constexpr double kEmbeddingSd = 0.005;
+
 static void make_random(const cactus_qwen_config& c, uint64_t seed, HostWeights& w) {
     const size_t H = c.hidden, F = c.ffn, hd = c.head_dim, gs = c.group_size;
     const size_t nq = (size_t)c.heads * hd, nkv = (size_t)c.kv_heads * hd;
@@ -113,9 +125,9 @@ static void make_random(const cactus_qwen_config& c, uint64_t seed, HostWeights&
         });
         return v;
     };
-    auto scales = [&](size_t n, double qmax) {
+    auto scales = [&](size_t n, double qmax, double sd) {
         std::vector<uint16_t> v(n);
-        parallel_fill(n, seed, tag++, [&](size_t i, uint64_t& s) { v[i] = f2h_host((float)(std::fabs(normal(s) * 0.02) / qmax)); });
+        parallel_fill(n, seed, tag++, [&](size_t i, uint64_t& s) { v[i] = f2h_host((float)(std::fabs(normal(s) * sd) / qmax)); });
         return v;
     };
     auto gauss = [&](size_t n, double mean, double sd) {
@@ -130,21 +142,21 @@ static void make_random(const cactus_qwen_config& c, uint64_t seed, HostWeights&
         w.q_norm.push_back(gauss(hd, 1.0, 0.02));
         w.k_norm.push_back(gauss(hd, 1.0, 0.02));
         w.q_w.push_back(codes8(nq * H));
-        w.q_s.push_back(scales(nq * (H / gs), 127.0));
+        w.q_s.push_back(scales(nq * (H / gs), 127.0, 0.02));
         w.k_w.push_back(codes8(nkv * H));
-        w.k_s.push_back(scales(nkv * (H / gs), 127.0));
+        w.k_s.push_back(scales(nkv * (H / gs), 127.0, 0.02));
         w.v_w.push_back(codes8(nkv * H));
-        w.v_s.push_back(scales(nkv * (H / gs), 127.0));
+        w.v_s.push_back(scales(nkv * (H / gs), 127.0, 0.02));
         w.o_w.push_back(codes8(H * nq));
-        w.o_s.push_back(scales(H * (nq / gs), 127.0));
+        w.o_s.push_back(scales(H * (nq / gs), 127.0, 0.02));
         w.gate_w.push_back(codes4(F, H));
-        w.gate_s.push_back(scales(F * (H / gs), 7.0));
+        w.gate_s.push_back(scales(F * (H / gs), 7.0, 0.02));
         w.up_w.push_back(codes4(F, H));
-        w.up_s.push_back(scales(F * (H / gs), 7.0));
+        w.up_s.push_back(scales(F * (H / gs), 7.0, 0.02));
         w.down_w.push_back(codes4(H, F));
-        w.down_s.push_back(scales(H * (F / gs), 7.0));
+        w.down_s.push_back(scales(H * (F / gs), 7.0, kDownScaleSd));
     }
-    w.emb = gauss((size_t)c.vocab * H, 0.0, 0.02);
+    w.emb = gauss((size_t)c.vocab * H, 0.0, kEmbeddingSd);
     w.out_norm = gauss(H, 1.0, 0.02);
     w.layers.resize(L);
     for (uint32_t l = 0; l < L; l++) {
@@ -221,6 +233,40 @@ int cactus_qwen_create_random(const cactus_qwen_config* cfg, uint64_t seed, void
         HostWeights w;
         make_random(*cfg, seed, w);
         *model = new QwenModel(*cfg, w.layers.data(), w.emb.data(), w.out_norm.data());
+    });
+}
+
+int cactus_qwen_random_weights(const cactus_qwen_config* cfg, uint64_t seed,
+                               cactus_qwen_layer_weights* layers_out_buffers, uint16_t* embedding,
+                               uint16_t* output_norm) {
+    return guarded([&] {
+        validate(cfg);
+        if (!layers_out_buffers || !embedding || !output_norm) throw std::runtime_error("null argument");
+        HostWeights w;
+        make_random(*cfg, seed, w);
+        const size_t H = cfg->hidden, F = cfg->ffn, hd = cfg->head_dim, gs = cfg->group_size;
+        const size_t nq = (size_t)cfg->heads * hd, nkv = (size_t)cfg->kv_heads * hd;
+        auto put = [](const void* dst, const void* src, size_t bytes) {
+            if (!dst) throw std::runtime_error("null weight buffer");
+            std::memcpy(const_cast<void*>(dst), src, bytes);
+        };
+        for (uint32_t l = 0; l < cfg->num_layers; l++) {
+            const cactus_qwen_layer_weights& s = w.layers[l];
+            const cactus_qwen_layer_weights& d = layers_out_buffers[l];
+            put(d.input_norm, s.input_norm, 2 * H);
+            put(d.post_norm, s.post_norm, 2 * H);
+            put(d.q_norm, s.q_norm, 2 * hd);
+            put(d.k_norm, s.k_norm, 2 * hd);
+            put(d.q_w, s.q_w, nq * H); put(d.q_s, s.q_s, 2 * nq * (H / gs));
+            put(d.k_w, s.k_w, nkv * H); put(d.k_s, s.k_s, 2 * nkv * (H / gs));
+            put(d.v_w, s.v_w, nkv * H); put(d.v_s, s.v_s, 2 * nkv * (H / gs));
+            put(d.o_w, s.o_w, H * nq); put(d.o_s, s.o_s, 2 * H * (nq / gs));
+            put(d.gate_w, s.gate_w, F * H / 2); put(d.gate_s, s.gate_s, 2 * F * (H / gs));
+            put(d.up_w, s.up_w, F * H / 2); put(d.up_s, s.up_s, 2 * F * (H / gs));
+            put(d.down_w, s.down_w, H * F / 2); put(d.down_s, s.down_s, 2 * H * (F / gs));
+        }
+        std::memcpy(embedding, w.emb.data(), 2 * w.emb.size());
+        std::memcpy(output_norm, w.out_norm.data(), 2 * H);
     });
 }
 
@@ -303,10 +349,10 @@ int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t*
 int cactus_qwen_last_logits(void* model, uint16_t* out) {
     return guarded([&] {
         QwenModel* m = static_cast<QwenModel*>(model);
-        if (m->last_logits_node() == SIZE_MAX)
-            throw std::runtime_error("logits are kept by the node-graph decode only (mode 0 or non-greedy)");
-        const BufferDesc& b = m->graph().get_output_buffer(m->last_logits_node());
-        check_hip(cactus_hip_memcpy_d2h(out, b.data, b.byte_size, m->stream()), "last_logits");
+        if (!out) throw std::runtime_error("null argument");
+        const void* src = m->last_logits_data();
+        if (!src) throw std::runtime_error("no decode step has run since the last reset or prefill");
+        check_hip(cactus_hip_memcpy_d2h(out, src, (size_t)m->config().vocab * 2, m->stream()), "last_logits");
     });
 }
 
@@ -314,11 +360,10 @@ int cactus_qwen_last_entropy(void* model, float* entropy) {
     return guarded([&] {
         QwenModel* m = static_cast<QwenModel*>(model);
         if (!entropy) throw std::runtime_error("null argument");
-        if (m->last_logits_node() == SIZE_MAX)
-            throw std::runtime_error("no logits kept: the greedy fused decode (mode 1) keeps none");
-        const BufferDesc& b = m->graph().get_output_buffer(m->last_logits_node());
+        const void* src = m->last_logits_data();
+        if (!src) throw std::runtime_error("no decode step has run since the last reset or prefill");
         DevBuf e(4);
-        check_hip(cactus_hip_logits_entropy_f16(static_cast<const uint16_t*>(b.data), b.shape.back(), e.as<float>(),
+        check_hip(cactus_hip_logits_entropy_f16(static_cast<const uint16_t*>(src), m->config().vocab, e.as<float>(),
                                                 m->stream()),
                   "entropy");
         check_hip(cactus_hip_memcpy_d2h(entropy, e.ptr, 4, m->stream()), "entropy");

@@ -35,6 +35,7 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     tokens_ = DevBuf(max_steps_ * 4);
     const size_t blocks = (c.vocab + 127) / 128;   // cactus_hip_decode_lm_head's scratch contract
     lm_scratch_ = DevBuf(256 + 8 * blocks);
+    logits_ = DevBuf((size_t)c.vocab * 2);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
     // the decode entry points ask for max_cache + 1 positions, max_cache
     // being the cache's slot count (context + 1)
@@ -125,7 +126,8 @@ void FusedDecoder::enqueue() {
                   "decode_down");
     }
     check_hip(cactus_hip_decode_lm_head(h, u16(m_.output_norm()), c.eps, u16(m_.embedding()), H, c.vocab, state,
-                                        tokens_.as<uint32_t>(), max_steps_, lm_scratch_.ptr, lm_scratch_.bytes, st),
+                                        tokens_.as<uint32_t>(), max_steps_, logits_.as<uint16_t>(), lm_scratch_.ptr,
+                                        lm_scratch_.bytes, st),
               "decode_lm_head");
 }
 
@@ -158,9 +160,11 @@ void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
                                  std::to_string(kv.max_seq_len) + " tokens; set a window or a larger context)");
     reserve(kv.total_seq_len + n, n);
     set_state(token);
-    // the fused step keeps neither the final hidden state nor the logits
+    // the fused step keeps the last step's logits (in logits_), not the
+    // final hidden state
     m_.last_hidden_ = SIZE_MAX;
     m_.last_logits_ = SIZE_MAX;
+    m_.fused_logits_ = false;
     // CACTUS_DECODE_EAGER=1 enqueues the step's kernels directly instead of
     // replaying the graph (same kernels and results; for kernel tracers)
     static const bool eager = [] {
@@ -188,6 +192,7 @@ void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
         else kv.resident = std::max(kv.resident, kv.current_seq_len);
     }
     check_hip(cactus_hip_memcpy_d2h(out, tokens_.ptr, n * 4, m_.stream()), "tokens");
+    m_.fused_logits_ = true;
 }
 
 uint32_t FusedDecoder::step(uint32_t token) {

@@ -111,6 +111,10 @@ public:
     void* stream() const { return stream_; }
     size_t last_hidden_node() const { return last_hidden_; }
     size_t last_logits_node() const { return last_logits_; }
+    // fp16 logits [vocab] of the last decode step, wherever that step kept
+    // them (the graph's logits node, or the fused decoder's buffer); null if
+    // none was kept since the last reset or prefill
+    const void* last_logits_data() const;
     const QwenLayer& layer(size_t i) const { return layers_[i]; }
     const DevBuf& embedding() const { return embedding_; }
     const DevBuf& output_norm() const { return out_norm_; }
@@ -137,6 +141,7 @@ private:
     float attn_scale_ = 0.0f;
     std::vector<size_t> k_nodes_, v_nodes_;
     size_t last_hidden_ = SIZE_MAX, last_logits_ = SIZE_MAX;
+    bool fused_logits_ = false;   // the last step was a fused one (logits in fused_->logits())
     int decode_mode_ = 0;
     float temperature_ = 0.0f, top_p_ = 0.0f;
     size_t top_k_ = 0, seed_ = 0;

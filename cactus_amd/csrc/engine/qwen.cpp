@@ -261,6 +261,14 @@ QwenModel::~QwenModel() {
 void QwenModel::reset() {
     cache_.reset();
     graph_->soft_reset();
+    last_hidden_ = last_logits_ = SIZE_MAX;
+    fused_logits_ = false;
+}
+
+const void* QwenModel::last_logits_data() const {
+    if (last_logits_ != SIZE_MAX) return graph_->get_output_buffer(last_logits_).data;
+    if (fused_logits_ && fused_) return fused_->logits().ptr;
+    return nullptr;
 }
 
 // Input of matmuls that share it: at prefill sizes its per-row INT8
@@ -390,6 +398,9 @@ void QwenModel::set_kv_window(size_t window, size_t sink) {
 void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
     if (tokens.empty()) return;
     const size_t chunk = cfg_.prefill_chunk ? cfg_.prefill_chunk : 256;
+    // the graph is rebuilt per chunk: no logits node survives a prefill
+    last_logits_ = SIZE_MAX;
+    fused_logits_ = false;
     auto process = [&](size_t b, size_t e) {
         std::vector<uint32_t> c(tokens.begin() + b, tokens.begin() + e);
         last_hidden_ = forward(c);
@@ -421,6 +432,7 @@ uint32_t QwenModel::decode(uint32_t token) {
         return fused_decode(*this, *fused_, token);
     }
     CactusGraph& g = *graph_;
+    fused_logits_ = false;
     size_t fin = forward({token});
     last_hidden_ = fin;
     size_t last = g.index(fin, 0, 0);

@@ -52,6 +52,26 @@ def layer_shapes(c: dict) -> dict:
     }
 
 
+def random_weights(cfg: dict, seed: int):
+    """The host weights Qwen(cfg, seed=seed) uploads (cactus_qwen_random_weights;
+    no device call): (layers, embedding, output_norm) as numpy arrays."""
+    lib = engine()
+    c = QwenConfig(**cfg)
+    shapes = layer_shapes(cfg)
+    layers = [{k: np.zeros(s, t) for k, (s, t) in shapes.items()} for _ in range(cfg["num_layers"])]
+    arr = (LayerWeights * cfg["num_layers"])()
+    for i, L in enumerate(layers):
+        for k in LAYER_FIELDS:
+            setattr(arr[i], k, L[k].ctypes.data)
+    emb = np.zeros((cfg["vocab"], cfg["hidden"]), np.uint16)
+    on = np.zeros(cfg["hidden"], np.uint16)
+    rc = lib.cactus_qwen_random_weights(ctypes.byref(c), ctypes.c_uint64(seed), arr, emb.ctypes.data,
+                                        on.ctypes.data)
+    if rc != 0:
+        raise NativeError(rc, lib.cactus_engine_last_error().decode(errors="replace"))
+    return layers, emb, on
+
+
 class Qwen:
     """Qwen3-architecture model on the GPU (mirrors Model init/prefill/decode)."""
 

@@ -64,9 +64,20 @@ const char* cactus_engine_last_error(void);
 int cactus_qwen_create(const cactus_qwen_config* cfg, const cactus_qwen_layer_weights* layers,
                        const uint16_t* embedding, const uint16_t* output_norm, void** model);
 /* Random-init weights of the same architecture, generated on the host from
- * `seed` (codes uniform, scales |N(0,0.02)|/qmax, norms 1+N(0,0.02),
- * embeddings N(0,0.02)). */
+ * `seed`: codes uniform, group scales |N(0,0.02)|/qmax (down projection
+ * |N(0,0.1)|/qmax), norms 1+N(0,0.02), embeddings N(0,0.005).  The two wider
+ * or narrower scales keep greedy decode from repeating one token (with all
+ * at 0.02 the residual stream of a deep random model loses its dependence on
+ * the input token).  Deterministic for a seed, whatever the host's core
+ * count. */
 int cactus_qwen_create_random(const cactus_qwen_config* cfg, uint64_t seed, void** model);
+/* The weights cactus_qwen_create_random(cfg, seed) uploads, written into
+ * caller-provided host buffers (the shapes of cactus_qwen_layer_weights; the
+ * const pointers of each layer entry name writable buffers).  Host only: no
+ * device is touched, so the same weights can feed a CPU model. */
+int cactus_qwen_random_weights(const cactus_qwen_config* cfg, uint64_t seed,
+                               cactus_qwen_layer_weights* layers_out_buffers, uint16_t* embedding,
+                               uint16_t* output_norm);
 int cactus_qwen_destroy(void* model);
 int cactus_qwen_reset(void* model);
 /* Selects the decode path: 0 = node-by-node graph (one C-ABI call per node,
@@ -104,12 +115,12 @@ int cactus_qwen_generate(void* model, const uint32_t* prompt, size_t n, size_t m
 /* Final hidden state (after the output norm) of the last forward, fp16
  * [rows][hidden] copied into `out` (capacity max_rows rows). */
 int cactus_qwen_last_hidden(void* model, uint16_t* out, size_t max_rows, size_t* rows);
-/* Logits of the last decode step, fp16 [vocab] (decode mode 0 only). */
+/* Logits of the last decode step, fp16 [vocab] (either decode mode; an
+ * error before the first step after a reset or prefill). */
 int cactus_qwen_last_logits(void* model, uint16_t* out);
 /* Model::decode's out_entropy (engine_model.cpp:255-290) for the last
  * decode step's logits: normalised softmax entropy in [0, 1], the
- * confidence signal of the reference's cloud handoff.  Needs a step that
- * kept its logits (decode mode 0, or non-greedy sampling). */
+ * confidence signal of the reference's cloud handoff. */
 int cactus_qwen_last_entropy(void* model, float* entropy);
 int cactus_qwen_cache_len(void* model, size_t* len);
 /* Copies layer `layer` of the INT8 KV cache (first cache_len tokens). */

@@ -391,11 +391,12 @@ int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_ra
                                      float* k_scales, float* v_scales, size_t max_cache,
                                      float* v_shadow, float scale, uint16_t* o, void* stream);
 /* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
- * and advances state.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */
+ * and advances state; logits_out (fp16 [N], or null) receives the logits
+ * row.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
                               const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
-                              uint32_t* tokens_out, size_t max_steps, void* scratch,
-                              size_t scratch_bytes, void* stream);
+                              uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,
+                              void* scratch, size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -40,6 +40,7 @@ _SIGS = {
     "orc_group_sums_int8": (None, [P, P, P, SZ, SZ, SZ, SZ]),
     "orc_unpack_int4_to_int8": (None, [P, P, SZ]),
     "orc_matmul_int8_mt": (None, [P, P, P, P, P, SZ, SZ, SZ, SZ, I]),
+    "orc_set_threads": (None, [I]),
     "orc_matmul_f16": (None, [P, P, P, SZ, SZ, SZ]),
     "orc_attention_f16": (None, [P, P, P, P, SZ, SZ, SZ, SZ, SZ, SZ, F, P, SZ, SZ, I]),
     "orc_attention_hybrid_int8_fp16": (None, [P, P, P, P, P, P, P, P, SZ, SZ, SZ, SZ, SZ, SZ,

@@ -16,6 +16,12 @@
 /* fp16 helpers                                                              */
 /* ------------------------------------------------------------------------ */
 
+/* Worker threads for the row/head loops below (1 = serial, the default).
+ * Each output element is computed by the same sequential code whatever the
+ * thread count, so results do not depend on it. */
+int orc_nt = 1;
+void orc_set_threads(int n) { orc_nt = n < 1 ? 1 : n; }
+
 static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float bits_f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
@@ -192,6 +198,7 @@ void orc_fp16_to_int8(const uint16_t* src, int8_t* dst, size_t count, float scal
 /* quantize_activations_fp16_to_int8 (graph_ops_nn.cpp:35-66) */
 void orc_quantize_activations(const uint16_t* x, int8_t* q, float* scales,
                               size_t M, size_t K) {
+#pragma omp parallel for num_threads(orc_nt) if (orc_nt > 1 && M > 1)
     for (size_t m = 0; m < M; m++) {
         float max_abs = orc_fp16_max_abs(x + m * K, K);
         float s = max_abs / 127.0f;
@@ -253,6 +260,7 @@ void orc_matmul_int8(const int8_t* A, const float* As, const int8_t* B, const ui
                      uint16_t* C, size_t M, size_t K, size_t N, size_t gs) {
     if (M == 0 || K == 0 || N == 0) return;
     const size_t G = K / gs;
+#pragma omp parallel for schedule(dynamic, 16) num_threads(orc_nt) if (orc_nt > 1)
     for (size_t n = 0; n < N; n++)
         matmul_grouped_rows(A, As, B + n * K, Bs + n * G, C, M, K, N, n, gs);
 }
@@ -262,12 +270,16 @@ void orc_matmul_int4(const int8_t* A, const float* As, const uint8_t* Bp, const 
                      uint16_t* C, size_t M, size_t K, size_t N, size_t gs) {
     if (M == 0 || K == 0 || N == 0) return;
     const size_t G = K / gs;
-    int8_t* row = (int8_t*)malloc(K);
-    for (size_t n = 0; n < N; n++) {
-        orc_unpack_int4_to_int8(Bp + n * (K / 2), row, K);
-        matmul_grouped_rows(A, As, row, Bs + n * G, C, M, K, N, n, gs);
+#pragma omp parallel num_threads(orc_nt) if (orc_nt > 1)
+    {
+        int8_t* row = (int8_t*)malloc(K);
+#pragma omp for schedule(dynamic, 16)
+        for (size_t n = 0; n < N; n++) {
+            orc_unpack_int4_to_int8(Bp + n * (K / 2), row, K);
+            matmul_grouped_rows(A, As, row, Bs + n * G, C, M, K, N, n, gs);
+        }
+        free(row);
     }
-    free(row);
 }
 
 /* Threaded CPU baseline: rows of B split over threads the way
@@ -310,6 +322,7 @@ void orc_matmul_f16(const uint16_t* a, const uint16_t* bT, uint16_t* c,
     const size_t K16 = (K / 16) * 16, K8 = (K / 8) * 8;
     for (size_t m = 0; m < M; m++) {
         const uint16_t* ar = a + m * K;
+#pragma omp parallel for schedule(dynamic, 256) num_threads(orc_nt) if (orc_nt > 1)
         for (size_t n = 0; n < N; n++) {
             const uint16_t* br = bT + n * K;
             uint16_t l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -363,8 +376,11 @@ void orc_attention_f16(const uint16_t* Q, const uint16_t* Kt, const uint16_t* Vt
     if (scale == 0.0f) scale = 1.0f / sqrtf((float)d);
     const size_t da = (d / 8) * 8;
     const size_t gq = Hq / Hkv;
+#pragma omp parallel num_threads(orc_nt) if (orc_nt > 1)
+    {
     float* acc = (float*)malloc(sizeof(float) * (d ? d : 1));
     float bsc[ATT_BLOCK];
+#pragma omp for collapse(3) schedule(dynamic, 4)
     for (size_t b = 0; b < B; b++)
     for (size_t h = 0; h < Hq; h++)
     for (size_t qp = 0; qp < S; qp++) {
@@ -440,6 +456,7 @@ void orc_attention_f16(const uint16_t* Q, const uint16_t* Kt, const uint16_t* Vt
         }
     }
     free(acc);
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -487,8 +504,11 @@ void orc_attention_hybrid_int8_fp16(const uint16_t* Q, const int8_t* Kc, const i
     const size_t da = (d / 8) * 8;
     const size_t gq = Hq / Hkv;
     const size_t nqg = (d + qgs - 1) / qgs;
+#pragma omp parallel num_threads(orc_nt) if (orc_nt > 1)
+    {
     float* acc = (float*)malloc(sizeof(float) * (d ? d : 1));
     float bsc[ATT_BLOCK];
+#pragma omp for collapse(3) schedule(dynamic, 4)
     for (size_t b = 0; b < B; b++)
     for (size_t h = 0; h < Hq; h++)
     for (size_t qp = 0; qp < S; qp++) {
@@ -563,6 +583,7 @@ void orc_attention_hybrid_int8_fp16(const uint16_t* Q, const int8_t* Kc, const i
         }
     }
     free(acc);
+    }
 }
 
 /* ------------------------------------------------------------------------ */
@@ -605,6 +626,7 @@ void orc_rms_norm_f16(const uint16_t* X, const uint16_t* W, uint16_t* Y, size_t 
                       size_t dims, float eps) {
     const size_t tile_end = dims >= 16 ? dims - 16 + 1 : 0;
     const size_t simd_end = dims >= 8 ? dims - 8 + 1 : 0;
+#pragma omp parallel for schedule(static) num_threads(orc_nt) if (orc_nt > 1 && rows > 64)
     for (size_t r = 0; r < rows; r++) {
         const uint16_t* x = X + r * dims;
         uint16_t* y = Y + r * dims;

@@ -59,6 +59,10 @@ void orc_group_sums_int8(const int8_t* A, const int8_t* B, int32_t* acc,
                          size_t M, size_t K, size_t N, size_t group_size);
 void orc_unpack_int4_to_int8(const uint8_t* packed, int8_t* unpacked, size_t count);
 /* threaded variants used only as the timed CPU baseline */
+/* Worker threads of the row/head loops (1 = serial, the default); results
+ * do not depend on it. */
+void orc_set_threads(int n);
+
 void orc_matmul_int8_mt(const int8_t* A, const float* A_scales,
                         const int8_t* B, const uint16_t* B_scales,
                         uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,

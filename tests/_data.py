@@ -25,10 +25,10 @@ def pack_int4(codes: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(lo | (hi << 4))
 
 
-def grouped_int4_weights(rng, N, K, gs):
-    """INT4 codes U{-7..7}, fp16 group scales |N(0,0.02)|/7."""
+def grouped_int4_weights(rng, N, K, gs, sd=0.02):
+    """INT4 codes U{-7..7}, fp16 group scales |N(0,sd)|/7."""
     codes = rng.integers(-7, 8, size=(N, K), dtype=np.int8)
-    Bs = f16(np.abs(rng.normal(0, 0.02, size=(N, K // gs))) / 7.0)
+    Bs = f16(np.abs(rng.normal(0, sd, size=(N, K // gs))) / 7.0)
     return codes, pack_int4(codes), Bs
 
 
@@ -44,9 +44,13 @@ def qwen_small_config(**over):
     return c
 
 
-def qwen_weights(rng, c):
+def qwen_weights(rng, c, down_sd=0.1, emb_sd=0.005):
     """Random-init weights of the architecture: INT8 g-grouped attention
-    projections, packed INT4 MLP, fp16 norms 1+N(0,0.02), embeddings N(0,0.02)."""
+    projections, packed INT4 MLP, fp16 norms 1+N(0,0.02).  Group scales are
+    |N(0,0.02)|/qmax except the down projection's |N(0,down_sd)|/7, and
+    embeddings are N(0,emb_sd): with those two at 0.02 the decode of these
+    random models repeats its input token forever (a residual stream still
+    dominated by the tied embedding row predicts that row's own token)."""
     H, F, hd, gs = c["hidden"], c["ffn"], c["head_dim"], c["group_size"]
     nq, nkv = c["heads"] * hd, c["kv_heads"] * hd
     layers = []
@@ -59,8 +63,9 @@ def qwen_weights(rng, c):
         for name, (n, k) in {"q": (nq, H), "k": (nkv, H), "v": (nkv, H), "o": (H, nq)}.items():
             L[name + "_w"], L[name + "_s"] = grouped_int8_weights(rng, n, k, gs)
         for name, (n, k) in {"gate": (F, H), "up": (F, H), "down": (H, F)}.items():
-            _, L[name + "_w"], L[name + "_s"] = grouped_int4_weights(rng, n, k, gs)
+            _, L[name + "_w"], L[name + "_s"] = grouped_int4_weights(rng, n, k, gs,
+                                                                     down_sd if name == "down" else 0.02)
         layers.append(L)
-    emb = f16(rng.normal(0, 0.02, (c["vocab"], H)))
+    emb = f16(rng.normal(0, emb_sd, (c["vocab"], H)))
     out_norm = f16(1 + rng.normal(0, 0.02, H))
     return layers, emb, out_norm

@@ -277,14 +277,17 @@ def test_lm_head_argmax_qwen_vocab(dev, orc):
 def test_decode_lm_head_state(dev, orc, K, N):
     """The decode step's LM head: token = argmax(matmul_f16(rms_norm(h),
     embedding)) written to tokens_out[step], step state advanced.  K % 64 == 0
-    takes the streamed kernel (ragged N), K = 200 the staged one."""
+    takes the streamed kernel (ragged N), K = 200 the staged one.  The
+    logits row is written on the second step only (logits_out null on the
+    first)."""
     say("decode_lm_head", K, N)
     rng = np.random.default_rng(K + N)
     h = f16(rng.normal(0, 1, (1, K)))
     w = f16(1 + rng.normal(0, 0.05, K))
     emb = f16(rng.normal(0, 0.02, (N, K)))
     eps = 1e-6
-    ref_tok = orc.argmax(orc.matmul_f16(orc.rms_norm(h, w, eps), emb)[0])
+    ref_logits = orc.matmul_f16(orc.rms_norm(h, w, eps), emb)[0]
+    ref_tok = orc.argmax(ref_logits)
     blocks = (N + 127) // 128
     scratch = dev.empty(256 + 8 * blocks)
     dev.cm.call("cactus_hip_memset", scratch.ptr, 0, 256 + 8 * blocks, None)
@@ -292,11 +295,13 @@ def test_decode_lm_head_state(dev, orc, K, N):
     dev.bufs.append(state)
     toks = dev.empty(16)
     hp, wp, ep = dev.put(h), dev.put(w), dev.put(emb)
-    for _ in range(2):   # steps 2 and 3; the argmax scratch resets itself
+    logits = dev.empty(2 * N)
+    for i in range(2):   # steps 2 and 3; the argmax scratch resets itself
         dev.cm.call("cactus_hip_decode_lm_head", hp, wp, ctypes.c_float(eps), ep, K, N, state.ptr, toks.ptr, 4,
-                    scratch.ptr, 256 + 8 * blocks, None)
+                    logits.ptr if i else None, scratch.ptr, 256 + 8 * blocks, None)
     out = dev.get(toks, np.uint32, 4)
     assert out[2] == ref_tok and out[3] == ref_tok, (out, ref_tok)
+    assert (dev.get(logits, np.uint16, N) == ref_logits).all()
     assert list(dev.get(state, np.uint32, 4)) == [ref_tok, 102, 102, 4]
 
 
