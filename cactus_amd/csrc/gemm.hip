@@ -587,9 +587,13 @@ static int gemm_scratch(hipStream_t st, size_t bytes, void** out) {
 constexpr size_t GEMM_MIN_M = 32;
 
 // Returns *handled = false when the shape is left to the GEMV path.
+// Activation codes ([M][K] int8, padded to 256 bytes) and row scales
+// ([M] fp32) of the MFMA path with FP16 activations.
+size_t gemm_act_scratch_bytes(size_t M, size_t K) { return ((M * K + 255) & ~(size_t)255) + M * sizeof(float); }
+
 int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
                       const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
-                      bool int4, hipStream_t st, bool* handled, const uint16_t* R) {
+                      bool int4, hipStream_t st, bool* handled, const uint16_t* R, void* ext_scratch) {
     *handled = false;
     if (M < GEMM_MIN_M || gs % 32 != 0 || N < 32) return CACTUS_HIP_OK;
     if (((uintptr_t)B & 15) != 0) return CACTUS_HIP_OK;
@@ -600,9 +604,12 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
     if (A16) {
         // per-row quantization into scratch (bit-identical to the fused GEMV's)
         const size_t qbytes = (M * K + 255) & ~(size_t)255;
-        void* scr = nullptr;
-        int rc = gemm_scratch(st, qbytes + M * sizeof(float), &scr);
-        if (rc) return rc;
+        void* scr = ext_scratch;
+        if (!scr) {
+            int rc = gemm_scratch(st, gemm_act_scratch_bytes(M, K), &scr);
+            if (rc) return rc;
+        }
+        int rc;
         int8_t* q = static_cast<int8_t*>(scr);
         float* s = reinterpret_cast<float*>(static_cast<char*>(scr) + qbytes);
         rc = cactus_hip_quantize_activations(A16, q, s, M, K, st);
@@ -633,3 +640,59 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
 }
 
 }  // namespace cactus_hip
+
+// ------------------------------------------------ no-allocation entry point
+// Activation codes and row scales of cactus_hip_matmul_int8_f16act_noalloc
+// live in this file-scope device array: each GPU the library runs on holds
+// its own copy until the process ends.  Host code never passes the array's
+// name to a kernel (on the host it names a stand-in, not device memory); it
+// uses the device address hipGetSymbolAddress returns, looked up once per
+// device with that device current.
+namespace cactus_hip {
+
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;   // 4 MiB
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_noalloc_mu;
+static void* g_noalloc_ptr[kMaxDevices];
+
+int grouped_dispatch(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
+                     const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs, bool int4,
+                     hipStream_t st, const uint16_t* R, void* ext_scratch);
+
+static int noalloc_scratch(void** out) {
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    CH_REQUIRE(dev >= 0 && dev < kMaxDevices, "matmul_int8_f16act_noalloc: device index above 63");
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(CACTUS_HIP_ERUNTIME, std::string("matmul_int8_f16act_noalloc: hipGetSymbolAddress(scratch): ") +
+                                                 hipGetErrorString(e));
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return CACTUS_HIP_OK;
+}
+
+}  // namespace cactus_hip
+
+extern "C" int cactus_hip_matmul_int8_f16act_noalloc(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                                     uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,
+                                                     void* stream) {
+    using namespace cactus_hip;
+    if (M == 0 || K == 0 || N == 0) return CACTUS_HIP_OK;
+    const size_t need = gemm_act_scratch_bytes(M, K);
+    if (need > kNoAllocScratchBytes)
+        return fail(CACTUS_HIP_EINVAL, "matmul_int8_f16act_noalloc: M x K = " + std::to_string(M) + " x " +
+                                           std::to_string(K) + " needs " + std::to_string(need) +
+                                           " bytes of activation scratch, above the 4 MiB static buffer");
+    void* scr = nullptr;
+    const int rc = noalloc_scratch(&scr);
+    if (rc) return rc;
+    return grouped_dispatch(A, nullptr, nullptr, reinterpret_cast<const uint8_t*>(B), B_scales, C, M, K, N,
+                            group_size, false, as_stream(stream), nullptr, scr);
+}

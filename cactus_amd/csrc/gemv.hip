@@ -463,7 +463,7 @@ namespace cactus_hip {
 int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, const uint8_t* B,
                       const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
                       bool int4, hipStream_t st, bool* handled,
-                      const uint16_t* R = nullptr);
+                      const uint16_t* R = nullptr, void* ext_scratch = nullptr);
 
 // C[i] = fp16(C[i] + R[i]): the residual add node after a small-M matmul
 __global__ void add_residual_kernel(uint16_t* C, const uint16_t* R, size_t n) {
@@ -471,16 +471,20 @@ __global__ void add_residual_kernel(uint16_t* C, const uint16_t* R, size_t n) {
         C[i] = hadd(C[i], R[i]);
 }
 
-static int grouped_dispatch(const uint16_t* A16, const int8_t* A8, const float* As,
-                            const uint8_t* B, const uint16_t* Bs, uint16_t* C, size_t M, size_t K,
-                            size_t N, size_t gs, bool int4, hipStream_t st, const uint16_t* R = nullptr) {
+// ext_scratch: caller-provided device memory for the MFMA path's activation
+// codes and row scales (at least gemm_act_scratch_bytes(M, K)), or null for
+// the library's own per-stream buffer.
+int grouped_dispatch(const uint16_t* A16, const int8_t* A8, const float* As,
+                     const uint8_t* B, const uint16_t* Bs, uint16_t* C, size_t M, size_t K,
+                     size_t N, size_t gs, bool int4, hipStream_t st, const uint16_t* R = nullptr,
+                     void* ext_scratch = nullptr) {
     if (M == 0 || K == 0 || N == 0) return CACTUS_HIP_OK;
     int rc = check_grouped_shape(M, K, N, gs, int4);
     if (rc) return rc;
     CH_REQUIRE(B && Bs && C && (A16 || (A8 && As)), "grouped matmul: null pointer");
     CH_REQUIRE(((uintptr_t)B & 15) == 0, "grouped matmul: weights must be 16-byte aligned");
     bool handled = false;
-    rc = gemm_grouped_mfma(A16, A8, As, B, Bs, C, M, K, N, gs, int4, st, &handled, R);
+    rc = gemm_grouped_mfma(A16, A8, As, B, Bs, C, M, K, N, gs, int4, st, &handled, R, ext_scratch);
     if (rc || handled) return rc;
     GemvArgs a{};
     a.A16 = A16; a.A8 = A8; a.As = As; a.B = B; a.Bs = Bs; a.C = C;

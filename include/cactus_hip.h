@@ -98,6 +98,20 @@ int cactus_hip_matmul_int4(const int8_t* A, const float* A_scales, const uint8_t
 int cactus_hip_matmul_int8_f16act(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
                                   uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,
                                   void* stream);
+/* No counterpart in the reference.  cactus_hip_matmul_int8_f16act for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): the same kernels
+ * and results, with the activation codes and row scales of the MFMA path
+ * (M >= 32) in a static 4 MiB device buffer instead of a buffer the library
+ * allocates.  Rejects, with CACTUS_HIP_EINVAL and before any launch, shapes
+ * whose ((M*K + 255) & ~255) + 4*M bytes exceed 4 MiB (e.g. M = 4096 at
+ * K = 1024).  Calls no hipMalloc / hipFree.  Every call on one GPU shares
+ * that GPU's buffer: calls that overlap on one GPU (two streams, two host
+ * threads) race.  Each call rewrites every byte it reads, so nothing
+ * carries over from the previous call. */
+int cactus_hip_matmul_int8_f16act_noalloc(const uint16_t* A, const int8_t* B, const uint16_t* B_scales,
+                                          uint16_t* C, size_t M, size_t K, size_t N, size_t group_size,
+                                          void* stream);
 int cactus_hip_matmul_int4_f16act(const uint16_t* A, const uint8_t* B_packed,
                                   const uint16_t* B_scales, uint16_t* C, size_t M, size_t K,
                                   size_t N, size_t group_size, void* stream);
