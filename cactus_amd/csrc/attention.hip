@@ -187,7 +187,8 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
         };
         if (HYBRID && kp < a.cache_len) {
             const int8_t* kr = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
-            const float* sr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
+            // scales carry no batch offset (kernel_attention.cpp:353)
+            const float* sr = a.ks + (kp * a.Hkv + kvh) * (size_t)a.nqg;
             uint2 kw[NC];
             float ksc[NC];
 #pragma unroll
@@ -382,7 +383,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     const float* ksr = nullptr;
     if (kint8) {
         krow8 = a.kc + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)d;
-        ksr = a.ks + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg;
+        ksr = a.ks + (kp * a.Hkv + kvh) * (size_t)a.nqg;   // no batch offset (kernel_attention.cpp:353)
     } else {
         const size_t kpos = HYBRID ? kp - a.cache_len : kp;
         const size_t klen = HYBRID ? a.new_len : a.Skv;
@@ -742,7 +743,8 @@ __global__ void __launch_bounds__(CH_MAX_THREADS) attn_chain_kernel(AttnArgs a_i
                 if (HYBRID && kp < a.cache_len) {
                     const size_t off = (b * a.cache_len + kp) * a.Hkv + kvh;
                     const int8_t* src = a.vc + off * d + dim0;
-                    const float sc = a.vs[off * a.nqg + dim0 / a.qgs];
+                    // value scales carry no batch offset (kernel_attention.cpp:424)
+                    const float sc = a.vs[(kp * a.Hkv + kvh) * a.nqg + dim0 / a.qgs];
                     int8_t cd[4];
                     if (vec_ok) {
                         const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
@@ -1167,7 +1169,7 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_dma_kern
         return vbase + (((b * vlen + kp) * a.Hkv + kvh) * (size_t)d + sl * 64 + cel) * ESZ;
     };
     auto scale_src = [&](size_t kp) -> const float* {
-        return a.vs + ((b * a.cache_len + kp) * a.Hkv + kvh) * (size_t)a.nqg + (sl * 64) / a.qgs;
+        return a.vs + (kp * a.Hkv + kvh) * (size_t)a.nqg + (sl * 64) / a.qgs;   // no batch offset (:424)
     };
     auto w_src = [&](int i) -> const float* {
         const int o = i * 64 * DW + lane * DW;
@@ -1850,7 +1852,7 @@ __global__ void __launch_bounds__(RW_THREADS) attn_rows_kernel(AttnArgs a_in, in
             if (HYBRID && kp < a.cache_len) {
                 const size_t off = (b * a.cache_len + kp) * a.Hkv + kvh;
                 r8[e] = *reinterpret_cast<const uint32_t*>(a.vc + off * d + dim0);
-                rsc[e] = a.vs[off * a.nqg + dim0 / a.qgs];
+                rsc[e] = a.vs[(kp * a.Hkv + kvh) * a.nqg + dim0 / a.qgs];   // no batch offset (:424)
             } else {
                 const size_t vpos = HYBRID ? kp - a.cache_len : kp;
                 const size_t vlen = HYBRID ? a.new_len : a.Skv;

@@ -1,0 +1,753 @@
+// attention_fast.hip -- split-K decode attention over the KV cache
+// (tolerance mode).
+//
+// The exact kernels of attention.hip reproduce the reference's value
+// accumulation, one fp32 FMA chain per (head, dim) over the keys in order
+// (kernel_attention.cpp:206-224, :416-441), which makes a decode step a
+// latency-bound walk over the context.  This file computes the same
+// function -- causal softmax(q k^T * scale) v with the reference's score
+// operands (fp16 q, fp16 or INT8-times-scale k, fp32 sums) -- as an
+// HBM-bound split-K ("flash decoding") reduction:
+//
+//   grid (splits, batch * kv_heads), 256 threads = 4 waves per workgroup;
+//   workgroup s owns a split of 64 keys (INT8 cache) or 128 keys (FP16) of
+//   one KV head and all the query heads that share it (GQA).  Each wave
+//   scores its keys, the workgroup takes its local max M and weights
+//   exp(s - M), and each wave accumulates its keys' value rows.  The
+//   workgroup writes (M, sum, acc[d]) per query head; the last
+//   workgroup of the KV head to finish (an atomic counter, reset by that
+//   workgroup) combines the splits:
+//       M* = max_s M_s,  L = sum_s e^(M_s - M*) l_s,
+//       o  = fp16( sum_s e^(M_s - M*) acc_s / L ).
+//
+// Only the order of the fp32 sums and the exponential differ from the
+// reference, so outputs agree with it to well within fp16 tolerance
+// (|gpu - ref| <= 1e-3 + 1e-2 |ref|), not bit for bit.  Positions at or
+// beyond cache_len read the FP16 "new" rows, as the hybrid kernel does
+// (kernel_attention.cpp:372-388).
+#include "hip_common.h"
+#include "decode_device.h"
+
+#include <map>
+#include <mutex>
+#include <utility>
+
+namespace cactus_hip {
+
+constexpr int FA_WAVES = 4;
+constexpr int FA_THREADS = 64 * FA_WAVES;
+// keys per wave: 32 (128-key splits; measured on MI355X at 4096 keys, 8 KV
+// heads: 12.9 us against 15.9 for 64-key and 15.6 for 256-key splits -- the
+// cross-XCD combine grows with the split count, the per-wave work with the
+// split size); for FP16 rows it also keeps each of the reference's 32-key
+// weight blocks inside one wave
+template <bool HYBRID> constexpr int fa_kpw() { return 32; }
+template <bool HYBRID> constexpr int fa_kpb() { return fa_kpw<HYBRID>() * FA_WAVES; }
+constexpr int FA_MAX_SPLITS = 512;               // the combine keeps every split's (M, sum) in LDS
+constexpr int FA_MAX_GQ = 4;
+
+struct FastArgs {
+    const uint16_t* q;        // prepared queries [B][Hq][d] (null with prep)
+    const uint16_t* k;        // FP16 keys: [B][Skv][Hkv][d] (FP16 form) or new rows [B][new][Hkv][d]
+    const uint16_t* v;
+    const int8_t* kc;         // INT8 cache [B][cache][Hkv][d] (hybrid form)
+    const int8_t* vc;
+    const float* ks;          // [B][cache][Hkv][nqg]
+    const float* vs;
+    uint16_t* o;              // [B][Hq][d]
+    float* part;              // [B*Hkv][nsplit][GQ][d + 4]: acc[d], M, sum, pad
+    uint32_t* cnt;            // [B*Hkv], zero between launches
+    int B, Hq, Hkv, nsplit, nqg;
+    size_t Skv;               // FP16 form: keys; hybrid: cache_len + new_len
+    size_t cache_len, new_len, pos_off, window;
+    float scale;
+    const uint32_t* dyn;      // decode step state {token, position, cache length, step} or null
+    // fused head preparation (decode step): raw rows, norm weights, RoPE
+    // tables and the cache the step's key and value are appended to
+    const uint16_t* q_raw; const uint16_t* k_raw; const uint16_t* v_raw;
+    const uint16_t* q_norm; const uint16_t* k_norm;
+    const uint16_t* cos_t; const uint16_t* sin_t;
+    float eps;
+    uint32_t table_pos;
+    int8_t* kc_w; int8_t* vc_w; float* ks_w; float* vs_w; float* vsh;
+    size_t sh_ntile, max_cache;
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// DPP lane moves within 16-lane rows (no LDS traffic)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane j <- 7 - j within 8 lanes
+constexpr int DPP_MIRROR = 0x140;      // lane j <- 15 - j within 16 lanes
+constexpr int DPP_ROR4 = 0x124;        // row_ror:4
+constexpr int DPP_ROR8 = 0x128;        // row_ror:8
+
+// sum over aligned groups of N lanes (N = 4, 8 or 16), in every lane of the group
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp_f<DPP_XOR1>(v);
+    v += dpp_f<DPP_XOR2>(v);
+    if (N >= 8) v += dpp_f<DPP_HALF_MIRROR>(v);
+    if (N >= 16) v += dpp_f<DPP_MIRROR>(v);
+    return v;
+}
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    v = __builtin_fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = __builtin_fmaxf(v, dpp_f<DPP_XOR2>(v));
+    if (N >= 8) v = __builtin_fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
+    if (N >= 16) v = __builtin_fmaxf(v, dpp_f<DPP_MIRROR>(v));
+    return v;
+}
+__device__ __forceinline__ float lane_bcast(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+// wave-wide max / sum, uniform result
+__device__ __forceinline__ float wave_max_u(float v) {
+    v = group_max<16>(v);
+    return __builtin_fmaxf(__builtin_fmaxf(lane_bcast(v, 0), lane_bcast(v, 16)),
+                           __builtin_fmaxf(lane_bcast(v, 32), lane_bcast(v, 48)));
+}
+__device__ __forceinline__ float wave_sum_u(float v) {
+    v = group_sum<16>(v);
+    return (lane_bcast(v, 0) + lane_bcast(v, 16)) + (lane_bcast(v, 32) + lane_bcast(v, 48));
+}
+__device__ __forceinline__ float agent_load(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// 16 bytes as two 8-byte agent-scope loads (the widest lock-free atomic)
+__device__ __forceinline__ f32x4 agent_load4(const float* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (f32x4){__builtin_bit_cast(float, (uint32_t)lo), __builtin_bit_cast(float, (uint32_t)(lo >> 32)),
+                   __builtin_bit_cast(float, (uint32_t)hi), __builtin_bit_cast(float, (uint32_t)(hi >> 32))};
+}
+__device__ __forceinline__ void agent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// LDS written by some lanes of a wave, then read by others: the wave's LDS
+// operations execute in order, so only the compiler must not move them
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// HYBRID: INT8 cache + FP16 new rows; otherwise FP16 keys and values.
+// PREP: q and the step's k come raw (head RMSNorm + RoPE here; the first
+// workgroup of each KV head also appends the step's k and v to the cache).
+//
+// Lane layout: a key row is CPL 16-byte chunks; CPL consecutive lanes read
+// one row (so each load instruction moves 64/CPL whole rows, coalesced) and
+// a lane owns the DPL dims of its chunk for its NI keys (one per load
+// instruction).  Scores are partial dots reduced over the CPL lanes of a
+// row; value sums stay per lane and are reduced over the rows at the end.
+template <bool HYBRID, bool PREP, int D, int GQ>
+__global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    static_assert(GQ >= 1 && GQ <= FA_MAX_GQ, "query heads per KV head");
+    constexpr int ESZ = HYBRID ? 1 : 2;            // bytes per cached element
+    constexpr int CPL = D * ESZ / 16;              // lanes (16-byte chunks) per row
+    constexpr int DPL = 16 / ESZ;                  // dims per lane
+    constexpr int R = 64 / CPL;                    // rows per load instruction
+    constexpr int FA_KPW = fa_kpw<HYBRID>(), FA_KPB = fa_kpb<HYBRID>();
+    constexpr int NI = FA_KPW / R;                 // load instructions (keys) per lane
+    static_assert(NI >= 1, "keys per wave");
+    static_assert(CPL >= 4 && CPL <= 16 && 64 % CPL == 0, "row layout");
+    __shared__ __align__(16) uint16_t qs[GQ][D];   // prepared queries, fp16
+    __shared__ __align__(16) uint16_t kn[D];       // prepared new key (PREP)
+    __shared__ __align__(16) uint16_t tmp[FA_WAVES][D];
+    __shared__ float redm[GQ][FA_WAVES], reds[GQ][FA_WAVES];
+    __shared__ __align__(16) float vsum[FA_WAVES * 4 * GQ * D];   // value sums per 16-lane row
+    __shared__ float ms[GQ * FA_MAX_SPLITS];       // combine: split maxima, then weights
+    __shared__ float ls[GQ * FA_MAX_SPLITS];       // combine: split sums
+    __shared__ float Ltot[GQ];
+    __shared__ bool last;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cl = lane % CPL, rl = lane / CPL;
+    const int bg = blockIdx.y;                    // b * Hkv + g
+    const int b = bg / a.Hkv, g = bg % a.Hkv;
+    const int s = blockIdx.x;
+
+    size_t cache_len = a.cache_len, pos = a.pos_off, Skv = a.Skv;
+    if (a.dyn) {
+        cache_len = a.dyn[2];
+        pos = a.dyn[1];
+        Skv = cache_len + a.new_len;
+    }
+    // causal key range of the query (kernel_attention.cpp:78-96, :328-337)
+    size_t kv_start = 0, kv_end = Skv;
+    if (!HYBRID && a.window > 0 && a.window < Skv && pos > a.window) kv_start = pos - a.window;
+    if (pos + 1 < kv_end) kv_end = pos + 1;
+    const size_t k0 = kv_start + (size_t)s * FA_KPB;
+    const size_t k1 = k0 + FA_KPB < kv_end ? k0 + FA_KPB : kv_end;
+    const bool has_keys = k0 < kv_end;
+    const bool has_new = HYBRID && has_keys && k1 > cache_len;
+    const bool appends = PREP && s == 0;
+    const bool prep_ok = !PREP || pos < a.table_pos;   // the host keeps positions inside the tables
+    const size_t wk0 = k0 + (size_t)wid * FA_KPW;      // this wave's first key
+
+    // ---- 1. key and value chunks, in flight first (key of instruction i:
+    // wk0 + i*R + rl)
+    i32x4 kch[NI], vch[NI];
+    float ksc[NI], vsc[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        kch[i] = vch[i] = (i32x4){0, 0, 0, 0};
+        ksc[i] = vsc[i] = 1.0f;
+        const size_t kp = wk0 + (size_t)i * R + rl;
+        if (!has_keys || kp >= k1) continue;
+        if (HYBRID) {
+            if (kp >= cache_len) continue;   // an FP16 new row: read below
+            const size_t row = ((size_t)b * cache_len + kp) * a.Hkv + g;
+            kch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.kc + row * D) + cl);
+            vch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.vc + row * D) + cl);
+            // scales carry no batch offset (kernel_attention.cpp:353, :424)
+            ksc[i] = a.ks[(kp * a.Hkv + g) * a.nqg];
+            vsc[i] = a.vs[(kp * a.Hkv + g) * a.nqg];
+        } else {
+            const size_t row = ((size_t)b * Skv + kp) * a.Hkv + g;
+            kch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.k + row * D) + cl);
+            vch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.v + row * D) + cl);
+        }
+    }
+
+    // ---- 2. queries (and the step's new key) into LDS
+    if (PREP) {
+        const int half = D / 2, end8 = (D / 8) * 8;
+        const bool need_k = has_new || appends;
+        const uint16_t* ct = a.cos_t + pos * half;
+        const uint16_t* st = a.sin_t + pos * half;
+        // q/k head RMSNorm then RoPE at the step's position, one wave per row
+        auto prep_row = [&](const uint16_t* src, const uint16_t* nw, uint16_t* dst) {
+            uint16_t* xs = tmp[wid];
+            for (int i = lane; i < D; i += 64) xs[i] = src[i];
+            wave_lds_sync();
+            float inv;
+            uint16_t hinv;
+            rms_stats_wave(xs, D, a.eps, inv, hinv);
+            uint16_t yv[D / 64];
+#pragma unroll
+            for (int j = 0; j < D / 64; j++)
+                yv[j] = rms_apply(xs[lane + 64 * j], nw[lane + 64 * j], lane + 64 * j, end8, inv, hinv);
+            wave_lds_sync();
+#pragma unroll
+            for (int j = 0; j < D / 64; j++) xs[lane + 64 * j] = yv[j];
+            wave_lds_sync();
+            rope_row(xs, D, ct, st, [&](int i, uint16_t v) { dst[i] = v; });
+        };
+        if (prep_ok) {
+            if (wid < GQ) prep_row(a.q_raw + ((size_t)b * a.Hq + g * GQ + wid) * D, a.q_norm, qs[wid]);
+            // the new key: wave GQ, or wave 0 after its query head when GQ == 4
+            if (need_k && wid == GQ % FA_WAVES) prep_row(a.k_raw + ((size_t)b * a.Hkv + g) * D, a.k_norm, kn);
+        }
+    } else {
+        for (int i = tid; i < GQ * D; i += FA_THREADS)
+            qs[i / D][i % D] = a.q[((size_t)b * a.Hq + g * GQ + i / D) * D + i % D];
+    }
+    __syncthreads();
+    if (appends && prep_ok && cache_len < a.max_cache && wid == GQ % FA_WAVES) {
+        // the step's key (prepared) and value to slot cache_len
+        // (engine_cache.cpp:234-267), with the exact mode's product tiles
+        const int ng = (D + 127) / 128;
+        const size_t row = (size_t)cache_len * a.Hkv + g;
+        kv_append_row(kn, a.kc_w + row * D, a.ks_w + row * ng, D);
+        kv_append_row(a.v_raw + ((size_t)b * a.Hkv + g) * D, a.vc_w + row * D, a.vs_w + row * ng, D, a.vsh,
+                      a.sh_ntile, cache_len, g);
+    }
+    // this lane's query dims, fp32, and (INT8) their sum
+    float qv[GQ][DPL], qsum[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        qsum[h] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            qv[h][e] = h2f(qs[h][cl * DPL + e]);
+            qsum[h] += qv[h][e];
+        }
+    }
+
+    // ---- 3. scores of the lane's NI keys
+    float sc[NI][GQ];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const size_t kp = wk0 + (size_t)i * R + rl;
+        const bool valid = has_keys && kp < k1;
+        float acc[GQ];
+#pragma unroll
+        for (int h = 0; h < GQ; h++) acc[h] = 0.0f;
+        if (HYBRID && valid && kp >= cache_len) {
+            // an FP16 new row (kernel_attention.cpp:372-388)
+            const uint16_t* kr = PREP ? kn : a.k + (((size_t)b * a.new_len + (kp - cache_len)) * a.Hkv + g) * D;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) {
+                const float kv = h2f(kr[cl * DPL + e]);
+#pragma unroll
+                for (int h = 0; h < GQ; h++) acc[h] = __builtin_fmaf(qv[h][e], kv, acc[h]);
+            }
+        } else {
+            const uint32_t w4[4] = {(uint32_t)kch[i].x, (uint32_t)kch[i].y, (uint32_t)kch[i].z, (uint32_t)kch[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (HYBRID) {
+                    // code + 128 as an unsigned byte; 128 * sum(q) comes off below
+                    const uint32_t u = w4[j] ^ 0x80808080u;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float kv = (float)((u >> (8 * e)) & 0xFFu);
+#pragma unroll
+                        for (int h = 0; h < GQ; h++) acc[h] = __builtin_fmaf(qv[h][j * 4 + e], kv, acc[h]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const float kv = h2f((uint16_t)(w4[j] >> (16 * e)));
+#pragma unroll
+                        for (int h = 0; h < GQ; h++) acc[h] = __builtin_fmaf(qv[h][j * 2 + e], kv, acc[h]);
+                    }
+                }
+            }
+            if (HYBRID)
+#pragma unroll
+                for (int h = 0; h < GQ; h++) acc[h] = __builtin_fmaf(-128.0f, qsum[h], acc[h]);
+        }
+        // the row's CPL partial dots
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            acc[h] = group_sum<CPL>(acc[h]);
+            const bool cached = HYBRID && kp < cache_len;
+            sc[i][h] = valid ? acc[h] * (cached ? ksc[i] : 1.0f) * a.scale : -__builtin_inff();
+        }
+    }
+
+    // ---- 4. workgroup max and weights
+    constexpr float LOG2E = 1.4426950408889634f;
+    float wm[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        float m = sc[0][h];
+#pragma unroll
+        for (int i = 1; i < NI; i++) m = __builtin_fmaxf(m, sc[i][h]);
+        wm[h] = wave_max_u(m);
+        if (lane == 0) redm[h][wid] = wm[h];
+    }
+    __syncthreads();
+    float M[GQ];
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        M[h] = redm[h][0];
+#pragma unroll
+        for (int w = 1; w < FA_WAVES; w++) M[h] = __builtin_fmaxf(M[h], redm[h][w]);
+    }
+    float p[NI][GQ];
+    if (HYBRID) {
+#pragma unroll
+        for (int i = 0; i < NI; i++)
+#pragma unroll
+            for (int h = 0; h < GQ; h++)
+                p[i][h] = sc[i][h] > -__builtin_inff() ? fast_exp2((sc[i][h] - M[h]) * LOG2E) : 0.0f;
+    } else {
+        // the reference weighs the first floor(n/4)*4 keys of each 32-key
+        // block (blocks from kv_start, n = min(32, Skv - block start)) by its
+        // second-order 2^x polynomial relative to the block max, the rest by
+        // exp (kernel_attention.cpp:160-204).  A wave holds exactly one
+        // block here (32 keys from a block boundary).
+        static_assert(HYBRID || FA_KPW == 32, "one 32-key block per wave");
+        const int bpoly = (int)(min((size_t)32, Skv > wk0 ? Skv - wk0 : (size_t)0) / 4) * 4;
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            const float bm = wm[h];
+            const float bscale = bm > -__builtin_inff() ? fast_exp2((bm - M[h]) * LOG2E) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int in_blk = i * R + rl;
+                const float sv = sc[i][h];
+                float w = 0.0f;
+                if (sv > -__builtin_inff())
+                    w = in_blk < bpoly ? poly_exp_weight(sv, bm) : fast_exp2((sv - bm) * LOG2E);
+                p[i][h] = w * bscale;
+            }
+        }
+    }
+    // block sum of the weights: every key counted once (by its cl == 0 lane)
+#pragma unroll
+    for (int h = 0; h < GQ; h++) {
+        float t = 0.0f;
+        if (cl == 0)
+#pragma unroll
+            for (int i = 0; i < NI; i++) t += p[i][h];
+        t = wave_sum_u(t);
+        if (lane == 0) reds[h][wid] = t;
+    }
+
+    // ---- 5. values: av[h][e] over the lane's keys; the rows of every wave
+    // are summed through LDS
+    float av[GQ][DPL];
+#pragma unroll
+    for (int h = 0; h < GQ; h++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) av[h][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+        const size_t kp = wk0 + (size_t)i * R + rl;
+        float vv[DPL];
+        float f = 1.0f;
+        if (HYBRID && has_keys && kp < k1 && kp >= cache_len) {
+            const uint16_t* vr = PREP ? a.v_raw + ((size_t)b * a.Hkv + g) * D
+                                      : a.v + (((size_t)b * a.new_len + (kp - cache_len)) * a.Hkv + g) * D;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) vv[e] = h2f(vr[cl * DPL + e]);
+        } else {
+            const uint32_t w4[4] = {(uint32_t)vch[i].x, (uint32_t)vch[i].y, (uint32_t)vch[i].z, (uint32_t)vch[i].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (HYBRID) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) vv[j * 4 + e] = (float)(int8_t)(w4[j] >> (8 * e));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 2; e++) vv[j * 2 + e] = h2f((uint16_t)(w4[j] >> (16 * e)));
+                }
+            }
+            if (HYBRID) f = vsc[i];
+        }
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            const float w = p[i][h] * f;
+#pragma unroll
+            for (int e = 0; e < DPL; e++) av[h][e] = __builtin_fmaf(w, vv[e], av[h][e]);
+        }
+    }
+    // rows of one 16-lane group first (DPP rotations keep the dims aligned:
+    // lanes i, i + CPL, ... of a row share their dims), then
+    // vsum[wave][row16][h][d] from the first CPL lanes of each 16-lane row
+#pragma unroll
+    for (int h = 0; h < GQ; h++)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) {
+            float v = av[h][e];
+            if (CPL == 4) v += dpp_f<DPP_ROR4>(v);
+            if (CPL <= 8) v += dpp_f<DPP_ROR8>(v);
+            av[h][e] = v;
+        }
+    if ((lane & 15) < CPL)
+#pragma unroll
+        for (int h = 0; h < GQ; h++) {
+            float* dst = &vsum[((wid * 4 + (lane >> 4)) * GQ + h) * D + cl * DPL];
+#pragma unroll
+            for (int e = 0; e < DPL; e += 4)
+                *reinterpret_cast<f32x4*>(dst + e) = (f32x4){av[h][e], av[h][e + 1], av[h][e + 2], av[h][e + 3]};
+        }
+    __syncthreads();
+
+    // ---- 6. this split's partial: (M, sum, acc[d]) per query head, written
+    // with agent-scope stores (visible to the combining workgroup on any XCD
+    // without a cache writeback)
+    constexpr int PS = D + 4;                     // floats per (split, head): acc[D], M, sum, 2 pad
+    float* part = a.part + ((size_t)bg * a.nsplit + s) * GQ * PS;
+    for (int i = tid; i < GQ * D; i += FA_THREADS) {
+        const int h = i / D, dm = i % D;
+        float t = 0.0f;
+#pragma unroll
+        for (int r = 0; r < FA_WAVES * 4; r++) t += vsum[(r * GQ + h) * D + dm];
+        agent_store(part + h * PS + dm, t);
+    }
+    if (tid < GQ) {
+        float l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < FA_WAVES; w++) l += reds[tid][w];
+        agent_store(part + tid * PS + D, has_keys ? M[tid] : -__builtin_inff());
+        agent_store(part + tid * PS + D + 1, l);
+    }
+    // every store of the workgroup has completed before the count goes up
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(a.cnt + bg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(a.nsplit - 1);
+    __syncthreads();
+    if (!last) return;
+
+    // ---- 7. the last workgroup of this KV head combines the splits that
+    // hold keys (nact <= FA_MAX_SPLITS, checked on the host), with agent-scope
+    // loads.  Thread t owns four consecutive outputs (group t % NG) and the
+    // splits t / NG, t / NG + TPG, ...: all of its 16-byte column loads and
+    // the splits' (M, sum) pairs are issued together; one wave per query head
+    // then forms M* and the weights e^(M_s - M*); the TPG partial sums of a
+    // group meet in LDS.
+    const int nact = kv_end > kv_start ? (int)((kv_end - kv_start + FA_KPB - 1) / FA_KPB) : 0;
+    const float* pb = a.part + (size_t)bg * a.nsplit * GQ * PS;
+    constexpr int NG = GQ * D / 4;                // float4 output groups
+    constexpr int TPG = FA_THREADS / NG;          // threads (split lanes) per group
+    constexpr int NCH = 96 / TPG > 0 ? (96 / TPG < 24 ? 96 / TPG : 24) : 1;   // loads in flight per thread
+    static_assert(FA_THREADS % NG == 0, "output groups");
+    const int gi = tid % NG, sj = tid / NG;
+    const int gh = (gi * 4) / D, gd = (gi * 4) % D;
+    f32x4 cv[NCH];
+#pragma unroll
+    for (int u = 0; u < NCH; u++) {
+        const int t = sj + u * TPG;
+        cv[u] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        if (t < nact)
+            cv[u] = agent_load4(pb + ((size_t)t * GQ + gh) * PS + gd);
+    }
+    for (int i = tid; i < nact * GQ; i += FA_THREADS) {
+        const float* pt = pb + (size_t)i * PS + D;
+        ms[i] = agent_load(pt);
+        ls[i] = agent_load(pt + 1);
+    }
+    __syncthreads();
+    if (wid < GQ) {
+        float mx = -__builtin_inff();
+        for (int t = lane; t < nact; t += 64) mx = __builtin_fmaxf(mx, ms[t * GQ + wid]);
+        mx = wave_max_u(mx);
+        float L = 0.0f;
+        for (int t = lane; t < nact; t += 64) {
+            const float m = ms[t * GQ + wid];
+            const float e = m > -__builtin_inff() ? fast_exp2((m - mx) * LOG2E) : 0.0f;
+            ms[t * GQ + wid] = e;
+            L = __builtin_fmaf(e, ls[t * GQ + wid], L);
+        }
+        L = wave_sum_u(L);
+        if (lane == 0) Ltot[wid] = L;
+    }
+    __syncthreads();
+    f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int u = 0; u < NCH; u++) {
+        const int t = sj + u * TPG;
+        if (t < nact) {
+            const float e = ms[t * GQ + gh];
+            acc.x = __builtin_fmaf(e, cv[u].x, acc.x);
+            acc.y = __builtin_fmaf(e, cv[u].y, acc.y);
+            acc.z = __builtin_fmaf(e, cv[u].z, acc.z);
+            acc.w = __builtin_fmaf(e, cv[u].w, acc.w);
+        }
+    }
+    for (int t = sj + NCH * TPG; t < nact; t += TPG) {
+        const f32x4 v = agent_load4(pb + ((size_t)t * GQ + gh) * PS + gd);
+        const float e = ms[t * GQ + gh];
+        acc.x = __builtin_fmaf(e, v.x, acc.x);
+        acc.y = __builtin_fmaf(e, v.y, acc.y);
+        acc.z = __builtin_fmaf(e, v.z, acc.z);
+        acc.w = __builtin_fmaf(e, v.w, acc.w);
+    }
+    f32x4* red4 = reinterpret_cast<f32x4*>(vsum);   // [TPG][NG]
+    red4[sj * NG + gi] = acc;
+    __syncthreads();
+    if (tid < NG) {
+        f32x4 t4 = red4[tid];
+        for (int j2 = 1; j2 < TPG; j2++) {
+            const f32x4 v = red4[j2 * NG + tid];
+            t4.x += v.x; t4.y += v.y; t4.z += v.z; t4.w += v.w;
+        }
+        const float L = Ltot[gh];
+        uint16_t* out = a.o + ((size_t)b * a.Hq + g * GQ + gh) * D + gd;
+        const uint32_t lo = (uint32_t)f2h(L > 0.0f ? t4.x / L : 0.0f) | ((uint32_t)f2h(L > 0.0f ? t4.y / L : 0.0f) << 16);
+        const uint32_t hi = (uint32_t)f2h(L > 0.0f ? t4.z / L : 0.0f) | ((uint32_t)f2h(L > 0.0f ? t4.w / L : 0.0f) << 16);
+        *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
+    }
+    if (tid == 0) __hip_atomic_store(a.cnt + bg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------ per-(device, stream) workspace
+struct FastWs {
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    size_t part_floats = 0, ncnt = 0;
+};
+static std::mutex g_fast_mu;
+static std::map<std::pair<int, void*>, FastWs> g_fast_ws;
+
+static int fast_ws(void* stream, size_t part_floats, size_t ncnt, FastWs* out) {
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_fast_mu);
+    FastWs& w = g_fast_ws[std::make_pair(dev, stream)];
+    if (w.part_floats < part_floats) {
+        // the previous buffers are kept: kernels queued on the stream may use them
+        void* p = nullptr;
+        CH_HIP(hipMalloc(&p, part_floats * sizeof(float)));
+        w.part = static_cast<float*>(p);
+        w.part_floats = part_floats;
+    }
+    if (w.ncnt < ncnt) {
+        void* p = nullptr;
+        CH_HIP(hipMalloc(&p, ncnt * sizeof(uint32_t)));
+        CH_HIP(hipMemsetAsync(p, 0, ncnt * sizeof(uint32_t), as_stream(stream)));
+        w.cnt = static_cast<uint32_t*>(p);
+        w.ncnt = ncnt;
+    }
+    *out = w;
+    return CACTUS_HIP_OK;
+}
+
+size_t fast_attention_splits(size_t keys, bool hybrid) {
+    const size_t kpb = hybrid ? fa_kpb<true>() : fa_kpb<false>();
+    return keys == 0 ? 1 : (keys + kpb - 1) / kpb;
+}
+
+template <bool HYBRID, bool PREP>
+static int launch_fast(const FastArgs& a, int d, int gq, hipStream_t st) {
+    const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * a.Hkv));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(FA_THREADS), 0, st, a);
+        return check_launch("attention (split-K)");
+    };
+#define FA_CASE(D_, G_) if (d == D_ && gq == G_) return go(attn_splitk_kernel<HYBRID, PREP, D_, G_>);
+    FA_CASE(128, 2) FA_CASE(128, 1) FA_CASE(128, 4) FA_CASE(64, 2) FA_CASE(64, 1) FA_CASE(64, 4)
+#undef FA_CASE
+    return fail(CACTUS_HIP_EUNSUPPORTED, "attention (split-K): head_dim 64/128 with 1, 2 or 4 query heads per KV head");
+}
+
+bool fast_attention_supported(size_t seq_len, size_t d, size_t gq, const void* mask) {
+    return seq_len == 1 && !mask && (d == 64 || d == 128) && (gq == 1 || gq == 2 || gq == 4);
+}
+
+// the combine holds every split's (M, sum) in LDS: at most FA_MAX_SPLITS splits
+constexpr size_t FA_MAX_KEYS_F16 = (size_t)FA_MAX_SPLITS * fa_kpb<false>();    // 65536
+constexpr size_t FA_MAX_KEYS_HYBRID = (size_t)FA_MAX_SPLITS * fa_kpb<true>();  // 32768
+
+int attention_fast_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, size_t B,
+                       size_t Skv, size_t Hq, size_t Hkv, size_t d, float scale, size_t pos_off, size_t window,
+                       void* stream) {
+    FastArgs a{};
+    a.q = q; a.k = k; a.v = v; a.o = o;
+    a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.nqg = 1;
+    a.Skv = Skv; a.cache_len = 0; a.new_len = 0; a.pos_off = pos_off; a.window = window; a.scale = scale;
+    size_t start = 0, end = Skv;
+    if (window > 0 && window < Skv && pos_off > window) start = pos_off - window;
+    if (pos_off + 1 < end) end = pos_off + 1;
+    a.nsplit = (int)fast_attention_splits(end > start ? end - start : 0, false);
+    FastWs w;
+    int rc = fast_ws(stream, B * Hkv * (size_t)a.nsplit * (Hq / Hkv) * (d + 4), B * Hkv, &w);
+    if (rc) return rc;
+    a.part = w.part; a.cnt = w.cnt;
+    return launch_fast<false, false>(a, (int)d, (int)(Hq / Hkv), as_stream(stream));
+}
+
+int attention_fast_hybrid(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+                          const uint16_t* k_new, const uint16_t* v_new, uint16_t* o, size_t B, size_t cache_len,
+                          size_t new_len, size_t Hq, size_t Hkv, size_t d, float scale, size_t pos_off, size_t qgs,
+                          void* stream) {
+    FastArgs a{};
+    a.q = q; a.k = k_new; a.v = v_new; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.o = o;
+    a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.nqg = (int)((d + qgs - 1) / qgs);
+    a.Skv = cache_len + new_len; a.cache_len = cache_len; a.new_len = new_len; a.pos_off = pos_off;
+    a.scale = scale;
+    size_t end = a.Skv;
+    if (pos_off + 1 < end) end = pos_off + 1;
+    a.nsplit = (int)fast_attention_splits(end, true);
+    FastWs w;
+    int rc = fast_ws(stream, B * Hkv * (size_t)a.nsplit * (Hq / Hkv) * (d + 4), B * Hkv, &w);
+    if (rc) return rc;
+    a.part = w.part; a.cnt = w.cnt;
+    return launch_fast<true, false>(a, (int)d, (int)(Hq / Hkv), as_stream(stream));
+}
+
+}  // namespace cactus_hip
+
+using namespace cactus_hip;
+
+extern "C" {
+
+int cactus_hip_attention_f16_fast(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                                  size_t batch, size_t seq_len, size_t kv_seq_len, size_t num_q_heads,
+                                  size_t num_kv_heads, size_t head_dim, float scale, const uint16_t* mask,
+                                  size_t position_offset, size_t window_size, int is_causal, void* stream) {
+    if (batch == 0 || seq_len == 0 || num_q_heads == 0 || head_dim == 0) return CACTUS_HIP_OK;
+    const bool fast = num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && is_causal &&
+                      fast_attention_supported(seq_len, head_dim, num_q_heads / num_kv_heads, mask) &&
+                      batch * num_kv_heads < 65536 && kv_seq_len <= FA_MAX_KEYS_F16 && ((uintptr_t)k & 15) == 0;
+    if (!fast)
+        return cactus_hip_attention_f16(q, k, v, o, batch, seq_len, kv_seq_len, num_q_heads, num_kv_heads,
+                                        head_dim, scale, mask, position_offset, window_size, is_causal, stream);
+    CH_REQUIRE(q && o && (kv_seq_len == 0 || (k && v)), "attention_f16_fast: null pointer");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)head_dim);
+    return attention_fast_f16(q, k, v, o, batch, kv_seq_len, num_q_heads, num_kv_heads, head_dim, scale,
+                              position_offset, window_size, stream);
+}
+
+int cactus_hip_attention_hybrid_int8_fp16_fast(const uint16_t* q, const int8_t* k_cached, const int8_t* v_cached,
+                                               const float* k_scales, const float* v_scales, const uint16_t* k_new,
+                                               const uint16_t* v_new, uint16_t* o, size_t batch, size_t seq_len,
+                                               size_t cache_len, size_t new_len, size_t num_q_heads,
+                                               size_t num_kv_heads, size_t head_dim, float scale,
+                                               size_t position_offset, int is_causal, size_t quant_group_size,
+                                               void* stream) {
+    if (batch == 0 || seq_len == 0 || num_q_heads == 0 || head_dim == 0) return CACTUS_HIP_OK;
+    const bool fast = num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && is_causal &&
+                      fast_attention_supported(seq_len, head_dim, num_q_heads / num_kv_heads, nullptr) &&
+                      quant_group_size >= head_dim && batch * num_kv_heads < 65536 &&
+                      cache_len + new_len <= FA_MAX_KEYS_HYBRID &&
+                      ((uintptr_t)k_cached & 15) == 0 && ((uintptr_t)v_cached & 15) == 0;
+    if (!fast)
+        return cactus_hip_attention_hybrid_int8_fp16(q, k_cached, v_cached, k_scales, v_scales, k_new, v_new, o,
+                                                     batch, seq_len, cache_len, new_len, num_q_heads,
+                                                     num_kv_heads, head_dim, scale, position_offset, is_causal,
+                                                     quant_group_size, stream);
+    CH_REQUIRE(q && o, "attention_hybrid_fast: null pointer");
+    CH_REQUIRE(cache_len == 0 || (k_cached && v_cached && k_scales && v_scales),
+               "attention_hybrid_fast: null cache pointer");
+    CH_REQUIRE(new_len == 0 || (k_new && v_new), "attention_hybrid_fast: null new K/V pointer");
+    if (scale == 0.0f) scale = 1.0f / sqrtf((float)head_dim);
+    return attention_fast_hybrid(q, k_cached, v_cached, k_scales, v_scales, k_new, v_new, o, batch, cache_len,
+                                 new_len, num_q_heads, num_kv_heads, head_dim, scale, position_offset,
+                                 quant_group_size, stream);
+}
+
+size_t cactus_hip_decode_attention_fast_workspace(size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                                  size_t max_cache) {
+    if (num_kv_heads == 0) return 0;
+    const size_t nsplit = fast_attention_splits(max_cache + 1, true);
+    return 256 + num_kv_heads * nsplit * (num_q_heads / num_kv_heads) * (head_dim + 4) * sizeof(float);
+}
+
+int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                          const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                          size_t num_q_heads, size_t num_kv_heads, size_t head_dim, float theta,
+                                          const uint32_t* state, int8_t* k_cache, int8_t* v_cache,
+                                          float* k_scales, float* v_scales, size_t max_cache, float* v_shadow,
+                                          float scale, uint16_t* o, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
+    CH_REQUIRE(q_raw && k_raw && v_raw && q_norm && k_norm && state && k_cache && v_cache && k_scales &&
+               v_scales && o && workspace, "decode_prep_attention_fast: null pointer");
+    CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && num_kv_heads <= 64,
+               "decode_prep_attention_fast: bad head counts");
+    CH_REQUIRE(fast_attention_supported(1, head_dim, num_q_heads / num_kv_heads, nullptr),
+               "decode_prep_attention_fast: head_dim 64 or 128 with 1, 2 or 4 query heads per KV head");
+    CH_REQUIRE(max_cache + 1 <= FA_MAX_KEYS_HYBRID, "decode_prep_attention_fast: cache longer than 32767 tokens");
+    CH_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
+               "decode_prep_attention_fast: misaligned cache or workspace");
+    CH_REQUIRE(workspace_bytes >= cactus_hip_decode_attention_fast_workspace(num_q_heads, num_kv_heads, head_dim,
+                                                                             max_cache),
+               "decode_prep_attention_fast: workspace too small");
+    const RopeTable* t = nullptr;
+    int rc = rope_table(max_cache + 1, head_dim, theta, &t);
+    if (rc) return rc;
+    FastArgs a{};
+    a.o = o;
+    a.B = 1; a.Hq = (int)num_q_heads; a.Hkv = (int)num_kv_heads; a.nqg = 1;
+    a.kc = k_cache; a.vc = v_cache; a.ks = k_scales; a.vs = v_scales;
+    a.cache_len = max_cache; a.new_len = 1; a.Skv = max_cache + 1; a.pos_off = max_cache;
+    a.scale = scale; a.dyn = state;
+    a.q_raw = q_raw; a.k_raw = k_raw; a.v_raw = v_raw; a.q_norm = q_norm; a.k_norm = k_norm;
+    a.cos_t = t->cos_d; a.sin_t = t->sin_d; a.eps = eps; a.table_pos = (uint32_t)t->npos;
+    a.kc_w = k_cache; a.vc_w = v_cache; a.ks_w = k_scales; a.vs_w = v_scales; a.vsh = v_shadow;
+    a.sh_ntile = (max_cache + 63) / 64; a.max_cache = max_cache;
+    a.nsplit = (int)fast_attention_splits(max_cache + 1, true);
+    a.cnt = static_cast<uint32_t*>(workspace);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+    return launch_fast<true, true>(a, (int)head_dim, (int)(num_q_heads / num_kv_heads), as_stream(stream));
+}
+
+}  // extern "C"

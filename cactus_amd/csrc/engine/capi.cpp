@@ -282,6 +282,10 @@ int cactus_qwen_set_decode_mode(void* model, int mode) {
     return guarded([&] { static_cast<QwenModel*>(model)->set_decode_mode(mode); });
 }
 
+int cactus_qwen_set_attention_mode(void* model, int mode) {
+    return guarded([&] { static_cast<QwenModel*>(model)->set_attention_mode(mode); });
+}
+
 int cactus_qwen_set_kv_window(void* model, size_t window, size_t sink) {
     return guarded([&] { static_cast<QwenModel*>(model)->set_kv_window(window, sink); });
 }

@@ -37,6 +37,9 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     lm_scratch_ = DevBuf(256 + 8 * blocks);
     logits_ = DevBuf((size_t)c.vocab * 2);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
+    // split-K attention workspace (tolerance mode): counters zeroed once
+    attn_ws_ = DevBuf(cactus_hip_decode_attention_fast_workspace(c.heads, c.kv_heads, hd, m.cache().slots));
+    check_hip(cactus_hip_memset(attn_ws_.ptr, 0, attn_ws_.bytes, m.stream()), "memset");
     // the decode entry points ask for max_cache + 1 positions, max_cache
     // being the cache's slot count (context + 1)
     rope_pos_ = m.cache().slots + 1;
@@ -71,6 +74,12 @@ FusedDecoder::~FusedDecoder() {
     if (graph_) cactus_hip_graph_destroy(graph_);
 }
 
+void FusedDecoder::invalidate() {
+    check_hip(cactus_hip_stream_sync(m_.stream()), "sync");
+    if (graph_) cactus_hip_graph_destroy(graph_);
+    graph_ = nullptr;
+}
+
 void FusedDecoder::enqueue() {
     const cactus_qwen_config& c = m_.config();
     void* st = m_.stream();
@@ -84,6 +93,7 @@ void FusedDecoder::enqueue() {
     // allows (one kernel fewer per layer)
     const size_t gqa = c.heads / c.kv_heads;
     const bool fused_prep = (hd == 64 || hd == 128) && (gqa == 1 || gqa == 2);
+    const bool tolerance = m_.attention_mode() == 1 && (hd == 64 || hd == 128) && (gqa == 1 || gqa == 2 || gqa == 4);
     check_hip(cactus_hip_decode_embed(u16(m_.embedding()), state, h, H, c.vocab, st), "decode_embed");
     for (uint32_t l = 0; l < c.num_layers; l++) {
         const QwenLayer& L = m_.layer(l);
@@ -92,7 +102,15 @@ void FusedDecoder::enqueue() {
                                         k_raw_.as<uint16_t>(), nkv, L.v_w.as<int8_t>(), u16(L.v_s),
                                         v_raw_.as<uint16_t>(), nkv, st),
                   "decode_qkv");
-        if (fused_prep) {
+        if (tolerance) {
+            check_hip(cactus_hip_decode_prep_attention_fast(
+                          q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(), u16(L.q_norm),
+                          u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd, c.rope_theta, state, kv.keys_mut(l),
+                          kv.values_mut(l), kv.key_scales_mut(l), kv.value_scales_mut(l), kv.slots,
+                          kv.value_products(l), m_.attention_scale(), attn_.as<uint16_t>(), attn_ws_.ptr,
+                          attn_ws_.bytes, st),
+                      "decode_prep_attention_fast");
+        } else if (fused_prep) {
             check_hip(cactus_hip_decode_prep_attention(
                           q_raw_.as<uint16_t>(), k_raw_.as<uint16_t>(), v_raw_.as<uint16_t>(), u16(L.q_norm),
                           u16(L.k_norm), c.eps, c.heads, c.kv_heads, hd, c.rope_theta, state, kv.keys_mut(l),
@@ -204,6 +222,14 @@ uint32_t FusedDecoder::step(uint32_t token) {
 uint32_t fused_decode(QwenModel& m, FusedDecoder& f, uint32_t token) {
     (void)m;
     return f.step(token);
+}
+
+void QwenModel::set_attention_mode(int mode) {
+    if (mode != 0 && mode != 1) throw std::runtime_error("attention mode must be 0 (exact) or 1 (tolerance)");
+    check_hip(cactus_hip_stream_sync(stream_), "sync");
+    attention_mode_ = mode;
+    graph_->set_attention_tolerance(mode == 1);
+    if (fused_) fused_->invalidate();
 }
 
 void QwenModel::set_decode_mode(int mode) {

@@ -98,6 +98,10 @@ public:
     // n greedy steps from `token` (decode mode 1 keeps them on the device)
     void decode_many(uint32_t token, size_t n, uint32_t* out);
     void set_decode_mode(int mode);
+    // 0: exact attention (bit-identical to the reference); 1: tolerance-mode
+    // split-K attention for decode-shaped queries (prefill stays exact)
+    void set_attention_mode(int mode);
+    int attention_mode() const { return attention_mode_; }
     void set_kv_window(size_t window, size_t sink);
     // Model::decode's temperature / top_p / top_k (engine_model.cpp:221-250);
     // all zero = greedy.  seed 0 = the reference's clock seed per step
@@ -143,6 +147,7 @@ private:
     size_t last_hidden_ = SIZE_MAX, last_logits_ = SIZE_MAX;
     bool fused_logits_ = false;   // the last step was a fused one (logits in fused_->logits())
     int decode_mode_ = 0;
+    int attention_mode_ = 0;
     float temperature_ = 0.0f, top_p_ = 0.0f;
     size_t top_k_ = 0, seed_ = 0;
     std::unique_ptr<FusedDecoder> fused_;

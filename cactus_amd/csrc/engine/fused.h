@@ -18,6 +18,8 @@ public:
     void run(uint32_t token, size_t n, uint32_t* out);
     // fp16 logits [vocab] of the last step run
     const DevBuf& logits() const { return logits_; }
+    // the captured step no longer matches the model's settings
+    void invalidate();
 
 private:
     void enqueue();            // all launches of one step on the model stream
@@ -28,7 +30,7 @@ private:
     void reserve(size_t positions, size_t steps);
 
     QwenModel& m_;
-    DevBuf state_, h_, q_raw_, k_raw_, v_raw_, q_rot_, k_rot_, attn_, mlp_, tokens_, lm_scratch_, logits_;
+    DevBuf state_, h_, q_raw_, k_raw_, v_raw_, q_rot_, k_rot_, attn_, mlp_, tokens_, lm_scratch_, logits_, attn_ws_;
     size_t max_steps_ = 0;
     size_t rope_pos_ = 0;      // positions the RoPE tables hold
     void* graph_ = nullptr;

@@ -193,6 +193,7 @@ size_t CactusGraph::attention(size_t q, size_t k, size_t v, float scale, size_t 
     p.position_offset = position_offset;
     p.window_size = window_size;
     p.is_causal = is_causal;
+    p.tolerance = attention_tolerance_;
     return add_node(OpType::ATTENTION, {q, k, v}, node(q).out.shape, Precision::FP16, p);
 }
 
@@ -210,6 +211,7 @@ size_t CactusGraph::attention_int8_hybrid(size_t q, size_t k_new, size_t v_new, 
     p.cache_seq_len = cache_len;
     p.num_kv_heads = num_kv_heads;
     p.head_dim = head_dim;
+    p.tolerance = attention_tolerance_;
     return add_node(OpType::ATTENTION_INT8_HYBRID, {q, k_new, v_new}, node(q).out.shape,
                     Precision::FP16, p);
 }
@@ -573,17 +575,18 @@ void CactusGraph::compute(GraphNode& n) {
             const auto& q = in(0).shape;
             const auto& k = in(1).shape;
             if (q.size() < 4) throw std::runtime_error("Attention operation requires 4D tensors");
-            check_hip(cactus_hip_attention_f16(u16(in(0).data), u16(in(1).data), u16(in(2).data), out16,
-                                               q[0], q[1], k[1], q[2], k[2], q[3], n.params.scale, nullptr,
-                                               n.params.position_offset, n.params.window_size,
-                                               n.params.is_causal ? 1 : 0, st),
+            check_hip((n.params.tolerance ? cactus_hip_attention_f16_fast : cactus_hip_attention_f16)(
+                          u16(in(0).data), u16(in(1).data), u16(in(2).data), out16, q[0], q[1], k[1], q[2], k[2],
+                          q[3], n.params.scale, nullptr, n.params.position_offset, n.params.window_size,
+                          n.params.is_causal ? 1 : 0, st),
                       "attention");
             return;
         }
         case OpType::ATTENTION_INT8_HYBRID: {  // graph_ops_nn.cpp:340-371
             const auto& q = in(0).shape;
             const auto& p = n.params;
-            check_hip(cactus_hip_attention_hybrid_int8_fp16(
+            check_hip((p.tolerance ? cactus_hip_attention_hybrid_int8_fp16_fast
+                                   : cactus_hip_attention_hybrid_int8_fp16)(
                           u16(in(0).data), p.cached_keys_int8, p.cached_values_int8, p.cached_k_scales,
                           p.cached_v_scales, u16(in(1).data), u16(in(2).data), out16, q[0], q[1],
                           p.cache_seq_len, in(1).shape[1], q[2], p.num_kv_heads, p.head_dim, p.scale,

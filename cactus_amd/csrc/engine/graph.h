@@ -103,6 +103,9 @@ struct OpParams {
     size_t cache_seq_len = 0;
     size_t num_kv_heads = 0;
     size_t head_dim = 0;
+    // attention nodes: the tolerance-mode split-K kernels for decode-shaped
+    // queries (cactus_hip_attention_*_fast) instead of the exact ones
+    bool tolerance = false;
 };
 
 struct GraphNode {
@@ -116,6 +119,8 @@ struct GraphNode {
 class CactusGraph {
 public:
     explicit CactusGraph(void* stream = nullptr);
+    // attention nodes built from now on run the tolerance-mode kernels
+    void set_attention_tolerance(bool on) { attention_tolerance_ = on; }
     ~CactusGraph();
     CactusGraph(const CactusGraph&) = delete;
     CactusGraph& operator=(const CactusGraph&) = delete;
@@ -181,6 +186,7 @@ public:
     size_t node_count() const { return nodes_.size(); }
 
 private:
+    bool attention_tolerance_ = false;
     size_t add_node(OpType op, const std::vector<size_t>& inputs, const std::vector<size_t>& shape,
                     Precision precision, const OpParams& params = {});
     GraphNode& node(size_t id);

@@ -120,6 +120,11 @@ class Qwen:
     def set_decode_mode(self, mode: int):
         self._check(self.lib.cactus_qwen_set_decode_mode(self.h, mode))
 
+    def set_attention_mode(self, mode: int):
+        """0: exact attention (bit-identical); 1: tolerance-mode split-K
+        attention for decode steps."""
+        self._check(self.lib.cactus_qwen_set_attention_mode(self.h, mode))
+
     def reset(self):
         self._check(self.lib.cactus_qwen_reset(self.h))
 

@@ -84,6 +84,13 @@ int cactus_qwen_reset(void* model);
  * the reference's structure), 1 = fused per-layer kernels replayed as one
  * HIP graph per token.  Both are bit-identical. */
 int cactus_qwen_set_decode_mode(void* model, int mode);
+/* Selects the attention arithmetic: 0 = exact (the reference's operation
+ * order, bit-identical; the default), 1 = tolerance mode: decode-shaped
+ * attention (one query row) runs the split-K kernels of
+ * cactus_hip_attention_*_fast / cactus_hip_decode_prep_attention_fast,
+ * within 1e-3 + 1e-2 |ref| of the reference per fp16 output; prefill chunks
+ * stay exact.  Applies to both decode modes. */
+int cactus_qwen_set_attention_mode(void* model, int mode);
 /* KVCache::set_window_size (engine/engine_cache.cpp:25-46): keep at most
  * `window` cached tokens -- the first `sink` of the sequence and the most
  * recent window - sink (update_from_graph, :103-330) -- while positions keep

@@ -174,7 +174,8 @@ int cactus_hip_attention_f16(const uint16_t* q, const uint16_t* k, const uint16_
                              size_t window_size, int is_causal, void* stream);
 /* cactus_attention_hybrid_int8_fp16 (kernel/kernel.h:100,
  * kernel_attention.cpp:257-482): positions < cache_len read the INT8 cache
- * (k_cached/v_cached [B][cache_len][Hkv][d], scales [B][cache_len][Hkv][G]),
+ * (k_cached/v_cached [B][cache_len][Hkv][d], scales [cache_len][Hkv][G] --
+ * one scale table for every batch row, as kernel_attention.cpp:353,424 index it),
  * later positions read k_new/v_new [B][new_len][Hkv][d] fp16. expf weights. */
 int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cached,
                                           const int8_t* v_cached, const float* k_scales,
@@ -184,6 +185,28 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
                                           size_t num_q_heads, size_t num_kv_heads,
                                           size_t head_dim, float scale, size_t position_offset,
                                           int is_causal, size_t quant_group_size, void* stream);
+/* Tolerance-mode variants of the two attention entry points above (same
+ * arguments and layouts; no reference counterpart of their own).  A decode
+ * query (seq_len 1, causal, no mask, head_dim 64 or 128, 1, 2 or 4 query
+ * heads per KV head; hybrid: quant_group_size >= head_dim) runs as a split-K
+ * reduction over 256-key splits with one combine, so the launch is bound by
+ * HBM bandwidth instead of the reference's sequential value accumulation.
+ * The result is the same softmax attention with a different fp32 summation
+ * order and exponential: within |gpu - ref| <= 1e-3 + 1e-2 |ref| of the
+ * reference, not bit-identical.  Every other shape runs the exact kernels. */
+int cactus_hip_attention_f16_fast(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                  uint16_t* o, size_t batch, size_t seq_len, size_t kv_seq_len,
+                                  size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
+                                  float scale, const uint16_t* mask, size_t position_offset,
+                                  size_t window_size, int is_causal, void* stream);
+int cactus_hip_attention_hybrid_int8_fp16_fast(const uint16_t* q, const int8_t* k_cached,
+                                               const int8_t* v_cached, const float* k_scales,
+                                               const float* v_scales, const uint16_t* k_new,
+                                               const uint16_t* v_new, uint16_t* o, size_t batch,
+                                               size_t seq_len, size_t cache_len, size_t new_len,
+                                               size_t num_q_heads, size_t num_kv_heads,
+                                               size_t head_dim, float scale, size_t position_offset,
+                                               int is_causal, size_t quant_group_size, void* stream);
 
 /* ------------------------------------------------ a7: KV quantization */
 /* No single reference function: an RMSNorm node (cactus_rms_norm_f16,
@@ -404,6 +427,23 @@ int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_ra
                                      const uint32_t* state, int8_t* k_cache, int8_t* v_cache,
                                      float* k_scales, float* v_scales, size_t max_cache,
                                      float* v_shadow, float scale, uint16_t* o, void* stream);
+/* cactus_hip_decode_prep_attention with the tolerance-mode split-K attention
+ * of cactus_hip_attention_hybrid_int8_fp16_fast (the head preparation and
+ * the KV append are bit-identical to the exact form; the attention output
+ * is within tolerance).  workspace: device memory of at least
+ * cactus_hip_decode_attention_fast_workspace(...) bytes, 256-byte aligned,
+ * zeroed once before first use (each launch leaves it reusable); one
+ * workspace per stream. */
+size_t cactus_hip_decode_attention_fast_workspace(size_t num_q_heads, size_t num_kv_heads,
+                                                  size_t head_dim, size_t max_cache);
+int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t* k_raw,
+                                          const uint16_t* v_raw, const uint16_t* q_norm,
+                                          const uint16_t* k_norm, float eps, size_t num_q_heads,
+                                          size_t num_kv_heads, size_t head_dim, float theta,
+                                          const uint32_t* state, int8_t* k_cache, int8_t* v_cache,
+                                          float* k_scales, float* v_scales, size_t max_cache,
+                                          float* v_shadow, float scale, uint16_t* o, void* workspace,
+                                          size_t workspace_bytes, void* stream);
 /* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
  * and advances state; logits_out (fp16 [N], or null) receives the logits
  * row.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */

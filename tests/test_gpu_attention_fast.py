@@ -1,0 +1,156 @@
+"""Tolerance-mode (split-K) decode attention against the oracle.
+
+cactus_hip_attention_f16_fast and cactus_hip_attention_hybrid_int8_fp16_fast
+compute the reference's softmax attention (kernel_attention.cpp:10-255,
+257-482) with a different fp32 summation order, so the bar is the
+tolerance of fp16 outputs: |gpu - ref| <= 1e-3 + 1e-2 |ref| per element,
+written in `close` below.  Shapes: config 4 (16 query / 8 KV heads,
+head_dim 128, 4096 context, RoPE theta 1e6 applied at positions 4095 for
+q and 0..4095 for k) in its FP16 and INT8-cache forms, split edges (1, 255,
+256, 257 keys), GQA 1/2/4, head_dim 64, batch 2, a sliding window, two new
+rows, a causal cut inside the keys, peaked scores, and shapes the fast
+path hands to the exact kernels (prefill rows, head_dim 40, a mask), which
+must then be bit-identical to the oracle.
+"""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from _data import f16
+
+pytestmark = pytest.mark.gpu
+
+ABS_TOL, REL_TOL = 1e-3, 1e-2
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def close(got, ref, what):
+    g = np.asarray(got, np.uint16).view(np.float16).astype(np.float64)
+    r = np.asarray(ref, np.uint16).view(np.float16).astype(np.float64)
+    err = np.abs(g - r)
+    bad = np.flatnonzero(err.ravel() > ABS_TOL + REL_TOL * np.abs(r).ravel())
+    assert bad.size == 0, f"{what}: {bad.size}/{r.size} outside tolerance, first at {bad[:5]}: " \
+                          f"got {g.ravel()[bad[:5]]} ref {r.ravel()[bad[:5]]}"
+    return float(err.max())
+
+
+class Dev:
+    def __init__(self, cm):
+        self.cm = cm
+        self.bufs = []
+
+    def put(self, arr):
+        b = self.cm.DeviceBuffer.from_numpy(np.ascontiguousarray(arr))
+        self.bufs.append(b)
+        return b.ptr
+
+    def empty(self, n):
+        b = self.cm.DeviceBuffer(n)
+        self.bufs.append(b)
+        return b
+
+    def get(self, buf, dtype, shape):
+        self.cm.call("cactus_hip_stream_sync", None)
+        return buf.to_numpy(dtype, shape)
+
+
+@pytest.fixture
+def dev(hip_ready):
+    d = Dev(hip_ready)
+    yield d
+    for b in d.bufs:
+        b.free()
+
+
+def _roped(orc, x, start):
+    """RoPE (theta 1e6) of [B, S, H, d] rows at positions start.. (a9)."""
+    return orc.rope(x, start, 1e6)
+
+
+@pytest.mark.parametrize("B,Skv,Hq,Hkv,d,pos,window,qmul", [
+    (1, 4096, 16, 8, 128, 4095, 0, 1.0),    # config 4, FP16 KV
+    (1, 1, 16, 8, 128, 0, 0, 1.0),
+    (1, 255, 4, 2, 128, 254, 0, 1.0),
+    (1, 256, 4, 4, 64, 255, 0, 1.0),
+    (1, 257, 8, 2, 128, 256, 0, 1.0),
+    (2, 700, 4, 1, 64, 699, 0, 1.0),
+    (1, 1000, 4, 2, 128, 600, 0, 1.0),     # causal cut: keys past the query position
+    (1, 900, 4, 2, 128, 899, 300, 1.0),    # sliding window
+    (1, 3000, 16, 8, 128, 2999, 0, 30.0),  # peaked scores
+])
+def test_attention_f16_fast(dev, orc, B, Skv, Hq, Hkv, d, pos, window, qmul):
+    say("attention_f16_fast", B, Skv, Hq, Hkv, d, pos, window, qmul)
+    rng = np.random.default_rng(Skv + d + Hq)
+    q = _roped(orc, f16(rng.normal(0, 1, (B, 1, Hq, d)) * qmul), pos)
+    k = _roped(orc, f16(rng.normal(0, 1, (B, Skv, Hkv, d))), 0)
+    v = f16(rng.normal(0, 1, (B, Skv, Hkv, d)))
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_f16(q, k, v, scale, pos_off=pos, window=window)
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_attention_f16_fast", dev.put(q), dev.put(k), dev.put(v), o.ptr, B, 1, Skv, Hq, Hkv, d,
+                ctypes.c_float(scale), None, pos, window, 1, None)
+    close(dev.get(o, np.uint16, q.shape), ref, "attention_f16_fast")
+
+
+@pytest.mark.parametrize("B,cache,new,Hq,Hkv,d,qmul", [
+    (1, 4095, 1, 16, 8, 128, 1.0),     # config 4, INT8 cache + the new FP16 row
+    (1, 0, 1, 16, 8, 128, 1.0),
+    (1, 255, 1, 4, 2, 128, 1.0),
+    (1, 256, 1, 4, 1, 64, 1.0),
+    (1, 511, 2, 8, 2, 128, 1.0),       # two new rows
+    (2, 1000, 1, 8, 2, 64, 1.0),
+    (1, 3000, 1, 16, 8, 128, 30.0),    # peaked scores
+])
+def test_attention_hybrid_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul):
+    say("attention_hybrid_fast", B, cache, new, Hq, Hkv, d, qmul)
+    rng = np.random.default_rng(cache + new + d + 7)
+    pos = cache + new - 1
+    kf = _roped(orc, f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d))), 0)
+    vf = f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d)))
+    kc = np.zeros((B, max(cache, 1), Hkv, d), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((B, max(cache, 1), Hkv, 1), np.float32)
+    vs = np.zeros_like(ks)
+    for b in range(B):
+        kc[b], ks[b] = orc.quantize_kv(kf[b])
+        vc[b], vs[b] = orc.quantize_kv(vf[b])
+    # one scale table for every batch row (kernel_attention.cpp:353,424)
+    kc, vc, ks, vs = (np.ascontiguousarray(x[:, :cache]) for x in (kc, vc, ks[:1], vs[:1]))
+    kn = _roped(orc, f16(rng.normal(0, 1, (B, new, Hkv, d))), cache)
+    vn = f16(rng.normal(0, 1, (B, new, Hkv, d)))
+    q = _roped(orc, f16(rng.normal(0, 1, (B, 1, Hq, d)) * qmul), pos)
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_hybrid(q, kc if cache else None, vc if cache else None, ks if cache else None,
+                               vs if cache else None, kn, vn, scale, pos_off=pos)
+    o = dev.empty(q.nbytes)
+    P = (lambda a: dev.put(a) if cache else None)
+    dev.cm.call("cactus_hip_attention_hybrid_int8_fp16_fast", dev.put(q), P(kc), P(vc), P(ks), P(vs), dev.put(kn),
+                dev.put(vn), o.ptr, B, 1, cache, new, Hq, Hkv, d, ctypes.c_float(scale), pos, 1, 128, None)
+    close(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid_fast")
+
+
+def test_fast_entries_hand_other_shapes_to_the_exact_kernels(dev, orc):
+    """Prefill rows, head_dim 40 and a mask run the exact kernels:
+    bit-identical to the oracle."""
+    rng = np.random.default_rng(5)
+    for S, Skv, d, masked in [(8, 64, 128, False), (1, 50, 40, False), (1, 45, 64, True)]:
+        say("attention_f16_fast -> exact", S, Skv, d, masked)
+        q = f16(rng.normal(0, 1, (1, S, 4, d)))
+        k = f16(rng.normal(0, 1, (1, Skv, 2, d)))
+        v = f16(rng.normal(0, 1, (1, Skv, 2, d)))
+        mask = f16((rng.random((1, S, Skv)) > 0.3).astype(np.float32)) if masked else None
+        scale = 1.0 / math.sqrt(d)
+        pos = Skv - S
+        ref = orc.attention_f16(q, k, v, scale, mask=mask, pos_off=pos)
+        o = dev.empty(q.nbytes)
+        dev.cm.call("cactus_hip_attention_f16_fast", dev.put(q), dev.put(k), dev.put(v), o.ptr, 1, S, Skv, 4, 2, d,
+                    ctypes.c_float(scale), dev.put(mask) if masked else None, pos, 0, 1, None)
+        got = dev.get(o, np.uint16, q.shape)
+        assert (got == ref).all(), (S, Skv, d, masked)

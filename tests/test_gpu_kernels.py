@@ -413,6 +413,29 @@ def _attention_hybrid(dev, orc, S, cache, new, Hq, Hkv, d, qmul):
     assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid")
 
 
+def test_attention_hybrid_batch2(dev, orc):
+    """Two batch rows: the codes are per batch row, the scale tables are the
+    first row's for both (kernel_attention.cpp:353,424 index them without
+    the batch)."""
+    say("attention_hybrid batch 2")
+    rng = np.random.default_rng(99)
+    B, S, cache, new, Hq, Hkv, d = 2, 3, 90, 3, 4, 2, 128
+    kc = rng.integers(-127, 128, (B, cache, Hkv, d), dtype=np.int8)
+    vc = rng.integers(-127, 128, (B, cache, Hkv, d), dtype=np.int8)
+    ks = np.abs(rng.normal(0, 0.02, (cache, Hkv, 1))).astype(np.float32)
+    vs = np.abs(rng.normal(0, 0.02, (cache, Hkv, 1))).astype(np.float32)
+    kn = f16(rng.normal(0, 1, (B, new, Hkv, d)))
+    vn = f16(rng.normal(0, 1, (B, new, Hkv, d)))
+    q = f16(rng.normal(0, 1, (B, S, Hq, d)))
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_hybrid(q, kc, vc, ks[None], vs[None], kn, vn, scale, pos_off=cache)
+    o = dev.empty(q.nbytes)
+    dev.cm.call("cactus_hip_attention_hybrid_int8_fp16", dev.put(q), dev.put(kc), dev.put(vc), dev.put(ks),
+                dev.put(vs), dev.put(kn), dev.put(vn), o.ptr, B, S, cache, new, Hq, Hkv, d, ctypes.c_float(scale),
+                cache, 1, 128, None)
+    assert_bits(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid batch 2")
+
+
 def _shadow_ref(vc, vs, cap, d):
     """Product tiles [kvh][slice][tile][64 dims][68 keys] of an INT8 cache
     (numpy float32 products, the rounding the value chain consumes)."""

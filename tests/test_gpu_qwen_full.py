@@ -1,0 +1,102 @@
+"""The full-shape Qwen3-0.6B-architecture run against the oracle's frozen run
+of the same workload (tests/golden/qwen3_0p6b_generate.npz, written by
+tests/golden/make_qwen_golden.py; no oracle at run time).
+
+Workload: 28 layers, hidden 1024, MLP 3072, 16/8 heads, head_dim 128,
+vocab 151936, group-32 INT8 attention projections and packed INT4 MLP,
+FP16 tied embeddings and norms, random-init weights of seed 6, a 4096-token
+prompt (seed 7) prefilled as prompt[:-1] in 256-token chunks, then 128
+greedy steps from prompt[-1] (engine_model.cpp:170-297,
+cactus_complete.cpp:196-204) -- the run bench.py times.
+
+Required bit for bit, in decode mode 0 (node graph) and mode 1 (fused
+kernels replayed as a HIP graph): every token id, every step's fp16 logits
+row (SHA-256), every layer's final INT8 KV cache (SHA-256) and, in mode 0,
+the last final hidden state.  Mode 1 is also run through generate(), the
+bench's own path (all 128 steps queued on the device with no host round
+trip).  The weights make 128 distinct ids (a CPU test checks the fixture),
+so token identity is not one repeated id.
+"""
+from __future__ import annotations
+
+import hashlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE / "golden"))
+
+pytestmark = pytest.mark.gpu
+
+FIXTURE = HERE / "golden" / "qwen3_0p6b_generate.npz"
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def sha(*arrays) -> bytes:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.digest()
+
+
+@pytest.fixture(scope="module")
+def full():
+    import cactus_amd
+    from cactus_amd.engine import Qwen
+    from make_qwen_golden import WEIGHT_SEED, workload
+    cactus_amd.call("cactus_hip_init", 0)
+    fx = dict(np.load(FIXTURE))
+    cfg, prompt = workload()
+    say("qwen3-0.6b full shape: create (seed 6)")
+    m = Qwen(cfg, seed=WEIGHT_SEED)
+    yield m, fx, cfg, prompt
+    m.close()
+
+
+def _first_diff(fx, step, lg):
+    ids = fx["top16_ids"][step]
+    return {"step": step, "oracle_top_ids": ids[:4].tolist(), "oracle_top_bits": fx["top16_bits"][step][:4].tolist(),
+            "gpu_bits_at_those_ids": lg[ids[:4]].tolist()}
+
+
+def _check_kv(m, fx, cfg):
+    assert m.cache_len() == int(fx["cache_len"])
+    for layer in range(cfg["num_layers"]):
+        assert sha(*m.read_kv(layer)) == fx["kv_sha256"][layer].tobytes(), f"kv cache layer {layer}"
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_qwen3_full_shape_step_by_step(full, mode):
+    m, fx, cfg, prompt = full
+    say("qwen3-0.6b full shape, step by step, mode", mode)
+    m.reset()
+    m.set_decode_mode(mode)
+    m.prefill(prompt[:-1])
+    tok = int(prompt[-1])
+    for i in range(len(fx["tokens"])):
+        tok = m.decode(tok)
+        lg = m.last_logits()
+        assert sha(lg) == fx["logits_sha256"][i].tobytes(), _first_diff(fx, i, lg)
+        assert tok == int(fx["tokens"][i]), (i, tok, int(fx["tokens"][i]))
+    _check_kv(m, fx, cfg)
+    if mode == 0:
+        assert sha(m.last_hidden()) == fx["hidden_sha256"].tobytes()
+
+
+def test_qwen3_full_shape_generate_fused(full):
+    """The bench's path: generate() in mode 1 (prefill, then all steps on the
+    device)."""
+    m, fx, cfg, prompt = full
+    say("qwen3-0.6b full shape, generate, mode 1")
+    m.reset()
+    m.set_decode_mode(1)
+    toks, _ = m.generate(prompt, len(fx["tokens"]))
+    assert toks.tolist() == fx["tokens"].tolist()
+    assert sha(m.last_logits()) == fx["logits_sha256"][-1].tobytes()
+    _check_kv(m, fx, cfg)
