@@ -60,6 +60,12 @@ class Dev:
         self.cm.call("cactus_hip_stream_sync", None)
         return buf.to_numpy(dtype, shape)
 
+    def get_ptr(self, ptr, dtype, shape):
+        out = np.empty(shape, dtype)
+        self.cm.call("cactus_hip_stream_sync", None)
+        self.cm.call("cactus_hip_memcpy_d2h", out.ctypes.data, ptr, out.nbytes, None)
+        return out
+
 
 @pytest.fixture
 def dev(hip_ready):
@@ -154,3 +160,51 @@ def test_fast_entries_hand_other_shapes_to_the_exact_kernels(dev, orc):
                     ctypes.c_float(scale), dev.put(mask) if masked else None, pos, 0, 1, None)
         got = dev.get(o, np.uint16, q.shape)
         assert (got == ref).all(), (S, Skv, d, masked)
+
+
+@pytest.mark.parametrize("cache,Hq,Hkv,d", [
+    (4095, 16, 8, 128), (4096, 16, 8, 128), (4097, 16, 8, 128),   # split edges of the config-4 shape
+    (127, 4, 2, 128), (128, 4, 2, 128), (129, 4, 2, 64), (300, 4, 4, 64), (0, 4, 2, 128),
+])
+def test_decode_prep_attention_fast(dev, orc, cache, Hq, Hkv, d):
+    """The fused decode step's attention in tolerance mode against the exact
+    fused entry point on the same cache and step state: the prepared key and
+    value appended to the cache (codes and scales) bit-identical, the output
+    within tolerance; run twice on one workspace (the split counters reset
+    themselves)."""
+    say("decode_prep_attention_fast", cache, Hq, Hkv, d)
+    rng = np.random.default_rng(cache * 3 + d + Hq)
+    cap = cache + 70
+    kc, ks = orc.quantize_kv(_roped(orc, f16(rng.normal(0, 1, (1, cap, Hkv, d))), 0)[0])
+    vc, vs = orc.quantize_kv(f16(rng.normal(0, 1, (cap, Hkv, d))))
+    q_raw = f16(rng.normal(0, 1, (Hq, d)))
+    k_raw = f16(rng.normal(0, 1, (Hkv, d)))
+    v_raw = f16(rng.normal(0, 1, (Hkv, d)))
+    qn = f16(rng.normal(1, 0.2, d))
+    kn = f16(rng.normal(1, 0.2, d))
+    eps, theta, scale = 1e-6, 1e6, 1.0 / math.sqrt(d)
+    state = dev.put(np.array([0, cache, cache, 0], np.uint32))
+    raw = [dev.put(x) for x in (q_raw, k_raw, v_raw, qn, kn)]
+    ws_bytes = dev.cm.hip().cactus_hip_decode_attention_fast_workspace(Hq, Hkv, d, cap)
+    ws = dev.empty(ws_bytes)
+    dev.cm.call("cactus_hip_memset", ws.ptr, 0, ws_bytes, None)
+    outs, rows = [], []
+    for fast in (False, True, True):
+        bufs = [dev.put(kc), dev.put(vc), dev.put(ks), dev.put(vs)]
+        o = dev.empty(q_raw.nbytes)
+        if fast:
+            dev.cm.call("cactus_hip_decode_prep_attention_fast", *raw, ctypes.c_float(eps), Hq, Hkv, d,
+                        ctypes.c_float(theta), state, *bufs, cap, None, ctypes.c_float(scale), o.ptr, ws.ptr, ws_bytes,
+                        None)
+        else:
+            dev.cm.call("cactus_hip_decode_prep_attention", *raw, ctypes.c_float(eps), Hq, Hkv, d,
+                        ctypes.c_float(theta), state, *bufs, cap, None, ctypes.c_float(scale), o.ptr, None)
+        outs.append(dev.get(o, np.uint16, (Hq, d)))
+        rows.append([dev.get_ptr(b, dt, shp)[cache] for b, dt, shp in
+                     zip(bufs, (np.int8, np.int8, np.float32, np.float32),
+                         ((cap, Hkv, d), (cap, Hkv, d), (cap, Hkv, 1), (cap, Hkv, 1)))])
+    for i in (1, 2):
+        for x, y in zip(rows[0], rows[i]):
+            assert (x == y).all(), "appended cache row"
+        close(outs[i], outs[0], "decode_prep_attention_fast")
+    assert (outs[1] == outs[2]).all(), "second launch on the same workspace"

@@ -100,3 +100,54 @@ def test_qwen3_full_shape_generate_fused(full):
     assert toks.tolist() == fx["tokens"].tolist()
     assert sha(m.last_logits()) == fx["logits_sha256"][-1].tobytes()
     _check_kv(m, fx, cfg)
+
+
+def test_qwen3_full_shape_tolerance_mode(full):
+    """Tolerance-mode attention (split-K decode attention, within 1e-3 +
+    1e-2 |ref| of the reference per fp16 output, tested kernel by kernel in
+    test_gpu_attention_fast.py) at model level.  The exact mode is first
+    checked against the fixture; then the tolerance mode is run teacher-forced
+    on the fixture's tokens and its logits compared step by step with the
+    exact mode's.  This random 28-layer model amplifies single-ulp attention
+    differences (measured: the first two steps bit-identical, later steps
+    2-13% relative L2 on the logits), so the bar is a loose relative L2 of
+    0.25 per step (garbage attention lands near 1) and the argmax agreeing on
+    at least half of the steps; the free-running token prefix that matches
+    the oracle is printed, not required."""
+    m, fx, cfg, prompt = full
+    toks = fx["tokens"]
+    say("qwen3-0.6b full shape, exact vs tolerance attention")
+    m.reset()
+    m.set_decode_mode(1)
+    m.set_attention_mode(0)
+    m.prefill(prompt[:-1])
+    ref = []
+    tok = int(prompt[-1])
+    for i in range(len(toks)):
+        t = m.decode(tok)
+        lg = m.last_logits()
+        assert sha(lg) == fx["logits_sha256"][i].tobytes(), i
+        ref.append(lg.view(np.float16).astype(np.float64))
+        tok = int(toks[i])
+        assert t == tok
+    m.reset()
+    m.set_attention_mode(1)
+    try:
+        m.prefill(prompt[:-1])
+        tok = int(prompt[-1])
+        rel, agree = [], 0
+        for i in range(len(toks)):
+            t = m.decode(tok)
+            g = m.last_logits().view(np.float16).astype(np.float64)
+            rel.append(float(np.linalg.norm(g - ref[i]) / np.linalg.norm(ref[i])))
+            agree += int(t == int(toks[i]))
+            tok = int(toks[i])
+        m.reset()
+        free, _ = m.generate(prompt, len(toks))
+    finally:
+        m.set_attention_mode(0)
+    prefix = int(np.argmax(free != toks)) if (free != toks).any() else len(toks)
+    print(f"[tolerance mode] max relative L2 of logits {max(rel):.4f}, argmax agreement {agree}/{len(toks)}, "
+          f"free-running tokens equal to the oracle's for the first {prefix} steps", flush=True)
+    assert max(rel) <= 0.25, rel
+    assert agree >= len(toks) // 2, agree
