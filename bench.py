@@ -13,7 +13,18 @@ from HBM.  Inputs are resident in HBM before the timed region starts.
 The same JSON line carries the CPU baseline: the CPU restatement of the
 reference kernel (oracle/, x86 build) timed on this host on a bounded sample
 of the same workload, with the reference's M=1 thread policy
-(min(pool, 4) threads, kernel_utils.h:446-453).
+(min(pool, 4) threads, kernel_utils.h:446-453); the host's core count and
+CPU model; and the other workloads the kernel layer is quoted on:
+
+  int4_gemv           INT4 GEMV M=1 K=3072 N=1024 g32, 604 rotated weight sets
+  prefill_gemm        INT8 M=512 K=1024 N=3072 and INT4 K=3072 N=1024 M=256/1
+  decode_attention    one decode query over 4096 positions, INT8 cache and
+                      FP16 K/V, exact and tolerance (split-K) modes, rotated
+                      over >= 1 GiB of caches
+  qwen3_0p6b_decode   Qwen3-0.6B-shape 4096-token prefill + 128 greedy steps,
+                      exact attention (tokens compared with the oracle's
+                      frozen run) and tolerance attention
+  qwen3_0p6b_decode_cpu_baseline   the oracle model's decode on the host
 """
 from __future__ import annotations
 
@@ -85,6 +96,162 @@ def bench_gemv(steps: int, warmup: int, R: int = 768):
 
 
 INT8_MFMA_PEAK_TOPS = 5000.0   # MI355X dense INT8 MFMA
+
+# Qwen3-0.6B down-projection GEMV, packed INT4 (config 3 at M=1)
+K4, N4 = 3072, 1024
+SET_BYTES_INT4 = N4 * K4 // 2 + 2 * N4 * (K4 // GS) + 2 * K4 + 2 * N4   # 1,777,664 algorithmic bytes
+
+
+def bench_gemv_int4(steps: int, warmup: int, R: int = 604):
+    """INT4 grouped GEMV M=1 K=3072 N=1024 g32 through the streaming GEMV:
+    one launch of the strided-batched entry over R distinct weight sets
+    (R x 1.78 MB > 1 GiB, so every launch streams from HBM)."""
+    import cactus_amd as cm
+    from _data import f16
+    rng = np.random.default_rng(3)
+    per = N4 * K4 // 2
+    pool = rng.integers(0, 256, size=(32, per), dtype=np.uint8)
+    B = cm.DeviceBuffer(R * per)
+    for r0 in range(0, R, pool.shape[0]):
+        n = min(pool.shape[0], R - r0)
+        cm.call("cactus_hip_memcpy_h2d", B.ptr + r0 * per, pool.ctypes.data, n * per, None)
+    Bs = cm.DeviceBuffer.from_numpy(f16(np.abs(rng.normal(0, 0.02, size=(R, N4, K4 // GS))) / 7.0))
+    A = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, size=(R, 1, K4))))
+    C = cm.DeviceBuffer(R * N4 * 2)
+    stream = cm.Stream()
+
+    def launch():
+        cm.call("cactus_hip_matmul_int4_f16act_batched", A.ptr, B.ptr, Bs.ptr, C.ptr, 1, K4, N4, GS, R,
+                K4, per, N4 * (K4 // GS), N4, stream.handle)
+
+    for _ in range(warmup):
+        launch()
+    stream.sync()
+    e0, e1 = cm.Event(), cm.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    stream.sync()
+    us = e0.elapsed_ms(e1) * 1e3 / steps
+    gbs = R * SET_BYTES_INT4 / (us * 1e-6) / 1e9
+    return {"workload": f"INT4 grouped GEMV M=1 K=3072 N=1024 group 32, FP16 activations quantized in-kernel; "
+                        f"one launch over {R} distinct weight sets",
+            "bytes_per_set": SET_BYTES_INT4, "sets_per_launch": R, "us_per_launch": round(us, 2),
+            "gbs": round(gbs, 1), "hbm_fraction": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+# KV-cache decode attention (config 4): 16 query / 8 KV heads, head_dim 128,
+# 4096 positions, one query row
+ATT_HQ, ATT_HKV, ATT_D, ATT_CTX = 16, 8, 128, 4096
+ATT_BYTES_F16 = 2 * ATT_CTX * ATT_HKV * ATT_D * 2 + 4 * ATT_HQ * ATT_D                 # 16,785,408
+ATT_BYTES_INT8 = 2 * ATT_CTX * ATT_HKV * ATT_D + 2 * ATT_CTX * ATT_HKV * 4 + 4 * ATT_HQ * ATT_D  # 8,658,944
+
+
+def _graph_time(fn, launches, rounds=4):
+    """us per call of `launches` calls captured into one HIP graph."""
+    import cactus_amd as cm
+    st = fn.stream
+    for i in range(min(launches, 4)):
+        fn(i)
+    st.sync()
+    cm.call("cactus_hip_graph_capture_begin", st.handle)
+    for i in range(launches):
+        fn(i)
+    ge = ctypes.c_void_p()
+    cm.call("cactus_hip_graph_capture_end", st.handle, ctypes.byref(ge))
+    cm.call("cactus_hip_graph_launch", ge, st.handle)
+    st.sync()
+    e0, e1 = cm.Event(), cm.Event()
+    e0.record(st)
+    for _ in range(rounds):
+        cm.call("cactus_hip_graph_launch", ge, st.handle)
+    e1.record(st)
+    st.sync()
+    cm.call("cactus_hip_graph_destroy", ge)
+    return e0.elapsed_ms(e1) * 1e3 / (launches * rounds)
+
+
+def bench_attention():
+    """Config 4 in both attention modes and both cache forms: each call one
+    decode query over 4096 positions; R distinct caches rotated (>= 1 GiB) so
+    every call streams its cache from HBM; timed as a HIP graph of R calls.
+    Also a single-set form (the same cache every call: L2/MALL-resident) and
+    a single-shot latency (one call between two events)."""
+    import cactus_amd as cm
+    from _data import f16
+    rng = np.random.default_rng(5)
+    Hq, Hkv, d, ctx = ATT_HQ, ATT_HKV, ATT_D, ATT_CTX
+    scale = ctypes.c_float(d ** -0.5)
+    st = cm.Stream()
+    out = {}
+    # INT8 cache (cache 4095 + one FP16 new row): the hybrid entry points
+    R8 = 124
+    cache = ctx - 1
+    row = cache * Hkv * d
+    codes = rng.integers(-127, 128, (row,), dtype=np.int8)
+    kc, vc = cm.DeviceBuffer(R8 * row), cm.DeviceBuffer(R8 * row)
+    for r in range(R8):
+        cm.call("cactus_hip_memcpy_h2d", kc.ptr + r * row, codes.ctypes.data, row, None)
+        cm.call("cactus_hip_memcpy_h2d", vc.ptr + r * row, codes.ctypes.data, row, None)
+    sc = np.abs(rng.normal(0, 0.02, (R8, cache, Hkv, 1))).astype(np.float32)
+    sbytes = sc[0].nbytes
+    ks, vs = cm.DeviceBuffer.from_numpy(sc), cm.DeviceBuffer.from_numpy(sc)
+    kn = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, (R8, 1, Hkv, d))))
+    vn = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, (R8, 1, Hkv, d))))
+    q = cm.DeviceBuffer.from_numpy(f16(rng.normal(0, 1, (R8, 1, Hq, d))))
+    o = cm.DeviceBuffer(R8 * Hq * d * 2)
+    for mode, name in (("exact", "cactus_hip_attention_hybrid_int8_fp16"),
+                       ("tolerance", "cactus_hip_attention_hybrid_int8_fp16_fast")):
+        def call(i, rot=True, name=name):
+            r = i % R8 if rot else 0
+            cm.call(name, q.ptr + r * Hq * d * 2, kc.ptr + r * row, vc.ptr + r * row, ks.ptr + r * sbytes,
+                    vs.ptr + r * sbytes, kn.ptr + r * Hkv * d * 2, vn.ptr + r * Hkv * d * 2, o.ptr + r * Hq * d * 2,
+                    1, 1, cache, 1, Hq, Hkv, d, scale, cache, 1, 128, st.handle)
+        call.stream = st
+        us = _graph_time(call, R8)
+        res = lambda i, call=call: call(i, rot=False)
+        res.stream = st
+        us_res = _graph_time(res, 50)
+        e0, e1 = cm.Event(), cm.Event()
+        st.sync()
+        e0.record(st)
+        call(0)
+        e1.record(st)
+        st.sync()
+        one = e0.elapsed_ms(e1) * 1e3
+        out[f"int8_cache_{mode}"] = {
+            "us_per_call": round(us, 2), "gbs": round(ATT_BYTES_INT8 / us / 1e3, 1),
+            "hbm_fraction": round(ATT_BYTES_INT8 / us / 1e3 / HBM_PEAK_GBS, 4),
+            "us_per_call_l2_mall_resident": round(us_res, 2), "us_single_shot": round(one, 2)}
+    del kc, vc, ks, vs
+    # FP16 K/V (4096 positions): the FP16 entry points
+    R16 = 64
+    row16 = ctx * Hkv * d
+    kv = f16(rng.normal(0, 1, (row16,)))
+    k16, v16 = cm.DeviceBuffer(R16 * row16 * 2), cm.DeviceBuffer(R16 * row16 * 2)
+    for r in range(R16):
+        cm.call("cactus_hip_memcpy_h2d", k16.ptr + r * row16 * 2, kv.ctypes.data, row16 * 2, None)
+        cm.call("cactus_hip_memcpy_h2d", v16.ptr + r * row16 * 2, kv.ctypes.data, row16 * 2, None)
+    for mode, name in (("exact", "cactus_hip_attention_f16"), ("tolerance", "cactus_hip_attention_f16_fast")):
+        def call(i, rot=True, name=name):
+            r = i % R16 if rot else 0
+            cm.call(name, q.ptr + (r % R8) * Hq * d * 2, k16.ptr + r * row16 * 2, v16.ptr + r * row16 * 2,
+                    o.ptr, 1, 1, ctx, Hq, Hkv, d, scale, None, ctx - 1, 0, 1, st.handle)
+        call.stream = st
+        us = _graph_time(call, R16)
+        res = lambda i, call=call: call(i, rot=False)
+        res.stream = st
+        us_res = _graph_time(res, 50)
+        out[f"fp16_{mode}"] = {
+            "us_per_call": round(us, 2), "gbs": round(ATT_BYTES_F16 / us / 1e3, 1),
+            "hbm_fraction": round(ATT_BYTES_F16 / us / 1e3 / HBM_PEAK_GBS, 4),
+            "us_per_call_l2_mall_resident": round(us_res, 2)}
+    out["workload"] = (f"decode attention, one query, {Hq} query / {Hkv} KV heads, head_dim {d}, {ctx} positions; "
+                       f"INT8 cache ({ATT_BYTES_INT8} B/call, {R8} caches rotated) and FP16 K/V "
+                       f"({ATT_BYTES_F16} B/call, {R16} rotated); exact = the reference's operation order, "
+                       f"tolerance = split-K (within 1e-3 + 1e-2|ref|)")
+    return out
 
 
 def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: int = 50, rounds: int = 5,
@@ -203,22 +370,25 @@ def cpu_baseline(seconds: float = 10.0):
                       f"x86 build of the CPU restatement, {threads} threads"}
 
 
-def bench_decode(prompt_len: int = 4096, new_tokens: int = 128, mode: int = 0):
-    """Qwen3-0.6B-architecture forward, random-init weights (INT4 MLP, INT8
-    attention projections, FP16 embeddings/norms): prefill of a 4096-token
-    random prompt through the reference's FFI flow, then greedy decode."""
-    from cactus_amd.engine import Qwen, qwen3_0p6b
-    cfg = qwen3_0p6b(max_seq=prompt_len + new_tokens + 64)
-    t0 = time.perf_counter()
-    m = Qwen(cfg, seed=6)
-    if mode:
-        m.set_decode_mode(mode)
-    init_s = time.perf_counter() - t0
-    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], prompt_len).astype(np.uint32)
+def host_info():
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": cpu}
+
+
+def _decode_run(m, cfg, prompt, new_tokens, attention_mode):
+    m.reset()
+    m.set_attention_mode(attention_mode)
     toks, t = m.generate(prompt, new_tokens)
     decode_steps = t.decode_tokens + 1
     decode_s = (t.decode_ms + t.first_decode_ms) / 1e3
-    ctx = prompt_len - 1 + new_tokens / 2
+    ctx = len(prompt) - 1 + new_tokens / 2
     # bytes per decoded token: every weight once (INT8 attention, INT4 MLP,
     # fp16 scales/norms), the tied FP16 LM head, and the INT8 KV cache at the
     # mean context
@@ -227,19 +397,72 @@ def bench_decode(prompt_len: int = 4096, new_tokens: int = 128, mode: int = 0):
     per_layer = (nq * H + 2 * nkv * H + H * nq) * (1 + 2 / gs) + 3 * F * H * (0.5 + 2 / gs) + 4 * H + 4 * hd
     kv = cfg["num_layers"] * 2 * cfg["kv_heads"] * (hd + 4) * ctx
     bytes_tok = cfg["num_layers"] * per_layer + cfg["vocab"] * H * 2 + kv
-    m.close()
-    return {
+    return toks, {
         "decode_tok_s": round(decode_steps / decode_s, 2),
         "prefill_tok_s": round(t.prefill_tokens / (t.prefill_ms / 1e3), 1),
         "decode_ms_per_token": round(decode_s * 1e3 / decode_steps, 3),
         "decode_hbm_fraction": round(bytes_tok * decode_steps / decode_s / 1e9 / HBM_PEAK_GBS, 4),
         "bytes_per_token": int(bytes_tok),
-        "decode_mode": mode,
-        "prompt_tokens": prompt_len,
-        "new_tokens": new_tokens,
-        "first_tokens": [int(x) for x in toks[:8]],
-        "init_s": round(init_s, 1),
+        "distinct_tokens": len(set(int(x) for x in toks)),
     }
+
+
+def bench_decode(prompt_len: int = 4096, new_tokens: int = 128, mode: int = 1):
+    """Qwen3-0.6B-architecture forward, random-init weights (INT4 MLP, INT8
+    attention projections, FP16 embeddings/norms): prefill of a 4096-token
+    random prompt through the reference's FFI flow, then greedy decode -- in
+    the exact attention mode (bit-identical to the reference's arithmetic;
+    its tokens are compared with the oracle's frozen run of this same
+    workload) and in the tolerance mode (split-K decode attention)."""
+    from cactus_amd.engine import Qwen, qwen3_0p6b
+    cfg = qwen3_0p6b(max_seq=prompt_len + new_tokens + 64)
+    t0 = time.perf_counter()
+    m = Qwen(cfg, seed=6)
+    if mode:
+        m.set_decode_mode(mode)
+    init_s = time.perf_counter() - t0
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], prompt_len).astype(np.uint32)
+    toks_exact, exact = _decode_run(m, cfg, prompt, new_tokens, 0)
+    toks_tol, tol = _decode_run(m, cfg, prompt, new_tokens, 1)
+    m.set_attention_mode(0)
+    m.close()
+    fx = ROOT / "tests" / "golden" / "qwen3_0p6b_generate.npz"
+    if fx.exists() and prompt_len == 4096 and new_tokens == 128:
+        ref = np.load(fx)["tokens"]
+        exact["tokens_equal_oracle"] = bool((toks_exact == ref).all())
+        same = toks_tol == ref
+        tol["tokens_equal_oracle_prefix"] = int(np.argmin(same)) if not same.all() else len(ref)
+    return {**exact, "decode_mode": mode, "attention": "exact", "prompt_tokens": prompt_len,
+            "new_tokens": new_tokens, "first_tokens": [int(x) for x in toks_exact[:8]], "init_s": round(init_s, 1),
+            "tolerance_attention": tol}
+
+
+def cpu_decode_baseline(seconds: float = 10.0, prompt_len: int = 32):
+    """The oracle's Qwen3-0.6B-shape model on this host's cores: a short
+    prefill (not timed), then greedy decode steps timed until `seconds` pass
+    (at least one).  The oracle runs its row and head loops on up to 16
+    threads; its decode at this short context is dominated by the 151936 x
+    1024 FP16 LM head, emulated in exact fp16 arithmetic."""
+    import oracle
+    from cactus_amd.engine import qwen3_0p6b, random_weights
+    threads = min(16, os.cpu_count() or 1)
+    oracle.lib().orc_set_threads(threads)
+    cfg = qwen3_0p6b(max_seq=prompt_len + 64)
+    layers, emb, on = random_weights(cfg, 6)
+    orc = oracle.OracleQwen(cfg, layers, emb, on)
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], prompt_len).astype(np.uint32)
+    orc.prefill(prompt[:-1], cfg["prefill_chunk"])
+    tok, n = int(prompt[-1]), 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        tok = orc.decode(tok)
+        n += 1
+    dt = time.perf_counter() - t0
+    orc.close()
+    oracle.lib().orc_set_threads(1)
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{n} greedy decode steps of the 28-layer Qwen3-0.6B-shape oracle model after a "
+                      f"{prompt_len - 1}-token prefill, {dt:.1f} s, {threads} threads"}
 
 
 def main():
@@ -252,6 +475,7 @@ def main():
                     help="1: fused decode step replayed as one HIP graph (default); 0: node-by-node graph")
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
+    ap.add_argument("--attention-only", action="store_true")
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--eager", action="store_true",
                     help="no HIP graphs: matmuls launched directly and the decode step enqueued per token "
@@ -272,6 +496,9 @@ def main():
     if args.decode_only:
         print(json.dumps(bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)), flush=True)
         return
+    if args.attention_only:
+        print(json.dumps(bench_attention()), flush=True)
+        return
     if args.copy_calibration:
         n = 1 << 30
         src, dst = cm.DeviceBuffer(n), cm.DeviceBuffer(n)
@@ -279,9 +506,12 @@ def main():
         cm.call("cactus_hip_stream_sync", None)
         del src, dst
     g = bench_gemv(args.steps, args.warmup)
+    g4 = bench_gemv_int4(args.steps, min(args.warmup, 50))
     gemms = bench_prefill_gemms(eager=args.eager)
+    att = bench_attention()
     dec = None if args.skip_decode else bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)
     cpu = cpu_baseline(args.cpu_seconds)
+    cpu_dec = None if args.skip_decode else cpu_decode_baseline(args.cpu_seconds)
     out = {
         "metric": "INT8 GEMV GB/s (% HBM peak) + Qwen3-0.6B-shape decode tok/s, 1 MI355X",
         "value": round(g["gbs"], 2),
@@ -311,8 +541,12 @@ def main():
             "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
+        "host": host_info(),
+        "int4_gemv": g4,
         "prefill_gemm": gemms,
+        "decode_attention": att,
         "qwen3_0p6b_decode": dec,
+        "qwen3_0p6b_decode_cpu_baseline": cpu_dec,
     }
     print(json.dumps(out), flush=True)
 

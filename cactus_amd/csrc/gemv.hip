@@ -584,4 +584,23 @@ int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,
     return launch_gemv<true, false>(a, batch, as_stream(stream));
 }
 
+int cactus_hip_matmul_int4_f16act_batched(const uint16_t* A, const uint8_t* B_packed,
+                                          const uint16_t* B_scales, uint16_t* C, size_t M,
+                                          size_t K, size_t N, size_t group_size, size_t batch,
+                                          size_t stride_a, size_t stride_b, size_t stride_bs,
+                                          size_t stride_c, void* stream) {
+    if (M == 0 || K == 0 || N == 0 || batch == 0) return CACTUS_HIP_OK;
+    int rc = check_grouped_shape(M, K, N, group_size, true);
+    if (rc) return rc;
+    CH_REQUIRE(A && B_packed && B_scales && C, "matmul_int4_f16act_batched: null pointer");
+    CH_REQUIRE(batch <= 65535, "matmul_int4_f16act_batched: batch must be <= 65535");
+    CH_REQUIRE(((uintptr_t)B_packed & 15) == 0 && stride_b % 16 == 0,
+               "matmul_int4_f16act_batched: weights must be 16-byte aligned");
+    GemvArgs a{};
+    a.A16 = A; a.B = B_packed; a.Bs = B_scales; a.C = C;
+    a.M = (int)M; a.K = (int)K; a.N = (int)N; a.gs = (int)group_size;
+    a.sA = stride_a; a.sB = stride_b; a.sBs = stride_bs; a.sC = stride_c;
+    return launch_gemv<true, true>(a, batch, as_stream(stream));
+}
+
 }  // extern "C"

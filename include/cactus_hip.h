@@ -142,6 +142,13 @@ int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,
                                           size_t K, size_t N, size_t group_size, size_t batch,
                                           size_t stride_a, size_t stride_b, size_t stride_bs,
                                           size_t stride_c, void* stream);
+/* The same for cactus_hip_matmul_int4_f16act (stride_b in bytes of packed
+ * weights, the other strides in elements).  No reference counterpart. */
+int cactus_hip_matmul_int4_f16act_batched(const uint16_t* A, const uint8_t* B_packed,
+                                          const uint16_t* B_scales, uint16_t* C, size_t M,
+                                          size_t K, size_t N, size_t group_size, size_t batch,
+                                          size_t stride_a, size_t stride_b, size_t stride_bs,
+                                          size_t stride_c, void* stream);
 /* cactus_unpack_int4_to_int8 (kernel/kernel.h:162, kernel_quants.cpp:295-351) */
 int cactus_hip_unpack_int4_to_int8(const uint8_t* packed, int8_t* unpacked, size_t count,
                                    void* stream);

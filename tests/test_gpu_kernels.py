@@ -228,6 +228,24 @@ def test_matmul_int8_batched_shapes(dev, orc, M, K, N, gs, R):
         assert_bits(got[r], orc.matmul_int8(rq, rs, ws[r][0], ws[r][1], gs), f"batch {r}")
 
 
+@pytest.mark.parametrize("M,K,N,gs,R", [(1, 3072, 1024, 32, 7), (2, 1024, 3072, 64, 3)])
+def test_matmul_int4_batched(dev, orc, M, K, N, gs, R):
+    """Strided-batched INT4 GEMV (the config-3 M=1 down-projection shape and
+    a gate/up shape), every problem against the oracle."""
+    say("matmul_int4_f16act_batched", M, K, N, gs, R)
+    rng = np.random.default_rng(M * K + N + R + 4)
+    xs = [activations(rng, M, K) for _ in range(R)]
+    ws = [grouped_int4_weights(rng, N, K, gs) for _ in range(R)]
+    C = dev.empty(R * M * N * 2)
+    dev.cm.call("cactus_hip_matmul_int4_f16act_batched", dev.put(np.stack(xs)),
+                dev.put(np.stack([w[1] for w in ws])), dev.put(np.stack([w[2] for w in ws])), C.ptr,
+                M, K, N, gs, R, M * K, N * K // 2, N * (K // gs), M * N, None)
+    got = dev.get(C, np.uint16, (R, M, N))
+    for r in range(R):
+        rq, rs = orc.quantize_activations(xs[r])
+        assert_bits(got[r], orc.matmul_int4(rq, rs, ws[r][1], ws[r][2], gs), f"batch {r}")
+
+
 def test_unpack_int4(dev, orc):
     say("unpack_int4")
     rng = np.random.default_rng(5)
