@@ -10,8 +10,9 @@
 //   2. top-k: the k-th largest value by a two-pass radix select over
 //      order-preserving 16-bit keys (high byte, then low byte, LDS
 //      histograms); values below it become -inf;
-//   3. top-p: the survivors (top_k <= 4096 plus ties, at most SP_CAND) are sorted descending by a
-//      bitonic sort in LDS (ties: ascending token, see the oracle), thread 0
+//   3. top-p: the survivors are sorted descending by a bitonic sort in LDS
+//      (up to SP_CAND of them; more go through topp_large's global sort)
+//      (ties: ascending token, see the oracle), thread 0
 //      forms the probabilities and the running sum in that order and every
 //      position from the first j > 0 whose sum exceeds top_p is removed;
 //   4. the final probabilities over the survivors in token order: parallel
@@ -30,8 +31,7 @@
 namespace cactus_hip {
 
 constexpr int SP_T = 1024;
-constexpr int SP_TOPK = 4096;          // largest top_k with top-p
-constexpr int SP_CAND = 16384;         // top-p candidates sorted in LDS (top_k plus ties)
+constexpr int SP_CAND = 16384;         // top-p candidates sorted in LDS; more take the global sort
 constexpr int SP_HIST = 128;           // kernel_nn.cpp:517
 constexpr uint16_t SP_NEG_INF = 0xFC00u;
 
@@ -84,6 +84,7 @@ struct SampleArgs {
     uint16_t* f;        // [V] filtered logits
     float* pv;          // [V] unnormalised probabilities of the survivors
     uint32_t* surv;     // [V] survivor tokens in order
+    uint32_t* sk;       // [next_pow2(V)] order keys of a large top-p
     uint32_t* hist;     // [1 + SP_HIST]: count, tokens
     size_t V, top_k;
     float top_p, u;
@@ -99,6 +100,179 @@ __device__ __forceinline__ uint32_t okey(uint16_t h) {
 }
 __device__ __forceinline__ uint16_t ukey(uint32_t k) {
     return (k & 0x8000u) ? (uint16_t)(k & 0x7FFFu) : (uint16_t)(~k & 0xFFFFu);
+}
+// the same for fp32 values
+__device__ __forceinline__ uint32_t okey32(float x) {
+    uint32_t u = __float_as_uint(x);
+    if (u == 0x80000000u) u = 0;   // -0 == +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ bool is_inf(float x) { return x == __builtin_inff() || x == -__builtin_inff(); }
+
+// ---------------------------------------------------------------- large top-p
+// More top-p candidates than the LDS sort holds (top_k 0 or large, a flat
+// distribution): their order keys (ascending key = descending value) are
+// sorted in a global buffer by a bitonic sort whose strides below one LDS
+// chunk run per chunk in LDS; thread 0 sums the probabilities in sorted
+// order and walks the running sum to the cut, reading the sorted arrays
+// chunk by chunk through LDS; then a token-order pass removes every
+// candidate past the cut: all keys beyond the cut key, and the cut key's
+// ties past the kept count in ascending token order (the reference's
+// std::sort leaves the order of ties unspecified; the oracle's is
+// ascending token, as in the LDS path).
+constexpr uint32_t TP_CHUNK = SP_CAND * 2;   // 32-bit entries per LDS chunk (the 128 KB candidate buffer)
+
+struct TopPF16 {
+    uint16_t* f;
+    __device__ bool removed(size_t i) const { return f[i] == SP_NEG_INF; }
+    __device__ uint32_t key(size_t i) const { return 0xFFFFu - okey(f[i]); }
+    __device__ float value(uint32_t k) const { return h2f(ukey(0xFFFFu - k)); }
+    __device__ void remove(size_t i) const { f[i] = SP_NEG_INF; }
+};
+struct TopPF32 {
+    float* f;
+    __device__ bool removed(size_t i) const { return is_inf(f[i]); }
+    __device__ uint32_t key(size_t i) const { return ~okey32(f[i]); }
+    __device__ float value(uint32_t k) const {
+        const uint32_t o = ~k;
+        return __uint_as_float((o & 0x80000000u) ? (o & 0x7FFFFFFFu) : ~o);
+    }
+    __device__ void remove(size_t i) const { f[i] = -__builtin_inff(); }
+};
+
+// compare-exchange of the pair (lo, lo + stride) for pair index p, into
+// ascending order where (index & size) == 0
+__device__ __forceinline__ void bitonic_pair(uint32_t* x, uint32_t p, uint32_t stride, uint32_t size,
+                                             uint32_t base) {
+    const uint32_t lo = 2 * p - (p & (stride - 1)), hi = lo + stride;
+    const bool up = ((base + lo) & size) == 0;
+    const uint32_t u = x[lo], v = x[hi];
+    if ((u > v) == up) {
+        x[lo] = v;
+        x[hi] = u;
+    }
+}
+
+// ascending sort of sk[0, n2), n2 a power of two (one workgroup)
+__device__ void bitonic_sort_global(uint32_t* sk, uint32_t n2, uint32_t* lds) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t C = n2 < TP_CHUNK ? n2 : TP_CHUNK;
+    auto chunk_stages = [&](uint32_t base, uint32_t size_lo, uint32_t size_hi, uint32_t stride_hi) {
+        for (uint32_t i = tid; i < C; i += SP_T) lds[i] = sk[base + i];
+        __syncthreads();
+        for (uint32_t size = size_lo; size <= size_hi; size <<= 1)
+            for (uint32_t stride = min(size >> 1, stride_hi); stride > 0; stride >>= 1) {
+                for (uint32_t p = tid; p < C / 2; p += SP_T) bitonic_pair(lds, p, stride, size, base);
+                __syncthreads();
+            }
+        for (uint32_t i = tid; i < C; i += SP_T) sk[base + i] = lds[i];
+        __syncthreads();
+    };
+    for (uint32_t base = 0; base < n2; base += C) chunk_stages(base, 2, C, C);
+    for (uint32_t size = 2 * C; size <= n2; size <<= 1) {
+        for (uint32_t stride = size >> 1; stride >= C; stride >>= 1) {
+            for (uint32_t p = tid; p < n2 / 2; p += SP_T) bitonic_pair(sk, p, stride, size, 0);
+            __syncthreads();
+        }
+        for (uint32_t base = 0; base < n2; base += C) chunk_stages(base, size, size, C >> 1);
+    }
+}
+
+// top-p over the V entries of ops that are not removed, n of them
+// (n > SP_CAND); sk holds next_pow2(V) entries, pv V floats (scratch)
+template <class Ops>
+__device__ void topp_large(const Ops& ops, size_t V, float top_p, uint32_t* sk, float* pv, uint32_t* lds,
+                           uint32_t* scan) {
+    __shared__ uint32_t tp[4];
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) tp[0] = 0;
+    __syncthreads();
+    for (size_t i = tid; i < V; i += SP_T)
+        if (!ops.removed(i)) sk[atomicAdd(&tp[0], 1u)] = ops.key(i);
+    __syncthreads();
+    const uint32_t n = tp[0];
+    uint32_t n2 = 1;
+    while (n2 < n) n2 <<= 1;
+    for (uint32_t j = n + tid; j < n2; j += SP_T) sk[j] = 0xFFFFFFFFu;
+    __syncthreads();
+    bitonic_sort_global(sk, n2, lds);
+
+    // probabilities in sorted order, their sum by thread 0 in that order
+    const float mx = ops.value(sk[0]);
+    for (uint32_t j = tid; j < n; j += SP_T) pv[j] = cactus_expf(ops.value(sk[j]) - mx);
+    __syncthreads();
+    float* fl = reinterpret_cast<float*>(lds);
+    float sum = 0.0f;
+    for (uint32_t c0 = 0; c0 < n; c0 += TP_CHUNK) {
+        const uint32_t m = min(TP_CHUNK, n - c0);
+        for (uint32_t j = tid; j < m; j += SP_T) fl[j] = pv[c0 + j];
+        __syncthreads();
+        if (tid == 0)
+            for (uint32_t j = 0; j < m; j++) sum += fl[j];
+        __syncthreads();
+    }
+    if (tid == 0) {
+        tp[1] = __float_as_uint(sum);
+        tp[2] = n;   // the cut: first position removed
+    }
+    __syncthreads();
+    sum = __uint_as_float(tp[1]);
+    for (uint32_t j = tid; j < n; j += SP_T) pv[j] = pv[j] / sum;
+    __syncthreads();
+    // the running sum; the first position j > 0 past top_p is the cut
+    float cum = 0.0f;
+    for (uint32_t c0 = 0; c0 < n && tp[2] == n; c0 += TP_CHUNK) {
+        const uint32_t m = min(TP_CHUNK, n - c0);
+        for (uint32_t j = tid; j < m; j += SP_T) fl[j] = pv[c0 + j];
+        __syncthreads();
+        if (tid == 0)
+            for (uint32_t j = 0; j < m; j++) {
+                cum += fl[j];
+                if (cum > top_p && c0 + j > 0) {
+                    tp[2] = c0 + j;
+                    break;
+                }
+            }
+        __syncthreads();
+    }
+    const uint32_t cut = tp[2];
+    if (cut >= n) return;
+    const uint32_t kc = sk[cut];
+    if (tid == 0) {
+        uint32_t lo = 0, hi = cut;   // first position of the cut key
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (sk[mid] < kc) lo = mid + 1;
+            else hi = mid;
+        }
+        tp[3] = cut - lo;   // ties of the cut key that stay
+    }
+    __syncthreads();
+    const uint32_t keep = tp[3];
+    const size_t per = (V + SP_T - 1) / SP_T;
+    const size_t t0 = (size_t)tid * per, t1 = t0 + per < V ? t0 + per : V;
+    uint32_t cnt = 0;
+    for (size_t i = t0; i < t1; i++) cnt += !ops.removed(i) && ops.key(i) == kc;
+    scan[tid] = cnt;
+    __syncthreads();
+    for (uint32_t o = 1; o < SP_T; o <<= 1) {   // inclusive scan
+        const uint32_t v = tid >= o ? scan[tid - o] : 0u;
+        __syncthreads();
+        scan[tid] += v;
+        __syncthreads();
+    }
+    uint32_t rank = scan[tid] - cnt;
+    for (size_t i = t0; i < t1; i++) {
+        if (ops.removed(i)) continue;
+        const uint32_t k = ops.key(i);
+        if (k > kc) {
+            ops.remove(i);
+        } else if (k == kc) {
+            if (rank >= keep) ops.remove(i);
+            rank++;
+        }
+    }
+    __syncthreads();
 }
 
 __global__ void __launch_bounds__(SP_T) sample_kernel(SampleArgs a) {
@@ -168,10 +342,8 @@ __global__ void __launch_bounds__(SP_T) sample_kernel(SampleArgs a) {
         __syncthreads();
         const uint32_t n = sh_u32[2];
         if (n > (uint32_t)SP_CAND) {
-            // more tied survivors than the sort holds: refused, loudly
-            if (tid == 0) *a.out = 0xFFFFFFFFu;
-            return;
-        }
+            topp_large(TopPF16{a.f}, V, a.top_p, a.sk, a.pv, reinterpret_cast<uint32_t*>(cand), scan);
+        } else {
         uint32_t n2 = 1;
         while (n2 < n) n2 <<= 1;
         for (uint32_t j = n + tid; j < n2; j += SP_T) cand[j] = ~0ull;
@@ -212,6 +384,7 @@ __global__ void __launch_bounds__(SP_T) sample_kernel(SampleArgs a) {
         __syncthreads();
         for (uint32_t j = sh_u32[3] + tid; j < n; j += SP_T) a.f[(uint32_t)cand[j]] = SP_NEG_INF;
         __syncthreads();
+        }
     }
 
     // 4. the draw over the survivors in token order (:592-651)
@@ -293,6 +466,7 @@ struct SampleF32Args {
     float* f;           // [V] filtered logits
     float* pv;          // [V] unnormalised probabilities of the survivors
     uint32_t* surv;     // [V] survivor tokens in order
+    uint32_t* sk;       // [next_pow2(V)] order keys of a large top-p
     size_t V, top_k;
     float top_p, u, temperature;
     int scale;          // temperature > 0
@@ -301,12 +475,6 @@ struct SampleF32Args {
     uint32_t bias_i[SP_BIAS];
 };
 
-__device__ __forceinline__ uint32_t okey32(float x) {
-    uint32_t u = __float_as_uint(x);
-    if (u == 0x80000000u) u = 0;   // -0 == +0
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ bool is_inf(float x) { return x == __builtin_inff() || x == -__builtin_inff(); }
 
 // workgroup max of f over [0, V) (every thread gets it)
 __device__ float wg_max(const float* f, size_t V, float* red) {
@@ -448,10 +616,8 @@ __global__ void __launch_bounds__(SP_T) sample_f32_kernel(SampleF32Args a) {
         __syncthreads();
         const uint32_t n = sh_u32[2];
         if (n > (uint32_t)SP_CAND) {
-            // more survivors than the sort holds: refused, loudly
-            if (tid == 0) *a.out = 0xFFFFFFFFu;
-            return;
-        }
+            topp_large(TopPF32{a.f}, V, a.top_p, a.sk, a.pv, reinterpret_cast<uint32_t*>(cand), scan);
+        } else {
         uint32_t n2 = 1;
         while (n2 < n) n2 <<= 1;
         for (uint32_t j = n + tid; j < n2; j += SP_T) cand[j] = ~0ull;
@@ -492,6 +658,7 @@ __global__ void __launch_bounds__(SP_T) sample_f32_kernel(SampleF32Args a) {
         __syncthreads();
         for (uint32_t j = sh_u32[3] + tid; j < n; j += SP_T) a.f[(uint32_t)cand[j]] = -__builtin_inff();
         __syncthreads();
+        }
     }
 
     // 5. the draw over the finite entries in token order (:394-444)
@@ -573,6 +740,7 @@ struct SampleState {
     float* f32 = nullptr;
     float* pv = nullptr;
     uint32_t* surv = nullptr;
+    uint32_t* sk = nullptr;
     size_t cap = 0;
     uint32_t* hist = nullptr;
 };
@@ -595,11 +763,15 @@ static int sample_state(size_t V, SampleState** out) {
         if (s.pv) CH_HIP(hipFree(s.pv));
         if (s.surv) CH_HIP(hipFree(s.surv));
         if (s.f32) CH_HIP(hipFree(s.f32));
-        s.f = nullptr; s.pv = nullptr; s.surv = nullptr; s.f32 = nullptr; s.cap = 0;
+        if (s.sk) CH_HIP(hipFree(s.sk));
+        s.f = nullptr; s.pv = nullptr; s.surv = nullptr; s.f32 = nullptr; s.sk = nullptr; s.cap = 0;
         CH_HIP(hipMalloc(&s.f, V * sizeof(uint16_t)));
         CH_HIP(hipMalloc(&s.pv, V * sizeof(float)));
         CH_HIP(hipMalloc(&s.surv, V * sizeof(uint32_t)));
         CH_HIP(hipMalloc(&s.f32, V * sizeof(float)));
+        size_t n2 = 1;
+        while (n2 < V) n2 <<= 1;
+        CH_HIP(hipMalloc(&s.sk, n2 * sizeof(uint32_t)));
         s.cap = V;
     }
     *out = &s;
@@ -623,9 +795,6 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, f
     }
     CH_REQUIRE(vocab < (1ull << 31), "sample: vocabulary too large");
     CH_REQUIRE(temperature >= 0.0f && temperature == temperature, "sample: temperature must be >= 0");
-    if (top_p > 0.0f && top_p < 1.0f && (top_k == 0 || top_k > (size_t)SP_TOPK))
-        return fail(CACTUS_HIP_EUNSUPPORTED,
-                    "sample: top-p is built over at most 4096 top-k survivors (1 <= top_k <= 4096)");
     SampleState* s = nullptr;
     int rc = sample_state(vocab, &s);
     if (rc) return rc;
@@ -641,6 +810,7 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab, f
     a.f = s->f;
     a.pv = s->pv;
     a.surv = s->surv;
+    a.sk = s->sk;
     a.hist = s->hist;
     a.V = vocab;
     a.top_k = top_k;
@@ -685,6 +855,7 @@ int cactus_hip_sample_f32(const float* logits, uint32_t* out, size_t vocab, floa
     a.f = s->f32;
     a.pv = s->pv;
     a.surv = s->surv;
+    a.sk = s->sk;
     a.V = vocab;
     a.top_k = top_k;
     a.top_p = top_p;

@@ -291,9 +291,10 @@ int cactus_hip_embedding_f16(const uint16_t* table, const float* ids, uint16_t* 
  * std::mt19937(random_seed) (a random seed for 0) through libc++'s
  * generate_canonical<float, 24>.  The reference's logit bias never reaches
  * its result and has no argument here; the f16 sampler has no min-p.
- * 0 < top_p < 1 needs 1 <= top_k <= 4096 (else CACTUS_HIP_EUNSUPPORTED); if
- * ties leave more than 16384 top-k survivors, *out is set to 0xFFFFFFFF.
- * Writes one uint32 to *out (device memory), stream-ordered. */
+ * Top-p works with any top_k (0: the whole vocabulary); the reference's
+ * unspecified order of tied values is taken as ascending token where a tie
+ * straddles the top-p cut.  Always writes a token id < vocab (0 when every
+ * logit is -inf) as one uint32 to *out (device memory), stream-ordered. */
 int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
                           float temperature, float top_p, size_t top_k, size_t random_seed,
                           void* stream);
@@ -304,9 +305,10 @@ int cactus_hip_sample_f16(const uint16_t* logits, uint32_t* out, size_t vocab,
  * CACTUS_HIP_EUNSUPPORTED), division by the temperature, top-k (ties at the
  * k-th value kept), min-p 0.15, top-p and the draw u from
  * std::mt19937(random_seed) (a random seed for 0) through libc++'s
- * generate_canonical<float, 24>.  No repetition penalty and no history.  If
- * more than 16384 entries reach top-p, *out is set to 0xFFFFFFFF.  Writes
- * one uint32 to *out (device memory), stream-ordered. */
+ * generate_canonical<float, 24>.  No repetition penalty and no history.
+ * Tied values straddling the top-p cut are taken in ascending token order.
+ * Always writes a token id < vocab (0 when nothing survives) as one uint32
+ * to *out (device memory), stream-ordered. */
 int cactus_hip_sample_f32(const float* logits, uint32_t* out, size_t vocab, float temperature, float top_p,
                           size_t top_k, size_t random_seed, const float* bias_values,
                           const uint32_t* bias_indices, size_t bias_count, void* stream);

@@ -43,7 +43,7 @@ def test_rejects_bad_shapes_without_launching():
     # GQA head counts
     assert lib.cactus_hip_attention_f16(p, p, p, p, 1, 1, 4, 3, 2, 128, ctypes.c_float(0), None, 0, 0,
                                         1, None) == -1
-    # top-p is built over at most 4096 top-k survivors
-    assert lib.cactus_hip_sample_f16(p, p, 10, ctypes.c_float(0.7), ctypes.c_float(0.9), 0, 0,
-                                     None) == -2
-    assert b"top-p" in lib.cactus_hip_last_error()
+    # a negative temperature is refused before anything is launched
+    assert lib.cactus_hip_sample_f16(p, p, 10, ctypes.c_float(-0.7), ctypes.c_float(0.9), 0, 0,
+                                     None) == -1
+    assert b"temperature" in lib.cactus_hip_last_error()

@@ -135,6 +135,9 @@ CONFIGS = [
     (1.0, 0.0, 1),
     (0.7, 0.0, 0),
     (0.0, 0.8, 10),
+    (1.0, 0.9, 0),       # top-p over the whole vocabulary
+    (2.5, 0.95, 0),      # flat: most of the vocabulary reaches top-p
+    (1.2, 0.8, 20000),   # top-k above the LDS sort
 ]
 
 
@@ -187,17 +190,31 @@ def test_sampler_ties(hip_ready, orc):
 
 
 @pytest.mark.gpu
-def test_sampler_refusals(hip_ready):
-    """top-p without a top-k of at most 4096 is refused; more than 16384
-    tied top-k survivors write 0xFFFFFFFF."""
+def test_sampler_large_top_p(hip_ready, orc):
+    """More top-p candidates than the LDS sort holds (16384): top-p with
+    top_k 0 on 151936 logits, a flat row of 20000 ties (top-k 10 keeps every
+    tie), ties straddling the cut on a coarse grid and a draw past a
+    repetition-penalised token: the oracle's token every time, never an
+    invalid id."""
     cm = hip_ready
-    run, _ = _gpu_sampler(cm)
-    say("sampler refusals")
-    x = f16(np.random.default_rng(1).normal(0, 1, 8000))
-    assert run(x, 1.0, 0.9, 0, 1)[0] == -2
-    assert run(x, 1.0, 0.9, 5000, 1)[0] == -2
-    flat = f16(np.zeros(20000))
-    assert run(flat, 1.0, 0.9, 10, 1) == (0, 0xFFFFFFFF)
+    run, history = _gpu_sampler(cm)
+    cm.call("cactus_hip_sample_history_reset", None)
+    s = orc.OracleSampler()
+    rng = np.random.default_rng(41)
+    cases = [(f16(rng.normal(0, 1, 151936)), (1.0, 0.9, 0)),
+             (f16(np.zeros(20000)), (1.0, 0.9, 10)),
+             (f16(np.zeros(20000)), (1.0, 0.3, 0)),
+             (f16(np.round(rng.normal(0, 1, 151936) * 4) / 4), (1.0, 0.7, 0)),
+             (f16(np.round(rng.normal(0, 1, 60000) * 2) / 2), (3.0, 0.5, 40000))]
+    for i, (x, cfg) in enumerate(cases):
+        for rep in range(3):
+            say("sampler large top-p", i, cfg, rep)
+            seed = int(rng.integers(1, 2**31))
+            rc, got = run(x, *cfg, seed)
+            assert rc == 0
+            assert got < x.size
+            assert got == s.sample(x, *cfg, seed), (i, cfg, rep)
+    assert (history() == s.history()).all()
 
 
 @pytest.mark.gpu

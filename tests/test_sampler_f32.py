@@ -187,8 +187,7 @@ def test_sampler_f32_ties_and_signed_zero(hip_ready, orc):
 
 @pytest.mark.gpu
 def test_sampler_f32_edges_and_refusals(hip_ready, orc):
-    """Infinities, more than 128 bias entries (refused) and more than 16384
-    entries reaching top-p (0xFFFFFFFF)."""
+    """Infinities and more than 128 bias entries (refused)."""
     cm = hip_ready
     run = _gpu_sampler_f32(cm)
     say("sampler_f32 edges")
@@ -197,5 +196,26 @@ def test_sampler_f32_edges_and_refusals(hip_ready, orc):
     assert run(f32([-np.inf, 2.0, -np.inf]), 1.0, 0.5, 2, 3) == (0, 1)
     x = f32(np.random.default_rng(2).normal(0, 1, 3000))
     assert run(x, 1.0, 0.0, 0, 1, [(i, 1.0) for i in range(129)])[0] == -2
-    flat = f32(np.zeros(20000))
-    assert run(flat, 1.0, 0.9, 0, 1) == (0, 0xFFFFFFFF)
+
+
+@pytest.mark.gpu
+def test_sampler_f32_large_top_p(hip_ready, orc):
+    """More than 16384 entries reaching top-p (min-p keeps a flat row whole):
+    20000 ties, a flat high-temperature row of 151936 logits and a coarse
+    grid whose ties straddle the cut; the oracle's token every time."""
+    cm = hip_ready
+    run = _gpu_sampler_f32(cm)
+    rng = np.random.default_rng(43)
+    cases = [(f32(np.zeros(20000)), (1.0, 0.9, 0)),
+             (f32(np.zeros(20000)), (1.0, 0.2, 0)),
+             (f32(rng.normal(0, 0.05, 151936)), (4.0, 0.95, 0)),
+             (f32(np.round(rng.normal(0, 0.1, 151936) * 20) / 20), (2.0, 0.6, 0)),
+             (f32(rng.normal(0, 0.02, 80000)), (1.0, 0.5, 50000))]
+    for i, (x, cfg) in enumerate(cases):
+        for rep in range(3):
+            say("sampler_f32 large top-p", i, cfg, rep)
+            seed = int(rng.integers(1, 2**31))
+            rc, got = run(x, *cfg, seed)
+            assert rc == 0
+            assert got < x.size
+            assert got == orc.sample_f32(x, *cfg, seed), (i, cfg, rep)
