@@ -476,6 +476,8 @@ def main():
     ap.add_argument("--skip-decode", action="store_true")
     ap.add_argument("--decode-only", action="store_true")
     ap.add_argument("--attention-only", action="store_true")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the prefill matmul leg (configs 2 and 3), e.g. under rocprofv3 --pmc with --eager")
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--eager", action="store_true",
                     help="no HIP graphs: matmuls launched directly and the decode step enqueued per token "
@@ -498,6 +500,9 @@ def main():
         return
     if args.attention_only:
         print(json.dumps(bench_attention()), flush=True)
+        return
+    if args.gemm_only:
+        print(json.dumps(bench_prefill_gemms(eager=args.eager)), flush=True)
         return
     if args.copy_calibration:
         n = 1 << 30
