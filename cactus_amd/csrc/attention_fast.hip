@@ -559,6 +559,361 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
     if (tid == 0) __hip_atomic_store(a.cnt + bg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ------------------------------------------------ prefill (many query rows)
+// Causal hybrid attention of a prefill chunk -- S query rows against the
+// INT8 cache and the chunk's own FP16 rows (kernel_attention.cpp:257-482)
+// -- as flash attention on FP16 MFMA (v_mfma_f32_16x16x32_f16), tolerance
+// mode.  A workgroup owns 16 * W query vectors of one KV head (vector m:
+// row m / GQ, head m % GQ; 16 per wave) and walks the keys in 32-key tiles
+// staged in LDS as FP16.  Key codes are exact in fp16 and their per-key
+// scale multiplies the score (s = scale_k (q . code) scale); value rows are
+// staged as fp16(code * scale_v) (normal-range fp16, relative error 2^-12),
+// so the weights enter the P V product as fp16(p) without a scale that
+// could push them into fp16's subnormal range.  FP16 rows carry scale 1.  Each wave computes the tile's
+// transposed scores S^T = K Q^T, so that a lane's scores are already the A
+// operand of the P V product for the same keys (lane l holds vector l % 16
+// and keys {4g + i, 16 + 4g + i}, g = l / 16); the V operand reads the
+// tile transposed in LDS in that key order.  The online softmax state
+// (running max, sum) stays in fp32 per vector, the output accumulates in
+// fp32 and is divided once at the end.
+constexpr int PF_T = 32;    // keys per tile
+
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h16x4 __attribute__((ext_vector_type(4)));
+
+struct PrefillArgs {
+    const uint16_t* q;        // [B][S][Hq][D]
+    const int8_t* kc;         // [B][cache][Hkv][D]
+    const int8_t* vc;
+    const float* ks;          // [cache][Hkv][nqg] (no batch offset, kernel_attention.cpp:353, :424)
+    const float* vs;
+    const uint16_t* kn;       // [B][new][Hkv][D]
+    const uint16_t* vn;
+    uint16_t* o;              // [B][S][Hq][D]
+    float* part;              // split partials [B*Hkv][nqb][nsplit][16 W][D + 4]: acc[D], max, sum
+    int B, S, Hq, Hkv, nqg;
+    int nsplit, tps;          // key splits per query block (1: no partials), tiles per split
+    size_t cache_len, new_len, pos_off;
+    float scale;
+};
+
+// tiles (32 keys) a query block reads: keys up to its last row's position
+__device__ __forceinline__ int pf_block_tiles(const PrefillArgs& a, int gm0, int nv, int gq) {
+    const int last_row = min(a.S - 1, (gm0 + nv - 1) / gq);
+    size_t kv_end = a.pos_off + (size_t)last_row + 1;
+    const size_t Skv = a.cache_len + a.new_len;
+    if (kv_end > Skv) kv_end = Skv;
+    return (int)((kv_end + PF_T - 1) / PF_T);
+}
+
+// max / sum over the four lanes l % 16 == c of a wave (lanes c, c + 16,
+// c + 32, c + 48), same bits in all four: v_permlane16_swap_b32 /
+// v_permlane32_swap_b32 on a value and its copy leave the lane's own value
+// in one register and its partner's (lane l ^ 16, l ^ 32) in the other.
+// Issued as inline assembly: the builtins' second result is lowered as a
+// copy of the first by this compiler.
+__device__ __forceinline__ void swap_pair16(float v, float& x, float& y) {
+    x = v;
+    y = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void swap_pair32(float v, float& x, float& y) {
+    x = v;
+    y = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ float xrow_max(float v) {
+    float x, y;
+    swap_pair16(v, x, y);
+    swap_pair32(__builtin_fmaxf(x, y), x, y);
+    return __builtin_fmaxf(x, y);
+}
+__device__ __forceinline__ float xrow_sum(float v) {
+    float x, y;
+    swap_pair16(v, x, y);
+    swap_pair32(x + y, x, y);
+    return x + y;
+}
+
+template <int D, int GQ, int W, int NB>
+__global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a) {
+    static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+    static_assert(64 * W >= 2 * D, "staging threads: 32 keys x D/16 pieces");
+    constexpr int NV = 16 * W;                 // query vectors per workgroup
+    constexpr int KS = D + 8;                  // LDS row of a key tile, halves
+    constexpr int VS = PF_T + 8;               // LDS row of a transposed value tile, halves
+    constexpr int CPR = D / 16;                // 16-dim pieces per key row
+    constexpr int NC = D / 32;                 // 32-dim MFMA steps of a score
+    constexpr int ND = D / 16;                 // 16-dim output blocks
+    __shared__ __align__(16) _Float16 ksh[2][PF_T][KS];
+    __shared__ __align__(16) _Float16 vt[2][D][VS];
+    __shared__ __align__(16) float ksc[2][PF_T];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lg = lane >> 4, lr = lane & 15;
+    const int bg = blockIdx.y, b = bg / a.Hkv, g = bg % a.Hkv;
+    const int qb = blockIdx.x / a.nsplit, sp_ = blockIdx.x % a.nsplit;
+    const int gm0 = qb * NV;
+    const size_t Skv = a.cache_len + a.new_len;
+    const int last_row = min(a.S - 1, (gm0 + NV - 1) / GQ);
+    size_t kv_end = a.pos_off + (size_t)last_row + 1;
+    if (kv_end > Skv) kv_end = Skv;
+    const int ntile_all = (int)((kv_end + PF_T - 1) / PF_T);
+    // this workgroup's split of the tiles
+    const int t_begin = sp_ * a.tps;
+    const int nt = min(ntile_all - t_begin, a.tps);
+    if (nt <= 0) return;   // no keys here; the combine counts only splits that hold some
+
+    // ---- this lane's query vector lr (B operand of S^T = K Q^T)
+    const int vm = gm0 + wid * 16 + lr;
+    const int vrow = vm / GQ;
+    const bool vok = vrow < a.S;
+    const size_t vpos = a.pos_off + (size_t)vrow;
+    h16x8 qv[NC];
+    {
+        const uint16_t* qp = a.q + (((size_t)b * a.S + (vok ? vrow : 0)) * a.Hq + (size_t)g * GQ + vm % GQ) * D;
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const uint4 u = vok ? *reinterpret_cast<const uint4*>(qp + 32 * c + 8 * lg) : make_uint4(0, 0, 0, 0);
+            qv[c] = __builtin_bit_cast(h16x8, u);
+        }
+    }
+
+    // ---- tile staging: thread -> (key sj, 16-dim piece sp), lanes of a
+    // wave on 32 different keys so the transposed value writes spread over
+    // the LDS banks.  Every tile issues the same loads -- the key's INT8
+    // cache piece and its FP16 new-row piece, each from a clamped in-bounds
+    // row -- and picks one when staging, so the loads take no branch and
+    // the compiler keeps NB tiles in flight (slot t % NB).
+    const int sj = tid % PF_T, sp = tid / PF_T;
+    const bool stager = sp < CPR;
+    const size_t rstride = (size_t)a.Hkv * D;   // elements between consecutive keys
+    const int8_t* kcb = nullptr;
+    const int8_t* vcb = nullptr;
+    const float* ksb = nullptr;
+    const float* vsb = nullptr;
+    const uint16_t* knb = nullptr;
+    const uint16_t* vnb = nullptr;
+    {
+        // a valid stand-in for a missing part (its values are never used)
+        const uint16_t* any16 = a.q;
+        if (a.cache_len > 0) {
+            kcb = a.kc + ((size_t)b * a.cache_len * a.Hkv + g) * D + 16 * sp;
+            vcb = a.vc + ((size_t)b * a.cache_len * a.Hkv + g) * D + 16 * sp;
+            ksb = a.ks + (size_t)g * a.nqg;
+            vsb = a.vs + (size_t)g * a.nqg;
+        } else {
+            kcb = vcb = reinterpret_cast<const int8_t*>(any16);
+            ksb = vsb = reinterpret_cast<const float*>(any16);
+        }
+        if (a.new_len > 0) {
+            knb = a.kn + ((size_t)b * a.new_len * a.Hkv + g) * D + 16 * sp;
+            vnb = a.vn + ((size_t)b * a.new_len * a.Hkv + g) * D + 16 * sp;
+        } else {
+            knb = vnb = any16;
+        }
+    }
+    const int clen = (int)a.cache_len, nlen = (int)a.new_len;
+    const size_t cstride = a.cache_len > 0 ? rstride : 0;   // stand-ins do not move
+    const size_t nstride = a.new_len > 0 ? rstride : 0;
+    const size_t sstride = a.cache_len > 0 ? (size_t)a.Hkv * a.nqg : 0;
+    struct Raw {
+        uint4 kc, vc;            // 16 INT8 codes
+        uint4 kn[2], vn[2];      // 16 FP16 values
+        float ks, vs;
+    };
+    Raw raw[NB];
+    auto fetch = [&](int t, Raw& r) {
+        const int kp = t * PF_T + sj;
+        const int ci = min(kp, max(clen - 1, 0)), ni = min(max(kp - clen, 0), max(nlen - 1, 0));
+        r.kc = *reinterpret_cast<const uint4*>(kcb + (size_t)ci * cstride);
+        r.vc = *reinterpret_cast<const uint4*>(vcb + (size_t)ci * cstride);
+        const uint4* k4 = reinterpret_cast<const uint4*>(knb + (size_t)ni * nstride);
+        const uint4* v4 = reinterpret_cast<const uint4*>(vnb + (size_t)ni * nstride);
+        r.kn[0] = k4[0];
+        r.kn[1] = k4[1];
+        r.vn[0] = v4[0];
+        r.vn[1] = v4[1];
+        r.ks = ksb[(size_t)ci * sstride];
+        r.vs = vsb[(size_t)ci * sstride];
+    };
+    auto stage = [&](int t, int buf, const Raw& r) {
+        if (!stager) return;
+        const int kp = t * PF_T + sj;
+        const bool live = kp < (int)kv_end, cached = kp < clen;
+        h16x8 k0, k1;
+        _Float16 vh[16];
+        if (cached) {
+            const uint32_t kw[4] = {r.kc.x, r.kc.y, r.kc.z, r.kc.w};
+            const uint32_t vw[4] = {r.vc.x, r.vc.y, r.vc.z, r.vc.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                k0[e] = (_Float16)(float)(int8_t)(kw[e >> 2] >> (8 * (e & 3)));
+                k1[e] = (_Float16)(float)(int8_t)(kw[2 + (e >> 2)] >> (8 * (e & 3)));
+            }
+#pragma unroll
+            for (int e = 0; e < 16; e++) vh[e] = (_Float16)((float)(int8_t)(vw[e >> 2] >> (8 * (e & 3))) * r.vs);
+        } else {
+            k0 = __builtin_bit_cast(h16x8, r.kn[0]);
+            k1 = __builtin_bit_cast(h16x8, r.kn[1]);
+            const h16x8 v0 = __builtin_bit_cast(h16x8, r.vn[0]), v1 = __builtin_bit_cast(h16x8, r.vn[1]);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                vh[e] = v0[e];
+                vh[8 + e] = v1[e];
+            }
+        }
+        if (!live) {
+            // keys past the block's causal end: zero values (their weights are 0)
+#pragma unroll
+            for (int e = 0; e < 16; e++) vh[e] = (_Float16)0.0f;
+        }
+        *reinterpret_cast<h16x8*>(&ksh[buf][sj][16 * sp]) = k0;
+        *reinterpret_cast<h16x8*>(&ksh[buf][sj][16 * sp + 8]) = k1;
+#pragma unroll
+        for (int e = 0; e < 16; e++) vt[buf][16 * sp + e][sj] = vh[e];
+        if (sp == 0) ksc[buf][sj] = (cached ? r.ks : 1.0f) * a.scale;
+    };
+
+    constexpr float LOG2E = 1.4426950408889634f;
+    const float NEG_INF = -__builtin_inff();
+    float m_run = NEG_INF, l_run = 0.0f;
+    f32x4 acc[ND];   // O^T: lane l holds dims 16 db + 4 lg + i of vector lr
+#pragma unroll
+    for (int db = 0; db < ND; db++) acc[db] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int u = 0; u < NB; u++) fetch(t_begin + u, raw[u]);   // clamped rows: in bounds past the split too
+    stage(t_begin, 0, raw[0]);
+    __syncthreads();
+    for (int l0 = 0; l0 < nt; l0 += NB)
+#pragma unroll
+    for (int u = 0; u < NB; u++) {
+        const int tl = l0 + u;
+        if (tl >= nt) break;
+        const int t = t_begin + tl;
+        const int buf = tl & 1;
+        // scores S^T for keys 16h + 4lg + i of the tile, vector lr
+        f32x4 st[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            st[h] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NC; c++) {
+                const h16x8 kv = *reinterpret_cast<const h16x8*>(&ksh[buf][16 * h + lr][32 * c + 8 * lg]);
+                st[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv[c], st[h], 0, 0, 0);
+            }
+        }
+        float s[8];
+        float mx = NEG_INF;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const f32x4 ksv = *reinterpret_cast<const f32x4*>(&ksc[buf][16 * h + 4 * lg]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const size_t kp = (size_t)t * PF_T + 16 * h + 4 * lg + i;
+                const bool ok = vok && kp < kv_end && kp <= vpos;
+                s[4 * h + i] = ok ? st[h][i] * ksv[i] : NEG_INF;
+                mx = __builtin_fmaxf(mx, s[4 * h + i]);
+            }
+        }
+        mx = xrow_max(mx);
+        const float m_new = __builtin_fmaxf(m_run, mx);
+        const bool live = m_new > NEG_INF;
+        const float corr = live ? fast_exp2((m_run - m_new) * LOG2E) : 1.0f;
+        float psum = 0.0f;
+        h16x8 pa;   // P^T operand: keys {4 lg + j, 16 + 4 lg + j} of vector lr
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float pv = (live && s[j] > NEG_INF) ? fast_exp2((s[j] - m_new) * LOG2E) : 0.0f;
+            psum += pv;
+            pa[j] = (_Float16)pv;
+        }
+        l_run = l_run * corr + xrow_sum(psum);
+        m_run = m_new;
+        // O^T += V^T P^T: A = V^T (dims 16 db + lr, the same 8 keys)
+#pragma unroll
+        for (int db = 0; db < ND; db++) {
+            const h16x4 v0 = *reinterpret_cast<const h16x4*>(&vt[buf][16 * db + lr][4 * lg]);
+            const h16x4 v1 = *reinterpret_cast<const h16x4*>(&vt[buf][16 * db + lr][16 + 4 * lg]);
+            const h16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pa, acc[db] * corr, 0, 0, 0);
+        }
+        // the next tile into the other LDS buffer (its last readers finished
+        // before the previous barrier), then tile t + NB into this slot
+        if (tl + 1 < nt) stage(t + 1, buf ^ 1, raw[(u + 1) % NB]);
+        if (tl + NB < nt) fetch(t + NB, raw[u]);
+        __syncthreads();
+    }
+
+    // ---- output: vector lr, dims 16 db + 4 lg + i
+    if (a.nsplit > 1) {
+        // this split's partial (acc, running max, sum) of the vector
+        const int nqb = (int)gridDim.x / a.nsplit;
+        float* pp = a.part + ((((size_t)bg * nqb + qb) * a.nsplit + sp_) * NV + wid * 16 + lr) * (D + 4);
+#pragma unroll
+        for (int db = 0; db < ND; db++) *reinterpret_cast<f32x4*>(pp + 16 * db + 4 * lg) = acc[db];
+        if (lg == 0) {
+            pp[D] = m_run;
+            pp[D + 1] = l_run;
+        }
+        return;
+    }
+    if (!vok) return;
+    uint16_t* op = a.o + (((size_t)b * a.S + vrow) * a.Hq + (size_t)g * GQ + vm % GQ) * D;
+    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+#pragma unroll
+    for (int db = 0; db < ND; db++) {
+        const uint32_t lo = (uint32_t)f2h(acc[db][0] * inv) | ((uint32_t)f2h(acc[db][1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f2h(acc[db][2] * inv) | ((uint32_t)f2h(acc[db][3] * inv) << 16);
+        *reinterpret_cast<uint2*>(op + 16 * db + 4 * lg) = make_uint2(lo, hi);
+    }
+}
+
+// Combine of the key splits: grid (query blocks, B * Hkv), 256 threads;
+// four threads per query vector, D/4 dims each.  M = max_s M_s,
+// L = sum_s e^(M_s - M) l_s, o = sum_s e^(M_s - M) acc_s / L.
+template <int D, int GQ, int NV>
+__global__ void __launch_bounds__(256) attn_prefill_combine_kernel(PrefillArgs a) {
+    static_assert(NV * 4 == 256, "four threads per vector");
+    constexpr int DQ = D / 4;
+    constexpr float LOG2E = 1.4426950408889634f;
+    const int tid = threadIdx.x, v = tid / 4, dq = (tid % 4) * DQ;
+    const int qb = blockIdx.x, bg = blockIdx.y, b = bg / a.Hkv, g = bg % a.Hkv;
+    const int gm0 = qb * NV;
+    const int ns = min(a.nsplit, (pf_block_tiles(a, gm0, NV, GQ) + a.tps - 1) / a.tps);
+    const int vm = gm0 + v, row = vm / GQ;
+    if (row >= a.S) return;
+    const float* pb = a.part + (((size_t)bg * gridDim.x + qb) * a.nsplit * NV + v) * (D + 4);
+    const size_t sstep = (size_t)NV * (D + 4);
+    float M = -__builtin_inff();
+    for (int s = 0; s < ns; s++) M = __builtin_fmaxf(M, pb[s * sstep + D]);
+    float L = 0.0f;
+    float out[DQ];
+#pragma unroll
+    for (int e = 0; e < DQ; e++) out[e] = 0.0f;
+    for (int s = 0; s < ns; s++) {
+        const float* ps = pb + s * sstep;
+        const float m = ps[D];
+        const float w = m > -__builtin_inff() ? fast_exp2((m - M) * LOG2E) : 0.0f;
+        L = __builtin_fmaf(w, ps[D + 1], L);
+#pragma unroll
+        for (int e = 0; e < DQ; e += 4) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(ps + dq + e);
+            out[e] = __builtin_fmaf(w, x[0], out[e]);
+            out[e + 1] = __builtin_fmaf(w, x[1], out[e + 1]);
+            out[e + 2] = __builtin_fmaf(w, x[2], out[e + 2]);
+            out[e + 3] = __builtin_fmaf(w, x[3], out[e + 3]);
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    uint16_t* op = a.o + (((size_t)b * a.S + row) * a.Hq + (size_t)g * GQ + vm % GQ) * D + dq;
+#pragma unroll
+    for (int e = 0; e < DQ; e += 2)
+        *reinterpret_cast<uint32_t*>(op + e) = (uint32_t)f2h(out[e] * inv) | ((uint32_t)f2h(out[e + 1] * inv) << 16);
+}
+
 // ------------------------------------------------ per-(device, stream) workspace
 struct FastWs {
     float* part = nullptr;
@@ -654,6 +1009,56 @@ int attention_fast_hybrid(const uint16_t* q, const int8_t* kc, const int8_t* vc,
     return launch_fast<true, false>(a, (int)d, (int)(Hq / Hkv), as_stream(stream));
 }
 
+bool fast_prefill_supported(size_t d, size_t gq) {
+    return (d == 64 || d == 128) && (gq == 1 || gq == 2 || gq == 4);
+}
+
+int attention_prefill_fast(const uint16_t* q, const int8_t* kc, const int8_t* vc, const float* ks, const float* vs,
+                           const uint16_t* k_new, const uint16_t* v_new, uint16_t* o, size_t B, size_t S,
+                           size_t cache_len, size_t new_len, size_t Hq, size_t Hkv, size_t d, float scale,
+                           size_t pos_off, size_t qgs, void* stream) {
+    constexpr int W = 4, NB = 3, NV = 16 * W;
+    PrefillArgs a{};
+    a.q = q; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.kn = k_new; a.vn = v_new; a.o = o;
+    a.B = (int)B; a.S = (int)S; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.nqg = (int)((d + qgs - 1) / qgs);
+    a.cache_len = cache_len; a.new_len = new_len; a.pos_off = pos_off; a.scale = scale;
+    const int gq = (int)(Hq / Hkv);
+    const size_t nqb = (S * gq + NV - 1) / NV;
+    // key splits: enough workgroups to cover the CUs, at least 8 tiles each
+    size_t kv_last = pos_off + S;
+    if (kv_last > cache_len + new_len) kv_last = cache_len + new_len;
+    const size_t tiles = (kv_last + PF_T - 1) / PF_T;
+    size_t nsplit = (512 + nqb * B * Hkv - 1) / (nqb * B * Hkv);
+    const size_t max_split = (tiles + 7) / 8;
+    if (nsplit > max_split) nsplit = max_split;
+    if (nsplit > 16) nsplit = 16;
+    if (nsplit < 1) nsplit = 1;
+    a.tps = (int)((tiles + nsplit - 1) / nsplit);
+    a.nsplit = (int)((tiles + a.tps - 1) / a.tps);
+    if (a.nsplit < 1) a.nsplit = 1;
+    if (a.nsplit > 1) {
+        FastWs w;
+        const int rc = fast_ws(stream, B * Hkv * nqb * (size_t)a.nsplit * NV * (d + 4), 0, &w);
+        if (rc) return rc;
+        a.part = w.part;
+    }
+    const dim3 grid((unsigned)(nqb * a.nsplit), (unsigned)(B * Hkv));
+    const dim3 cgrid((unsigned)nqb, (unsigned)(B * Hkv));
+    auto go = [&](auto kern, auto comb) {
+        hipLaunchKernelGGL(kern, grid, dim3(64 * W), 0, as_stream(stream), a);
+        int rc = check_launch("attention (prefill, MFMA)");
+        if (rc || a.nsplit == 1) return rc;
+        hipLaunchKernelGGL(comb, cgrid, dim3(256), 0, as_stream(stream), a);
+        return check_launch("attention (prefill, split combine)");
+    };
+#define PF_CASE(D_, G_) \
+    if (d == D_ && gq == G_) \
+        return go(attn_prefill_mfma_kernel<D_, G_, W, NB>, attn_prefill_combine_kernel<D_, G_, NV>);
+    PF_CASE(128, 2) PF_CASE(128, 1) PF_CASE(128, 4) PF_CASE(64, 2) PF_CASE(64, 1) PF_CASE(64, 4)
+#undef PF_CASE
+    return fail(CACTUS_HIP_EUNSUPPORTED, "attention (prefill, MFMA): head_dim 64/128 with 1, 2 or 4 query heads per KV head");
+}
+
 }  // namespace cactus_hip
 
 using namespace cactus_hip;
@@ -685,11 +1090,27 @@ int cactus_hip_attention_hybrid_int8_fp16_fast(const uint16_t* q, const int8_t* 
                                                size_t position_offset, int is_causal, size_t quant_group_size,
                                                void* stream) {
     if (batch == 0 || seq_len == 0 || num_q_heads == 0 || head_dim == 0) return CACTUS_HIP_OK;
+    const bool aligned16 = ((uintptr_t)k_cached & 15) == 0 && ((uintptr_t)v_cached & 15) == 0;
+    // prefill rows: flash attention on FP16 MFMA
+    const bool prefill = seq_len > 1 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && is_causal &&
+                         fast_prefill_supported(head_dim, num_q_heads / num_kv_heads) &&
+                         quant_group_size >= head_dim && batch * num_kv_heads < 65536 && aligned16 &&
+                         ((uintptr_t)q & 15) == 0 && ((uintptr_t)k_new & 15) == 0 && ((uintptr_t)v_new & 15) == 0 &&
+                         seq_len * (num_q_heads / num_kv_heads) < (1ull << 31);
+    if (prefill) {
+        CH_REQUIRE(q && o, "attention_hybrid_fast: null pointer");
+        CH_REQUIRE(cache_len == 0 || (k_cached && v_cached && k_scales && v_scales),
+                   "attention_hybrid_fast: null cache pointer");
+        CH_REQUIRE(new_len == 0 || (k_new && v_new), "attention_hybrid_fast: null new K/V pointer");
+        if (scale == 0.0f) scale = 1.0f / sqrtf((float)head_dim);
+        return attention_prefill_fast(q, k_cached, v_cached, k_scales, v_scales, k_new, v_new, o, batch, seq_len,
+                                      cache_len, new_len, num_q_heads, num_kv_heads, head_dim, scale,
+                                      position_offset, quant_group_size, stream);
+    }
     const bool fast = num_kv_heads > 0 && num_q_heads % num_kv_heads == 0 && is_causal &&
                       fast_attention_supported(seq_len, head_dim, num_q_heads / num_kv_heads, nullptr) &&
                       quant_group_size >= head_dim && batch * num_kv_heads < 65536 &&
-                      cache_len + new_len <= FA_MAX_KEYS_HYBRID &&
-                      ((uintptr_t)k_cached & 15) == 0 && ((uintptr_t)v_cached & 15) == 0;
+                      cache_len + new_len <= FA_MAX_KEYS_HYBRID && aligned16;
     if (!fast)
         return cactus_hip_attention_hybrid_int8_fp16(q, k_cached, v_cached, k_scales, v_scales, k_new, v_new, o,
                                                      batch, seq_len, cache_len, new_len, num_q_heads,

@@ -9,8 +9,10 @@ head_dim 128, 4096 context, RoPE theta 1e6 applied at positions 4095 for
 q and 0..4095 for k) in its FP16 and INT8-cache forms, split edges (1, 255,
 256, 257 keys), GQA 1/2/4, head_dim 64, batch 2, a sliding window, two new
 rows, a causal cut inside the keys, peaked scores, and shapes the fast
-path hands to the exact kernels (prefill rows, head_dim 40, a mask), which
-must then be bit-identical to the oracle.
+path hands to the exact kernels (FP16 prefill rows, head_dim 40, a mask),
+which must then be bit-identical to the oracle.  Prefill rows of the hybrid
+form run the FP16-MFMA flash kernel (chunk shapes of a 4096-token prefill,
+with and without key splits and their combine).
 """
 import ctypes
 import math
@@ -208,3 +210,46 @@ def test_decode_prep_attention_fast(dev, orc, cache, Hq, Hkv, d):
             assert (x == y).all(), "appended cache row"
         close(outs[i], outs[0], "decode_prep_attention_fast")
     assert (outs[1] == outs[2]).all(), "second launch on the same workspace"
+
+
+@pytest.mark.parametrize("B,cache,new,Hq,Hkv,d,qmul", [
+    (1, 3840, 256, 16, 8, 128, 1.0),   # the last 256-row chunk of a 4096-token prefill
+    (1, 0, 256, 16, 8, 128, 1.0),      # the first chunk: new rows only
+    (1, 700, 100, 8, 2, 128, 1.0),     # GQA 4, ragged row count
+    (2, 129, 37, 4, 4, 64, 1.0),       # batch 2, head_dim 64, GQA 1
+    (1, 1000, 256, 16, 8, 128, 6.0),   # peaked scores
+    (1, 3, 5, 4, 2, 128, 1.0),         # tiny
+])
+def test_attention_hybrid_prefill_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul):
+    """Prefill rows (S = new rows at positions cache..cache+new-1, causal)
+    through the FP16-MFMA flash kernel, against the oracle's hybrid
+    attention within 1e-3 + 1e-2 |ref|.  The peaked case keeps the score
+    spread below ~88: the reference rescales by expf(previous block max -
+    this block max) (kernel_attention.cpp:395-403), which overflows when a
+    later block's maximum lies that far below an earlier one, and then
+    writes a zero row (:465-469); the tolerance mode computes the softmax
+    itself there."""
+    say("attention_hybrid_prefill_fast", B, cache, new, Hq, Hkv, d, qmul)
+    rng = np.random.default_rng(cache * 5 + new + d)
+    kf = _roped(orc, f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d))), 0)
+    vf = f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d)))
+    kc = np.zeros((B, max(cache, 1), Hkv, d), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((B, max(cache, 1), Hkv, 1), np.float32)
+    vs = np.zeros_like(ks)
+    for b in range(B):
+        kc[b], ks[b] = orc.quantize_kv(kf[b])
+        vc[b], vs[b] = orc.quantize_kv(vf[b])
+    kc, vc, ks, vs = (np.ascontiguousarray(x[:, :cache]) for x in (kc, vc, ks[:1], vs[:1]))
+    kn = _roped(orc, f16(rng.normal(0, 1, (B, new, Hkv, d))), cache)
+    vn = f16(rng.normal(0, 1, (B, new, Hkv, d)))
+    q = _roped(orc, f16(rng.normal(0, 1, (B, new, Hq, d)) * qmul), cache)
+    scale = 1.0 / math.sqrt(d)
+    ref = orc.attention_hybrid(q, kc if cache else None, vc if cache else None, ks if cache else None,
+                               vs if cache else None, kn, vn, scale, pos_off=cache)
+    o = dev.empty(q.nbytes)
+    P = (lambda a: dev.put(a) if cache else None)
+    dev.cm.call("cactus_hip_attention_hybrid_int8_fp16_fast", dev.put(q), P(kc), P(vc), P(ks), P(vs), dev.put(kn),
+                dev.put(vn), o.ptr, B, new, cache, new, Hq, Hkv, d, ctypes.c_float(scale), cache, 1, 128, None)
+    err = close(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid_prefill_fast")
+    print(f"[prefill fast] max abs error {err:.2e}", flush=True)
