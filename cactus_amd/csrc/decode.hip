@@ -45,6 +45,7 @@ __global__ void dec_embed_kernel(const uint16_t* __restrict__ table, const uint3
 
 // ----------------------------------------------------------------- GEMV
 enum { PRO_PLAIN = 0, PRO_NORM = 1 };
+constexpr int DEC_SCL = 2;   // group scales per thread of a decode matmul tile
 enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SILUMUL = 2 };
 
 struct DecSeg {
@@ -93,33 +94,11 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     };
     auto vrow_valid = [&](int vr) { return EPI == EPI_SILUMUL ? ((vr < rows ? vr : vr - rows) < nr) : vr < nr; };
 
-    // 1. weights in flight first
-    i32x4 wreg[CH];
-    int crow[CH], ccol[CH];
-#pragma unroll
-    for (int i = 0; i < CH; i++) {
-        const int c = tid + i * GEMV_THREADS;
-        crow[i] = c / cpr;
-        ccol[i] = c - crow[i] * cpr;
-        wreg[i] = (i32x4){0, 0, 0, 0};
-        if (crow[i] < vrows && vrow_valid(crow[i]))
-            wreg[i] = __builtin_nontemporal_load(
-                reinterpret_cast<const i32x4*>(row_ptr(crow[i]) + (size_t)ccol[i] * 16));
-    }
-    // 2. group scales
-    for (int i = tid; i < vrows * G; i += GEMV_THREADS) {
-        const int vr = i / G, g = i % G;
-        uint16_t v = 0;
-        if (vrow_valid(vr)) {
-            if (EPI == EPI_SILUMUL && vr >= rows) v = a.seg[1].Bs[(size_t)(n0 + vr - rows) * G + g];
-            else v = sg.Bs[(size_t)(n0 + vr) * G + g];
-        }
-        scl[i] = v;
-    }
-    // 3. activation: optional RMSNorm, then per-row quantization.  Thread t
-    // owns the 8-element chunks t + 256 j in registers; the LDS copy feeds
-    // the RMS chains.
-    constexpr int CPT = 4;    // chunks per thread (K <= 8192)
+    // 1. loads, in the order they are needed: the activation row (and the
+    // RMSNorm weights, the residual) first -- the prologue waits for these
+    // only, its loads being the oldest in flight -- then the weight tile,
+    // then the group scales into registers
+    constexpr int CPT = 4;    // activation chunks of 8 per thread (K <= 8192)
     const int nch = K / 8;
     uint4 xv[CPT], wv[CPT];
 #pragma unroll
@@ -132,8 +111,39 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
             if (PRO == PRO_NORM) wv[j] = reinterpret_cast<const uint4*>(a.norm_w)[c];
         }
     }
-    uint16_t resv = 0;   // residual of this thread's first row, early
-    if (EPI == EPI_RESID && tid < nr) resv = a.res[n0 + tid];
+    // the residual of this thread's first row (clamped row: branch-free, so
+    // no wait is forced here)
+    uint16_t resv = 0;
+    if (EPI == EPI_RESID) resv = a.res[n0 + min(tid, nr - 1)];
+    i32x4 wreg[CH];
+    int crow[CH], ccol[CH];
+#pragma unroll
+    for (int i = 0; i < CH; i++) {
+        const int c = tid + i * GEMV_THREADS;
+        crow[i] = c / cpr;
+        ccol[i] = c - crow[i] * cpr;
+        // branch-free: a chunk outside the tile reads row 0 of the tile and
+        // its dot product is dropped below
+        const int vr = crow[i] < vrows && vrow_valid(crow[i]) ? crow[i] : 0;
+        wreg[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(row_ptr(vr) + (size_t)ccol[i] * 16));
+    }
+    // group scales: at most DEC_SCL per thread (checked by the launcher),
+    // loaded branch-free from clamped entries and zeroed when stored, so the
+    // compiler does not wait for them (nor for the weights before them) here
+    uint16_t sreg[DEC_SCL];
+    bool sval[DEC_SCL];
+#pragma unroll
+    for (int u = 0; u < DEC_SCL; u++) {
+        const int i = tid + u * GEMV_THREADS;
+        const int vr = i < vrows * G ? i / G : 0, g = i < vrows * G ? i % G : 0;
+        sval[u] = i < vrows * G && vrow_valid(vr);
+        const bool up = EPI == EPI_SILUMUL && vr >= rows;
+        const int r = sval[u] ? (up ? vr - rows : vr) : 0;
+        sreg[u] = (up && sval[u] ? a.seg[1].Bs : sg.Bs)[(size_t)(n0 + r) * G + g];
+    }
+    // 2. activation: optional RMSNorm, then per-row quantization.  Thread t
+    // owns the 8-element chunks t + 256 j in registers; the LDS copy feeds
+    // the RMS chains.
     auto elem = [](const uint4& v, int e) -> uint16_t {
         const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
         return (uint16_t)(e & 1 ? w >> 16 : w & 0xFFFF);
@@ -193,9 +203,12 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
             }
         }
     }
+#pragma unroll
+    for (int u = 0; u < DEC_SCL; u++)
+        if (tid + u * GEMV_THREADS < vrows * G) scl[tid + u * GEMV_THREADS] = sval[u] ? sreg[u] : (uint16_t)0;
     __syncthreads();
 
-    // 4. dot products and exact group sums
+    // 3. dot products and exact group sums
 #pragma unroll
     for (int i = 0; i < CH; i++) {
         const bool valid = crow[i] < vrows && vrow_valid(crow[i]);
@@ -206,7 +219,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     }
     __syncthreads();
 
-    // 5. reference epilogue
+    // 4. reference epilogue
     auto chain = [&](int vr) {
         float rs = 0.0f;
         const int32_t* ar = acc + vr * G;
@@ -261,6 +274,7 @@ static int launch_dec_gemv(DecGemvArgs a, int nseg, hipStream_t st) {
     if (rows < 1) rows = 1;
     while (rows > 1 && (size_t)ceil_div(totalN, rows) < 512) rows = (rows + 1) / 2;
     CH_REQUIRE(rows * cpr * vmul <= 2 * GEMV_THREADS, "decode matmul: K too large");
+    CH_REQUIRE(rows * vmul * G <= DEC_SCL * GEMV_THREADS, "decode matmul: too many groups per tile");
     a.rows = rows;
     const int ch = (rows * cpr * vmul + GEMV_THREADS - 1) / GEMV_THREADS;
     const size_t smem = dec_gemv_smem(a.K, rows * vmul, G);
