@@ -389,15 +389,23 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         const size_t klen = HYBRID ? a.new_len : a.Skv;
         krow16 = a.k + ((b * klen + kpos) * a.Hkv + kvh) * (size_t)d;
     }
+    // decode form: the lane's INT8 key row, loaded branch-free (a lane
+    // without a cached key reads a stand-in row, its values unused) so no
+    // wait is forced at the load; issued after the head preparation's own
+    // loads when that runs here
     uint4 pre[PRE ? D / 16 : 1];
     float pres = 0.0f;
-    if constexpr (PRE) {
-        if (kload && kint8) {
+    auto preload = [&]() {
+        if constexpr (PRE) {
+            const bool own = kload && kint8;
+            const void* stand_in = a.prep.q_raw ? (const void*)a.prep.q_raw : (const void*)a.q;
+            const int8_t* src = own ? krow8 : reinterpret_cast<const int8_t*>(stand_in);
+            const float* ssrc = own ? ksr : reinterpret_cast<const float*>(stand_in);
 #pragma unroll
-            for (int m = 0; m < D / 16; m++) pre[m] = *reinterpret_cast<const uint4*>(krow8 + 16 * m);
-            pres = ksr[0];
+            for (int m = 0; m < D / 16; m++) pre[m] = *reinterpret_cast<const uint4*>(src + 16 * m);
+            pres = ssrc[0];
         }
-    }
+    };
     // decode form with the head preparation fused in (one wave, one row):
     // q of the group's heads and, in the chunk holding it, the new key row
     // get the reference's head RMSNorm and RoPE here (the step's attn_prep
@@ -430,6 +438,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             const size_t trow = (size_t)(tab_ok ? pos : 0) * half;
             const uint16_t cv = lane < half ? a.prep.cos_t[trow + lane] : (uint16_t)0;
             const uint16_t sv = lane < half ? a.prep.sin_t[trow + lane] : (uint16_t)0;
+            preload();   // (the appender too: no branch around loads)
             // rows r < nq: q heads h0 + r; row NQ: the new key
 #pragma unroll
             for (int r = 0; r <= NQ; r++)
@@ -492,6 +501,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         }
     }
     if (!(PRE && NW == 1) || !a.prep.q_raw) {
+        preload();
         for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
             const int v = i / D, dim = i % D;
             const int qp = qp0 + v / gq;
