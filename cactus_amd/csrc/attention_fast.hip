@@ -196,60 +196,108 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
     const bool prep_ok = !PREP || pos < a.table_pos;   // the host keeps positions inside the tables
     const size_t wk0 = k0 + (size_t)wid * FA_KPW;      // this wave's first key
 
+    // ---- 0. (fused step) the head preparation's inputs, loaded first and
+    // branch-free (clamped rows and table position; values unused where no
+    // preparation runs), so preparing them waits for these only and the key
+    // and value rows below stay in flight meanwhile
+    constexpr int EPL = D / 64;                        // elements per lane of a row
+    const bool do_q = PREP && prep_ok && wid < GQ;
+    const bool do_k = PREP && prep_ok && (has_new || appends) && wid == GQ % FA_WAVES;
+    uint16_t pq[EPL], pqn[EPL], pk[EPL], pkn[EPL];
+    uint16_t pcv = 0, psv = 0;
+    if constexpr (PREP) {
+        const uint16_t* qsrc = a.q_raw + ((size_t)b * a.Hq + g * GQ + min(wid, GQ - 1)) * D;
+        const uint16_t* ksrc = a.k_raw + ((size_t)b * a.Hkv + g) * D;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            pq[j] = qsrc[lane + 64 * j];
+            pqn[j] = a.q_norm[lane + 64 * j];
+            pk[j] = ksrc[lane + 64 * j];
+            pkn[j] = a.k_norm[lane + 64 * j];
+        }
+        const size_t tpos = prep_ok ? pos : 0;
+        const int hl = min(lane, D / 2 - 1);
+        pcv = a.cos_t[tpos * (D / 2) + hl];
+        psv = a.sin_t[tpos * (D / 2) + hl];
+    }
+
     // ---- 1. key and value chunks, in flight first (key of instruction i:
     // wk0 + i*R + rl)
+    // Branch-free: a lane without a cached key of its own reads row 0 (or a
+    // stand-in when there is no cache) and its data are never used -- a
+    // branch around the loads made the compiler wait for each instruction's
+    // rows before issuing the next.
     i32x4 kch[NI], vch[NI];
     float ksc[NI], vsc[NI];
+    const void* stand_in = PREP ? (const void*)a.q_raw : (const void*)a.q;
+    const bool has_rows = HYBRID ? cache_len > 0 : Skv > 0;
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-        kch[i] = vch[i] = (i32x4){0, 0, 0, 0};
-        ksc[i] = vsc[i] = 1.0f;
         const size_t kp = wk0 + (size_t)i * R + rl;
-        if (!has_keys || kp >= k1) continue;
-        if (HYBRID) {
-            if (kp >= cache_len) continue;   // an FP16 new row: read below
-            const size_t row = ((size_t)b * cache_len + kp) * a.Hkv + g;
-            kch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.kc + row * D) + cl);
-            vch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.vc + row * D) + cl);
-            // scales carry no batch offset (kernel_attention.cpp:353, :424)
-            ksc[i] = a.ks[(kp * a.Hkv + g) * a.nqg];
-            vsc[i] = a.vs[(kp * a.Hkv + g) * a.nqg];
-        } else {
-            const size_t row = ((size_t)b * Skv + kp) * a.Hkv + g;
-            kch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.k + row * D) + cl);
-            vch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(a.v + row * D) + cl);
+        const bool own = has_keys && kp < k1 && (!HYBRID || kp < cache_len);   // FP16 new rows: read below
+        const size_t kr = own ? kp : 0;
+        const char* kb = reinterpret_cast<const char*>(stand_in);
+        const char* vb = kb;
+        const float* ksp = reinterpret_cast<const float*>(stand_in);
+        const float* vsp = ksp;
+        if (has_rows) {
+            if (HYBRID) {
+                const size_t row = ((size_t)b * cache_len + kr) * a.Hkv + g;
+                kb = reinterpret_cast<const char*>(a.kc + row * D);
+                vb = reinterpret_cast<const char*>(a.vc + row * D);
+                // scales carry no batch offset (kernel_attention.cpp:353, :424)
+                ksp = a.ks + (kr * a.Hkv + g) * a.nqg;
+                vsp = a.vs + (kr * a.Hkv + g) * a.nqg;
+            } else {
+                const size_t row = ((size_t)b * Skv + kr) * a.Hkv + g;
+                kb = reinterpret_cast<const char*>(a.k + row * D);
+                vb = reinterpret_cast<const char*>(a.v + row * D);
+            }
         }
+        kch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(kb) + cl);
+        vch[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(vb) + cl);
+        ksc[i] = HYBRID ? *ksp : 1.0f;
+        vsc[i] = HYBRID ? *vsp : 1.0f;
     }
 
     // ---- 2. queries (and the step's new key) into LDS
     if (PREP) {
-        const int half = D / 2, end8 = (D / 8) * 8;
-        const bool need_k = has_new || appends;
-        const uint16_t* ct = a.cos_t + pos * half;
-        const uint16_t* st = a.sin_t + pos * half;
+        const int half = D / 2, end8 = (D / 8) * 8, vh = (half / 8) * 8;
         // q/k head RMSNorm then RoPE at the step's position, one wave per row
-        auto prep_row = [&](const uint16_t* src, const uint16_t* nw, uint16_t* dst) {
+        // (rope_row's arithmetic, with this lane's table entries in registers)
+        auto prep_row = [&](const uint16_t (&xr)[EPL], const uint16_t (&nr)[EPL], uint16_t* dst) {
             uint16_t* xs = tmp[wid];
-            for (int i = lane; i < D; i += 64) xs[i] = src[i];
+#pragma unroll
+            for (int j = 0; j < EPL; j++) xs[lane + 64 * j] = xr[j];
             wave_lds_sync();
             float inv;
             uint16_t hinv;
             rms_stats_wave(xs, D, a.eps, inv, hinv);
-            uint16_t yv[D / 64];
+            uint16_t yv[EPL];
 #pragma unroll
-            for (int j = 0; j < D / 64; j++)
-                yv[j] = rms_apply(xs[lane + 64 * j], nw[lane + 64 * j], lane + 64 * j, end8, inv, hinv);
+            for (int j = 0; j < EPL; j++) yv[j] = rms_apply(xr[j], nr[j], lane + 64 * j, end8, inv, hinv);
             wave_lds_sync();
 #pragma unroll
-            for (int j = 0; j < D / 64; j++) xs[lane + 64 * j] = yv[j];
+            for (int j = 0; j < EPL; j++) xs[lane + 64 * j] = yv[j];
             wave_lds_sync();
-            rope_row(xs, D, ct, st, [&](int i, uint16_t v) { dst[i] = v; });
+            if (lane < half) {
+                const uint16_t x1 = xs[lane], x2 = xs[lane + half];
+                uint16_t o1, o2;
+                if (lane < vh) {
+                    o1 = hfma(x2 ^ 0x8000u, psv, hmul(x1, pcv));
+                    o2 = hfma(x1, psv, hmul(x2, pcv));
+                } else {
+                    const float fa = h2f(x1), fb = h2f(x2), cf = h2f(pcv), sf = h2f(psv);
+                    o1 = f2h(fa * cf - fb * sf);
+                    o2 = f2h(fb * cf + fa * sf);
+                }
+                dst[lane] = o1;
+                dst[lane + half] = o2;
+            }
         };
-        if (prep_ok) {
-            if (wid < GQ) prep_row(a.q_raw + ((size_t)b * a.Hq + g * GQ + wid) * D, a.q_norm, qs[wid]);
-            // the new key: wave GQ, or wave 0 after its query head when GQ == 4
-            if (need_k && wid == GQ % FA_WAVES) prep_row(a.k_raw + ((size_t)b * a.Hkv + g) * D, a.k_norm, kn);
-        }
+        if (do_q) prep_row(pq, pqn, qs[wid]);
+        // the new key: wave GQ, or wave 0 after its query head when GQ == 4
+        if (do_k) prep_row(pk, pkn, kn);
     } else {
         for (int i = tid; i < GQ * D; i += FA_THREADS)
             qs[i / D][i % D] = a.q[((size_t)b * a.Hq + g * GQ + i / D) * D + i % D];
@@ -419,6 +467,12 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
                 }
             }
             if (HYBRID) f = vsc[i];
+            if (!(has_keys && kp < k1)) {
+                // a key outside the split: its (unused) data contribute nothing
+                f = 0.0f;
+#pragma unroll
+                for (int e = 0; e < DPL; e++) vv[e] = 0.0f;
+            }
         }
 #pragma unroll
         for (int h = 0; h < GQ; h++) {
