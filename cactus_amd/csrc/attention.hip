@@ -942,9 +942,9 @@ struct CdCfg {
 // (the running max is the last finite block max), else NEG_INF (the block
 // leaves the accumulators unscaled); bsum[blk] is the block's flagged sum.
 // One whole wave.
+__device__ __forceinline__ void chain_corr_scan(int nb, float* corr);
 __device__ __forceinline__ void chain_corr(const AttnArgs& a, size_t row, int nb, float* corr, float* bsum) {
     const int lane = threadIdx.x & 63;
-    const float NEG_INF = -__builtin_inff();
     const float* bm = a.bmax + row * a.nbstride;
     const float* bsm = a.bsum + row * a.nbstride;
 #pragma unroll 4
@@ -952,6 +952,12 @@ __device__ __forceinline__ void chain_corr(const AttnArgs& a, size_t row, int nb
         corr[i] = bm[i];
         bsum[i] = bsm[i];
     }
+    chain_corr_scan(nb, corr);
+}
+// block maxima in corr[0, nb) -> the corrections, in place (one wave)
+__device__ __forceinline__ void chain_corr_scan(int nb, float* corr) {
+    const int lane = threadIdx.x & 63;
+    const float NEG_INF = -__builtin_inff();
     float carry = NEG_INF;
     for (int c0 = 0; c0 < nb; c0 += 64) {
         const int i = c0 + lane;
@@ -1546,6 +1552,17 @@ __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_s_barrier();
 }
 
+// s_waitcnt vmcnt(min(y, N) * PER) for a wave-uniform y (y <= 0: vmcnt(0))
+template <int PER, int N>
+__device__ __forceinline__ void wait_younger(int y) {
+    if constexpr (N <= 0) {
+        wait_dma<0>();
+    } else {
+        if (y >= N) wait_dma<N * PER>();
+        else wait_younger<PER, N - 1>(y);
+    }
+}
+
 template <int D, int NH, int DR, int NP>
 __global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs a_in, int nbmax) {
     using C = PairCfg<NH, DR, NP>;
@@ -1637,9 +1654,29 @@ __global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs
     float pf_p = 0.0f, pf_w = 0.0f;
     const bool pf = a.cache_len < rke;
     if (!is_chain) {
+        // the row's block maxima and sums come by LDS DMA ahead of the ring
+        // (exec-masked to the row's nb entries), so waiting for them -- an
+        // explicit vmcnt that leaves the ring's DMA in flight -- does not
+        // wait for the tiles
+        const bool corr_wave = pw < NH;
+        if (corr_wave) {
+            const float* bm = a.bmax + (row0 + pw) * a.nbstride;
+            const float* bsm = a.bsum + (row0 + pw) * a.nbstride;
+            const uint32_t cl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(corr_s + pw * nbmax);
+            const uint32_t sl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(bsum_s + pw * nbmax);
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                if (c0 + lane < nb) {
+                    lds_dma<4>(bm + c0 + lane, cl + 4 * c0);
+                    lds_dma<4>(bsm + c0 + lane, sl + 4 * c0);
+                }
+            }
+        }
         for (int t = 0; t < D - 1; t++)
             if (t < nst) issue(t);
-        if (pw < NH) chain_corr(a, row0 + pw, nb, corr_s + pw * nbmax, bsum_s + pw * nbmax);
+        if (corr_wave) {
+            wait_younger<C::PER, D - 1>(min(D - 1, nst));   // the corrections' DMA has landed
+            chain_corr_scan(nb, corr_s + pw * nbmax);
+        }
     } else if (pf && dlane) {
         pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
         if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
