@@ -39,6 +39,30 @@ struct GemvArgs {
 // tile t is dotted, and the activation prologue runs while tile 0 loads.
 // Group sums of a tile go to one of two LDS buffers; after a barrier the
 // tile's epilogue (one thread per output) runs the reference fma chain.
+// the reference epilogue of one output, r = fma((float)acc_g, Bs_g, r) over
+// ascending groups (kernel_gemm.cpp:311-324), from the group sums and
+// scales in LDS: the reads of EPB groups are issued together, so the chain
+// waits for LDS once per EPB steps instead of once per step (8: the
+// headline kernel stays at 64 VGPRs, 8 waves per SIMD)
+template <int EPB = 8>
+__device__ __forceinline__ float group_epilogue(const int32_t* ag, const uint16_t* sg, int G) {
+    float rs = 0.0f;
+    int g = 0;
+    for (; g + EPB <= G; g += EPB) {
+        int av[EPB];
+        uint16_t sv[EPB];
+#pragma unroll
+        for (int j = 0; j < EPB; j++) {
+            av[j] = ag[g + j];
+            sv[j] = sg[g + j];
+        }
+#pragma unroll
+        for (int j = 0; j < EPB; j++) rs = __builtin_fmaf((float)av[j], h2f(sv[j]), rs);
+    }
+    for (; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+    return rs;
+}
+
 template <int MR, bool F16ACT, bool INT4, int CH>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, int m0) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -151,8 +175,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
             const int m = o / nr, r = o % nr;
             const int32_t* ag = accb + (m * rows + r) * G;
             const uint16_t* sg = sclb + r * G;
-            float rs = 0.0f;
-            for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+            const float rs = group_epilogue(ag, sg, G);
             a.C[bi * a.sC + (size_t)(m0 + m) * a.N + n0 + r] = f2h(rs * rsc[m]);
         }
 #pragma unroll
@@ -293,8 +316,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             const int m = o / nr, r = o - (o / nr) * nr;
             const int32_t* ag = acc + (m * rows + r) * G;
             const uint16_t* sg = scl + r * G;
-            float rs = 0.0f;
-            for (int g = 0; g < G; g++) rs = __builtin_fmaf((float)ag[g], h2f(sg[g]), rs);
+            const float rs = group_epilogue(ag, sg, G);
             float s = rsm[0];
 #pragma unroll
             for (int mm = 1; mm < MR; mm++)
