@@ -925,46 +925,78 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
     }
 }
 
-// Combine of the key splits: grid (query blocks, B * Hkv), 256 threads;
-// four threads per query vector, D/4 dims each.  M = max_s M_s,
-// L = sum_s e^(M_s - M) l_s, o = sum_s e^(M_s - M) acc_s / L.
+// Combine of the key splits: grid (query blocks x NV / 16, B * Hkv), 256
+// threads; a workgroup takes 16 query vectors, 16 threads per vector with
+// D/16 dims each.  M = max_s M_s, L = sum_s e^(M_s - M) l_s,
+// o = sum_s e^(M_s - M) acc_s / L.  Loads are branch-free (clamped splits,
+// weight 0 past the block's split count) and issued per batch of splits.
+constexpr int PF_MAX_SPLITS = 16;
+
 template <int D, int GQ, int NV>
 __global__ void __launch_bounds__(256) attn_prefill_combine_kernel(PrefillArgs a) {
-    static_assert(NV * 4 == 256, "four threads per vector");
-    constexpr int DQ = D / 4;
+    constexpr int VPW = 16, DS = D / 16, SB = 4;
     constexpr float LOG2E = 1.4426950408889634f;
-    const int tid = threadIdx.x, v = tid / 4, dq = (tid % 4) * DQ;
-    const int qb = blockIdx.x, bg = blockIdx.y, b = bg / a.Hkv, g = bg % a.Hkv;
+    const int tid = threadIdx.x, vl = tid / 16, dq = (tid % 16) * DS;
+    const int qb = blockIdx.x / (NV / VPW), v = (blockIdx.x % (NV / VPW)) * VPW + vl;
+    const int bg = blockIdx.y, b = bg / a.Hkv, g = bg % a.Hkv;
+    const int nqb = (int)gridDim.x / (NV / VPW);
     const int gm0 = qb * NV;
     const int ns = min(a.nsplit, (pf_block_tiles(a, gm0, NV, GQ) + a.tps - 1) / a.tps);
     const int vm = gm0 + v, row = vm / GQ;
     if (row >= a.S) return;
-    const float* pb = a.part + (((size_t)bg * gridDim.x + qb) * a.nsplit * NV + v) * (D + 4);
+    uint16_t* op = a.o + (((size_t)b * a.S + row) * a.Hq + (size_t)g * GQ + vm % GQ) * D + dq;
+    if (ns <= 0) {   // no key tile reaches this block: zero rows, as with L = 0
+#pragma unroll
+        for (int e = 0; e < DS; e += 2) *reinterpret_cast<uint32_t*>(op + e) = 0u;
+        return;
+    }
+    const float* pb = a.part + (((size_t)bg * nqb + qb) * a.nsplit * NV + v) * (D + 4);
     const size_t sstep = (size_t)NV * (D + 4);
+    float ms[PF_MAX_SPLITS], ls[PF_MAX_SPLITS];
+#pragma unroll
+    for (int s = 0; s < PF_MAX_SPLITS; s++) {
+        const float* ps = pb + (size_t)min(s, ns - 1) * sstep;
+        ms[s] = ps[D];
+        ls[s] = ps[D + 1];
+    }
     float M = -__builtin_inff();
-    for (int s = 0; s < ns; s++) M = __builtin_fmaxf(M, pb[s * sstep + D]);
+#pragma unroll
+    for (int s = 0; s < PF_MAX_SPLITS; s++)
+        if (s < ns) M = __builtin_fmaxf(M, ms[s]);
     float L = 0.0f;
-    float out[DQ];
 #pragma unroll
-    for (int e = 0; e < DQ; e++) out[e] = 0.0f;
-    for (int s = 0; s < ns; s++) {
-        const float* ps = pb + s * sstep;
-        const float m = ps[D];
-        const float w = m > -__builtin_inff() ? fast_exp2((m - M) * LOG2E) : 0.0f;
-        L = __builtin_fmaf(w, ps[D + 1], L);
+    for (int s = 0; s < PF_MAX_SPLITS; s++) {
+        ms[s] = (s < ns && ms[s] > -__builtin_inff()) ? fast_exp2((ms[s] - M) * LOG2E) : 0.0f;   // weights
+        L = __builtin_fmaf(ms[s], ls[s], L);
+    }
+    float out[DS];
 #pragma unroll
-        for (int e = 0; e < DQ; e += 4) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(ps + dq + e);
-            out[e] = __builtin_fmaf(w, x[0], out[e]);
-            out[e + 1] = __builtin_fmaf(w, x[1], out[e + 1]);
-            out[e + 2] = __builtin_fmaf(w, x[2], out[e + 2]);
-            out[e + 3] = __builtin_fmaf(w, x[3], out[e + 3]);
+    for (int e = 0; e < DS; e++) out[e] = 0.0f;
+#pragma unroll
+    for (int s0 = 0; s0 < PF_MAX_SPLITS; s0 += SB) {
+        if (s0 >= ns) break;
+        f32x4 x[SB][DS / 4];
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const float* ps = pb + (size_t)min(s0 + u, ns - 1) * sstep + dq;
+#pragma unroll
+            for (int e = 0; e < DS / 4; e++) x[u][e] = *reinterpret_cast<const f32x4*>(ps + 4 * e);
+        }
+#pragma unroll
+        for (int u = 0; u < SB; u++) {
+            const float w = ms[s0 + u];
+#pragma unroll
+            for (int e = 0; e < DS / 4; e++) {
+                out[4 * e] = __builtin_fmaf(w, x[u][e][0], out[4 * e]);
+                out[4 * e + 1] = __builtin_fmaf(w, x[u][e][1], out[4 * e + 1]);
+                out[4 * e + 2] = __builtin_fmaf(w, x[u][e][2], out[4 * e + 2]);
+                out[4 * e + 3] = __builtin_fmaf(w, x[u][e][3], out[4 * e + 3]);
+            }
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    uint16_t* op = a.o + (((size_t)b * a.S + row) * a.Hq + (size_t)g * GQ + vm % GQ) * D + dq;
 #pragma unroll
-    for (int e = 0; e < DQ; e += 2)
+    for (int e = 0; e < DS; e += 2)
         *reinterpret_cast<uint32_t*>(op + e) = (uint32_t)f2h(out[e] * inv) | ((uint32_t)f2h(out[e + 1] * inv) << 16);
 }
 
@@ -1085,7 +1117,7 @@ int attention_prefill_fast(const uint16_t* q, const int8_t* kc, const int8_t* vc
     size_t nsplit = (512 + nqb * B * Hkv - 1) / (nqb * B * Hkv);
     const size_t max_split = (tiles + 7) / 8;
     if (nsplit > max_split) nsplit = max_split;
-    if (nsplit > 16) nsplit = 16;
+    if (nsplit > PF_MAX_SPLITS) nsplit = PF_MAX_SPLITS;
     if (nsplit < 1) nsplit = 1;
     a.tps = (int)((tiles + nsplit - 1) / nsplit);
     a.nsplit = (int)((tiles + a.tps - 1) / a.tps);
@@ -1097,7 +1129,7 @@ int attention_prefill_fast(const uint16_t* q, const int8_t* kc, const int8_t* vc
         a.part = w.part;
     }
     const dim3 grid((unsigned)(nqb * a.nsplit), (unsigned)(B * Hkv));
-    const dim3 cgrid((unsigned)nqb, (unsigned)(B * Hkv));
+    const dim3 cgrid((unsigned)(nqb * (NV / 16)), (unsigned)(B * Hkv));
     auto go = [&](auto kern, auto comb) {
         hipLaunchKernelGGL(kern, grid, dim3(64 * W), 0, as_stream(stream), a);
         int rc = check_launch("attention (prefill, MFMA)");
