@@ -640,10 +640,62 @@ void CactusGraph::compute(GraphNode& n) {
     }
 }
 
+// Consecutive matmul nodes over one pre-quantized activation (the q/k/v and
+// gate/up projections, model_qwen.cpp:55-57 and :112-113) with weights of one
+// format, K and group size run as one launch; each output is what its own
+// node computes.  Returns the number of nodes computed from node i (0: node
+// i is not such a run).
+size_t CactusGraph::compute_shared_matmuls(size_t i) {
+    auto eligible = [&](const GraphNode& n) {
+        if (n.op != OpType::MATMUL || !n.params.pretransposed_rhs) return false;
+        const BufferDesc& a = node(n.inputs[0]).out;
+        const BufferDesc& b = node(n.inputs[1]).out;
+        return a.precision == Precision::INT8 && a.activation_scales && (b.is_packed_int4() || b.is_grouped_int8());
+    };
+    const GraphNode& n0 = *nodes_[i];
+    if (!eligible(n0)) return 0;
+    const BufferDesc& a = node(n0.inputs[0]).out;
+    const BufferDesc& b0 = node(n0.inputs[1]).out;
+    const size_t K = a.shape.back(), M = a.total_size / K;
+    if (M < 32) return 0;   // decode sizes: the fused GEMV per node
+    size_t count = 1;
+    while (count < 3 && i + count < nodes_.size()) {
+        const GraphNode& nj = *nodes_[i + count];
+        if (!eligible(nj) || nj.inputs[0] != n0.inputs[0]) break;
+        const BufferDesc& bj = node(nj.inputs[1]).out;
+        if (bj.is_packed_int4() != b0.is_packed_int4() || bj.group_size != b0.group_size) break;
+        count++;
+    }
+    if (count < 2) return 0;
+    const void* B[3];
+    const uint16_t* Bs[3];
+    uint16_t* C[3];
+    size_t N[3];
+    for (size_t j = 0; j < count; j++) {
+        GraphNode& nj = *nodes_[i + j];
+        if (j > 0) allocate(nj);
+        const BufferDesc& b = node(nj.inputs[1]).out;
+        B[j] = b.is_packed_int4() ? b.packed_int4 : b.data;
+        Bs[j] = static_cast<const uint16_t*>(b.scales);
+        C[j] = static_cast<uint16_t*>(nj.out.data);
+        N[j] = nj.out.shape.back();
+    }
+    check_hip(cactus_hip_matmul_grouped_multi(static_cast<const int8_t*>(a.data),
+                                              static_cast<const float*>(a.activation_scales), count, B, Bs, C, N, M,
+                                              K, b0.group_size, b0.is_packed_int4() ? 1 : 0, stream_),
+              "matmul (shared activation)");
+    return count;
+}
+
 void CactusGraph::execute() {
-    for (auto& n : nodes_) {
-        allocate(*n);
-        compute(*n);
+    for (size_t i = 0; i < nodes_.size(); i++) {
+        allocate(*nodes_[i]);
+        const size_t done = compute_shared_matmuls(i);
+        if (done) {
+            i += done - 1;
+            continue;
+        }
+        compute(*nodes_[i]);
     }
     if (embed_err_) {
         int err = 0;

@@ -193,6 +193,7 @@ private:
     const GraphNode& node(size_t id) const;
     void allocate(GraphNode& n);
     void compute(GraphNode& n);
+    size_t compute_shared_matmuls(size_t i);
     void release_outputs();
 
     void* stream_;

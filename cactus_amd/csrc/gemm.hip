@@ -59,6 +59,15 @@ struct GemmArgs {
     uint16_t* C;          // [M][N] fp16
     int M, K, N, gs;
     const uint16_t* R = nullptr;   // [M][N] fp16 residual added to C (the add node), or null
+    // Up to two further problems over the same A, M, K and group size (the
+    // LDS kernel only): workgroups with blockIdx.x >= bx[i] take problem
+    // i + 1, with its own weights, scales, output and N (no residual).
+    int np = 1;
+    int bx[2] = {0, 0};
+    const uint8_t* Bx[2] = {nullptr, nullptr};
+    const uint16_t* Bsx[2] = {nullptr, nullptr};
+    uint16_t* Cx[2] = {nullptr, nullptr};
+    int Nx[2] = {0, 0};
 };
 
 // Workgroup: 4 waves, 64 rows x 64*NW columns; wave (wv >> 1, wv & 1) owns
@@ -231,13 +240,25 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 }
 
 template <class C, bool INT4>
-__global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a0) {
     extern __shared__ __align__(16) uint8_t smem[];
+    // the problem of this workgroup (selects, not indexing: the arguments stay scalar)
+    GemmArgs a = a0;
+    int bxi = blockIdx.x;
+    if (a0.np > 1 && bxi >= a0.bx[0]) {
+        const bool p2 = a0.np > 2 && bxi >= a0.bx[1];
+        bxi -= p2 ? a0.bx[1] : a0.bx[0];
+        a.B = p2 ? a0.Bx[1] : a0.Bx[0];
+        a.Bs = p2 ? a0.Bsx[1] : a0.Bsx[0];
+        a.C = p2 ? a0.Cx[1] : a0.Cx[0];
+        a.N = p2 ? a0.Nx[1] : a0.Nx[0];
+        a.R = nullptr;
+    }
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int K = a.K, N = a.N, M = a.M;
     const int NK = K / 32, G = NK / C::KSUB, NSTAGE = NK / C::SG;
-    const int mb = blockIdx.y * C::BM, nb = blockIdx.x * C::BN;
+    const int mb = blockIdx.y * C::BM, nb = bxi * C::BN;
     const int wm = wv / C::WGN, wn = wv % C::WGN;
     const size_t brow = INT4 ? (size_t)K / 2 : (size_t)K;
     const int q = lane >> 4, l16 = lane & 15;
@@ -492,8 +513,14 @@ static bool launch_lds(const GemmArgs& a, hipStream_t st) {
             return false;
         }
     }
-    const dim3 grid(ceil_div(a.N, C::BN), ceil_div(a.M, C::BM));
-    hipLaunchKernelGGL((gemm_lds_kernel<C, INT4>), grid, dim3(C::NT), lds, st, a);
+    GemmArgs b = a;
+    int gx = ceil_div(a.N, C::BN);
+    for (int i = 0; i + 1 < a.np; i++) {
+        b.bx[i] = gx;
+        gx += ceil_div(a.Nx[i], C::BN);
+    }
+    const dim3 grid(gx, ceil_div(a.M, C::BM));
+    hipLaunchKernelGGL((gemm_lds_kernel<C, INT4>), grid, dim3(C::NT), lds, st, b);
     return true;
 }
 
@@ -520,7 +547,9 @@ static int pick_tile(const GemmArgs& a, bool int4) {
     for (int i = 0; i < (int)(sizeof(kTiles) / sizeof(kTiles[0])); i++) {
         const TileChoice& t = kTiles[i];
         const int nw = t.wgm * t.wgn, bm = t.wm * t.wgm, bn = t.wn * t.wgn;
-        const double wgs = (double)ceil_div(a.M, bm) * ceil_div(a.N, bn);
+        int nblk = ceil_div(a.N, bn);
+        for (int p = 0; p + 1 < a.np; p++) nblk += ceil_div(a.Nx[p], bn);
+        const double wgs = (double)ceil_div(a.M, bm) * nblk;
         const double rounds = std::ceil(wgs / kCUs);
         const double waves_per_simd = nw / 4.0;
         const double cyc_per_instr = waves_per_simd >= 3 ? 2.4 : waves_per_simd >= 2 ? 3.5 : 7.0;
@@ -637,6 +666,31 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
     }
     *handled = true;
     return check_launch("grouped matmul (mfma)");
+}
+
+// Matmuls of one pre-quantized activation against np weight matrices (same
+// K, group size and format) in one launch of the LDS kernel.  Returns
+// *handled = false when the shape is left to one launch per problem.
+int gemm_grouped_mfma_multi(const int8_t* A8, const float* As, int np, const uint8_t* const* B,
+                            const uint16_t* const* Bs, uint16_t* const* C, const size_t* N, size_t M, size_t K,
+                            size_t gs, bool int4, hipStream_t st, bool* handled) {
+    *handled = false;
+    if (np < 1 || np > 3 || M < GEMM_MIN_M || gs % 32 != 0) return CACTUS_HIP_OK;
+    if (((uintptr_t)A8 & 15) != 0 || M >= (1u << 30) || K >= (1u << 20)) return CACTUS_HIP_OK;
+    for (int p = 0; p < np; p++)
+        if (N[p] < 32 || N[p] >= (1u << 30) || ((uintptr_t)B[p] & 15) != 0 || ((uintptr_t)Bs[p] & 3) != 0)
+            return CACTUS_HIP_OK;
+    GemmArgs a{A8, As, B[0], Bs[0], C[0], (int)M, (int)K, (int)N[0], (int)gs, nullptr};
+    a.np = np;
+    for (int p = 1; p < np; p++) {
+        a.Bx[p - 1] = B[p];
+        a.Bsx[p - 1] = Bs[p];
+        a.Cx[p - 1] = C[p];
+        a.Nx[p - 1] = (int)N[p];
+    }
+    if (!(int4 ? launch_lds_any<true>(a, st) : launch_lds_any<false>(a, st))) return CACTUS_HIP_OK;
+    *handled = true;
+    return check_launch("grouped matmul (mfma, lds, several weights)");
 }
 
 }  // namespace cactus_hip

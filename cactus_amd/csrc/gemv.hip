@@ -486,6 +486,9 @@ int gemm_grouped_mfma(const uint16_t* A16, const int8_t* A8, const float* As, co
                       const uint16_t* Bs, uint16_t* C, size_t M, size_t K, size_t N, size_t gs,
                       bool int4, hipStream_t st, bool* handled,
                       const uint16_t* R = nullptr, void* ext_scratch = nullptr);
+int gemm_grouped_mfma_multi(const int8_t* A8, const float* As, int np, const uint8_t* const* B,
+                            const uint16_t* const* Bs, uint16_t* const* C, const size_t* N, size_t M, size_t K,
+                            size_t gs, bool int4, hipStream_t st, bool* handled);
 
 // C[i] = fp16(C[i] + R[i]): the residual add node after a small-M matmul
 __global__ void add_residual_kernel(uint16_t* C, const uint16_t* R, size_t n) {
@@ -585,6 +588,33 @@ int cactus_hip_matmul_int4_f16act_add(const uint16_t* A, const uint8_t* B_packed
     CH_REQUIRE(residual || M * K * N == 0, "matmul_add: null residual");
     return grouped_dispatch(A, nullptr, nullptr, B_packed, B_scales, C, M, K, N, group_size, true,
                             as_stream(stream), residual);
+}
+
+int cactus_hip_matmul_grouped_multi(const int8_t* A, const float* A_scales, size_t count, const void* const* B,
+                                    const uint16_t* const* B_scales, uint16_t* const* C, const size_t* N, size_t M,
+                                    size_t K, size_t group_size, int int4, void* stream) {
+    CH_REQUIRE(count >= 1 && count <= 3, "matmul_grouped_multi: count must be 1, 2 or 3");
+    CH_REQUIRE(B && B_scales && C && N, "matmul_grouped_multi: null pointer");
+    if (M == 0 || K == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(A && A_scales, "matmul_grouped_multi: null pointer");
+    const uint8_t* bp[3];
+    for (size_t i = 0; i < count; i++) {
+        int rc = check_grouped_shape(M, K, N[i], group_size, int4 != 0);
+        if (rc) return rc;
+        CH_REQUIRE(B[i] && B_scales[i] && C[i], "matmul_grouped_multi: null pointer");
+        CH_REQUIRE(((uintptr_t)B[i] & 15) == 0, "matmul_grouped_multi: weights must be 16-byte aligned");
+        CH_REQUIRE(N[i] > 0, "matmul_grouped_multi: every N must be positive");
+        bp[i] = static_cast<const uint8_t*>(B[i]);
+    }
+    const hipStream_t st = as_stream(stream);
+    bool handled = false;
+    int rc = gemm_grouped_mfma_multi(A, A_scales, (int)count, bp, B_scales, C, N, M, K, group_size, int4 != 0, st,
+                                     &handled);
+    if (rc || handled) return rc;
+    // one launch per problem: the same per-output arithmetic
+    for (size_t i = 0; i < count && rc == 0; i++)
+        rc = grouped_dispatch(nullptr, A, A_scales, bp[i], B_scales[i], C[i], M, K, N[i], group_size, int4 != 0, st);
+    return rc;
 }
 
 int cactus_hip_matmul_int8_f16act_batched(const uint16_t* A, const int8_t* B,

@@ -132,6 +132,16 @@ int cactus_hip_matmul_int8_f16act_add(const uint16_t* A, const int8_t* B, const 
 int cactus_hip_matmul_int4_f16act_add(const uint16_t* A, const uint8_t* B_packed, const uint16_t* B_scales,
                                       const uint16_t* residual, uint16_t* C, size_t M, size_t K, size_t N,
                                       size_t group_size, void* stream);
+/* No single reference function: `count` (1..3) grouped matmuls that share one
+ * pre-quantized activation, C[i] = A x B[i]^T as cactus_hip_matmul_int8
+ * (int4 = 0, B[i] [N[i]][K] int8) or cactus_hip_matmul_int4 (int4 = 1,
+ * B[i] [N[i]][K/2] packed), each identical to its own call.  The q/k/v and
+ * gate/up projections of model_qwen.cpp:55-57 and :112-113 run as one
+ * launch instead of three or two.  B, B_scales, C and N are host arrays of
+ * `count` entries; M, K and group_size are shared. */
+int cactus_hip_matmul_grouped_multi(const int8_t* A, const float* A_scales, size_t count, const void* const* B,
+                                    const uint16_t* const* B_scales, uint16_t* const* C, const size_t* N, size_t M,
+                                    size_t K, size_t group_size, int int4, void* stream);
 /* Strided-batched form of cactus_hip_matmul_int8_f16act: `batch` independent
  * problems, problem i at A + i*stride_a, B + i*stride_b, B_scales +
  * i*stride_bs, C + i*stride_c (strides in elements).  No reference

@@ -47,3 +47,12 @@ def test_rejects_bad_shapes_without_launching():
     assert lib.cactus_hip_sample_f16(p, p, 10, ctypes.c_float(-0.7), ctypes.c_float(0.9), 0, 0,
                                      None) == -1
     assert b"temperature" in lib.cactus_hip_last_error()
+    # the merged matmul takes one to three weight sets
+    arr = (ctypes.c_void_p * 4)(16, 16, 16, 16)
+    ns = (ctypes.c_size_t * 4)(64, 64, 64, 64)
+    for cnt in (0, 4):
+        assert lib.cactus_hip_matmul_grouped_multi(p, p, cnt, arr, arr, arr, ns, 32, 64, 32, 0, None) == -1
+        assert b"count" in lib.cactus_hip_last_error()
+    ns[1] = 8
+    assert lib.cactus_hip_matmul_grouped_multi(p, p, 2, arr, arr, arr, ns, 32, 96, 48, 0, None) == -1
+    assert b"group_size" in lib.cactus_hip_last_error()

@@ -768,3 +768,39 @@ def test_matmul_add_fused(dev, orc, M, K, N, gs, int4, shift):
     C2 = dev.empty(M * N * 2)
     dev.cm.call(f"cactus_hip_matmul_{kind}_f16act_add", dev.put(x), Bp, Bsp, Rp, C2.ptr, M, K, N, gs, None)
     assert_bits(dev.get(C2, np.uint16, (M, N)), want, f"matmul_{kind}_f16act_add")
+
+
+@pytest.mark.parametrize("M,K,Ns,gs,int4", [(256, 1024, (2048, 1024, 1024), 32, False),   # Qwen3-0.6B q/k/v chunk
+                                            (256, 1024, (3072, 3072), 32, True),          # its gate/up
+                                            (100, 640, (200, 96, 136), 32, False),        # ragged tiles
+                                            (33, 1024, (520, 1000), 64, True),
+                                            (40, 512, (96, 64, 32), 128, False),
+                                            (512, 1024, (3072, 3072), 32, False),
+                                            (5, 1024, (64, 128, 96), 32, False),          # small M: one GEMV each
+                                            (64, 1024, (256,), 32, True)])
+def test_matmul_grouped_multi(dev, orc, M, K, Ns, gs, int4):
+    """Several grouped matmuls over one pre-quantized activation in one call
+    (the merged q/k/v and gate/up launches): every output bit-identical to
+    the oracle's matmul of its own weights."""
+    say("matmul_grouped_multi", M, K, Ns, gs, int4)
+    rng = np.random.default_rng(M + K + sum(Ns) + int4)
+    x = activations(rng, M, K)
+    rq, rs = orc.quantize_activations(x)
+    cnt = len(Ns)
+    Bp, Bsp, Cs, refs = [], [], [], []
+    for N in Ns:
+        if int4:
+            _, B, Bs = grouped_int4_weights(rng, N, K, gs)
+            refs.append(orc.matmul_int4(rq, rs, B, Bs, gs))
+        else:
+            B, Bs = grouped_int8_weights(rng, N, K, gs)
+            refs.append(orc.matmul_int8(rq, rs, B, Bs, gs))
+        Bp.append(dev.put(B))
+        Bsp.append(dev.put(Bs))
+        Cs.append(dev.empty(M * N * 2))
+    arr = lambda vals, t: (t * cnt)(*vals)
+    dev.cm.call("cactus_hip_matmul_grouped_multi", dev.put(rq), dev.put(rs), cnt, arr(Bp, ctypes.c_void_p),
+                arr(Bsp, ctypes.c_void_p), arr([c.ptr for c in Cs], ctypes.c_void_p), arr(Ns, ctypes.c_size_t),
+                M, K, gs, int(int4), None)
+    for i, N in enumerate(Ns):
+        assert_bits(dev.get(Cs[i], np.uint16, (M, N)), refs[i], f"matmul_grouped_multi problem {i}")
