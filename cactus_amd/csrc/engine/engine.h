@@ -71,7 +71,8 @@ public:
     size_t resident = 0;   // tokens the reference's per-layer vectors would hold
 
 private:
-    void put(size_t l, const void* k, const void* v, size_t row0, size_t n, size_t at, void* stream);
+    void put(const std::vector<const void*>& k, const std::vector<const void*>& v, size_t row0, size_t n, size_t at,
+             void* stream);
     void shift(size_t dst, size_t src, size_t count, uint32_t* state, uint32_t len, void* stream);
     std::vector<DevBuf> k_, v_, ks_, vs_, vsh_;
     DevBuf table_, temp_;   // device layer records and move buffer of cactus_hip_kv_window_shift

@@ -89,21 +89,20 @@ void KVCache::set_window(size_t window, size_t sink, void* stream) {
     resident = window;
 }
 
-// quantize rows [row0, row0 + n) of one layer's new K/V into slots [at, at + n)
-void KVCache::put(size_t l, const void* kf, const void* vf, size_t row0, size_t n, size_t at, void* stream) {
+// quantize rows [row0, row0 + n) of every layer's new K/V into slots
+// [at, at + n), with their value products: one launch for all layers
+void KVCache::put(const std::vector<const void*>& k, const std::vector<const void*>& v, size_t row0, size_t n,
+                  size_t at, void* stream) {
     if (n == 0) return;
-    const size_t row = num_kv_heads * head_dim, srow = num_kv_heads * groups();
-    const uint16_t* k = static_cast<const uint16_t*>(kf) + row0 * row;
-    const uint16_t* v = static_cast<const uint16_t*>(vf) + row0 * row;
-    check_hip(cactus_hip_quantize_kv_fp16_to_int8(k, keys_mut(l) + at * row, key_scales_mut(l) + at * srow, n,
-                                                  num_kv_heads, head_dim, GROUP, stream),
-              "kv update (keys)");
-    check_hip(cactus_hip_quantize_kv_fp16_to_int8(v, values_mut(l) + at * row, value_scales_mut(l) + at * srow, n,
-                                                  num_kv_heads, head_dim, GROUP, stream),
-              "kv update (values)");
-    check_hip(cactus_hip_kv_shadow_update(values(l), value_scales(l), value_products(l), at, n, num_kv_heads,
-                                          head_dim, GROUP, slots, stream),
-              "kv update (value products)");
+    const size_t row = num_kv_heads * head_dim;
+    std::vector<const uint16_t*> kr(num_layers), vr(num_layers);
+    for (size_t l = 0; l < num_layers; l++) {
+        kr[l] = static_cast<const uint16_t*>(k[l]) + row0 * row;
+        vr[l] = static_cast<const uint16_t*>(v[l]) + row0 * row;
+    }
+    check_hip(cactus_hip_kv_append_layers(table_.as<cactus_hip_kv_layer>(), kr.data(), vr.data(), num_layers, n, at,
+                                          num_kv_heads, head_dim, GROUP, slots, stream),
+              "kv update");
 }
 
 void KVCache::shift(size_t dst, size_t src, size_t count, uint32_t* state, uint32_t len, void* stream) {
@@ -126,20 +125,18 @@ void KVCache::update(const std::vector<const void*>& k, const std::vector<const 
     if (old == 0) {
         // the K/V nodes hold all new_total rows (:131-232)
         if (!sliding) {
-            for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, nt, 0, stream);
+            put(k, v, 0, nt, 0, stream);
             resident = nt;
         } else {
             // sinks are written only when the storage was not window-sized
             const bool first = resident != W;
             const size_t skip = nt - W;
-            for (size_t l = 0; l < num_layers; l++) {
-                if (first) put(l, k[l], v[l], 0, S, 0, stream);
-                put(l, k[l], v[l], S + skip, W - S, S, stream);
-            }
+            if (first) put(k, v, 0, S, 0, stream);
+            put(k, v, S + skip, W - S, S, stream);
             resident = W;
         }
     } else if (!sliding) {
-        for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, seq, old, stream);
+        put(k, v, 0, seq, old, stream);
         resident = nt;   // std::vector::resize to the new total (:238-240)
     } else {
         // window full: keep the sinks, slide the rest (:268-327); the
@@ -150,7 +147,7 @@ void KVCache::update(const std::vector<const void*>& k, const std::vector<const 
                                      " sinks (the step must not exceed window - sink)");
         const size_t tts = W - S - seq;
         if (tts > 0 && old > S && old - tts > S) shift(S, old - tts, tts, nullptr, 0, stream);
-        for (size_t l = 0; l < num_layers; l++) put(l, k[l], v[l], 0, seq, W - seq, stream);
+        put(k, v, 0, seq, W - seq, stream);
         resident = W;
     }
     current_seq_len = sliding ? W : nt;

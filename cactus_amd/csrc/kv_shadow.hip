@@ -11,6 +11,9 @@
 // rewritten whenever keys are appended (prefill chunks here, decode steps in
 // decode.hip).  Batch 1.
 #include "hip_common.h"
+#include "quant_device.h"
+
+#include <algorithm>
 
 namespace cactus_hip {
 
@@ -106,6 +109,62 @@ __global__ void kv_shift_in_kernel(const KvLayer* __restrict__ layers, const uns
     if (state && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) state[2] = cache_len;
 }
 
+// ---------------------------------------------------------------- append
+// New K/V rows of every layer into the cache in one launch: grid (tokens,
+// layers), 256 threads.  Wave w of a workgroup takes the (K or V, head,
+// 128-group) units w, w + 4, ...; each unit is quantized as
+// quantize_kv_kernel does it (group max, scale, codes: body rne-saturating,
+// tail roundf), and a value unit also writes its products (float)code *
+// scale into the tile layout of kv_shadow_kernel.
+constexpr int KV_APPEND_MAX_LAYERS = 64;
+struct KvAppendSrc {
+    const uint16_t* k[KV_APPEND_MAX_LAYERS];
+    const uint16_t* v[KV_APPEND_MAX_LAYERS];
+};
+
+__global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restrict__ layers, KvAppendSrc src,
+                                                        size_t at, int Hkv, int d, size_t ntile) {
+    const int l = blockIdx.y;
+    const KvLayer L = layers[l];
+    const size_t i = blockIdx.x, key = at + i;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int ng = (d + 127) / 128, nsl = (d + 63) / 64;
+    const int units = Hkv * ng;
+    const size_t tt = key / KS_T;
+    const int jj = (int)(key % KS_T);
+    for (int w = wave; w < 2 * units; w += 4) {
+        const bool isv = w >= units;
+        const int hg = isv ? w - units : w, h = hg / ng, g = hg % ng;
+        const int g0 = g * 128, cnt = min(128, d - g0);
+        const uint16_t* x = (isv ? src.v[l] : src.k[l]) + (i * Hkv + h) * d + g0;
+        int8_t* o = (isv ? L.v : L.k) + (key * Hkv + h) * d + g0;
+        float m = 0.0f;
+        for (int j = lane; j < cnt; j += 64) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(x[j])));
+        m = wave_max(m);
+        const float sc = row_scale_from_max(m);
+        const float inv = 1.0f / sc;
+        const int body = (cnt / 8) * 8;
+        for (int j = lane; j < cnt; j += 64) {
+            const float v = h2f(x[j]) * inv;
+            const int32_t c = (j < body) ? cvt_rne_sat(v) : (int32_t)__builtin_roundf(v);
+            const int8_t code = (int8_t)sat8(c);
+            o[j] = code;
+            if (isv && L.sh) {
+                const int dim = g0 + j, sl = dim / 64, dl = dim % 64;
+                L.sh[(((size_t)h * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = (float)code * sc;
+            }
+        }
+        if (lane == 0) (isv ? L.vs : L.ks)[(key * Hkv + h) * ng + g] = sc;
+    }
+    // product rows of the padding dimensions [d, 64 nsl) hold zeros
+    const int pad = nsl * 64 - d;
+    if (L.sh && pad > 0)
+        for (int x = threadIdx.x; x < Hkv * pad; x += blockDim.x) {
+            const int h = x / pad, dim = d + x % pad, sl = dim / 64, dl = dim % 64;
+            L.sh[(((size_t)h * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = 0.0f;
+        }
+}
+
 __global__ void kv_set_len_kernel(uint32_t* state, uint32_t cache_len) {
     if (threadIdx.x == 0) state[2] = cache_len;
 }
@@ -137,6 +196,35 @@ int cactus_hip_kv_shadow_update(const int8_t* v_cache, const float* v_scales, fl
                        as_stream(stream), v_cache, v_scales, shadow, start, (int)kv_heads, (int)head_dim,
                        (int)quant_group_size, ntile);
     return check_launch("kv_shadow_update");
+}
+
+int cactus_hip_kv_append_layers(const cactus_hip_kv_layer* layers, const uint16_t* const* k_rows,
+                                const uint16_t* const* v_rows, size_t nlayers, size_t count, size_t at,
+                                size_t kv_heads, size_t head_dim, size_t group_size, size_t max_seq,
+                                void* stream) {
+    if (count == 0 || nlayers == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE(layers && k_rows && v_rows, "kv_append_layers: null pointer");
+    CH_REQUIRE(head_dim % 8 == 0 && head_dim > 0 && head_dim <= 256 && group_size == 128,
+               "kv_append_layers: head_dim must be a multiple of 8 (<= 256), group size 128");
+    CH_REQUIRE(kv_heads > 0 && kv_heads < 65536 && count < (1u << 31) && nlayers < 65536,
+               "kv_append_layers: bad sizes");
+    CH_REQUIRE(at + count <= max_seq, "kv_append_layers: keys beyond the cache capacity");
+    const size_t ntile = (max_seq + KS_T - 1) / KS_T;
+    const KvLayer* L = reinterpret_cast<const KvLayer*>(layers);
+    for (size_t l0 = 0; l0 < nlayers; l0 += KV_APPEND_MAX_LAYERS) {
+        const size_t nl = std::min<size_t>(KV_APPEND_MAX_LAYERS, nlayers - l0);
+        KvAppendSrc src{};
+        for (size_t l = 0; l < nl; l++) {
+            CH_REQUIRE(k_rows[l0 + l] && v_rows[l0 + l], "kv_append_layers: null row pointer");
+            src.k[l] = k_rows[l0 + l];
+            src.v[l] = v_rows[l0 + l];
+        }
+        hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)count, (unsigned)nl), dim3(256), 0, as_stream(stream),
+                           L + l0, src, at, (int)kv_heads, (int)head_dim, ntile);
+        const int rc = check_launch("kv_append_layers");
+        if (rc) return rc;
+    }
+    return CACTUS_HIP_OK;
 }
 
 static size_t kv_shift_token_bytes(size_t kv_heads, size_t head_dim) {

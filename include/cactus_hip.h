@@ -386,6 +386,18 @@ typedef struct {
 } cactus_hip_kv_layer;
 int cactus_hip_kv_shift_temp_bytes(size_t nlayers, size_t count, size_t kv_heads, size_t head_dim,
                                    size_t* bytes);
+/* No single reference function: the cache append of engine_cache.cpp:131-267
+ * (cactus_quantize_kv_fp16_to_int8 of each layer's new K and V rows,
+ * kernel_quants.cpp:223-293) for every layer in one launch, with the value
+ * products of cactus_hip_kv_shadow_update for records whose shadow is not
+ * NULL; identical to those calls layer by layer.  `layers` is a DEVICE array
+ * of nlayers records; k_rows / v_rows are HOST arrays of nlayers device
+ * pointers to [count][kv_heads][head_dim] fp16 rows, written to cache slots
+ * [at, at + count).  Quantization group 128 (the cache's). */
+int cactus_hip_kv_append_layers(const cactus_hip_kv_layer* layers, const uint16_t* const* k_rows,
+                                const uint16_t* const* v_rows, size_t nlayers, size_t count, size_t at,
+                                size_t kv_heads, size_t head_dim, size_t group_size, size_t max_seq,
+                                void* stream);
 int cactus_hip_kv_window_shift(const cactus_hip_kv_layer* layers, size_t nlayers, size_t kv_heads,
                                size_t head_dim, size_t max_seq, size_t dst, size_t src, size_t count,
                                void* temp, size_t temp_bytes, uint32_t* state, uint32_t cache_len,

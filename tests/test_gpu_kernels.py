@@ -597,6 +597,54 @@ def test_quantize_kv(dev, orc, S, H, d, gs):
     assert_bits(dev.get(q, np.int8, (S, H, d)), rq, "kv codes")
 
 
+@pytest.mark.parametrize("Hkv,d,count,at", [(8, 128, 256, 0), (2, 128, 37, 50), (2, 72, 9, 60), (1, 256, 3, 130)])
+def test_kv_append_layers(dev, orc, Hkv, d, count, at):
+    """The all-layer cache append equals, layer by layer, the quantization
+    of the new K and V rows (oracle: codes and scales at slots [at, at +
+    count), nothing else written) and the value products of
+    cactus_hip_kv_shadow_update over the same cache."""
+    say("kv_append_layers", Hkv, d, count, at)
+    nl, cap = 3, 300
+    rng = np.random.default_rng(Hkv * d + count + at)
+    ng = (d + 127) // 128
+    shb = ctypes.c_size_t()
+    dev.cm.call("cactus_hip_kv_shadow_bytes", cap, Hkv, d, ctypes.byref(shb))
+    recs, cache, srcs, want = [], [], [], []
+    for l in range(nl):
+        kf = f16(rng.normal(0, 1 + l, (count, Hkv, d)))
+        vf = f16(rng.normal(0, 2, (count, Hkv, d)))
+        init_c = rng.integers(-128, 128, (2, cap, Hkv, d), dtype=np.int8)
+        init_s = rng.random((2, cap, Hkv, ng), dtype=np.float32)
+        bufs = [dev.put(init_c[0]), dev.put(init_c[1]), dev.put(init_s[0]), dev.put(init_s[1]),
+                dev.put(np.zeros(shb.value // 4, np.float32))]
+        recs.append(bufs)
+        srcs.append((dev.put(kf), dev.put(vf)))
+        kc, ks = orc.quantize_kv(kf)
+        vc, vs = orc.quantize_kv(vf)
+        wc, ws = init_c.copy(), init_s.copy()
+        wc[0, at:at + count], wc[1, at:at + count] = kc, vc
+        ws[0, at:at + count], ws[1, at:at + count] = ks, vs
+        want.append((wc, ws))
+    table = dev.put(np.array(recs, np.uint64))
+    karr = (ctypes.c_void_p * nl)(*[k for k, _ in srcs])
+    varr = (ctypes.c_void_p * nl)(*[v for _, v in srcs])
+    dev.cm.call("cactus_hip_kv_append_layers", table, karr, varr, nl, count, at, Hkv, d, 128, cap, None)
+    for l in range(nl):
+        kb, vb, ksb, vsb, shp = recs[l]
+        wc, ws = want[l]
+        assert_bits(dev.get_ptr(kb, np.int8, (cap, Hkv, d)), wc[0], f"layer {l} key codes")
+        assert_bits(dev.get_ptr(vb, np.int8, (cap, Hkv, d)), wc[1], f"layer {l} value codes")
+        assert_bits(dev.get_ptr(ksb, np.float32, (cap, Hkv, ng)).view(np.uint32), ws[0].view(np.uint32),
+                    f"layer {l} key scales")
+        assert_bits(dev.get_ptr(vsb, np.float32, (cap, Hkv, ng)).view(np.uint32), ws[1].view(np.uint32),
+                    f"layer {l} value scales")
+        ref_sh = dev.empty(shb.value)
+        dev.cm.call("cactus_hip_memset", ref_sh.ptr, 0, shb.value, None)
+        dev.cm.call("cactus_hip_kv_shadow_update", vb, vsb, ref_sh.ptr, at, count, Hkv, d, 128, cap, None)
+        assert_bits(dev.get_ptr(shp, np.uint32, shb.value // 4), dev.get(ref_sh, np.uint32, shb.value // 4),
+                    f"layer {l} value products")
+
+
 # ------------------------------------------------------------------ a8-a14
 @pytest.mark.parametrize("rows,dims,eps", [(1, 1024, 1e-6), (256, 1024, 1e-6), (4096, 128, 1e-6),
                                            (3, 1000, 1e-5), (2, 1004, 1e-5), (1, 8, 1e-5)])
