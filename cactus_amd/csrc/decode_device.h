@@ -58,22 +58,27 @@ __device__ __forceinline__ uint16_t rms_apply(uint16_t x, uint16_t w, int i, int
 // tables' row for the position: pairs (i, i + d/2); the 8-aligned part of
 // the half row in fp16 arithmetic, the tail in fp32.  Writes the rotated
 // fp16 values through out(i, value).  One whole wave.
+// one rotated pair (i, i + d/2): fp16 arithmetic below vh = 8-aligned half, fp32 above
+__device__ __forceinline__ void rope_pair(uint16_t x1, uint16_t x2, uint16_t c, uint16_t s, bool fp16_part,
+                                          uint16_t& o1, uint16_t& o2) {
+    if (fp16_part) {
+        o1 = hfma(x2 ^ 0x8000u, s, hmul(x1, c));
+        o2 = hfma(x1, s, hmul(x2, c));
+    } else {
+        const float fa = h2f(x1), fb = h2f(x2), cf = h2f(c), sf = h2f(s);
+        o1 = f2h(fa * cf - fb * sf);
+        o2 = f2h(fb * cf + fa * sf);
+    }
+}
+
 template <class Out>
 __device__ __forceinline__ void rope_row(const uint16_t* ys, int d, const uint16_t* ct, const uint16_t* stb,
                                          Out out) {
     const int lane = threadIdx.x & 63;
     const int half = d / 2, vh = (half / 8) * 8;
     for (int i = lane; i < half; i += 64) {
-        const uint16_t x1 = ys[i], x2 = ys[i + half], c = ct[i], s = stb[i];
         uint16_t o1, o2;
-        if (i < vh) {
-            o1 = hfma(x2 ^ 0x8000u, s, hmul(x1, c));
-            o2 = hfma(x1, s, hmul(x2, c));
-        } else {
-            const float fa = h2f(x1), fb = h2f(x2), cf = h2f(c), sf = h2f(s);
-            o1 = f2h(fa * cf - fb * sf);
-            o2 = f2h(fb * cf + fa * sf);
-        }
+        rope_pair(ys[i], ys[i + half], ct[i], stb[i], i < vh, o1, o2);
         out(i, o1);
         out(i + half, o2);
     }

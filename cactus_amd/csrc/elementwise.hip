@@ -184,33 +184,81 @@ __global__ void __launch_bounds__(256) softmax_kernel(const uint16_t* __restrict
 // ---------------------------------------------------------------- SiLU, add, mul
 // The per-head RMSNorm of q and k (the q_norm / k_norm nodes,
 // kernel_attention.cpp:484-563) followed by RoPE (:565-676) at the rows'
-// positions: one wave per (token, head) row, the row and its normalized
-// values in LDS.  The same results as cactus_hip_rms_norm_f16 then
-// cactus_hip_rope_f16.
-__global__ void __launch_bounds__(256) rms_rope_rows_kernel(const uint16_t* __restrict__ X,
-                                                            const uint16_t* __restrict__ W,
-                                                            uint16_t* __restrict__ Y, const uint16_t* __restrict__ ct,
-                                                            const uint16_t* __restrict__ stb, size_t rows, int S,
-                                                            int H, int d, size_t start_pos, float eps) {
+// positions: one wave per (token, head) row.  Every global load of a row --
+// its values, the norm weights, the two table entries of each pair -- is
+// issued up front (clamped indices, no branches), so the wave waits for
+// memory once; the row and its normalized values pass through LDS for the
+// RMS chains and the pairing.  Up to two problems (q and k) per launch:
+// workgroups from nblk0 on take problem 1.  The same results as
+// cactus_hip_rms_norm_f16 then cactus_hip_rope_f16.
+struct RopeRowsArgs {
+    const uint16_t* X[2];
+    const uint16_t* W[2];
+    uint16_t* Y[2];
+    size_t rows[2];
+    int H[2];
+    int nblk0;
+    const uint16_t* ct;
+    const uint16_t* stb;
+    int S, d;
+    size_t start_pos;
+    float eps;
+};
+
+__global__ void __launch_bounds__(256) rms_rope_rows_kernel(RopeRowsArgs a) {
     __shared__ uint16_t buf[4][2][256];
+    constexpr int EPL = 4, PPL = 2;   // elements and pairs per lane (d <= 256)
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const size_t r = (size_t)blockIdx.x * 4 + wv;
-    if (r >= rows) return;   // the whole wave: no workgroup barrier below
-    const int s = (int)((r / H) % S);   // row = (b * S + s) * H + h
+    const bool p1 = (int)blockIdx.x >= a.nblk0;
+    const size_t r = (size_t)(p1 ? (int)blockIdx.x - a.nblk0 : (int)blockIdx.x) * 4 + wv;
+    if (r >= (p1 ? a.rows[1] : a.rows[0])) return;   // the whole wave: no workgroup barrier below
+    const uint16_t* X = p1 ? a.X[1] : a.X[0];
+    const uint16_t* W = p1 ? a.W[1] : a.W[0];
+    uint16_t* Y = p1 ? a.Y[1] : a.Y[0];
+    const int H = p1 ? a.H[1] : a.H[0];
+    const int d = a.d, half = d / 2, end8 = (d / 8) * 8, vh = (half / 8) * 8;
+    const int s = (int)((r / H) % a.S);   // row = (b * S + s) * H + h
+    const uint16_t* xr = X + r * d;
+    const size_t toff = (a.start_pos + s) * (size_t)half;
+    uint16_t xv[EPL], wgt[EPL], cv[PPL], sv[PPL];
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        const int i = min(lane + 64 * k, d - 1);
+        xv[k] = xr[i];
+        wgt[k] = W[i];
+    }
+#pragma unroll
+    for (int k = 0; k < PPL; k++) {
+        const int i = min(lane + 64 * k, half - 1);
+        cv[k] = a.ct[toff + i];
+        sv[k] = a.stb[toff + i];
+    }
     uint16_t* xs = buf[wv][0];
     uint16_t* ys = buf[wv][1];
-    const uint16_t* xr = X + r * d;
-    for (int i = lane; i < d; i += 64) xs[i] = xr[i];
+#pragma unroll
+    for (int k = 0; k < EPL; k++)
+        if (lane + 64 * k < d) xs[lane + 64 * k] = xv[k];
     wave_lds_order();
     float inv;
     uint16_t hinv;
-    rms_stats_wave(xs, d, eps, inv, hinv);
-    const int end8 = (d / 8) * 8;
-    for (int i = lane; i < d; i += 64) ys[i] = rms_apply(xs[i], W[i], i, end8, inv, hinv);
+    rms_stats_wave(xs, d, a.eps, inv, hinv);
+#pragma unroll
+    for (int k = 0; k < EPL; k++) {
+        const int i = lane + 64 * k;
+        if (i < d) ys[i] = rms_apply(xv[k], wgt[k], i, end8, inv, hinv);
+    }
     wave_lds_order();
-    const size_t toff = (start_pos + s) * (size_t)(d / 2);
     uint16_t* yr = Y + r * d;
-    rope_row(ys, d, ct + toff, stb + toff, [&](int i, uint16_t v) { yr[i] = v; });
+#pragma unroll
+    for (int k = 0; k < PPL; k++) {
+        const int i = lane + 64 * k;
+        if (i < half) {
+            uint16_t o1, o2;
+            rope_pair(ys[i], ys[i + half], cv[k], sv[k], i < vh, o1, o2);
+            yr[i] = o1;
+            yr[i + half] = o2;
+        }
+    }
 }
 
 __global__ void silu_kernel(const uint16_t* __restrict__ X, uint16_t* __restrict__ Y, size_t n) {
@@ -323,17 +371,35 @@ int cactus_hip_rope_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq
 int cactus_hip_rms_norm_rope_f16(const uint16_t* x, const uint16_t* weight, uint16_t* y, size_t batch,
                                  size_t seq_len, size_t num_heads, size_t head_dim, size_t start_pos, float theta,
                                  float eps, void* stream) {
-    const size_t rows = batch * seq_len * num_heads;
-    if (rows == 0) return CACTUS_HIP_OK;
-    CH_REQUIRE(x && weight && y, "rms_norm_rope: null pointer");
+    return cactus_hip_rms_norm_rope_qk_f16(x, weight, y, num_heads, nullptr, nullptr, nullptr, 0, batch, seq_len,
+                                           head_dim, start_pos, theta, eps, stream);
+}
+
+int cactus_hip_rms_norm_rope_qk_f16(const uint16_t* q, const uint16_t* q_weight, uint16_t* q_out, size_t q_heads,
+                                    const uint16_t* k, const uint16_t* k_weight, uint16_t* k_out, size_t kv_heads,
+                                    size_t batch, size_t seq_len, size_t head_dim, size_t start_pos, float theta,
+                                    float eps, void* stream) {
+    const size_t rq = batch * seq_len * q_heads, rk = batch * seq_len * kv_heads;
+    if (rq + rk == 0) return CACTUS_HIP_OK;
+    CH_REQUIRE((rq == 0 || (q && q_weight && q_out)) && (rk == 0 || (k && k_weight && k_out)),
+               "rms_norm_rope: null pointer");
     CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, "rms_norm_rope: head_dim must be even, <= 256");
-    CH_REQUIRE(rows / 4 < (1u << 31), "rms_norm_rope: too many rows");
+    CH_REQUIRE((rq + 3) / 4 + (rk + 3) / 4 < (1u << 31), "rms_norm_rope: too many rows");
     const RopeTable* t = nullptr;
     int rc = rope_table(seq_len + start_pos, head_dim, theta, &t);
     if (rc) return rc;
-    hipLaunchKernelGGL(rms_rope_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, as_stream(stream), x,
-                       weight, y, t->cos_d, t->sin_d, rows, (int)seq_len, (int)num_heads, (int)head_dim, start_pos,
-                       eps);
+    RopeRowsArgs a{};
+    // problem 0 is the first non-empty one
+    const bool only_k = rq == 0;
+    a.X[0] = only_k ? k : q;  a.W[0] = only_k ? k_weight : q_weight;  a.Y[0] = only_k ? k_out : q_out;
+    a.rows[0] = only_k ? rk : rq;  a.H[0] = (int)(only_k ? kv_heads : q_heads);
+    a.X[1] = k;  a.W[1] = k_weight;  a.Y[1] = k_out;
+    a.rows[1] = only_k ? 0 : rk;  a.H[1] = (int)(kv_heads ? kv_heads : 1);
+    a.nblk0 = (int)((a.rows[0] + 3) / 4);
+    a.ct = t->cos_d;  a.stb = t->sin_d;
+    a.S = (int)seq_len;  a.d = (int)head_dim;  a.start_pos = start_pos;  a.eps = eps;
+    const size_t blocks = a.nblk0 + (a.rows[1] + 3) / 4;
+    hipLaunchKernelGGL(rms_rope_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), a);
     return check_launch("rms_norm_rope");
 }
 

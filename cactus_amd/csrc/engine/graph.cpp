@@ -687,10 +687,34 @@ size_t CactusGraph::compute_shared_matmuls(size_t i) {
     return count;
 }
 
+// Two consecutive head RMSNorm + RoPE nodes of one sequence (q and k,
+// model_qwen.cpp:63-70 and :78-80) run as one launch.  Returns 2 when nodes
+// i and i + 1 were computed, else 0.
+size_t CactusGraph::compute_qk_rope(size_t i) {
+    if (i + 1 >= nodes_.size()) return 0;
+    GraphNode& a = *nodes_[i];
+    GraphNode& b = *nodes_[i + 1];
+    if (a.op != OpType::RMS_NORM_ROPE || b.op != OpType::RMS_NORM_ROPE) return 0;
+    const auto& sa = node(a.inputs[0]).out.shape;
+    const auto& sb = node(b.inputs[0]).out.shape;
+    if (sa[0] != sb[0] || sa[1] != sb[1] || sa[3] != sb[3] || a.params.position_offset != b.params.position_offset ||
+        a.params.theta != b.params.theta || a.params.epsilon != b.params.epsilon)
+        return 0;
+    allocate(b);
+    auto u16 = [&](size_t id) { return static_cast<const uint16_t*>(node(id).out.data); };
+    check_hip(cactus_hip_rms_norm_rope_qk_f16(u16(a.inputs[0]), u16(a.inputs[1]), static_cast<uint16_t*>(a.out.data),
+                                              sa[2], u16(b.inputs[0]), u16(b.inputs[1]),
+                                              static_cast<uint16_t*>(b.out.data), sb[2], sa[0], sa[1], sa[3],
+                                              a.params.position_offset, a.params.theta, a.params.epsilon, stream_),
+              "rms_norm_rope (q and k)");
+    return 2;
+}
+
 void CactusGraph::execute() {
     for (size_t i = 0; i < nodes_.size(); i++) {
         allocate(*nodes_[i]);
-        const size_t done = compute_shared_matmuls(i);
+        size_t done = compute_shared_matmuls(i);
+        if (!done) done = compute_qk_rope(i);
         if (done) {
             i += done - 1;
             continue;

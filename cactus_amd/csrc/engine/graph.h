@@ -194,6 +194,7 @@ private:
     void allocate(GraphNode& n);
     void compute(GraphNode& n);
     size_t compute_shared_matmuls(size_t i);
+    size_t compute_qk_rope(size_t i);
     void release_outputs();
 
     void* stream_;

@@ -300,9 +300,11 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos, size_t resid
     size_t q4, k4;
     size_t v4 = g.reshape(v, {1, S, nkv, hd});
     if (cfg_.rope_theta > 0) {
-        // the head RMSNorm and RoPE of q and of k, one node each
-        q4 = g.rms_norm_rope(g.reshape(q, {1, S, nh, hd}), L.n_q_norm, cfg_.eps, cfg_.rope_theta, pos);
-        k4 = g.rms_norm_rope(g.reshape(k, {1, S, nkv, hd}), L.n_k_norm, cfg_.eps, cfg_.rope_theta, pos);
+        // the head RMSNorm and RoPE of q and of k, one node each (adjacent:
+        // the executor runs the pair as one launch)
+        const size_t q_in = g.reshape(q, {1, S, nh, hd}), k_in = g.reshape(k, {1, S, nkv, hd});
+        q4 = g.rms_norm_rope(q_in, L.n_q_norm, cfg_.eps, cfg_.rope_theta, pos);
+        k4 = g.rms_norm_rope(k_in, L.n_k_norm, cfg_.eps, cfg_.rope_theta, pos);
     } else {
         q = g.reshape(q, {S * nh, hd});
         q = g.rms_norm(q, L.n_q_norm, cfg_.eps);

@@ -31,6 +31,24 @@ __global__ void fp16_to_int8_kernel(const uint16_t* __restrict__ src, int8_t* __
         dst[i] = quant_code(h2f(src[i]), inv, i >= body);
 }
 
+// element e of eight fp16 values held in a uint4
+__device__ __forceinline__ uint16_t u4_get(const uint4& v, int e) {
+    const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    return (uint16_t)(e & 1 ? w >> 16 : w & 0xFFFF);
+}
+__device__ __forceinline__ void u4_set(uint4& v, int e, uint16_t h) {
+    uint32_t& w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    w = e & 1 ? (w & 0xFFFFu) | ((uint32_t)h << 16) : (w & 0xFFFF0000u) | h;
+}
+
+// rows of K % 8 == 0 values (K <= 8192) at 16-byte aligned fp16 inputs and
+// 8-byte aligned codes: the register path of the row kernels
+constexpr int VEC_CPT = 4;   // 8-value chunks per thread
+__device__ __forceinline__ bool vec_rows_ok(const uint16_t* x, const uint16_t* w, const int8_t* q, int K) {
+    return (K & 7) == 0 && K <= 256 * 8 * VEC_CPT && ((((uintptr_t)x | (uintptr_t)w) & 15) == 0) &&
+           (((uintptr_t)q & 7) == 0);
+}
+
 // One workgroup per row: scale and codes of quantize_activations_fp16_to_int8.
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x,
                                                             int8_t* __restrict__ q,
@@ -38,6 +56,41 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
     __shared__ float red[4];
     const size_t row = blockIdx.x;
     const uint16_t* xr = x + row * (size_t)K;
+    if (blockDim.x == 256 && vec_rows_ok(x, x, q, K)) {
+        // the row in registers: one load, one reduction, codes from registers
+        const int tid = threadIdx.x, nch = K >> 3;
+        uint4 xv[VEC_CPT];
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++) xv[j] = reinterpret_cast<const uint4*>(xr)[min(tid + 256 * j, nch - 1)];
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++)
+            if (tid + 256 * j < nch)
+#pragma unroll
+                for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(u4_get(xv[j], e))));
+        m = wave_max(m);
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+        const float s = row_scale_from_max(mx);
+        const float inv = 1.0f / s;
+        int8_t* qr = q + row * (size_t)K;
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++) {
+            const int c = tid + 256 * j;
+            if (c < nch) {
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    lo |= (uint32_t)(uint8_t)quant_code(h2f(u4_get(xv[j], e)), inv, false) << (8 * e);
+                    hi |= (uint32_t)(uint8_t)quant_code(h2f(u4_get(xv[j], 4 + e)), inv, false) << (8 * e);
+                }
+                *reinterpret_cast<uint2*>(qr + 8 * c) = make_uint2(lo, hi);
+            }
+        }
+        if (tid == 0) scales[row] = s;
+        return;
+    }
     const float m = block_max_abs_f16(xr, K, red);
     const float s = row_scale_from_max(m);
     const float inv = 1.0f / s;
@@ -56,12 +109,75 @@ __global__ void __launch_bounds__(256) rms_quant_rows_kernel(const uint16_t* __r
                                                              const uint16_t* __restrict__ w,
                                                              int8_t* __restrict__ q, float* __restrict__ scales,
                                                              int K, float eps) {
-    extern __shared__ uint16_t xs[];   // the row, then its normalized values
+    extern __shared__ __align__(16) uint16_t xs[];   // the row, then its normalized values
     __shared__ float red[4];
     __shared__ float st[2];
     const int tid = threadIdx.x;
     const size_t row = blockIdx.x;
     const uint16_t* xr = x + row * (size_t)K;
+    if (vec_rows_ok(x, w, q, K)) {
+        // 16-byte chunks: the row and its weights loaded up front (clamped,
+        // branch-free), normalized and quantized in registers
+        const int nch = K >> 3;
+        uint4 xv[VEC_CPT], wv[VEC_CPT];
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++) {
+            const int c = min(tid + 256 * j, nch - 1);
+            xv[j] = reinterpret_cast<const uint4*>(xr)[c];
+            wv[j] = reinterpret_cast<const uint4*>(w)[c];
+        }
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++)
+            if (tid + 256 * j < nch) reinterpret_cast<uint4*>(xs)[tid + 256 * j] = xv[j];
+        __syncthreads();
+        if (tid < 64) {
+            float inv;
+            uint16_t hinv;
+            rms_stats_wave(xs, K, eps, inv, hinv);
+            if (tid == 0) {
+                st[0] = inv;
+                st[1] = __builtin_bit_cast(float, (uint32_t)hinv);
+            }
+        }
+        __syncthreads();
+        const float inv = st[0];
+        const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, st[1]);
+        float m = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++) {
+            const int c = tid + 256 * j;
+            if (c < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const uint16_t y = rms_apply(u4_get(xv[j], e), u4_get(wv[j], e), 8 * c + e, K, inv, hinv);
+                    u4_set(xv[j], e, y);
+                    m = __builtin_fmaxf(m, __builtin_fabsf(h2f(y)));
+                }
+            }
+        }
+        m = wave_max(m);
+        if ((tid & 63) == 0) red[tid >> 6] = m;
+        __syncthreads();
+        const float mx = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+        const float s = row_scale_from_max(mx);
+        const float inv_s = 1.0f / s;
+        int8_t* qr = q + row * (size_t)K;
+#pragma unroll
+        for (int j = 0; j < VEC_CPT; j++) {
+            const int c = tid + 256 * j;
+            if (c < nch) {
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    lo |= (uint32_t)(uint8_t)quant_code(h2f(u4_get(xv[j], e)), inv_s, false) << (8 * e);
+                    hi |= (uint32_t)(uint8_t)quant_code(h2f(u4_get(xv[j], 4 + e)), inv_s, false) << (8 * e);
+                }
+                *reinterpret_cast<uint2*>(qr + 8 * c) = make_uint2(lo, hi);
+            }
+        }
+        if (tid == 0) scales[row] = s;
+        return;
+    }
     for (int i = tid; i < K; i += 256) xs[i] = xr[i];
     __syncthreads();
     if (tid < 64) {

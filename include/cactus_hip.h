@@ -240,6 +240,15 @@ int cactus_hip_rms_norm_quantize_f16(const uint16_t* x, const uint16_t* weight, 
 int cactus_hip_rms_norm_rope_f16(const uint16_t* x, const uint16_t* weight, uint16_t* y, size_t batch,
                                  size_t seq_len, size_t num_heads, size_t head_dim, size_t start_pos, float theta,
                                  float eps, void* stream);
+/* No single reference function: the q and k head RMSNorm + RoPE nodes of
+ * model_qwen.cpp:63-70 and :78-80 in one launch, each output identical to
+ * cactus_hip_rms_norm_rope_f16 on that tensor alone.  q [batch][seq_len]
+ * [q_heads][head_dim] and k [..][kv_heads][head_dim] with their own norm
+ * weights; either head count may be 0. */
+int cactus_hip_rms_norm_rope_qk_f16(const uint16_t* q, const uint16_t* q_weight, uint16_t* q_out, size_t q_heads,
+                                    const uint16_t* k, const uint16_t* k_weight, uint16_t* k_out, size_t kv_heads,
+                                    size_t batch, size_t seq_len, size_t head_dim, size_t start_pos, float theta,
+                                    float eps, void* stream);
 /* No single reference function: the SwiGLU nodes silu(gate) * up
  * (cactus_silu_f16, kernel_nn.cpp:12-44; cactus_multiply_f16,
  * kernel_blas.cpp:291-316) fused with the row quantization of the matmul

@@ -67,7 +67,7 @@ def assert_bits(got, ref, what):
 
 
 # ------------------------------------------------------------------ a1
-@pytest.mark.parametrize("M,K", [(1, 640), (1, 1024), (3, 1001), (512, 1024), (2, 3072)])
+@pytest.mark.parametrize("M,K", [(1, 640), (1, 1024), (3, 1001), (512, 1024), (2, 3072), (2, 8192), (3, 8200)])
 def test_quantize_activations(dev, orc, M, K):
     say("quantize_activations", M, K)
     rng = np.random.default_rng(M * 7 + K)
@@ -736,7 +736,8 @@ def test_sample_greedy(dev, orc):
     assert rc == -2  # CACTUS_HIP_EUNSUPPORTED
 
 
-@pytest.mark.parametrize("M,K", [(256, 1024), (33, 1001), (1, 3072), (512, 2048), (40, 16)])
+@pytest.mark.parametrize("M,K", [(256, 1024), (33, 1001), (1, 3072), (512, 2048), (40, 16), (2, 8192),
+                                 (3, 8200)])
 def test_rms_norm_quantize_fused(dev, orc, M, K):
     """The fused RMSNorm + row quantization equals cactus_hip_rms_norm_f16
     followed by cactus_hip_quantize_activations, and the oracle's pair."""
@@ -769,7 +770,8 @@ def test_silu_mul_quantize_fused(dev, orc, M, K):
     assert_bits(dev.get(q, np.int8, (M, K)), rq, "codes")
 
 
-@pytest.mark.parametrize("S,H,d,pos", [(256, 16, 128, 3840), (1, 8, 128, 4095), (7, 4, 64, 0), (5, 2, 12, 9)])
+@pytest.mark.parametrize("S,H,d,pos", [(256, 16, 128, 3840), (1, 8, 128, 4095), (7, 4, 64, 0), (5, 2, 12, 9),
+                                       (3, 2, 256, 17), (6, 3, 200, 40)])
 def test_rms_norm_rope_fused(dev, orc, S, H, d, pos):
     """The head RMSNorm then RoPE in one launch equals the oracle's pair."""
     say("rms_norm_rope", S, H, d, pos)
@@ -781,6 +783,27 @@ def test_rms_norm_rope_fused(dev, orc, S, H, d, pos):
                 ctypes.c_float(1e6), ctypes.c_float(1e-6), None)
     ref = orc.rope(orc.rms_norm(x.reshape(S * H, d), w, 1e-6).reshape(1, S, H, d), pos, 1e6)
     assert_bits(dev.get(y, np.uint16, x.shape), ref, "rms_norm_rope")
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,d,pos", [(256, 16, 8, 128, 3840), (1, 16, 8, 128, 77), (5, 3, 1, 200, 2),
+                                            (4, 2, 0, 64, 0), (4, 0, 2, 64, 5)])
+def test_rms_norm_rope_qk(dev, orc, S, Hq, Hkv, d, pos):
+    """The q and k head RMSNorm + RoPE in one launch: each output equals the
+    oracle's pair on that tensor (either head count may be zero)."""
+    say("rms_norm_rope_qk", S, Hq, Hkv, d, pos)
+    rng = np.random.default_rng(S + Hq + Hkv + d + pos)
+    xs = [f16(rng.normal(0, 1.5, (1, S, H, d))) for H in (Hq, Hkv)]
+    ws = [f16(1 + rng.normal(0, 0.05, d)) for _ in range(2)]
+    ys = [dev.empty(max(x.nbytes, 2)) for x in xs]
+    ptr = lambda x: dev.put(x) if x.size else None
+    dev.cm.call("cactus_hip_rms_norm_rope_qk_f16", ptr(xs[0]), dev.put(ws[0]), ys[0].ptr, Hq, ptr(xs[1]),
+                dev.put(ws[1]), ys[1].ptr, Hkv, 1, S, d, pos, ctypes.c_float(1e6), ctypes.c_float(1e-6), None)
+    for x, w, y, what in zip(xs, ws, ys, ("q", "k")):
+        if x.size == 0:
+            continue
+        H = x.shape[2]
+        ref = orc.rope(orc.rms_norm(x.reshape(S * H, d), w, 1e-6).reshape(1, S, H, d), pos, 1e6)
+        assert_bits(dev.get(y, np.uint16, x.shape), ref, f"rms_norm_rope_qk ({what})")
 
 
 @pytest.mark.parametrize("M,K,N,gs,int4,shift", [(256, 1024, 1024, 32, False, 0), (256, 3072, 1024, 32, True, 0),
