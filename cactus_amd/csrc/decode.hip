@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 
     int8_t* actq = reinterpret_cast<int8_t*>(smem);                          // K
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + ((K + 15) & ~15));     // K
-    int32_t* acc = reinterpret_cast<int32_t*>(xs + ((K + 7) & ~7));         // vrows*G
+    int32_t* acc = reinterpret_cast<int32_t*>(xs + ((K + 7) & ~7) + 16 * RMS_T_PAD);   // vrows*G
     uint16_t* scl = reinterpret_cast<uint16_t*>(acc + vrows * G);           // vrows*G
     float* red = reinterpret_cast<float*>(scl + ((vrows * G + 1) & ~1));    // 8
 
@@ -153,16 +153,27 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         w = e & 1 ? (w & 0xFFFFu) | ((uint32_t)h << 16) : (w & 0xFFFF0000u) | h;
     };
     if (PRO == PRO_NORM) {
+        // rows of a multiple of 128 values go chain-major into LDS (the RMS
+        // chains then read 64 values per wait), others as they are
+        const bool chain_major = (K & 127) == 0;
 #pragma unroll
         for (int j = 0; j < CPT; j++) {
             const int c = tid + j * GEMV_THREADS;
-            if (c < nch) reinterpret_cast<uint4*>(xs)[c] = xv[j];
+            if (c < nch) {
+                if (chain_major) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) xs[rms_t_index(8 * c + e, K)] = elem(xv[j], e);
+                } else {
+                    reinterpret_cast<uint4*>(xs)[c] = xv[j];
+                }
+            }
         }
         __syncthreads();
         if (tid < 64) {
             float inv;
             uint16_t hinv;
-            rms_stats_wave(xs, K, a.eps, inv, hinv);
+            if (chain_major) rms_stats_wave_t(xs, K, a.eps, inv, hinv);
+            else rms_stats_wave(xs, K, a.eps, inv, hinv);
             if (tid == 0) { red[4] = inv; red[5] = __builtin_bit_cast(float, (uint32_t)hinv); }
         }
         __syncthreads();
@@ -192,15 +203,21 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     const float as = row_scale_from_max(mx);
     const float inv_s = 1.0f / as;
     const int body = (K / 8) * 8;
+    // the 8 codes of a chunk land in the chunk's own 8 bytes (act_pos only
+    // permutes within a chunk): one 8-byte LDS store per chunk
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
         const int c = tid + j * GEMV_THREADS;
         if (c < nch) {
+            uint32_t lo = 0, hi = 0;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const int i = 8 * c + e;
-                actq[act_pos<INT4>(i)] = quant_code(h2f(elem(xv[j], e)), inv_s, i >= body);
+                const int i = 8 * c + e, pos = act_pos<INT4>(i) - 8 * c;
+                const uint32_t code = (uint8_t)quant_code(h2f(elem(xv[j], e)), inv_s, i >= body);
+                if (pos < 4) lo |= code << (8 * pos);
+                else hi |= code << (8 * (pos - 4));
             }
+            *reinterpret_cast<uint2*>(actq + 8 * c) = make_uint2(lo, hi);
         }
     }
 #pragma unroll
@@ -220,23 +237,39 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     __syncthreads();
 
     // 4. reference epilogue
+    // one row's chain over its G groups; the next 16 groups' sums and scales
+    // are read from LDS while the current 16 FMAs run
     auto chain = [&](int vr) {
         float rs = 0.0f;
         const int32_t* ar = acc + vr * G;
         const uint16_t* sr = scl + vr * G;
-        int g = 0;
-        for (; g + 16 <= G; g += 16) {
-            int av[16];
-            uint16_t sv[16];
+        const int G16 = G & ~15;
+        int av[2][16];
+        uint16_t sv[2][16];
+        if (G16 > 0) {
 #pragma unroll
             for (int j = 0; j < 16; j++) {
-                av[j] = ar[g + j];
-                sv[j] = sr[g + j];
+                av[0][j] = ar[j];
+                sv[0][j] = sr[j];
             }
-#pragma unroll
-            for (int j = 0; j < 16; j++) rs = __builtin_fmaf((float)av[j], h2f(sv[j]), rs);
         }
-        for (; g < G; g++) rs = __builtin_fmaf((float)ar[g], h2f(sr[g]), rs);
+        for (int g = 0; g < G16; g += 32) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int gb = g + 16 * h;
+                if (gb < G16) {
+                    const int gn = min(gb + 16, G16 - 16);   // clamped prefetch: re-reads the last block
+#pragma unroll
+                    for (int j = 0; j < 16; j++) {
+                        av[h ^ 1][j] = ar[gn + j];
+                        sv[h ^ 1][j] = sr[gn + j];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 16; j++) rs = __builtin_fmaf((float)av[h][j], h2f(sv[h][j]), rs);
+                }
+            }
+        }
+        for (int g = G16; g < G; g++) rs = __builtin_fmaf((float)ar[g], h2f(sr[g]), rs);
         return f2h(rs * as);
     };
     for (int r = tid; r < nr; r += GEMV_THREADS) {
@@ -257,7 +290,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 }
 
 static size_t dec_gemv_smem(int K, int vrows, int G) {
-    size_t s = (size_t)((K + 15) & ~15) + (size_t)((K + 7) & ~7) * 2;
+    size_t s = (size_t)((K + 15) & ~15) + ((size_t)((K + 7) & ~7) + 16 * RMS_T_PAD) * 2;
     s += (size_t)vrows * G * 4 + (size_t)((vrows * G + 1) & ~1) * 2 + 8 * 4;
     return (s + 15) & ~(size_t)15;
 }

@@ -7,6 +7,18 @@
 namespace cactus_hip {
 
 // ----------------------------------------------------------------- RMSNorm
+// lanes 0..3: ((c_l + c_{l+4}) + c_{l+8}) + c_{l+12} of the 16 chain sums
+// (row_shl DPP moves within the first 16-lane row)
+__device__ __forceinline__ float rms_chain_combine4(float c) {
+    const int b = __builtin_bit_cast(int, c);
+    const float c4 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x104, 0xF, 0xF, false));
+    const float c8 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x108, 0xF, 0xF, false));
+    const float c12 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x10C, 0xF, 0xF, false));
+    return ((c + c4) + c8) + c12;
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
 // 1/rms of an fp16 row held in LDS, in the reference's order (16 fp32 FMA
 // chains, kernel_attention.cpp:500-538).  Called by one whole wave; every
 // lane returns inv and fp16(inv).
@@ -34,16 +46,55 @@ __device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float 
             chain = __builtin_fmaf(a, a, chain);
         }
     }
-    const float c4 = __shfl(chain, (lane + 4) & 63, 64);
-    const float c8 = __shfl(chain, (lane + 8) & 63, 64);
-    const float c12 = __shfl(chain, (lane + 12) & 63, 64);
-    const float t = ((chain + c4) + c8) + c12;
-    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    const float t = rms_chain_combine4(chain);
+    const float t0 = lane_value(t, 0), t1 = lane_value(t, 1), t2 = lane_value(t, 2), t3 = lane_value(t, 3);
     float ss = (t0 + t1) + (t2 + t3);
     for (int k = end8; k < n; k++) {
         const float a = h2f(xs[k]);
         ss = __builtin_fmaf(a, a, ss);
     }
+    const float rms = __builtin_sqrtf(ss / (float)n + eps);
+    inv = 1.0f / rms;
+    hinv = f2h(inv);
+}
+
+// rms_stats_wave over a row stored chain-major in LDS: chain l's values
+// x[16 i + l] at xt[l * (n / 16 + 8) + i] (8 elements of padding per chain
+// keep the 16 chains' 16-byte reads on distinct banks).  n % 128 == 0.  Each
+// chain lane loads 64 values at a time with eight 16-byte reads before its
+// FMAs, so the chain waits for LDS once per 64 steps; the same arithmetic
+// and order as rms_stats_wave.
+constexpr int RMS_T_PAD = 8;
+__device__ __forceinline__ int rms_t_index(int k, int n) {
+    return (k & 15) * (n / 16 + RMS_T_PAD) + (k >> 4);
+}
+__device__ __forceinline__ void rms_stats_wave_t(const uint16_t* xt, int n, float eps, float& inv,
+                                                 uint16_t& hinv) {
+    const int lane = threadIdx.x & 63;
+    const int n16 = n / 16, nb = n16 / 8;
+    float chain = 0.0f;
+    if (lane < 16) {
+        const uint4* p = reinterpret_cast<const uint4*>(xt + lane * (n16 + RMS_T_PAD));
+        for (int b = 0; b < nb; b += 8) {
+            uint4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = p[min(b + j, nb - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                if (b + j < nb) {
+                    const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float x = h2f((uint16_t)(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFF));
+                        chain = __builtin_fmaf(x, x, chain);
+                    }
+                }
+            }
+        }
+    }
+    const float t = rms_chain_combine4(chain);
+    const float t0 = lane_value(t, 0), t1 = lane_value(t, 1), t2 = lane_value(t, 2), t3 = lane_value(t, 3);
+    const float ss = (t0 + t1) + (t2 + t3);
     const float rms = __builtin_sqrtf(ss / (float)n + eps);
     inv = 1.0f / rms;
     hinv = f2h(inv);

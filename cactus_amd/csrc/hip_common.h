@@ -226,10 +226,22 @@ __device__ __forceinline__ void fmac_row_bcast(float& acc, float wv, float p) {
 }
 
 // ---------------------------------------------------------- wave reductions
+// Wave-wide max, uniform result; called by whole waves (all 64 lanes
+// active).  DPP moves within each 16-lane row (VALU speed, no LDS round
+// trips), then the four rows' maxima by readlane.  fmax is exact, so the
+// reduction order does not matter.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move_keep(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, 0xF, 0xF, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = __builtin_fmaxf(v, dpp_move_keep<0xB1>(v));    // quad_perm [1,0,3,2]
+    v = __builtin_fmaxf(v, dpp_move_keep<0x4E>(v));    // quad_perm [2,3,0,1]
+    v = __builtin_fmaxf(v, dpp_move_keep<0x141>(v));   // row_half_mirror
+    v = __builtin_fmaxf(v, dpp_move_keep<0x140>(v));   // row_mirror
+    auto lane_v = [&](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l)); };
+    return __builtin_fmaxf(__builtin_fmaxf(lane_v(0), lane_v(16)), __builtin_fmaxf(lane_v(32), lane_v(48)));
 }
 __device__ __forceinline__ int wave_sum_i32(int v) {
 #pragma unroll

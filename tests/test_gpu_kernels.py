@@ -725,15 +725,63 @@ def test_sample_greedy(dev, orc):
     dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.0), ctypes.c_float(0.0), 0, 0,
                 None)
     assert dev.get(out, np.uint32, 1)[0] == orc.argmax(logits) == 77
-    # the full sampler (tests/test_sampler.py covers it in depth); top-p
-    # without a top-k is refused
-    dev.cm.call("cactus_hip_sample_history_reset", None)
-    dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 20, 1, None)
-    assert dev.get(out, np.uint32, 1)[0] == orc.OracleSampler().sample(logits, 0.7, 0.9, 20, 1)
-    dev.cm.call("cactus_hip_sample_history_reset", None)
-    rc = dev.cm.hip().cactus_hip_sample_f16(lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), 0,
-                                            1, None)
-    assert rc == -2  # CACTUS_HIP_EUNSUPPORTED
+    # the full sampler (tests/test_sampler.py covers it in depth), with a
+    # top-k and with top-p over the whole vocabulary (top_k 0)
+    for top_k in (20, 0):
+        dev.cm.call("cactus_hip_sample_history_reset", None)
+        dev.cm.call("cactus_hip_sample_f16", lp, out.ptr, V, ctypes.c_float(0.7), ctypes.c_float(0.9), top_k, 1,
+                    None)
+        assert dev.get(out, np.uint32, 1)[0] == orc.OracleSampler().sample(logits, 0.7, 0.9, top_k, 1)
+
+
+@pytest.mark.parametrize("K,gs,Nq,Nkv,F", [(1024, 32, 2048, 1024, 3072), (640, 32, 1024, 256, 2048),
+                                            (1040, 16, 160, 96, 200), (256, 128, 128, 40, 96)])
+def test_decode_step_matmuls(dev, orc, K, gs, Nq, Nkv, F):
+    """The decode step's matmul kernels against the oracle's node chains, bit
+    for bit: RMSNorm + q/k/v (INT8), RMSNorm + gate/up (INT4) + SiLU * up,
+    and the INT8 / INT4 projections with the residual add.  Rows of a
+    multiple of 128 values take the chain-major RMS path, others (K 1040)
+    the row-major one."""
+    say("decode step matmuls", K, gs, Nq, Nkv, F)
+    rng = np.random.default_rng(K + gs + F)
+    eps = 1e-6
+    h = f16(rng.normal(0, 1.5, (1, K)))
+    nw = f16(1 + rng.normal(0, 0.05, K))
+    xq, xs = orc.quantize_activations(orc.rms_norm(h, nw, eps))
+    hp, nwp = dev.put(h), dev.put(nw)
+    ws = [grouped_int8_weights(rng, n, K, gs) for n in (Nq, Nkv, Nkv)]
+    outs = [dev.empty(n * 2) for n in (Nq, Nkv, Nkv)]
+    args = []
+    for (B, Bs), o in zip(ws, outs):
+        args += [dev.put(B), dev.put(Bs), o.ptr, B.shape[0]]
+    dev.cm.call("cactus_hip_decode_qkv", hp, nwp, ctypes.c_float(eps), K, gs, *args, None)
+    for (B, Bs), o, what in zip(ws, outs, "qkv"):
+        assert_bits(dev.get(o, np.uint16, (1, B.shape[0])), orc.matmul_int8(xq, xs, B, Bs, gs), f"decode {what}")
+    # gate/up (INT4, group 32) with SiLU * up; INT4 needs K % 32 == 0
+    if K % 32 == 0:
+        _, Wg, Sg = grouped_int4_weights(rng, F, K, 32)
+        _, Wu, Su = grouped_int4_weights(rng, F, K, 32)
+        m = dev.empty(F * 2)
+        dev.cm.call("cactus_hip_decode_mlp_up", hp, nwp, ctypes.c_float(eps), K, 32, dev.put(Wg), dev.put(Sg),
+                    dev.put(Wu), dev.put(Su), F, m.ptr, None)
+        want = orc.multiply(orc.silu(orc.matmul_int4(xq, xs, Wg, Sg, 32)), orc.matmul_int4(xq, xs, Wu, Su, 32))
+        assert_bits(dev.get(m, np.uint16, (1, F)), want, "decode gate/up")
+    # projections with the residual add: INT8 (K -> Nq) and INT4 (F -> K)
+    a = f16(rng.normal(0, 1, (1, Nq)))
+    Wo, So = grouped_int8_weights(rng, K, Nq, gs)
+    hr = dev.put(h)
+    dev.cm.call("cactus_hip_decode_matmul_residual", dev.put(a), Nq, gs, dev.put(Wo), dev.put(So), K, 0, hr, None)
+    aq, as_ = orc.quantize_activations(a)
+    want_o = orc.add(h, orc.matmul_int8(aq, as_, Wo, So, gs))
+    assert_bits(dev.get_ptr(hr, np.uint16, (1, K)), want_o, "decode o-proj + residual")
+    if F % 32 == 0:
+        mm = f16(rng.normal(0, 1, (1, F)))
+        _, Wd, Sd = grouped_int4_weights(rng, K, F, 32)
+        hd = dev.put(h)
+        dev.cm.call("cactus_hip_decode_matmul_residual", dev.put(mm), F, 32, dev.put(Wd), dev.put(Sd), K, 1, hd, None)
+        mq, ms = orc.quantize_activations(mm)
+        assert_bits(dev.get_ptr(hd, np.uint16, (1, K)), orc.add(h, orc.matmul_int4(mq, ms, Wd, Sd, 32)),
+                    "decode down + residual")
 
 
 @pytest.mark.parametrize("M,K", [(256, 1024), (33, 1001), (1, 3072), (512, 2048), (40, 16), (2, 8192),
