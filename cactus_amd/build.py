@@ -40,10 +40,13 @@ HIP_FLAGS = [
     "-Wno-unused-function",
 ]
 CXX_FLAGS = ["-O2", "-fPIC", "-std=c++17", "-Wall", "-ffp-contract=off"]
-# per-source additions: the MFMA matmul keeps its int32 accumulators in
-# ordinary VGPRs, so the fp32 epilogue reads them without v_accvgpr_read copies
+# per-source additions: MFMA accumulators in ordinary VGPRs, so the VALU
+# work on them (the matmul's fp32 group epilogue, the attention's per-tile
+# rescale) needs no v_accvgpr_read / v_accvgpr_write copies
 HIP_FILE_FLAGS = {
     "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # the prefill attention scales its output accumulators every key tile
+    "attention_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

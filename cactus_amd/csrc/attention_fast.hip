@@ -724,6 +724,10 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
     const int vrow = vm / GQ;
     const bool vok = vrow < a.S;
     const size_t vpos = a.pos_off + (size_t)vrow;
+    // the wave's first row (its smallest position) and whether all its rows exist
+    const int wrow0 = (gm0 + wid * 16) / GQ, wrow1 = (gm0 + wid * 16 + 15) / GQ;
+    const bool wave_all_rows = wrow1 < a.S;
+    const size_t wave_min_pos = a.pos_off + (size_t)wrow0;
     h16x8 qv[NC];
     {
         const uint16_t* qp = a.q + (((size_t)b * a.S + (vok ? vrow : 0)) * a.Hq + (size_t)g * GQ + vm % GQ) * D;
@@ -799,15 +803,33 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
         h16x8 k0, k1;
         _Float16 vh[16];
         if (cached) {
-            const uint32_t kw[4] = {r.kc.x, r.kc.y, r.kc.z, r.kc.w};
-            const uint32_t vw[4] = {r.vc.x, r.vc.y, r.vc.z, r.vc.w};
+            // key codes to exact fp16: the biased byte b ^ 0x80 = b + 128
+            // under the exponent byte 0x64 reads as 1024 + b + 128, and 1152
+            // comes off in packed fp16 (integers below 2048 are exact)
+            const uint32_t kx[4] = {r.kc.x ^ 0x80808080u, r.kc.y ^ 0x80808080u, r.kc.z ^ 0x80808080u,
+                                    r.kc.w ^ 0x80808080u};
+            typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+            const h16x2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                k0[e] = (_Float16)(float)(int8_t)(kw[e >> 2] >> (8 * (e & 3)));
-                k1[e] = (_Float16)(float)(int8_t)(kw[2 + (e >> 2)] >> (8 * (e & 3)));
+            for (int j = 0; j < 4; j++) {
+                const h16x2 lo = __builtin_bit_cast(h16x2, __builtin_amdgcn_perm(0x64646464u, kx[j], 0x04010400u)) - bias;
+                const h16x2 hi = __builtin_bit_cast(h16x2, __builtin_amdgcn_perm(0x64646464u, kx[j], 0x04030402u)) - bias;
+                h16x8& kd = j < 2 ? k0 : k1;
+                const int e0 = 4 * (j & 1);
+                kd[e0] = lo[0];
+                kd[e0 + 1] = lo[1];
+                kd[e0 + 2] = hi[0];
+                kd[e0 + 3] = hi[1];
             }
+            // values fp16(fp32(code * scale)): with u = code + 128 (an unsigned
+            // byte), fma(u, scale, -128 scale) is that fp32 product exactly
+            // (one rounding of u scale - 128 scale = code scale; -128 scale is exact)
+            const float ms = -128.0f * r.vs;
+            const uint32_t vx[4] = {r.vc.x ^ 0x80808080u, r.vc.y ^ 0x80808080u, r.vc.z ^ 0x80808080u,
+                                    r.vc.w ^ 0x80808080u};
 #pragma unroll
-            for (int e = 0; e < 16; e++) vh[e] = (_Float16)((float)(int8_t)(vw[e >> 2] >> (8 * (e & 3))) * r.vs);
+            for (int e = 0; e < 16; e++)
+                vh[e] = (_Float16)fp32_barrier(__builtin_fmaf((float)((vx[e >> 2] >> (8 * (e & 3))) & 0xFFu), r.vs, ms));
         } else {
             k0 = __builtin_bit_cast(h16x8, r.kn[0]);
             k1 = __builtin_bit_cast(h16x8, r.kn[1]);
@@ -861,14 +883,22 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
         }
         float s[8];
         float mx = NEG_INF;
+        // a tile below every row's causal end and the key range needs no
+        // mask (wave-uniform test); the others mask key by key
+        const size_t tile_last = (size_t)t * PF_T + PF_T - 1;
+        const bool interior = wave_all_rows && tile_last < kv_end && tile_last <= wave_min_pos;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const f32x4 ksv = *reinterpret_cast<const f32x4*>(&ksc[buf][16 * h + 4 * lg]);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const size_t kp = (size_t)t * PF_T + 16 * h + 4 * lg + i;
-                const bool ok = vok && kp < kv_end && kp <= vpos;
-                s[4 * h + i] = ok ? st[h][i] * ksv[i] : NEG_INF;
+                if (interior) {
+                    s[4 * h + i] = st[h][i] * ksv[i];
+                } else {
+                    const size_t kp = (size_t)t * PF_T + 16 * h + 4 * lg + i;
+                    const bool ok = vok && kp < kv_end && kp <= vpos;
+                    s[4 * h + i] = ok ? st[h][i] * ksv[i] : NEG_INF;
+                }
                 mx = __builtin_fmaxf(mx, s[4 * h + i]);
             }
         }
