@@ -9,9 +9,9 @@
 // operands (fp16 q, fp16 or INT8-times-scale k, fp32 sums) -- as an
 // HBM-bound split-K ("flash decoding") reduction:
 //
-//   grid (splits, batch * kv_heads), 256 threads = 4 waves per workgroup;
-//   workgroup s owns a split of 64 keys (INT8 cache) or 128 keys (FP16) of
-//   one KV head and all the query heads that share it (GQA).  Each wave
+//   grid (splits, batch * kv_heads), 512 threads = 8 waves per workgroup;
+//   workgroup s owns a split of 256 keys (32 per wave) of one KV head and
+//   all the query heads that share it (GQA).  Each wave
 //   scores its keys, the workgroup takes its local max M and weights
 //   exp(s - M), and each wave accumulates its keys' value rows.  The
 //   workgroup writes (M, sum, acc[d]) per query head; the last
@@ -34,13 +34,13 @@
 
 namespace cactus_hip {
 
-constexpr int FA_WAVES = 4;
+constexpr int FA_WAVES = 8;
 constexpr int FA_THREADS = 64 * FA_WAVES;
-// keys per wave: 32 (128-key splits; measured on MI355X at 4096 keys, 8 KV
-// heads: 12.9 us against 15.9 for 64-key and 15.6 for 256-key splits -- the
-// cross-XCD combine grows with the split count, the per-wave work with the
-// split size); for FP16 rows it also keeps each of the reference's 32-key
-// weight blocks inside one wave
+// keys per wave: 32, eight waves: 256-key splits (measured on MI355X at 4096
+// INT8 keys, 8 KV heads, 124 rotated caches: 10.6 us against 11.9 with four
+// waves (128-key splits, 272 workgroups on 256 CUs), 11.2 with six, 12.3
+// with twelve, 11.2 with eight waves of 16 keys); for FP16 rows 32 keys per
+// wave also keep each of the reference's 32-key weight blocks inside one wave
 template <bool HYBRID> constexpr int fa_kpw() { return 32; }
 template <bool HYBRID> constexpr int fa_kpb() { return fa_kpw<HYBRID>() * FA_WAVES; }
 constexpr int FA_MAX_SPLITS = 512;               // the combine keeps every split's (M, sum) in LDS
@@ -1085,8 +1085,8 @@ bool fast_attention_supported(size_t seq_len, size_t d, size_t gq, const void* m
 }
 
 // the combine holds every split's (M, sum) in LDS: at most FA_MAX_SPLITS splits
-constexpr size_t FA_MAX_KEYS_F16 = (size_t)FA_MAX_SPLITS * fa_kpb<false>();    // 65536
-constexpr size_t FA_MAX_KEYS_HYBRID = (size_t)FA_MAX_SPLITS * fa_kpb<true>();  // 32768
+constexpr size_t FA_MAX_KEYS_F16 = (size_t)FA_MAX_SPLITS * fa_kpb<false>();    // 131072
+constexpr size_t FA_MAX_KEYS_HYBRID = (size_t)FA_MAX_SPLITS * fa_kpb<true>();  // 131072
 
 int attention_fast_f16(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o, size_t B,
                        size_t Skv, size_t Hq, size_t Hkv, size_t d, float scale, size_t pos_off, size_t window,

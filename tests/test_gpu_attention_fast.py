@@ -167,6 +167,7 @@ def test_fast_entries_hand_other_shapes_to_the_exact_kernels(dev, orc):
 @pytest.mark.parametrize("cache,Hq,Hkv,d", [
     (4095, 16, 8, 128), (4096, 16, 8, 128), (4097, 16, 8, 128),   # split edges of the config-4 shape
     (127, 4, 2, 128), (128, 4, 2, 128), (129, 4, 2, 64), (300, 4, 4, 64), (0, 4, 2, 128),
+    (255, 4, 2, 128), (256, 4, 2, 128), (511, 4, 2, 64),                 # 256-key split edges
 ])
 def test_decode_prep_attention_fast(dev, orc, cache, Hq, Hkv, d):
     """The fused decode step's attention in tolerance mode against the exact
