@@ -239,6 +239,12 @@ size_t CactusGraph::embedding(size_t table, size_t indices) {
                     Precision::FP16);
 }
 
+size_t CactusGraph::embedding_checked_ids(size_t table, size_t indices) {
+    const size_t id = embedding(table, indices);
+    node(id).params.ids_checked = true;
+    return id;
+}
+
 size_t CactusGraph::index(size_t input, size_t index_value, int dim) {
     const auto& s = node(input).out.shape;
     if (dim != 0 || s.empty()) throw std::runtime_error("index: only dim 0 is built");
@@ -609,10 +615,15 @@ void CactusGraph::compute(GraphNode& n) {
             const BufferDesc& ids = in(1);
             if (t.precision != Precision::FP16 || ids.precision != Precision::FP32)
                 throw std::runtime_error("embedding: FP16 table with FP32 indices only");
-            if (!embed_err_) check_hip(cactus_hip_malloc(reinterpret_cast<void**>(&embed_err_), 4), "malloc");
-            check_hip(cactus_hip_memset(embed_err_, 0, 4, st), "memset");
+            int* err = nullptr;
+            if (!n.params.ids_checked) {
+                if (!embed_err_) check_hip(cactus_hip_malloc(reinterpret_cast<void**>(&embed_err_), 4), "malloc");
+                check_hip(cactus_hip_memset(embed_err_, 0, 4, st), "memset");
+                err = embed_err_;
+                embed_check_pending_ = true;
+            }
             check_hip(cactus_hip_embedding_f16(u16(t.data), static_cast<const float*>(ids.data), out16,
-                                               ids.total_size, t.shape[1], t.shape[0], embed_err_, st),
+                                               ids.total_size, t.shape[1], t.shape[0], err, st),
                       "embedding");
             return;
         }
@@ -721,7 +732,8 @@ void CactusGraph::execute() {
         }
         compute(*nodes_[i]);
     }
-    if (embed_err_) {
+    if (embed_check_pending_) {
+        embed_check_pending_ = false;
         int err = 0;
         check_hip(cactus_hip_memcpy_d2h(&err, embed_err_, 4, stream_), "embedding check");
         if (err) throw std::runtime_error("Embedding index out of bounds");

@@ -95,6 +95,7 @@ struct OpParams {
     std::vector<float> bias_values;       // logit bias (graph_builder.cpp:411-418)
     std::vector<uint32_t> bias_indices;
     size_t index_value = 0;
+    bool ids_checked = false;   // EMBEDDING: indices validated on the host (no device check)
     // ATTENTION_INT8_HYBRID (graph_builder.cpp:301-316)
     const int8_t* cached_keys_int8 = nullptr;
     const int8_t* cached_values_int8 = nullptr;
@@ -151,6 +152,9 @@ public:
     size_t add(size_t a, size_t b);
     size_t multiply(size_t a, size_t b);
     size_t embedding(size_t table, size_t indices);
+    // the same node for indices the caller has already checked against the
+    // table's row count on the host: execute() then needs no device read-back
+    size_t embedding_checked_ids(size_t table, size_t indices);
     size_t index(size_t input, size_t index_value, int dim);
     size_t reshape(size_t input, const std::vector<size_t>& new_shape);
     // random_seed 0: the reference's seed, the clock at build time
@@ -210,6 +214,7 @@ private:
     void* quant_scales_ = nullptr;
     size_t quant_cap_ = 0, quant_rows_cap_ = 0;
     int* embed_err_ = nullptr;
+    bool embed_check_pending_ = false;   // an unchecked embedding ran in this execute()
     // device copies of loaded tensor files
     std::unordered_map<std::string, size_t> weight_cache_;
     std::vector<void*> owned_weights_;

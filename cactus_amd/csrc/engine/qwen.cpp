@@ -368,8 +368,14 @@ size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
     g.soft_reset();
     const size_t S = tokens.size();
     const size_t pos = cache_.total_seq_len;
+    // the reference's out-of-range check (graph_ops_tensor.cpp:256-263), on
+    // the host ids before anything is launched
+    for (uint32_t t : tokens)
+        if (t >= cfg_.vocab)
+            throw std::runtime_error("Embedding index out of bounds: " + std::to_string(t) + " >= " +
+                                     std::to_string(cfg_.vocab));
     size_t ids = g.input({S}, Precision::FP32);
-    size_t h = g.embedding(n_embedding_, ids);
+    size_t h = g.embedding_checked_ids(n_embedding_, ids);
     std::vector<float> idf(S);
     for (size_t i = 0; i < S; i++) idf[i] = static_cast<float>(tokens[i]);
     g.set_input(ids, idf.data(), Precision::FP32);

@@ -101,3 +101,26 @@ def test_qwen_fused_decode_continues_after_reset():
     for layer in range(cfg["num_layers"]):
         for a, b in zip(gpu.read_kv(layer), orc.read_kv(layer)):
             assert (a == b).all(), f"kv cache layer {layer}"
+
+
+def test_qwen_prefill_rejects_out_of_range_token():
+    """A prompt id at or past the vocabulary is refused with the reference's
+    embedding error (graph_ops_tensor.cpp:256-263) before anything runs, and
+    the model stays usable: the next prompt matches the oracle."""
+    say("qwen out-of-range token")
+    cfg = qwen_small_config()
+    rng = np.random.default_rng(12)
+    w = qwen_weights(rng, cfg)
+    import cactus_amd
+    from cactus_amd.engine import Qwen
+    import oracle
+    cactus_amd.call("cactus_hip_init", 0)
+    gpu = Qwen(cfg, *w)
+    bad = np.array([3, cfg["vocab"], 5], np.uint32)
+    with pytest.raises(Exception, match="Embedding index out of bounds"):
+        gpu.prefill(bad)
+    gpu.reset()
+    p = rng.integers(0, cfg["vocab"], 40).astype(np.uint32)
+    toks, _ = gpu.generate(p, 4)
+    ref = oracle.OracleQwen(cfg, *w).generate(p, 4, cfg["prefill_chunk"])
+    assert list(toks) == list(ref)
