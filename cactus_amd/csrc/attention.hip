@@ -257,9 +257,7 @@ __global__ void __launch_bounds__(256) attn_scores_kernel(AttnArgs a_in) {
     for (int hh = 0; hh < gq; hh++) {
         float s = score[hh];
         // max over the 32 lanes of this block (half-wave reduction)
-        float m = s;
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off, 64));
+        const float m = half_wave_max(s);
         float w = 0.0f;
         if (in_block) {
             if (jl < vs4) w = poly_exp_weight(s, m);
@@ -625,9 +623,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
                 else if (a.mask && h2f(a.mask[(b * a.S + qp) * a.Skv + kp]) == 0.0f) sc = NEG_INF;
             }
         }
-        float mx = sc;
-#pragma unroll
-        for (int off = 16; off > 0; off >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float mx = half_wave_max(sc);
         const int vs4 = HYBRID ? 0 : (bsz / 4) * 4;
         float w = 0.0f;
         if (in_block) {

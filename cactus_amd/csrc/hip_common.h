@@ -235,6 +235,20 @@ __device__ __forceinline__ float dpp_move_keep(float v) {
     const int b = __builtin_bit_cast(int, v);
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, 0xF, 0xF, false));
 }
+// Max over the 32-lane half of the wave holding this lane (lanes 0-31 or
+// 32-63), every lane of the half gets it; whole waves.  DPP within each
+// 16-lane row, then v_permlane16_swap_b32 (lane l and l ^ 16 exchange; the
+// instruction as inline assembly: this compiler lowers the builtin's second
+// result as a copy of the first).  fmax is exact: the order does not matter.
+__device__ __forceinline__ float half_wave_max(float v) {
+    v = __builtin_fmaxf(v, dpp_move_keep<0xB1>(v));
+    v = __builtin_fmaxf(v, dpp_move_keep<0x4E>(v));
+    v = __builtin_fmaxf(v, dpp_move_keep<0x141>(v));
+    v = __builtin_fmaxf(v, dpp_move_keep<0x140>(v));
+    float x = v, y = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+    return __builtin_fmaxf(x, y);
+}
 __device__ __forceinline__ float wave_max(float v) {
     v = __builtin_fmaxf(v, dpp_move_keep<0xB1>(v));    // quad_perm [1,0,3,2]
     v = __builtin_fmaxf(v, dpp_move_keep<0x4E>(v));    // quad_perm [2,3,0,1]
