@@ -689,11 +689,11 @@ __device__ __forceinline__ float xrow_sum(float v) {
     return x + y;
 }
 
-template <int D, int GQ, int W, int NB>
+template <int D, int GQ, int W, int NB, int VB>
 __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a) {
     static_assert(D == 64 || D == 128, "head_dim 64 or 128");
     static_assert(64 * W >= 2 * D, "staging threads: 32 keys x D/16 pieces");
-    constexpr int NV = 16 * W;                 // query vectors per workgroup
+    constexpr int NV = 16 * W * VB;            // query vectors per workgroup (16 VB per wave)
     constexpr int KS = D + 8;                  // LDS row of a key tile, halves
     constexpr int VS = PF_T + 8;               // LDS row of a transposed value tile, halves
     constexpr int CPR = D / 16;                // 16-dim pieces per key row
@@ -719,22 +719,32 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
     const int nt = min(ntile_all - t_begin, a.tps);
     if (nt <= 0) return;   // no keys here; the combine counts only splits that hold some
 
-    // ---- this lane's query vector lr (B operand of S^T = K Q^T)
-    const int vm = gm0 + wid * 16 + lr;
-    const int vrow = vm / GQ;
-    const bool vok = vrow < a.S;
-    const size_t vpos = a.pos_off + (size_t)vrow;
+    // ---- this lane's query vectors: lr of each of the wave's VB blocks of
+    // 16 (B operands of S^T = K Q^T; every key and value fragment read from
+    // LDS feeds VB MFMAs, and the blocks' softmax chains interleave)
+    int vm[VB], vrow[VB];
+    bool vok[VB];
+    size_t vpos[VB];
+#pragma unroll
+    for (int vb = 0; vb < VB; vb++) {
+        vm[vb] = gm0 + (wid * VB + vb) * 16 + lr;
+        vrow[vb] = vm[vb] / GQ;
+        vok[vb] = vrow[vb] < a.S;
+        vpos[vb] = a.pos_off + (size_t)vrow[vb];
+    }
     // the wave's first row (its smallest position) and whether all its rows exist
-    const int wrow0 = (gm0 + wid * 16) / GQ, wrow1 = (gm0 + wid * 16 + 15) / GQ;
+    const int wrow0 = (gm0 + wid * 16 * VB) / GQ, wrow1 = (gm0 + wid * 16 * VB + 16 * VB - 1) / GQ;
     const bool wave_all_rows = wrow1 < a.S;
     const size_t wave_min_pos = a.pos_off + (size_t)wrow0;
-    h16x8 qv[NC];
-    {
-        const uint16_t* qp = a.q + (((size_t)b * a.S + (vok ? vrow : 0)) * a.Hq + (size_t)g * GQ + vm % GQ) * D;
+    h16x8 qv[VB][NC];
+#pragma unroll
+    for (int vb = 0; vb < VB; vb++) {
+        const uint16_t* qp =
+            a.q + (((size_t)b * a.S + (vok[vb] ? vrow[vb] : 0)) * a.Hq + (size_t)g * GQ + vm[vb] % GQ) * D;
 #pragma unroll
         for (int c = 0; c < NC; c++) {
-            const uint4 u = vok ? *reinterpret_cast<const uint4*>(qp + 32 * c + 8 * lg) : make_uint4(0, 0, 0, 0);
-            qv[c] = __builtin_bit_cast(h16x8, u);
+            const uint4 u = vok[vb] ? *reinterpret_cast<const uint4*>(qp + 32 * c + 8 * lg) : make_uint4(0, 0, 0, 0);
+            qv[vb][c] = __builtin_bit_cast(h16x8, u);
         }
     }
 
@@ -854,10 +864,15 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
 
     constexpr float LOG2E = 1.4426950408889634f;
     const float NEG_INF = -__builtin_inff();
-    float m_run = NEG_INF, l_run = 0.0f;
-    f32x4 acc[ND];   // O^T: lane l holds dims 16 db + 4 lg + i of vector lr
+    float m_run[VB], l_run[VB];
+    f32x4 acc[VB][ND];   // O^T: lane l holds dims 16 db + 4 lg + i of vector lr of each block
 #pragma unroll
-    for (int db = 0; db < ND; db++) acc[db] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int vb = 0; vb < VB; vb++) {
+        m_run[vb] = NEG_INF;
+        l_run[vb] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < ND; db++) acc[vb][db] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+    }
 
 #pragma unroll
     for (int u = 0; u < NB; u++) fetch(t_begin + u, raw[u]);   // clamped rows: in bounds past the split too
@@ -870,59 +885,70 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
         if (tl >= nt) break;
         const int t = t_begin + tl;
         const int buf = tl & 1;
-        // scores S^T for keys 16h + 4lg + i of the tile, vector lr
-        f32x4 st[2];
+        // scores S^T for keys 16h + 4lg + i of the tile, vector lr of each block
+        f32x4 st[VB][2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            st[h] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int vb = 0; vb < VB; vb++) st[vb][h] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int c = 0; c < NC; c++) {
                 const h16x8 kv = *reinterpret_cast<const h16x8*>(&ksh[buf][16 * h + lr][32 * c + 8 * lg]);
-                st[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv[c], st[h], 0, 0, 0);
+#pragma unroll
+                for (int vb = 0; vb < VB; vb++)
+                    st[vb][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qv[vb][c], st[vb][h], 0, 0, 0);
             }
         }
-        float s[8];
-        float mx = NEG_INF;
         // a tile below every row's causal end and the key range needs no
         // mask (wave-uniform test); the others mask key by key
         const size_t tile_last = (size_t)t * PF_T + PF_T - 1;
         const bool interior = wave_all_rows && tile_last < kv_end && tile_last <= wave_min_pos;
+        const f32x4 ksv0 = *reinterpret_cast<const f32x4*>(&ksc[buf][4 * lg]);
+        const f32x4 ksv1 = *reinterpret_cast<const f32x4*>(&ksc[buf][16 + 4 * lg]);
+        float corr[VB];
+        h16x8 pa[VB];   // P^T operands: keys {4 lg + j, 16 + 4 lg + j} of vector lr
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const f32x4 ksv = *reinterpret_cast<const f32x4*>(&ksc[buf][16 * h + 4 * lg]);
+        for (int vb = 0; vb < VB; vb++) {
+            float s[8];
+            float mx = NEG_INF;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                if (interior) {
-                    s[4 * h + i] = st[h][i] * ksv[i];
-                } else {
-                    const size_t kp = (size_t)t * PF_T + 16 * h + 4 * lg + i;
-                    const bool ok = vok && kp < kv_end && kp <= vpos;
-                    s[4 * h + i] = ok ? st[h][i] * ksv[i] : NEG_INF;
+            for (int h = 0; h < 2; h++) {
+                const f32x4 ksv = h ? ksv1 : ksv0;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (interior) {
+                        s[4 * h + i] = st[vb][h][i] * ksv[i];
+                    } else {
+                        const size_t kp = (size_t)t * PF_T + 16 * h + 4 * lg + i;
+                        const bool ok = vok[vb] && kp < kv_end && kp <= vpos[vb];
+                        s[4 * h + i] = ok ? st[vb][h][i] * ksv[i] : NEG_INF;
+                    }
+                    mx = __builtin_fmaxf(mx, s[4 * h + i]);
                 }
-                mx = __builtin_fmaxf(mx, s[4 * h + i]);
             }
-        }
-        mx = xrow_max(mx);
-        const float m_new = __builtin_fmaxf(m_run, mx);
-        const bool live = m_new > NEG_INF;
-        const float corr = live ? fast_exp2((m_run - m_new) * LOG2E) : 1.0f;
-        float psum = 0.0f;
-        h16x8 pa;   // P^T operand: keys {4 lg + j, 16 + 4 lg + j} of vector lr
+            mx = xrow_max(mx);
+            const float m_new = __builtin_fmaxf(m_run[vb], mx);
+            const bool live = m_new > NEG_INF;
+            corr[vb] = live ? fast_exp2((m_run[vb] - m_new) * LOG2E) : 1.0f;
+            float psum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float pv = (live && s[j] > NEG_INF) ? fast_exp2((s[j] - m_new) * LOG2E) : 0.0f;
-            psum += pv;
-            pa[j] = (_Float16)pv;
+            for (int j = 0; j < 8; j++) {
+                const float pv = (live && s[j] > NEG_INF) ? fast_exp2((s[j] - m_new) * LOG2E) : 0.0f;
+                psum += pv;
+                pa[vb][j] = (_Float16)pv;
+            }
+            l_run[vb] = l_run[vb] * corr[vb] + xrow_sum(psum);
+            m_run[vb] = m_new;
         }
-        l_run = l_run * corr + xrow_sum(psum);
-        m_run = m_new;
         // O^T += V^T P^T: A = V^T (dims 16 db + lr, the same 8 keys)
 #pragma unroll
         for (int db = 0; db < ND; db++) {
             const h16x4 v0 = *reinterpret_cast<const h16x4*>(&vt[buf][16 * db + lr][4 * lg]);
             const h16x4 v1 = *reinterpret_cast<const h16x4*>(&vt[buf][16 * db + lr][16 + 4 * lg]);
             const h16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pa, acc[db] * corr, 0, 0, 0);
+#pragma unroll
+            for (int vb = 0; vb < VB; vb++)
+                acc[vb][db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pa[vb], acc[vb][db] * corr[vb], 0, 0, 0);
         }
         // the next tile into the other LDS buffer (its last readers finished
         // before the previous barrier), then tile t + NB into this slot
@@ -931,27 +957,31 @@ __global__ void __launch_bounds__(64 * W) attn_prefill_mfma_kernel(PrefillArgs a
         __syncthreads();
     }
 
-    // ---- output: vector lr, dims 16 db + 4 lg + i
-    if (a.nsplit > 1) {
-        // this split's partial (acc, running max, sum) of the vector
-        const int nqb = (int)gridDim.x / a.nsplit;
-        float* pp = a.part + ((((size_t)bg * nqb + qb) * a.nsplit + sp_) * NV + wid * 16 + lr) * (D + 4);
+    // ---- output: vector lr of each block, dims 16 db + 4 lg + i
 #pragma unroll
-        for (int db = 0; db < ND; db++) *reinterpret_cast<f32x4*>(pp + 16 * db + 4 * lg) = acc[db];
-        if (lg == 0) {
-            pp[D] = m_run;
-            pp[D + 1] = l_run;
+    for (int vb = 0; vb < VB; vb++) {
+        if (a.nsplit > 1) {
+            // this split's partial (acc, running max, sum) of the vector
+            const int nqb = (int)gridDim.x / a.nsplit;
+            float* pp = a.part +
+                        ((((size_t)bg * nqb + qb) * a.nsplit + sp_) * NV + (wid * VB + vb) * 16 + lr) * (D + 4);
+#pragma unroll
+            for (int db = 0; db < ND; db++) *reinterpret_cast<f32x4*>(pp + 16 * db + 4 * lg) = acc[vb][db];
+            if (lg == 0) {
+                pp[D] = m_run[vb];
+                pp[D + 1] = l_run[vb];
+            }
+            continue;
         }
-        return;
-    }
-    if (!vok) return;
-    uint16_t* op = a.o + (((size_t)b * a.S + vrow) * a.Hq + (size_t)g * GQ + vm % GQ) * D;
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+        if (!vok[vb]) continue;
+        uint16_t* op = a.o + (((size_t)b * a.S + vrow[vb]) * a.Hq + (size_t)g * GQ + vm[vb] % GQ) * D;
+        const float inv = l_run[vb] > 0.0f ? 1.0f / l_run[vb] : 0.0f;
 #pragma unroll
-    for (int db = 0; db < ND; db++) {
-        const uint32_t lo = (uint32_t)f2h(acc[db][0] * inv) | ((uint32_t)f2h(acc[db][1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f2h(acc[db][2] * inv) | ((uint32_t)f2h(acc[db][3] * inv) << 16);
-        *reinterpret_cast<uint2*>(op + 16 * db + 4 * lg) = make_uint2(lo, hi);
+        for (int db = 0; db < ND; db++) {
+            const uint32_t lo = (uint32_t)f2h(acc[vb][db][0] * inv) | ((uint32_t)f2h(acc[vb][db][1] * inv) << 16);
+            const uint32_t hi = (uint32_t)f2h(acc[vb][db][2] * inv) | ((uint32_t)f2h(acc[vb][db][3] * inv) << 16);
+            *reinterpret_cast<uint2*>(op + 16 * db + 4 * lg) = make_uint2(lo, hi);
+        }
     }
 }
 
@@ -1133,19 +1163,19 @@ int attention_prefill_fast(const uint16_t* q, const int8_t* kc, const int8_t* vc
                            const uint16_t* k_new, const uint16_t* v_new, uint16_t* o, size_t B, size_t S,
                            size_t cache_len, size_t new_len, size_t Hq, size_t Hkv, size_t d, float scale,
                            size_t pos_off, size_t qgs, void* stream) {
-    constexpr int W = 4, NB = 3, NV = 16 * W;
+    constexpr int W = 4, NB = 2, VB = 2, NV = 16 * W * VB;
     PrefillArgs a{};
     a.q = q; a.kc = kc; a.vc = vc; a.ks = ks; a.vs = vs; a.kn = k_new; a.vn = v_new; a.o = o;
     a.B = (int)B; a.S = (int)S; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.nqg = (int)((d + qgs - 1) / qgs);
     a.cache_len = cache_len; a.new_len = new_len; a.pos_off = pos_off; a.scale = scale;
     const int gq = (int)(Hq / Hkv);
     const size_t nqb = (S * gq + NV - 1) / NV;
-    // key splits: enough workgroups to cover the CUs, at least 8 tiles each
+    // key splits: enough workgroups to cover the CUs, at least 4 tiles each
     size_t kv_last = pos_off + S;
     if (kv_last > cache_len + new_len) kv_last = cache_len + new_len;
     const size_t tiles = (kv_last + PF_T - 1) / PF_T;
     size_t nsplit = (512 + nqb * B * Hkv - 1) / (nqb * B * Hkv);
-    const size_t max_split = (tiles + 7) / 8;
+    const size_t max_split = (tiles + 3) / 4;
     if (nsplit > max_split) nsplit = max_split;
     if (nsplit > PF_MAX_SPLITS) nsplit = PF_MAX_SPLITS;
     if (nsplit < 1) nsplit = 1;
@@ -1169,7 +1199,7 @@ int attention_prefill_fast(const uint16_t* q, const int8_t* kc, const int8_t* vc
     };
 #define PF_CASE(D_, G_) \
     if (d == D_ && gq == G_) \
-        return go(attn_prefill_mfma_kernel<D_, G_, W, NB>, attn_prefill_combine_kernel<D_, G_, NV>);
+        return go(attn_prefill_mfma_kernel<D_, G_, W, NB, VB>, attn_prefill_combine_kernel<D_, G_, NV>);
     PF_CASE(128, 2) PF_CASE(128, 1) PF_CASE(128, 4) PF_CASE(64, 2) PF_CASE(64, 1) PF_CASE(64, 4)
 #undef PF_CASE
     return fail(CACTUS_HIP_EUNSUPPORTED, "attention (prefill, MFMA): head_dim 64/128 with 1, 2 or 4 query heads per KV head");
