@@ -486,6 +486,8 @@ def main():
     ap.add_argument("--attention-only", action="store_true")
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill matmul leg (configs 2 and 3), e.g. under rocprofv3 --pmc with --eager")
+    ap.add_argument("--gemv-only", action="store_true",
+                    help="only the INT8 (config 1) and INT4 (config 3, M=1) streaming GEMV legs, e.g. under rocprofv3 --pmc")
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--eager", action="store_true",
                     help="no HIP graphs: matmuls launched directly and the decode step enqueued per token "
@@ -511,6 +513,11 @@ def main():
         return
     if args.gemm_only:
         print(json.dumps(bench_prefill_gemms(eager=args.eager)), flush=True)
+        return
+    if args.gemv_only:
+        g = bench_gemv(args.steps, args.warmup)
+        print(json.dumps({"int8_gemv_gbs": round(g["gbs"], 1), "int4_gemv": bench_gemv_int4(args.steps, min(args.warmup, 50))}),
+              flush=True)
         return
     if args.copy_calibration:
         n = 1 << 30
