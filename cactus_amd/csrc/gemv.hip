@@ -63,6 +63,27 @@ __device__ __forceinline__ float group_epilogue(const int32_t* ag, const uint16_
     return rs;
 }
 
+// The same chain over group sums and scales that the lanes producing them
+// already converted to fp32 ((float)acc and the fp16 scale are exact): the
+// chain lane only reads and FMAs.
+template <int EPB = 8>
+__device__ __forceinline__ float group_epilogue_f(const float* ag, const float* sg, int G) {
+    float rs = 0.0f;
+    int g = 0;
+    for (; g + EPB <= G; g += EPB) {
+        float av[EPB], sv[EPB];
+#pragma unroll
+        for (int j = 0; j < EPB; j++) {
+            av[j] = ag[g + j];
+            sv[j] = sg[g + j];
+        }
+#pragma unroll
+        for (int j = 0; j < EPB; j++) rs = __builtin_fmaf(av[j], sv[j], rs);
+    }
+    for (; g < G; g++) rs = __builtin_fmaf(ag[g], sg[g], rs);
+    return rs;
+}
+
 template <int MR, bool F16ACT, bool INT4, int CH>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, int m0) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -202,7 +223,13 @@ static size_t gemv_smem(int MR, int K, int rows, int G) {
 // scales into the wave's own LDS slice, the loads of its next tile, then the
 // reference epilogue (kernel_gemm.cpp:311-324) by one lane per output while
 // those loads are in flight.
-template <int MR, bool F16ACT, bool INT4, int CH>
+//
+// FE (INT4 with 32-wide groups: one 16-byte chunk per group): the lane that
+// owns a chunk also owns its group, so it stores the group sum and the
+// group scale already converted to fp32, in rows padded by 4 floats (the
+// epilogue lanes read distinct banks); the K=3072 epilogue of 96 groups per
+// output then costs one FMA per group instead of two converts and an FMA.
+template <int MR, bool F16ACT, bool INT4, int CH, bool FE = false>
 __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int m0) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int K = a.K, gs = a.gs, G = K / gs;
@@ -219,13 +246,16 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
     const int cpr = INT4 ? K / 32 : K / 16;  // 16-byte chunks per row
     const int P = INT4 ? gs / 32 : gs / 16;  // chunks per group (power of 2, <= 64)
     const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
-    const int acc_words = MR * rows * G;
-    const int wave_bytes = ((acc_words * 4 + 15) & ~15) + ((rows * G * 2 + 15) & ~15);
+    const int Gs = FE ? G + 4 : G;   // row stride of the group sums and scales
+    const int acc_words = MR * rows * Gs;
+    const int wave_bytes = ((acc_words * 4 + 15) & ~15) + ((rows * Gs * (FE ? 4 : 2) + 15) & ~15);
 
     int8_t* actq = reinterpret_cast<int8_t*>(smem);  // MR*K
     unsigned char* wbase = smem + ((MR * K + 15) & ~15) + wid * wave_bytes;
     int32_t* acc = reinterpret_cast<int32_t*>(wbase);                                 // [MR][rows][G]
     uint16_t* scl = reinterpret_cast<uint16_t*>(wbase + ((acc_words * 4 + 15) & ~15));  // [rows][G]
+    float* accf = reinterpret_cast<float*>(acc);                                      // FE: [MR][rows][Gs]
+    float* sclf = reinterpret_cast<float*>(scl);                                      // FE: [rows][Gs]
     float* rsc = reinterpret_cast<float*>(smem + ((MR * K + 15) & ~15) + 4 * wave_bytes);  // MR
     float* red = rsc + MR;                                                                // 4
 
@@ -291,8 +321,14 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
         const int nr = min(rows, a.N - n0);
         const int nch = nr * cpr;
 #pragma unroll
-        for (int i = 0; i < CH; i++)
-            if (i * 64 + lane < nr * G) scl[i * 64 + lane] = sv[i];
+        for (int i = 0; i < CH; i++) {
+            if constexpr (FE) {
+                // one group per chunk: scale index = chunk index
+                if (i * 64 + lane < nch) sclf[crow[i] * Gs + ccol[i]] = h2f(sv[i]);
+            } else {
+                if (i * 64 + lane < nr * G) scl[i * 64 + lane] = sv[i];
+            }
+        }
 #pragma unroll
         for (int i = 0; i < CH; i++) {
             const bool valid = i * 64 + lane < nch;
@@ -305,8 +341,12 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             if (valid && (lane & (P - 1)) == 0) {
                 const int g = ccol[i] / P;
 #pragma unroll
-                for (int m = 0; m < MR; m++)
-                    if (m < mr) acc[(m * rows + crow[i]) * G + g] = dot[m];
+                for (int m = 0; m < MR; m++) {
+                    if (m < mr) {
+                        if constexpr (FE) accf[(m * rows + crow[i]) * Gs + g] = (float)dot[m];
+                        else acc[(m * rows + crow[i]) * G + g] = dot[m];
+                    }
+                }
             }
         }
         if (t + 4 < t1) load_tile(t + 4);
@@ -314,9 +354,14 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
         // reference epilogue, one lane per output of this tile
         for (int o = lane; o < mr * nr; o += 64) {
             const int m = o / nr, r = o - (o / nr) * nr;
-            const int32_t* ag = acc + (m * rows + r) * G;
-            const uint16_t* sg = scl + r * G;
-            const float rs = group_epilogue(ag, sg, G);
+            float rs;
+            if constexpr (FE) {
+                rs = group_epilogue_f<4>(accf + (m * rows + r) * Gs, sclf + r * Gs, G);
+            } else {
+                const int32_t* ag = acc + (m * rows + r) * G;
+                const uint16_t* sg = scl + r * G;
+                rs = group_epilogue(ag, sg, G);
+            }
             float s = rsm[0];
 #pragma unroll
             for (int mm = 1; mm < MR; mm++)
@@ -327,15 +372,23 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
     }
 }
 
-static size_t gemv_wave_smem(int MR, int K, int rows, int G) {
-    const size_t wave = (size_t)((MR * rows * G * 4 + 15) & ~15) + (size_t)((rows * G * 2 + 15) & ~15);
+static size_t gemv_wave_smem(int MR, int K, int rows, int G, bool fe = false) {
+    const int Gs = fe ? G + 4 : G;
+    const size_t wave = (size_t)((MR * rows * Gs * 4 + 15) & ~15) + (size_t)((rows * Gs * (fe ? 4 : 2) + 15) & ~15);
     return (size_t)((MR * K + 15) & ~15) + 4 * wave + (size_t)(MR + 4) * 4;
 }
 
 template <int MR, bool F16ACT, bool INT4, int CH>
-static int launch_gemv_wave_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st) {
+static int launch_gemv_wave_t(const GemvArgs& a, size_t batch, int m0, size_t smem, hipStream_t st, bool fe) {
     const int ntiles = (a.N + a.rows - 1) / a.rows;
     dim3 grid(ceil_div(ntiles, a.tiles), (unsigned)batch);
+    if constexpr (INT4) {
+        if (fe) {
+            hipLaunchKernelGGL((gemv_wave_kernel<MR, F16ACT, INT4, CH, true>), grid, dim3(GEMV_THREADS), smem,
+                               st, a, m0);
+            return check_launch("gemv_wave");
+        }
+    }
     hipLaunchKernelGGL((gemv_wave_kernel<MR, F16ACT, INT4, CH>), grid, dim3(GEMV_THREADS), smem,
                        st, a, m0);
     return check_launch("gemv_wave");
@@ -343,15 +396,15 @@ static int launch_gemv_wave_t(const GemvArgs& a, size_t batch, int m0, size_t sm
 
 template <int MR, bool F16ACT, bool INT4>
 static int launch_gemv_wave_ch(const GemvArgs& a, size_t batch, int m0, size_t smem, int ch,
-                               hipStream_t st) {
+                               hipStream_t st, bool fe) {
     switch (ch) {
-        case 1: return launch_gemv_wave_t<MR, F16ACT, INT4, 1>(a, batch, m0, smem, st);
-        case 2: return launch_gemv_wave_t<MR, F16ACT, INT4, 2>(a, batch, m0, smem, st);
-        case 3: return launch_gemv_wave_t<MR, F16ACT, INT4, 3>(a, batch, m0, smem, st);
-        case 4: return launch_gemv_wave_t<MR, F16ACT, INT4, 4>(a, batch, m0, smem, st);
-        case 5: return launch_gemv_wave_t<MR, F16ACT, INT4, 5>(a, batch, m0, smem, st);
-        case 6: return launch_gemv_wave_t<MR, F16ACT, INT4, 6>(a, batch, m0, smem, st);
-        default: return launch_gemv_wave_t<MR, F16ACT, INT4, 8>(a, batch, m0, smem, st);
+        case 1: return launch_gemv_wave_t<MR, F16ACT, INT4, 1>(a, batch, m0, smem, st, fe);
+        case 2: return launch_gemv_wave_t<MR, F16ACT, INT4, 2>(a, batch, m0, smem, st, fe);
+        case 3: return launch_gemv_wave_t<MR, F16ACT, INT4, 3>(a, batch, m0, smem, st, fe);
+        case 4: return launch_gemv_wave_t<MR, F16ACT, INT4, 4>(a, batch, m0, smem, st, fe);
+        case 5: return launch_gemv_wave_t<MR, F16ACT, INT4, 5>(a, batch, m0, smem, st, fe);
+        case 6: return launch_gemv_wave_t<MR, F16ACT, INT4, 6>(a, batch, m0, smem, st, fe);
+        default: return launch_gemv_wave_t<MR, F16ACT, INT4, 8>(a, batch, m0, smem, st, fe);
     }
 }
 
@@ -414,8 +467,10 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
     const int cpr = INT4 ? a.K / 32 : a.K / 16;
     const int MR = a.M >= 4 ? 4 : (a.M >= 2 ? 2 : 1);
     int wch = 0, wrows = 0;
+    // INT4 with 32-wide groups: one group per chunk, fp32 epilogue operands
+    const bool fe = INT4 && a.gs == 32;
     if (pick_wave_tile(cpr, a.N, batch, &wch, &wrows) &&
-        gemv_wave_smem(MR, a.K, wrows, G) <= 60 * 1024) {
+        gemv_wave_smem(MR, a.K, wrows, G, fe) <= 60 * 1024) {
         // wave tiles per workgroup: 4 (one per wave) up to 4*8, aiming at
         // about three resident rounds of 2048 workgroups
         const size_t nt = ceil_div(a.N, (size_t)wrows);
@@ -425,12 +480,12 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
         size_t nb = ceil_div(nt, 4 * per);
         a.rows = wrows;
         a.tiles = (int)ceil_div(nt, nb);  // balanced: every workgroup but the last full
-        const size_t smem = gemv_wave_smem(MR, a.K, wrows, G);
+        const size_t smem = gemv_wave_smem(MR, a.K, wrows, G, fe);
         for (int m0 = 0; m0 < a.M; m0 += MR) {
             int rc;
-            if (MR == 4) rc = launch_gemv_wave_ch<4, F16ACT, INT4>(a, batch, m0, smem, wch, st);
-            else if (MR == 2) rc = launch_gemv_wave_ch<2, F16ACT, INT4>(a, batch, m0, smem, wch, st);
-            else rc = launch_gemv_wave_ch<1, F16ACT, INT4>(a, batch, m0, smem, wch, st);
+            if (MR == 4) rc = launch_gemv_wave_ch<4, F16ACT, INT4>(a, batch, m0, smem, wch, st, fe);
+            else if (MR == 2) rc = launch_gemv_wave_ch<2, F16ACT, INT4>(a, batch, m0, smem, wch, st, fe);
+            else rc = launch_gemv_wave_ch<1, F16ACT, INT4>(a, batch, m0, smem, wch, st, fe);
             if (rc) return rc;
         }
         return CACTUS_HIP_OK;
