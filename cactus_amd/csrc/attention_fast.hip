@@ -141,8 +141,9 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // HYBRID: INT8 cache + FP16 new rows; otherwise FP16 keys and values.
-// PREP: q and the step's k come raw (head RMSNorm + RoPE here; the first
-// workgroup of each KV head also appends the step's k and v to the cache).
+// PREP: q and the step's k come raw (head RMSNorm + RoPE here); one extra
+// workgroup per KV head (blockIdx.x == nsplit) only prepares the step's k
+// and appends it and v to the cache, off the splits' critical path.
 //
 // Lane layout: a key row is CPL 16-byte chunks; CPL consecutive lanes read
 // one row (so each load instruction moves 64/CPL whole rows, coalesced) and
@@ -192,7 +193,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
     const size_t k1 = k0 + FA_KPB < kv_end ? k0 + FA_KPB : kv_end;
     const bool has_keys = k0 < kv_end;
     const bool has_new = HYBRID && has_keys && k1 > cache_len;
-    const bool appends = PREP && s == 0;
+    const bool appends = PREP && s == a.nsplit;
     const bool prep_ok = !PREP || pos < a.table_pos;   // the host keeps positions inside the tables
     const size_t wk0 = k0 + (size_t)wid * FA_KPW;      // this wave's first key
 
@@ -201,7 +202,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
     // preparation runs), so preparing them waits for these only and the key
     // and value rows below stay in flight meanwhile
     constexpr int EPL = D / 64;                        // elements per lane of a row
-    const bool do_q = PREP && prep_ok && wid < GQ;
+    const bool do_q = PREP && prep_ok && wid < GQ && !appends;
     const bool do_k = PREP && prep_ok && (has_new || appends) && wid == GQ % FA_WAVES;
     uint16_t pq[EPL], pqn[EPL], pk[EPL], pkn[EPL];
     uint16_t pcv = 0, psv = 0;
@@ -312,6 +313,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
         kv_append_row(a.v_raw + ((size_t)b * a.Hkv + g) * D, a.vc_w + row * D, a.vs_w + row * ng, D, a.vsh,
                       a.sh_ntile, cache_len, g);
     }
+    if (appends) return;   // the appending workgroup holds no split
     // this lane's query dims, fp32, and (INT8) their sum
     float qv[GQ][DPL], qsum[GQ];
 #pragma unroll
@@ -1099,7 +1101,7 @@ size_t fast_attention_splits(size_t keys, bool hybrid) {
 
 template <bool HYBRID, bool PREP>
 static int launch_fast(const FastArgs& a, int d, int gq, hipStream_t st) {
-    const dim3 grid((unsigned)a.nsplit, (unsigned)(a.B * a.Hkv));
+    const dim3 grid((unsigned)(a.nsplit + (PREP ? 1 : 0)), (unsigned)(a.B * a.Hkv));
     auto go = [&](auto kern) {
         hipLaunchKernelGGL(kern, grid, dim3(FA_THREADS), 0, st, a);
         return check_launch("attention (split-K)");
