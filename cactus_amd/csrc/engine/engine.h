@@ -45,6 +45,13 @@ public:
     // Throws where the reference's update is undefined (a sliding step
     // longer than window - sink) or the storage would overflow.
     void update(const std::vector<const void*>& k, const std::vector<const void*>& v, size_t seq, void* stream);
+    // The non-sliding append of update() split in two, for a prefill whose
+    // chunks overlap on two streams: put_layer writes layer l's seq new rows
+    // at slot `at` (the cache length before the chunk), appended() then
+    // advances the lengths once for the chunk.  Callers check fits(seq).
+    bool fits(size_t seq) const { return window_size == 0 && current_seq_len + seq <= max_seq_len; }
+    void put_layer(size_t l, const void* k, const void* v, size_t seq, size_t at, void* stream);
+    void appended(size_t seq);
     // After a one-token decode step into a full window (the fused path):
     // the step attended over all `window` cached tokens plus its own and
     // appended at slot `window` (the spare slot); tokens [sink + 1, window + 1)
@@ -144,7 +151,19 @@ private:
     size_t n_embedding_ = 0, n_out_norm_ = 0;
     KVCache cache_;
     float attn_scale_ = 0.0f;
-    std::vector<size_t> k_nodes_, v_nodes_;
+    std::vector<size_t> k_nodes_, v_nodes_, att_nodes_;
+    // Prefill with consecutive chunks overlapping on two streams: chunk i of
+    // n runs on graph_ / stream_ when n - 1 - i is even, else on graph2_ /
+    // stream2_ (so the last chunk is on graph_).  Each chunk appends layer
+    // l's KV rows as soon as they exist and records kv_ev_[parity][l]; the
+    // next chunk's layer-l attention waits for that event.
+    void prefill_overlapped(const std::vector<uint32_t>& tokens, size_t chunk);
+    void add_weight_nodes(CactusGraph& g);
+    CactusGraph* cur_ = nullptr;   // the graph the builders extend
+    void* stream2_ = nullptr;
+    std::unique_ptr<CactusGraph> graph2_;
+    std::vector<void*> kv_ev_[2];
+    void* join_ev_ = nullptr;
     size_t last_hidden_ = SIZE_MAX, last_logits_ = SIZE_MAX;
     bool fused_logits_ = false;   // the last step was a fused one (logits in fused_->logits())
     int decode_mode_ = 0;

@@ -722,15 +722,23 @@ size_t CactusGraph::compute_qk_rope(size_t i) {
 }
 
 void CactusGraph::execute() {
+    const bool hooks = !before_.empty() || !after_.empty();
+    auto run = [](std::unordered_map<size_t, std::function<void()>>& m, size_t id) {
+        auto it = m.find(id);
+        if (it != m.end()) it->second();
+    };
     for (size_t i = 0; i < nodes_.size(); i++) {
         allocate(*nodes_[i]);
+        if (hooks) run(before_, nodes_[i]->id);
         size_t done = compute_shared_matmuls(i);
         if (!done) done = compute_qk_rope(i);
-        if (done) {
-            i += done - 1;
-            continue;
+        if (!done) {
+            compute(*nodes_[i]);
+            done = 1;
         }
-        compute(*nodes_[i]);
+        if (hooks)
+            for (size_t j = i; j < i + done; j++) run(after_, nodes_[j]->id);
+        i += done - 1;
     }
     if (embed_check_pending_) {
         embed_check_pending_ = false;
@@ -759,6 +767,8 @@ void CactusGraph::soft_reset() {
     // graph_execute.cpp:640-675: keep INPUT nodes whose data is external
     // (weights), drop everything else; buffers go back to the pool
     check_hip(cactus_hip_stream_sync(stream_), "soft_reset sync");
+    before_.clear();
+    after_.clear();
     std::vector<std::unique_ptr<GraphNode>> keep;
     size_t max_id = 0;
     bool any = false;
@@ -782,6 +792,8 @@ void CactusGraph::soft_reset() {
 
 void CactusGraph::hard_reset() {
     release_outputs();
+    before_.clear();
+    after_.clear();
     nodes_.clear();
     index_.clear();
     host_mirror_.clear();

@@ -12,6 +12,7 @@
 #include <memory>
 #include <stdexcept>
 #include <string>
+#include <functional>
 #include <unordered_map>
 #include <vector>
 
@@ -183,6 +184,12 @@ public:
     void save_node(size_t node, const std::string& filename);
 
     // --- execution
+    // Callbacks run by execute() on the host around a node's launch: `before`
+    // just before it is enqueued, `after` once it (with the nodes the
+    // executor merges into the same launch) has been enqueued.  Keyed by node
+    // id; soft_reset drops them.  Used to order work across streams.
+    void before_node(size_t id, std::function<void()> f) { before_[id] = std::move(f); }
+    void after_node(size_t id, std::function<void()> f) { after_[id] = std::move(f); }
     void execute();
     void soft_reset();   // drop all non-INPUT nodes (weights stay)
     void hard_reset();
@@ -202,6 +209,7 @@ private:
     void release_outputs();
 
     void* stream_;
+    std::unordered_map<size_t, std::function<void()>> before_, after_;
     size_t next_id_ = 0;
     std::vector<std::unique_ptr<GraphNode>> nodes_;
     std::unordered_map<size_t, size_t> index_;

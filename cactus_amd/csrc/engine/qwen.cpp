@@ -154,6 +154,22 @@ void KVCache::update(const std::vector<const void*>& k, const std::vector<const 
     total_seq_len += seq;
 }
 
+void KVCache::put_layer(size_t l, const void* k, const void* v, size_t seq, size_t at, void* stream) {
+    if (seq == 0) return;
+    const uint16_t* kr = static_cast<const uint16_t*>(k);
+    const uint16_t* vr = static_cast<const uint16_t*>(v);
+    check_hip(cactus_hip_kv_append_layers(table_.as<cactus_hip_kv_layer>() + l, &kr, &vr, 1, seq, at, num_kv_heads,
+                                          head_dim, GROUP, slots, stream),
+              "kv update (layer)");
+}
+
+void KVCache::appended(size_t seq) {
+    if (!fits(seq)) throw std::runtime_error("KV cache: overlapped append beyond the capacity or into a window");
+    current_seq_len += seq;
+    total_seq_len += seq;
+    resident = current_seq_len;
+}
+
 void KVCache::slide_after_step(uint32_t* state, void* stream) {
     const size_t W = window_size, S = sink_size;
     if (W == 0 || current_seq_len != W) throw std::runtime_error("slide_after_step: the window is not full");
@@ -184,16 +200,8 @@ QwenModel::QwenModel(const cactus_qwen_config& cfg, const cactus_qwen_layer_weig
     // engine_model.cpp:125-129
     attn_scale_ = 1.0f / std::sqrt(static_cast<float>(hd));
 
-    CactusGraph& g = *graph_;
-    auto weight = [&](const std::vector<size_t>& shape, Precision p, void* dev) {
-        size_t id = g.input(shape, p);
-        g.set_external_input(id, dev, p);
-        return id;
-    };
     embedding_ = upload_buf(embedding, (size_t)cfg.vocab * H * 2, stream_);
     out_norm_ = upload_buf(output_norm, H * 2, stream_);
-    n_embedding_ = weight({cfg.vocab, H}, Precision::FP16, embedding_.ptr);
-    n_out_norm_ = weight({H}, Precision::FP16, out_norm_.ptr);
     layers_.resize(cfg.num_layers);
     for (uint32_t l = 0; l < cfg.num_layers; l++) {
         const cactus_qwen_layer_weights& w = lw[l];
@@ -216,42 +224,68 @@ QwenModel::QwenModel(const cactus_qwen_config& cfg, const cactus_qwen_layer_weig
         L.up_s = upload_buf(w.up_s, F * (H / gs) * 2, stream_);
         L.down_w = upload_buf(w.down_w, H * F / 2, stream_);
         L.down_s = upload_buf(w.down_s, H * (F / gs) * 2, stream_);
-        // QwenModel::load_weights_to_graph (model_qwen.cpp:17-49)
-        L.n_input_norm = weight({H}, Precision::FP16, L.input_norm.ptr);
-        L.n_post_norm = weight({H}, Precision::FP16, L.post_norm.ptr);
-        L.n_q_norm = weight({hd}, Precision::FP16, L.q_norm.ptr);
-        L.n_k_norm = weight({hd}, Precision::FP16, L.k_norm.ptr);
-        L.n_q = weight({nq, H}, Precision::INT8, L.q_w.ptr);
-        g.set_grouped_scales(L.n_q, gs, H / gs, L.q_s.ptr);
-        L.n_k = weight({nkv, H}, Precision::INT8, L.k_w.ptr);
-        g.set_grouped_scales(L.n_k, gs, H / gs, L.k_s.ptr);
-        L.n_v = weight({nkv, H}, Precision::INT8, L.v_w.ptr);
-        g.set_grouped_scales(L.n_v, gs, H / gs, L.v_s.ptr);
-        L.n_o = weight({H, nq}, Precision::INT8, L.o_w.ptr);
-        g.set_grouped_scales(L.n_o, gs, nq / gs, L.o_s.ptr);
-        // packed INT4 MLP weights keep their shape in elements
-        L.n_gate = weight({F, H}, Precision::INT8, L.gate_w.ptr);
-        g.set_grouped_scales(L.n_gate, gs, H / gs, L.gate_s.ptr);
-        g.set_packed_int4(L.n_gate, L.gate_w.ptr, F * H / 2);
-        L.n_up = weight({F, H}, Precision::INT8, L.up_w.ptr);
-        g.set_grouped_scales(L.n_up, gs, H / gs, L.up_s.ptr);
-        g.set_packed_int4(L.n_up, L.up_w.ptr, F * H / 2);
-        L.n_down = weight({H, F}, Precision::INT8, L.down_w.ptr);
-        g.set_grouped_scales(L.n_down, gs, F / gs, L.down_s.ptr);
-        g.set_packed_int4(L.n_down, L.down_w.ptr, H * F / 2);
     }
+    add_weight_nodes(*graph_);
+    cur_ = graph_.get();
     cache_.init(cfg.num_layers, cfg.max_seq, cfg.kv_heads, hd);
     check_hip(cactus_hip_rope_reserve(cfg.max_seq + 1, hd, cfg.rope_theta), "rope_reserve");
     check_hip(cactus_hip_stream_sync(stream_), "init sync");
     k_nodes_.assign(cfg.num_layers, SIZE_MAX);
     v_nodes_.assign(cfg.num_layers, SIZE_MAX);
+    att_nodes_.assign(cfg.num_layers, SIZE_MAX);
+}
+
+// QwenModel::load_weights_to_graph (model_qwen.cpp:17-49): the weights as
+// external INPUT nodes.  A fresh graph gets the same node ids in the same
+// order, so the layers' ids hold for graph_ and graph2_ alike.
+void QwenModel::add_weight_nodes(CactusGraph& g) {
+    const cactus_qwen_config& cfg = cfg_;
+    const size_t H = cfg.hidden, F = cfg.ffn, hd = cfg.head_dim, gs = cfg.group_size;
+    const size_t nq = (size_t)cfg.heads * hd, nkv = (size_t)cfg.kv_heads * hd;
+    const bool first = &g == graph_.get();
+    auto weight = [&](size_t& id_out, const std::vector<size_t>& shape, Precision p, void* dev) {
+        const size_t id = g.input(shape, p);
+        g.set_external_input(id, dev, p);
+        if (first) id_out = id;
+        else if (id != id_out) throw std::runtime_error("second prefill graph: weight node ids differ");
+        return id;
+    };
+    weight(n_embedding_, {cfg.vocab, H}, Precision::FP16, embedding_.ptr);
+    weight(n_out_norm_, {H}, Precision::FP16, out_norm_.ptr);
+    for (uint32_t l = 0; l < cfg.num_layers; l++) {
+        QwenLayer& L = layers_[l];
+        weight(L.n_input_norm, {H}, Precision::FP16, L.input_norm.ptr);
+        weight(L.n_post_norm, {H}, Precision::FP16, L.post_norm.ptr);
+        weight(L.n_q_norm, {hd}, Precision::FP16, L.q_norm.ptr);
+        weight(L.n_k_norm, {hd}, Precision::FP16, L.k_norm.ptr);
+        g.set_grouped_scales(weight(L.n_q, {nq, H}, Precision::INT8, L.q_w.ptr), gs, H / gs, L.q_s.ptr);
+        g.set_grouped_scales(weight(L.n_k, {nkv, H}, Precision::INT8, L.k_w.ptr), gs, H / gs, L.k_s.ptr);
+        g.set_grouped_scales(weight(L.n_v, {nkv, H}, Precision::INT8, L.v_w.ptr), gs, H / gs, L.v_s.ptr);
+        g.set_grouped_scales(weight(L.n_o, {H, nq}, Precision::INT8, L.o_w.ptr), gs, nq / gs, L.o_s.ptr);
+        // packed INT4 MLP weights keep their shape in elements
+        const size_t ng = weight(L.n_gate, {F, H}, Precision::INT8, L.gate_w.ptr);
+        g.set_grouped_scales(ng, gs, H / gs, L.gate_s.ptr);
+        g.set_packed_int4(ng, L.gate_w.ptr, F * H / 2);
+        const size_t nu = weight(L.n_up, {F, H}, Precision::INT8, L.up_w.ptr);
+        g.set_grouped_scales(nu, gs, H / gs, L.up_s.ptr);
+        g.set_packed_int4(nu, L.up_w.ptr, F * H / 2);
+        const size_t nd = weight(L.n_down, {H, F}, Precision::INT8, L.down_w.ptr);
+        g.set_grouped_scales(nd, gs, F / gs, L.down_s.ptr);
+        g.set_packed_int4(nd, L.down_w.ptr, H * F / 2);
+    }
 }
 
 QwenModel::~QwenModel() {
     cactus_hip_stream_sync(stream_);
+    if (stream2_) cactus_hip_stream_sync(stream2_);
     fused_.reset();
     graph_.reset();
+    graph2_.reset();
     layers_.clear();
+    for (auto& evs : kv_ev_)
+        for (void* e : evs) cactus_hip_event_destroy(e);
+    if (join_ev_) cactus_hip_event_destroy(join_ev_);
+    if (stream2_) cactus_hip_stream_destroy(stream2_);
     cactus_hip_stream_destroy(stream_);
 }
 
@@ -273,7 +307,7 @@ const void* QwenModel::last_logits_data() const {
 // matmul node would compute for itself) runs once as a node of its own;
 // a decode-sized GEMV quantizes inside its kernel at no extra launch.
 size_t QwenModel::shared_matmul_input(size_t x) {
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     const BufferDesc& b = g.get_output_buffer(x);
     if (b.precision == Precision::INT8) return x;   // already codes with row scales
     return b.shape[0] >= 32 ? g.quantize_activations(x) : x;
@@ -282,14 +316,14 @@ size_t QwenModel::shared_matmul_input(size_t x) {
 // The RMSNorm in front of q/k/v and of gate/up feeds only those matmuls: at
 // prefill sizes it is one node with their row quantization.
 size_t QwenModel::norm_for_matmuls(size_t h, size_t weight) {
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     if (g.get_output_buffer(h).shape[0] >= 32) return g.rms_norm_quantize(h, weight, cfg_.eps);
     return g.rms_norm(h, weight, cfg_.eps);
 }
 
 // model_qwen.cpp:51-106
 size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos, size_t residual) {
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     const QwenLayer& L = layers_[l];
     const size_t hd = cfg_.head_dim, nh = cfg_.heads, nkv = cfg_.kv_heads;
     const size_t xq = shared_matmul_input(x);
@@ -322,6 +356,7 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos, size_t resid
                                       cache_.current_seq_len, nkv, hd);
     else
         att = g.attention(q4, k4, v4, attn_scale_, pos);
+    att_nodes_[l] = att;
     att = g.reshape(att, {S, hd * nh});
     if (residual != NO_RESIDUAL) return g.matmul_add(att, L.n_o, residual);
     return g.matmul(att, L.n_o, true);
@@ -329,7 +364,7 @@ size_t QwenModel::build_attention(size_t x, uint32_t l, size_t pos, size_t resid
 
 // model_qwen.cpp:109-117
 size_t QwenModel::build_mlp(size_t x, uint32_t l, size_t residual) {
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     const QwenLayer& L = layers_[l];
     const size_t xq = shared_matmul_input(x);
     size_t gate = g.matmul(xq, L.n_gate, true);
@@ -349,7 +384,7 @@ size_t QwenModel::build_mlp(size_t x, uint32_t l, size_t residual) {
 
 // model_qwen.cpp:120-129
 size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     const QwenLayer& L = layers_[l];
     size_t x = norm_for_matmuls(h, L.n_input_norm);
     // at prefill sizes the residual adds ride on the o-proj and down matmuls
@@ -364,7 +399,7 @@ size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
 // model_qwen.cpp:132-172 (use_cache = true)
 size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
     if (tokens.empty()) throw std::runtime_error("Token sequence cannot be empty");
-    CactusGraph& g = *graph_;
+    CactusGraph& g = *cur_;
     g.soft_reset();
     const size_t S = tokens.size();
     const size_t pos = cache_.total_seq_len;
@@ -403,6 +438,10 @@ void QwenModel::set_kv_window(size_t window, size_t sink) {
 void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
     if (tokens.empty()) return;
     const size_t chunk = cfg_.prefill_chunk ? cfg_.prefill_chunk : 256;
+    if (tokens.size() > chunk && cache_.fits(tokens.size())) {
+        prefill_overlapped(tokens, chunk);
+        return;
+    }
     // the graph is rebuilt per chunk: no logits node survives a prefill
     last_logits_ = SIZE_MAX;
     fused_logits_ = false;
@@ -419,6 +458,74 @@ void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
     const size_t full = (tokens.size() - 1) / chunk;
     for (size_t i = 0; i < full; i++) process(i * chunk, (i + 1) * chunk);
     process(full * chunk, tokens.size());
+}
+
+// The chunks of engine_model.cpp:170-219 (the same boundaries and the
+// same nodes as prefill's serial loop) with consecutive chunks overlapping
+// on two streams.  Chunk c + 1 reads chunk c's KV rows only in its
+// attention nodes, so chunk c appends each layer's rows right after that
+// layer's k/v nodes (one launch per layer instead of one per chunk, the same
+// bytes) and records an event that chunk c + 1's attention of the layer
+// waits for.  Every kernel sees the inputs of the serial order: the results
+// are bit-identical to it.
+void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t chunk) {
+    const size_t L = cfg_.num_layers;
+    if (!graph2_) {
+        check_hip(cactus_hip_stream_create(&stream2_), "stream_create");
+        graph2_ = std::make_unique<CactusGraph>(stream2_);
+        add_weight_nodes(*graph2_);
+        for (auto& evs : kv_ev_) {
+            evs.assign(L, nullptr);
+            for (void*& e : evs) check_hip(cactus_hip_event_create(&e), "event_create");
+        }
+        check_hip(cactus_hip_event_create(&join_ev_), "event_create");
+    }
+    graph2_->set_attention_tolerance(attention_mode_ == 1);
+    // stream2_ starts after everything already queued on stream_ (the cache
+    // contents the first chunk attends to)
+    check_hip(cactus_hip_event_record(join_ev_, stream_), "event_record");
+    check_hip(cactus_hip_stream_wait_event(stream2_, join_ev_), "stream_wait_event");
+    last_logits_ = SIZE_MAX;
+    fused_logits_ = false;
+    std::vector<std::pair<size_t, size_t>> bounds;
+    const size_t full = (tokens.size() - 1) / chunk;
+    for (size_t i = 0; i < full; i++) bounds.emplace_back(i * chunk, (i + 1) * chunk);
+    bounds.emplace_back(full * chunk, tokens.size());
+    const size_t n = bounds.size();
+    try {
+        for (size_t i = 0; i < n; i++) {
+            const int par = (int)((n - 1 - i) % 2);
+            CactusGraph& g = par == 0 ? *graph_ : *graph2_;
+            void* st = par == 0 ? stream_ : stream2_;
+            cur_ = &g;
+            const std::vector<uint32_t> c(tokens.begin() + bounds[i].first, tokens.begin() + bounds[i].second);
+            last_hidden_ = forward(c);
+            const size_t at = cache_.current_seq_len, seq = c.size();
+            for (size_t l = 0; l < L; l++) {
+                const size_t kn = k_nodes_[l], vn = v_nodes_[l];
+                void* ev = kv_ev_[par][l];
+                g.after_node(kn, [this, &g, l, kn, vn, seq, at, st, ev] {
+                    cache_.put_layer(l, g.get_output_buffer(kn).data, g.get_output_buffer(vn).data, seq, at, st);
+                    check_hip(cactus_hip_event_record(ev, st), "event_record");
+                });
+                if (i > 0) {
+                    void* prev = kv_ev_[1 - par][l];
+                    g.before_node(att_nodes_[l], [st, prev] {
+                        check_hip(cactus_hip_stream_wait_event(st, prev), "stream_wait_event");
+                    });
+                }
+            }
+            g.execute();
+            cache_.appended(seq);
+        }
+    } catch (...) {
+        cur_ = graph_.get();
+        throw;
+    }
+    cur_ = graph_.get();
+    // later work on stream_ (decode, reset) follows all of stream2_'s
+    check_hip(cactus_hip_event_record(join_ev_, stream2_), "event_record");
+    check_hip(cactus_hip_stream_wait_event(stream_, join_ev_), "stream_wait_event");
 }
 
 // engine_model.cpp:221-297, greedy

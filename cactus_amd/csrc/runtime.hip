@@ -144,6 +144,12 @@ int cactus_hip_event_record(void* event, void* stream) {
     return CACTUS_HIP_OK;
 }
 
+int cactus_hip_stream_wait_event(void* stream, void* event) {
+    CH_REQUIRE(event, "stream_wait_event: null event");
+    CH_HIP(hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0));
+    return CACTUS_HIP_OK;
+}
+
 int cactus_hip_event_elapsed_ms(void* start, void* end, float* ms) {
     CH_REQUIRE(ms, "event_elapsed_ms: null");
     CH_HIP(hipEventSynchronize(reinterpret_cast<hipEvent_t>(end)));

@@ -53,6 +53,9 @@ int         cactus_hip_stream_sync(void* stream);
 int         cactus_hip_event_create(void** event);
 int         cactus_hip_event_destroy(void* event);
 int         cactus_hip_event_record(void* event, void* stream);
+/* later work on `stream` waits for the event's last record (cross-stream
+ * ordering; no reference counterpart) */
+int         cactus_hip_stream_wait_event(void* stream, void* event);
 int         cactus_hip_event_elapsed_ms(void* start, void* end, float* ms);
 /* Stream capture into a HIP graph (the fused decode step is captured once
  * and replayed per token).  No reference counterpart. */
