@@ -203,8 +203,8 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     const float as = row_scale_from_max(mx);
     const float inv_s = 1.0f / as;
     const int body = (K / 8) * 8;
-    // the 8 codes of a chunk land in the chunk's own 8 bytes (act_pos only
-    // permutes within a chunk): one 8-byte LDS store per chunk
+    // the 8 codes of a chunk in its own 8 bytes (INT4: the nib_pack8
+    // layout): one 8-byte LDS store per chunk
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
         const int c = tid + j * GEMV_THREADS;
@@ -212,12 +212,12 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
             uint32_t lo = 0, hi = 0;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const int i = 8 * c + e, pos = act_pos<INT4>(i) - 8 * c;
+                const int i = 8 * c + e;
                 const uint32_t code = (uint8_t)quant_code(h2f(elem(xv[j], e)), inv_s, i >= body);
-                if (pos < 4) lo |= code << (8 * pos);
-                else hi |= code << (8 * (pos - 4));
+                if (e < 4) lo |= code << (8 * e);
+                else hi |= code << (8 * (e - 4));
             }
-            *reinterpret_cast<uint2*>(actq + 8 * c) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(actq + 8 * c) = INT4 ? nib_pack8(lo, hi) : make_uint2(lo, hi);
         }
     }
 #pragma unroll
@@ -391,18 +391,24 @@ struct LmDecArgs {
 
 // LM head + greedy argmax, streamed: each wave owns 64 vocabulary rows (one
 // per lane) and moves them through its own ring of LMS_D slots by LDS DMA
-// (64 k-values of 64 rows per slot, 8 KB), LMS_D - 1 chunks ahead, with no
+// (LMS_KC k-values of 64 rows per slot), LMS_D - 1 chunks ahead, with no
 // cross-wave barrier in the K loop.  Consecutive lanes fetch consecutive
 // 16-byte pieces of one row; piece p of row r sits in slot position
-// p ^ (r & 7), so the per-lane row reads of one piece hit distinct banks.
+// p ^ (r % pieces per row), so the per-lane row reads of one piece spread
+// over the banks.
 // Each lane's dot is the reference's 8-lane fp16 accumulation in k order.
-// (eight waves per workgroup sharing one RMSNorm prologue and a two-slot
-// ring per wave measured fastest on MI355X: 74 us for the 151936 x 1024
-// Qwen3 head against 101 us with two waves and three slots)
-constexpr int LMS_WAVES = 8, LMS_THREADS = 64 * LMS_WAVES;
-constexpr int LMS_KC = 64;                              // k-values per chunk
-constexpr int LMS_D = 2;                                // ring slots per wave
-constexpr int LMS_SLOT = 64 * LMS_KC * 2;               // 8 KB
+// Ten waves per workgroup (one RMSNorm prologue) with three 4 KB slots
+// each: the 151936 x 1024 Qwen3 head is 238 workgroups, at most one per CU
+// (a workgroup takes ~130 KB of LDS).  Measured on MI355X, standalone: 67 us
+// against 74-78 us for eight waves with two 8 KB slots (297 workgroups, so
+// 41 CUs ran two in turn), 71.5 us for twelve waves, 85-106 us with 2 KB
+// slots; 101 us for two waves.
+constexpr int LMS_WAVES = 10, LMS_THREADS = 64 * LMS_WAVES;
+constexpr int LMS_KC = 32;                              // k-values per chunk
+constexpr int LMS_D = 3;                                // ring slots per wave
+constexpr int LMS_SLOT = 64 * LMS_KC * 2;               // 4 KB
+constexpr int LMS_P2 = 1024;                            // power of two >= LMS_THREADS (argmax tree)
+static_assert(LMS_P2 >= LMS_THREADS && LMS_P2 / 2 < LMS_THREADS, "argmax tree");
 constexpr int LMS_NI = LMS_SLOT / 1024;                 // DMA instructions per chunk
 static_assert(LMS_D >= 2 && LMS_D <= 4, "wait counts below");
 
@@ -418,12 +424,14 @@ __global__ void __launch_bounds__(LMS_THREADS) dec_lm_head_stream_kernel(LmDecAr
     const int row0 = (blockIdx.x * LMS_WAVES + wid) * 64;
     const int nk = K / LMS_KC;
 
-    // DMA sources: instruction j moves rows 8 j + lane / 8, piece (lane % 8) ^ (row % 8)
+    // DMA sources: a row's chunk is PPR 16-byte pieces; instruction j moves
+    // rows (64 / PPR) j + lane / PPR, piece (lane % PPR) ^ (row % PPR)
+    constexpr int PPR = LMS_KC / 8;
     const uint16_t* src[LMS_NI];
 #pragma unroll
     for (int j = 0; j < LMS_NI; j++) {
-        const int r = 8 * j + (lane >> 3);
-        const int pc = (lane & 7) ^ (r & 7);
+        const int r = (64 / PPR) * j + lane / PPR;
+        const int pc = (lane % PPR) ^ (r % PPR);
         src[j] = p.b + (size_t)min(row0 + r, N - 1) * K + pc * 8;
     }
     auto issue = [&](int k) {
@@ -469,7 +477,7 @@ __global__ void __launch_bounds__(LMS_THREADS) dec_lm_head_stream_kernel(LmDecAr
         const unsigned char* rp = rowp + (k % LMS_D) * LMS_SLOT;
 #pragma unroll
         for (int ch = 0; ch < LMS_KC / 8; ch++) {
-            const uint4 bv = *reinterpret_cast<const uint4*>(rp + ((ch ^ (lane & 7)) * 16));
+            const uint4 bv = *reinterpret_cast<const uint4*>(rp + ((ch ^ (lane % PPR)) * 16));
             const uint4 av = *reinterpret_cast<const uint4*>(as + k * LMS_KC + ch * 8);
             f16_step(acc, av, bv);
         }
@@ -487,8 +495,8 @@ __global__ void __launch_bounds__(LMS_THREADS) dec_lm_head_stream_kernel(LmDecAr
     __shared__ uint32_t bi_s[LMS_THREADS];
     __shared__ bool last;
     auto reduce = [&]() {
-        for (int w = LMS_THREADS / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w) {
+        for (int w = LMS_P2 / 2; w > 0; w >>= 1) {
+            if ((int)threadIdx.x < w && (int)threadIdx.x + w < LMS_THREADS) {
                 const float ov = bv_s[threadIdx.x + w];
                 const uint32_t oi = bi_s[threadIdx.x + w];
                 const float mv = bv_s[threadIdx.x];

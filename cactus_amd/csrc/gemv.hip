@@ -143,12 +143,31 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
             const float mx = block_max_abs_f16(x, K, red);
             const float s = row_scale_from_max(mx);
             const float inv = 1.0f / s;
-            for (int i = tid; i < K; i += GEMV_THREADS)
-                actq[m * K + act_pos<INT4>(i)] = quant_code(h2f(x[i]), inv, i >= body);
+            if constexpr (INT4) {
+                for (int r = tid; r < K / 8; r += GEMV_THREADS) {
+                    uint32_t w2[2] = {0, 0};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        w2[e >> 2] |= (uint32_t)(uint8_t)quant_code(h2f(x[8 * r + e]), inv, 8 * r + e >= body)
+                                      << (8 * (e & 3));
+                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                }
+            } else {
+                for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = quant_code(h2f(x[i]), inv, i >= body);
+            }
             if (tid == 0) rsc[m] = s;
         } else {
             const int8_t* x = a.A8 + bi * a.sA + (size_t)(m0 + m) * K;
-            for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + act_pos<INT4>(i)] = x[i];
+            if constexpr (INT4) {
+                for (int r = tid; r < K / 8; r += GEMV_THREADS) {
+                    uint32_t w2[2] = {0, 0};   // byte loads: the codes carry no alignment promise
+#pragma unroll
+                    for (int e = 0; e < 8; e++) w2[e >> 2] |= (uint32_t)(uint8_t)x[8 * r + e] << (8 * (e & 3));
+                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                }
+            } else {
+                for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = x[i];
+            }
             if (tid == 0) rsc[m] = a.As[bi * (a.sA / K) + m0 + m];
         }
     }
@@ -302,12 +321,31 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             const float mx = block_max_abs_f16(x, K, red);
             const float s = row_scale_from_max(mx);
             const float inv = 1.0f / s;
-            for (int i = tid; i < K; i += GEMV_THREADS)
-                actq[m * K + act_pos<INT4>(i)] = quant_code(h2f(x[i]), inv, i >= body);
+            if constexpr (INT4) {
+                for (int r = tid; r < K / 8; r += GEMV_THREADS) {
+                    uint32_t w2[2] = {0, 0};
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        w2[e >> 2] |= (uint32_t)(uint8_t)quant_code(h2f(x[8 * r + e]), inv, 8 * r + e >= body)
+                                      << (8 * (e & 3));
+                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                }
+            } else {
+                for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = quant_code(h2f(x[i]), inv, i >= body);
+            }
             if (tid == 0) rsc[m] = s;
         } else {
             const int8_t* x = a.A8 + bi * a.sA + (size_t)(m0 + m) * K;
-            for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + act_pos<INT4>(i)] = x[i];
+            if constexpr (INT4) {
+                for (int r = tid; r < K / 8; r += GEMV_THREADS) {
+                    uint32_t w2[2] = {0, 0};   // byte loads: the codes carry no alignment promise
+#pragma unroll
+                    for (int e = 0; e < 8; e++) w2[e >> 2] |= (uint32_t)(uint8_t)x[8 * r + e] << (8 * (e & 3));
+                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                }
+            } else {
+                for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = x[i];
+            }
             if (tid == 0) rsc[m] = a.As[bi * (a.sA / K) + m0 + m];
         }
     }

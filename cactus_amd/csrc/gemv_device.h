@@ -8,43 +8,56 @@ namespace cactus_hip {
 
 constexpr int GEMV_THREADS = 256;
 
-// position of activation element i in LDS; INT4 stores each 8-element run as
-// its 4 even elements followed by its 4 odd elements so that one dword pairs
-// with the low nibbles and the next with the high nibbles of a weight dword
-template <bool INT4>
-__device__ __forceinline__ int act_pos(int i) {
-    if (!INT4) return i;
-    const int j = i & 7;
-    return (i & ~7) + ((j & 1) ? 4 : 0) + (j >> 1);
+// INT4 activation layout in LDS: each run of 8 codes c_0..c_7 (INT8 codes,
+// |c| <= 127) as two dwords, H with nibble i = c_i >> 4 and L with nibble i
+// = (c_i & 15) - 8, both signed 4-bit, so that c_i = 16 h_i + l_i + 8 and a
+// weight dword w of 8 signed nibbles dots as
+//   sum c_i w_i = 16 dot8(H, w) + dot8(L, w) + 8 dot8(1..1, w)
+// with v_dot8_i32_i4 (exact int32, no nibble expansion).  `lo` holds codes
+// 0-3 as bytes, `hi` codes 4-7.
+__device__ __forceinline__ uint2 nib_pack8(uint32_t lo, uint32_t hi) {
+    // nibbles at bits 8j..8j+3 (j = 0..3) -> bits 4j..4j+3
+    auto squeeze = [](uint32_t a) {
+        a = (a | (a >> 4)) & 0x00FF00FFu;
+        return (a | (a >> 8)) & 0x0000FFFFu;
+    };
+    const uint32_t h = squeeze((lo >> 4) & 0x0F0F0F0Fu) | (squeeze((hi >> 4) & 0x0F0F0F0Fu) << 16);
+    const uint32_t l = squeeze((lo & 0x0F0F0F0Fu) ^ 0x08080808u) | (squeeze((hi & 0x0F0F0F0Fu) ^ 0x08080808u) << 16);
+    return make_uint2(h, l);
 }
 
 // dot product of one 16-byte weight chunk with the matching activation codes
+// (INT8: 16 codes as bytes; INT4: 32 codes in the nib_pack8 layout, two
+// dwords per 8 codes)
 template <bool INT4>
 __device__ __forceinline__ int chunk_dot(const int8_t* act, int col, i32x4 w) {
-    int s = 0;
     if (!INT4) {
         const i32x4 av = *reinterpret_cast<const i32x4*>(act + col * 16);
+        int s = 0;
         s = __builtin_amdgcn_sdot4(av.x, w.x, s, false);
         s = __builtin_amdgcn_sdot4(av.y, w.y, s, false);
         s = __builtin_amdgcn_sdot4(av.z, w.z, s, false);
         s = __builtin_amdgcn_sdot4(av.w, w.w, s, false);
+        return s;
     } else {
         const i32x4* ap = reinterpret_cast<const i32x4*>(act + col * 32);
-        const i32x4 a0 = ap[0], a1 = ap[1];
-        const uint32_t wv[4] = {(uint32_t)w.x, (uint32_t)w.y, (uint32_t)w.z, (uint32_t)w.w};
-        const int ae[4] = {a0.x, a0.z, a1.x, a1.z};
-        const int ao[4] = {a0.y, a0.w, a1.y, a1.w};
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            // nibbles moved to the top of each byte: 16 * code
-            const int lo = (int)((wv[j] << 4) & 0xF0F0F0F0u);
-            const int hi = (int)(wv[j] & 0xF0F0F0F0u);
-            s = __builtin_amdgcn_sdot4(ae[j], lo, s, false);
-            s = __builtin_amdgcn_sdot4(ao[j], hi, s, false);
-        }
-        s >>= 4;  // exact: every product carried a factor 16
+        const i32x4 a0 = ap[0], a1 = ap[1];   // {H0, L0, H1, L1}, {H2, L2, H3, L3}
+        constexpr int ONES = 0x11111111;
+        int sh = 0, sl = 0, sw = 0;
+        sh = __builtin_amdgcn_sdot8(a0.x, w.x, sh, false);
+        sl = __builtin_amdgcn_sdot8(a0.y, w.x, sl, false);
+        sw = __builtin_amdgcn_sdot8(ONES, w.x, sw, false);
+        sh = __builtin_amdgcn_sdot8(a0.z, w.y, sh, false);
+        sl = __builtin_amdgcn_sdot8(a0.w, w.y, sl, false);
+        sw = __builtin_amdgcn_sdot8(ONES, w.y, sw, false);
+        sh = __builtin_amdgcn_sdot8(a1.x, w.z, sh, false);
+        sl = __builtin_amdgcn_sdot8(a1.y, w.z, sl, false);
+        sw = __builtin_amdgcn_sdot8(ONES, w.z, sw, false);
+        sh = __builtin_amdgcn_sdot8(a1.z, w.w, sh, false);
+        sl = __builtin_amdgcn_sdot8(a1.w, w.w, sl, false);
+        sw = __builtin_amdgcn_sdot8(ONES, w.w, sw, false);
+        return sh * 16 + sl + sw * 8;
     }
-    return s;
 }
 
 // exact int32 sum over aligned groups of P consecutive lanes (P = 1..64)
