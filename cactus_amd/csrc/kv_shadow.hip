@@ -111,8 +111,10 @@ __global__ void kv_shift_in_kernel(const KvLayer* __restrict__ layers, const uns
 
 // ---------------------------------------------------------------- append
 // New K/V rows of every layer into the cache in one launch: grid (tokens,
-// layers), 256 threads.  Wave w of a workgroup takes the (K or V, head,
-// 128-group) units w, w + 4, ...; each unit is quantized as
+// layers, unit slices), 256 threads.  Wave w of slice z takes the (K or V,
+// head, 128-group) units 4 z + w, 4 z + w + 4 Z, ... (one each when Z
+// covers them: their load -> max -> store chains run side by side in
+// separate workgroups); each unit is quantized as
 // quantize_kv_kernel does it (group max, scale, codes: body rne-saturating,
 // tail roundf), and a value unit also writes its products (float)code *
 // scale into the tile layout of kv_shadow_kernel.
@@ -132,7 +134,7 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restric
     const int units = Hkv * ng;
     const size_t tt = key / KS_T;
     const int jj = (int)(key % KS_T);
-    for (int w = wave; w < 2 * units; w += 4) {
+    for (int w = wave + 4 * (int)blockIdx.z; w < 2 * units; w += 4 * (int)gridDim.z) {
         const bool isv = w >= units;
         const int hg = isv ? w - units : w, h = hg / ng, g = hg % ng;
         const int g0 = g * 128, cnt = min(128, d - g0);
@@ -158,7 +160,7 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restric
     }
     // product rows of the padding dimensions [d, 64 nsl) hold zeros
     const int pad = nsl * 64 - d;
-    if (L.sh && pad > 0)
+    if (L.sh && pad > 0 && blockIdx.z == 0)
         for (int x = threadIdx.x; x < Hkv * pad; x += blockDim.x) {
             const int h = x / pad, dim = d + x % pad, sl = dim / 64, dl = dim % 64;
             L.sh[(((size_t)h * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = 0.0f;
@@ -206,7 +208,7 @@ int cactus_hip_kv_append_layers(const cactus_hip_kv_layer* layers, const uint16_
     CH_REQUIRE(layers && k_rows && v_rows, "kv_append_layers: null pointer");
     CH_REQUIRE(head_dim % 8 == 0 && head_dim > 0 && head_dim <= 256 && group_size == 128,
                "kv_append_layers: head_dim must be a multiple of 8 (<= 256), group size 128");
-    CH_REQUIRE(kv_heads > 0 && kv_heads < 65536 && count < (1u << 31) && nlayers < 65536,
+    CH_REQUIRE(kv_heads > 0 && kv_heads <= 4096 && count < (1u << 31) && nlayers < 65536,
                "kv_append_layers: bad sizes");
     CH_REQUIRE(at + count <= max_seq, "kv_append_layers: keys beyond the cache capacity");
     const size_t ntile = (max_seq + KS_T - 1) / KS_T;
@@ -219,8 +221,10 @@ int cactus_hip_kv_append_layers(const cactus_hip_kv_layer* layers, const uint16_
             src.k[l] = k_rows[l0 + l];
             src.v[l] = v_rows[l0 + l];
         }
-        hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)count, (unsigned)nl), dim3(256), 0, as_stream(stream),
-                           L + l0, src, at, (int)kv_heads, (int)head_dim, ntile);
+        // one unit per wave: 2 * kv_heads * groups units over slices of 4
+        const unsigned slices = (unsigned)((2 * kv_heads * ((head_dim + 127) / 128) + 3) / 4);
+        hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)count, (unsigned)nl, slices), dim3(256), 0,
+                           as_stream(stream), L + l0, src, at, (int)kv_heads, (int)head_dim, ntile);
         const int rc = check_launch("kv_append_layers");
         if (rc) return rc;
     }
