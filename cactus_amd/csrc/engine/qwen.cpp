@@ -237,7 +237,7 @@ QwenModel::QwenModel(const cactus_qwen_config& cfg, const cactus_qwen_layer_weig
 
 // QwenModel::load_weights_to_graph (model_qwen.cpp:17-49): the weights as
 // external INPUT nodes.  A fresh graph gets the same node ids in the same
-// order, so the layers' ids hold for graph_ and graph2_ alike.
+// order, so the layers' ids hold for graph_ and the prefill graphs alike.
 void QwenModel::add_weight_nodes(CactusGraph& g) {
     const cactus_qwen_config& cfg = cfg_;
     const size_t H = cfg.hidden, F = cfg.ffn, hd = cfg.head_dim, gs = cfg.group_size;
@@ -277,15 +277,15 @@ void QwenModel::add_weight_nodes(CactusGraph& g) {
 
 QwenModel::~QwenModel() {
     cactus_hip_stream_sync(stream_);
-    if (stream2_) cactus_hip_stream_sync(stream2_);
+    for (void* st : pf_streams_) cactus_hip_stream_sync(st);
     fused_.reset();
     graph_.reset();
-    graph2_.reset();
+    pf_graphs_.clear();
     layers_.clear();
     for (auto& evs : kv_ev_)
         for (void* e : evs) cactus_hip_event_destroy(e);
-    if (join_ev_) cactus_hip_event_destroy(join_ev_);
-    if (stream2_) cactus_hip_stream_destroy(stream2_);
+    for (void* e : join_ev_) cactus_hip_event_destroy(e);
+    for (void* st : pf_streams_) cactus_hip_stream_destroy(st);
     cactus_hip_stream_destroy(stream_);
 }
 
@@ -462,7 +462,7 @@ void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
 
 // The chunks of engine_model.cpp:170-219 (the same boundaries and the
 // same nodes as prefill's serial loop) with consecutive chunks overlapping
-// on two streams.  Chunk c + 1 reads chunk c's KV rows only in its
+// on several streams.  Chunk c + 1 reads chunk c's KV rows only in its
 // attention nodes, so chunk c appends each layer's rows right after that
 // layer's k/v nodes (one launch per layer instead of one per chunk, the same
 // bytes) and records an event that chunk c + 1's attention of the layer
@@ -470,21 +470,30 @@ void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
 // are bit-identical to it.
 void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t chunk) {
     const size_t L = cfg_.num_layers;
-    if (!graph2_) {
-        check_hip(cactus_hip_stream_create(&stream2_), "stream_create");
-        graph2_ = std::make_unique<CactusGraph>(stream2_);
-        add_weight_nodes(*graph2_);
-        for (auto& evs : kv_ev_) {
-            evs.assign(L, nullptr);
-            for (void*& e : evs) check_hip(cactus_hip_event_create(&e), "event_create");
+    constexpr int NS = kPrefillStreams;
+    if (pf_graphs_.empty()) {
+        for (int p = 1; p < NS; p++) {
+            void* st = nullptr;
+            check_hip(cactus_hip_stream_create(&st), "stream_create");
+            pf_streams_.push_back(st);
+            pf_graphs_.push_back(std::make_unique<CactusGraph>(st));
+            add_weight_nodes(*pf_graphs_.back());
         }
-        check_hip(cactus_hip_event_create(&join_ev_), "event_create");
+        kv_ev_.assign(NS, std::vector<void*>(L, nullptr));
+        for (auto& evs : kv_ev_)
+            for (void*& e : evs) check_hip(cactus_hip_event_create(&e), "event_create");
+        join_ev_.assign(NS, nullptr);
+        for (void*& e : join_ev_) check_hip(cactus_hip_event_create(&e), "event_create");
     }
-    graph2_->set_attention_tolerance(attention_mode_ == 1);
-    // stream2_ starts after everything already queued on stream_ (the cache
-    // contents the first chunk attends to)
-    check_hip(cactus_hip_event_record(join_ev_, stream_), "event_record");
-    check_hip(cactus_hip_stream_wait_event(stream2_, join_ev_), "stream_wait_event");
+    auto graph_of = [&](int p) -> CactusGraph& { return p == 0 ? *graph_ : *pf_graphs_[p - 1]; };
+    auto stream_of = [&](int p) { return p == 0 ? stream_ : pf_streams_[p - 1]; };
+    // the other streams start after everything already queued on stream_
+    // (the cache contents the first chunk attends to)
+    check_hip(cactus_hip_event_record(join_ev_[0], stream_), "event_record");
+    for (int p = 1; p < NS; p++) {
+        graph_of(p).set_attention_tolerance(attention_mode_ == 1);
+        check_hip(cactus_hip_stream_wait_event(stream_of(p), join_ev_[0]), "stream_wait_event");
+    }
     last_logits_ = SIZE_MAX;
     fused_logits_ = false;
     std::vector<std::pair<size_t, size_t>> bounds;
@@ -494,9 +503,9 @@ void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t c
     const size_t n = bounds.size();
     try {
         for (size_t i = 0; i < n; i++) {
-            const int par = (int)((n - 1 - i) % 2);
-            CactusGraph& g = par == 0 ? *graph_ : *graph2_;
-            void* st = par == 0 ? stream_ : stream2_;
+            const int par = (int)((n - 1 - i) % NS), prev = (par + 1) % NS;
+            CactusGraph& g = graph_of(par);
+            void* st = stream_of(par);
             cur_ = &g;
             const std::vector<uint32_t> c(tokens.begin() + bounds[i].first, tokens.begin() + bounds[i].second);
             last_hidden_ = forward(c);
@@ -509,9 +518,9 @@ void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t c
                     check_hip(cactus_hip_event_record(ev, st), "event_record");
                 });
                 if (i > 0) {
-                    void* prev = kv_ev_[1 - par][l];
-                    g.before_node(att_nodes_[l], [st, prev] {
-                        check_hip(cactus_hip_stream_wait_event(st, prev), "stream_wait_event");
+                    void* pe = kv_ev_[prev][l];
+                    g.before_node(att_nodes_[l], [st, pe] {
+                        check_hip(cactus_hip_stream_wait_event(st, pe), "stream_wait_event");
                     });
                 }
             }
@@ -523,9 +532,11 @@ void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t c
         throw;
     }
     cur_ = graph_.get();
-    // later work on stream_ (decode, reset) follows all of stream2_'s
-    check_hip(cactus_hip_event_record(join_ev_, stream2_), "event_record");
-    check_hip(cactus_hip_stream_wait_event(stream_, join_ev_), "stream_wait_event");
+    // later work on stream_ (decode, reset) follows all of the other streams'
+    for (int p = 1; p < NS; p++) {
+        check_hip(cactus_hip_event_record(join_ev_[p], stream_of(p)), "event_record");
+        check_hip(cactus_hip_stream_wait_event(stream_, join_ev_[p]), "stream_wait_event");
+    }
 }
 
 // engine_model.cpp:221-297, greedy

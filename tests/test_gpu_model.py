@@ -128,9 +128,9 @@ def test_qwen_prefill_rejects_out_of_range_token():
 
 @pytest.mark.parametrize("chunk,lens", [(64, (150,)), (64, (200,)), (32, (70, 130))])
 def test_qwen_overlapped_prefill_matches_oracle(chunk, lens):
-    """Multi-chunk prompts run their chunks overlapped on two streams (chunk
+    """Multi-chunk prompts run their chunks overlapped on three streams (chunk
     c + 1's layer-l attention ordered after chunk c's layer-l KV append):
-    an odd chunk count (the first chunk on the second stream), an even one,
+    three and four chunks (the first on the third and on the second stream),
     and a second prompt prefilled onto a cache that already holds the first
     -- final hidden states, KV caches and the following greedy tokens
     bit-identical to the oracle's serial chunked prefill."""
