@@ -277,7 +277,9 @@ __global__ void __launch_bounds__(C::NT) gemm_lds_kernel(GemmArgs a0) {
 #pragma unroll
     for (int i = 0; i < C::NI; i++) {
         const int u = (wv + C::NW * i) * 64 + lane;
-        src[i] = reinterpret_cast<const uint8_t*>(a.A);
+        // units past U pad the last instruction: a fixed 16-byte read of the
+        // weights, never used
+        src[i] = a.B;
         inc[i] = 0;
         if (u < C::A_U) {
             const int row = u / C::PA, p = (u % C::PA) ^ (row & 7);
