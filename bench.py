@@ -25,6 +25,10 @@ CPU model; and the other workloads the kernel layer is quoted on:
                       exact attention (tokens compared with the oracle's
                       frozen run) and tolerance attention
   qwen3_0p6b_decode_cpu_baseline   the oracle model's decode on the host
+  qwen3_0p6b_prefill_cpu_baseline  the oracle model's prefill of 128 prompt
+                                   tokens on the host
+  prefill_gemm_cpu_baseline        config 2 (INT8 M=512 matmul with row
+                                   quantization) by the oracle on the host
 """
 from __future__ import annotations
 
@@ -378,6 +382,59 @@ def cpu_baseline(seconds: float = 10.0, nsets: int = 768):
                       f"x86 build of the CPU restatement, {threads} threads (the reference's M=1 pool)"}
 
 
+def cpu_gemm_baseline(seconds: float = 10.0, M: int = 512, K: int = 1024, N: int = 3072, gs: int = 32):
+    """The prefill matmul of config 2 on this host's cores: per-row
+    activation quantization, then the grouped INT8 matmul of the CPU
+    restatement with the reference's M > 1 thread policy (the whole pool,
+    kernel_utils.h:439-456), timed until `seconds` pass (at least once)."""
+    import oracle
+    from _data import f16
+    L = oracle.lib()
+    threads = min(16, os.cpu_count() or 1)
+    rng = np.random.default_rng(M + K + N)
+    x = f16(rng.normal(0, 1, (M, K)))
+    B = rng.integers(-127, 128, (N, K), dtype=np.int8)
+    Bs = f16(np.abs(rng.normal(0, 0.02, (N, K // gs))) / 127.0)
+    q = np.empty((M, K), np.int8)
+    s = np.empty(M, np.float32)
+    C = np.empty((M, N), np.uint16)
+    P = oracle.ptr
+    n = 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        L.orc_quantize_activations(P(x), P(q), P(s), M, K)
+        L.orc_matmul_int8_mt(P(q), P(s), P(B), P(Bs), P(C), M, K, N, gs, threads)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(2.0 * M * K * N * n / dt / 1e12, 4), "unit": "TOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} calls of the INT8 M={M} K={K} N={N} g{gs} matmul with FP16 activations "
+                      f"quantized per row, {dt:.1f} s, x86 build of the CPU restatement, {threads} threads"}
+
+
+def cpu_prefill_baseline(tokens: int = 128):
+    """The oracle's Qwen3-0.6B-shape model prefilling the first `tokens`
+    tokens of the bench prompt on this host's cores (one chunk, 16 threads
+    at most): a bounded sample of the GPU line's 4096-token prefill, whose
+    per-token cost only grows with the context."""
+    import oracle
+    from cactus_amd.engine import qwen3_0p6b, random_weights
+    threads = min(16, os.cpu_count() or 1)
+    oracle.lib().orc_set_threads(threads)
+    cfg = qwen3_0p6b(max_seq=tokens + 64)
+    layers, emb, on = random_weights(cfg, 6)
+    orc = oracle.OracleQwen(cfg, layers, emb, on)
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], 4096).astype(np.uint32)
+    t0 = time.perf_counter()
+    orc.prefill(prompt[:tokens], cfg["prefill_chunk"])
+    dt = time.perf_counter() - t0
+    orc.close()
+    oracle.lib().orc_set_threads(1)
+    return {"value": round(tokens / dt, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"prefill of the first {tokens} prompt tokens by the 28-layer Qwen3-0.6B-shape "
+                      f"oracle model, {dt:.1f} s, {threads} threads"}
+
+
 def host_info():
     cpu = "unknown"
     try:
@@ -537,6 +594,8 @@ def main():
     dec = None if args.skip_decode else bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)
     cpu = cpu_baseline(args.cpu_seconds)
     cpu_dec = None if args.skip_decode else cpu_decode_baseline(args.cpu_seconds)
+    cpu_gemm = cpu_gemm_baseline(args.cpu_seconds)
+    cpu_pf = None if args.skip_decode else cpu_prefill_baseline()
     out = {
         "metric": "INT8 GEMV GB/s (% HBM peak) + Qwen3-0.6B-shape decode tok/s, 1 MI355X",
         "value": round(g["gbs"], 2),
@@ -572,6 +631,8 @@ def main():
         "decode_attention": att,
         "qwen3_0p6b_decode": dec,
         "qwen3_0p6b_decode_cpu_baseline": cpu_dec,
+        "qwen3_0p6b_prefill_cpu_baseline": cpu_pf,
+        "prefill_gemm_cpu_baseline": cpu_gemm,
     }
     print(json.dumps(out), flush=True)
 
