@@ -462,12 +462,13 @@ void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
 
 // The chunks of engine_model.cpp:170-219 (the same boundaries and the
 // same nodes as prefill's serial loop) with consecutive chunks overlapping
-// on several streams.  Chunk c + 1 reads chunk c's KV rows only in its
+// on several streams.  A chunk reads the earlier chunks' KV rows only in its
 // attention nodes, so chunk c appends each layer's rows right after that
 // layer's k/v nodes (one launch per layer instead of one per chunk, the same
-// bytes) and records an event that chunk c + 1's attention of the layer
-// waits for.  Every kernel sees the inputs of the serial order: the results
-// are bit-identical to it.
+// bytes); before its attention node of the layer it waits for chunk c - 1's
+// event of the layer and then records its own, which therefore follows the
+// appends of chunks 0..c of that layer.  Every kernel sees the inputs of the
+// serial order: the results are bit-identical to it.
 void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t chunk) {
     const size_t L = cfg_.num_layers;
     constexpr int NS = kPrefillStreams;
@@ -513,16 +514,18 @@ void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t c
             for (size_t l = 0; l < L; l++) {
                 const size_t kn = k_nodes_[l], vn = v_nodes_[l];
                 void* ev = kv_ev_[par][l];
-                g.after_node(kn, [this, &g, l, kn, vn, seq, at, st, ev] {
+                void* pe = i > 0 ? kv_ev_[prev][l] : nullptr;
+                g.after_node(kn, [this, &g, l, kn, vn, seq, at, st] {
                     cache_.put_layer(l, g.get_output_buffer(kn).data, g.get_output_buffer(vn).data, seq, at, st);
+                });
+                // the layer's event is recorded after this chunk's own wait
+                // for the previous chunk's event, so it covers the appends of
+                // every earlier chunk, not only this one's: a later chunk's
+                // attention reads all of them
+                g.before_node(att_nodes_[l], [st, pe, ev] {
+                    if (pe) check_hip(cactus_hip_stream_wait_event(st, pe), "stream_wait_event");
                     check_hip(cactus_hip_event_record(ev, st), "event_record");
                 });
-                if (i > 0) {
-                    void* pe = kv_ev_[prev][l];
-                    g.before_node(att_nodes_[l], [st, pe] {
-                        check_hip(cactus_hip_stream_wait_event(st, pe), "stream_wait_event");
-                    });
-                }
             }
             g.execute();
             cache_.appended(seq);
