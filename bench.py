@@ -25,7 +25,7 @@ CPU model; and the other workloads the kernel layer is quoted on:
                       exact attention (tokens compared with the oracle's
                       frozen run) and tolerance attention
   qwen3_0p6b_decode_cpu_baseline   the oracle model's decode on the host
-  qwen3_0p6b_prefill_cpu_baseline  the oracle model's prefill of 128 prompt
+  qwen3_0p6b_prefill_cpu_baseline  the oracle model's prefill of 512 prompt
                                    tokens on the host
   prefill_gemm_cpu_baseline        config 2 (INT8 M=512 matmul with row
                                    quantization) by the oracle on the host
@@ -412,9 +412,9 @@ def cpu_gemm_baseline(seconds: float = 10.0, M: int = 512, K: int = 1024, N: int
                       f"quantized per row, {dt:.1f} s, x86 build of the CPU restatement, {threads} threads"}
 
 
-def cpu_prefill_baseline(tokens: int = 128):
+def cpu_prefill_baseline(tokens: int = 512):
     """The oracle's Qwen3-0.6B-shape model prefilling the first `tokens`
-    tokens of the bench prompt on this host's cores (one chunk, 16 threads
+    tokens of the bench prompt on this host's cores (256-token chunks, 16 threads
     at most): a bounded sample of the GPU line's 4096-token prefill, whose
     per-token cost only grows with the context."""
     import oracle
