@@ -1300,7 +1300,7 @@ int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t*
     CH_REQUIRE(workspace_bytes >= cactus_hip_decode_attention_fast_workspace(num_q_heads, num_kv_heads, head_dim,
                                                                              max_cache),
                "decode_prep_attention_fast: workspace too small");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     int rc = rope_table(max_cache + 1, head_dim, theta, &t);
     if (rc) return rc;
     FastArgs a{};
@@ -1310,7 +1310,7 @@ int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t*
     a.cache_len = max_cache; a.new_len = 1; a.Skv = max_cache + 1; a.pos_off = max_cache;
     a.scale = scale; a.dyn = state;
     a.q_raw = q_raw; a.k_raw = k_raw; a.v_raw = v_raw; a.q_norm = q_norm; a.k_norm = k_norm;
-    a.cos_t = t->cos_d; a.sin_t = t->sin_d; a.eps = eps; a.table_pos = (uint32_t)t->npos;
+    a.cos_t = t.cos_d; a.sin_t = t.sin_d; a.eps = eps; a.table_pos = (uint32_t)t.npos;
     a.kc_w = k_cache; a.vc_w = v_cache; a.ks_w = k_scales; a.vs_w = v_scales; a.vsh = v_shadow;
     a.sh_ntile = (max_cache + 63) / 64; a.max_cache = max_cache;
     a.nsplit = (int)fast_attention_splits(max_cache + 1, true);

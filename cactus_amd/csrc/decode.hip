@@ -724,16 +724,16 @@ int cactus_hip_decode_attn_prep(const uint16_t* q_raw, const uint16_t* k_raw, co
     CH_REQUIRE(q_raw && k_raw && v_raw && q_norm && k_norm && state && q_out && k_out && k_cache &&
                v_cache && k_scales && v_scales, "decode_attn_prep: null pointer");
     CH_REQUIRE(head_dim >= 8 && head_dim <= 256 && head_dim % 2 == 0, "decode_attn_prep: head_dim");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     int rc = rope_table(max_cache + 1, head_dim, theta, &t);
     if (rc) return rc;
     PrepArgs a{};
     a.q_raw = q_raw; a.k_raw = k_raw; a.v_raw = v_raw; a.q_norm = q_norm; a.k_norm = k_norm;
     a.q_out = q_out; a.k_out = k_out; a.kc = k_cache; a.vc = v_cache; a.ks = k_scales; a.vs = v_scales;
-    a.cos_t = t->cos_d; a.sin_t = t->sin_d; a.st = state; a.eps = eps;
+    a.cos_t = t.cos_d; a.sin_t = t.sin_d; a.st = state; a.eps = eps;
     a.Hq = (int)num_q_heads; a.Hkv = (int)num_kv_heads; a.d = (int)head_dim;
     a.max_cache = (uint32_t)max_cache;
-    a.table_pos = (uint32_t)t->npos;
+    a.table_pos = (uint32_t)t.npos;
     a.vsh = v_shadow;
     a.sh_ntile = (max_cache + 63) / 64;
     hipLaunchKernelGGL(dec_attn_prep_kernel, dim3((unsigned)(num_q_heads + num_kv_heads)), dim3(64), 0,
@@ -767,11 +767,11 @@ int cactus_hip_decode_prep_attention(const uint16_t* q_raw, const uint16_t* k_ra
                v_scales && o, "decode_prep_attention: null pointer");
     CH_REQUIRE(num_kv_heads > 0 && num_q_heads % num_kv_heads == 0, "decode_prep_attention: bad head counts");
     CH_REQUIRE(head_dim == 64 || head_dim == 128, "decode_prep_attention: head_dim must be 64 or 128");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     int rc = rope_table(max_cache + 1, head_dim, theta, &t);
     if (rc) return rc;
-    return attention_hybrid_decode_prep(q_raw, k_raw, v_raw, q_norm, k_norm, eps, t->cos_d, t->sin_d,
-                                        (uint32_t)t->npos, k_cache, v_cache, k_scales, v_scales, v_shadow, o,
+    return attention_hybrid_decode_prep(q_raw, k_raw, v_raw, q_norm, k_norm, eps, t.cos_d, t.sin_d,
+                                        (uint32_t)t.npos, k_cache, v_cache, k_scales, v_scales, v_shadow, o,
                                         (int)num_q_heads, (int)num_kv_heads, (int)head_dim, scale, state,
                                         max_cache, (max_cache + 63) / 64, stream);
 }

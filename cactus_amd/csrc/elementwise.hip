@@ -77,7 +77,7 @@ static std::map<std::tuple<int, size_t, uint32_t>, RopeTable> g_rope;
 // Table of precompute_rope_tables_f16 (kernel_attention.cpp:588-612), built
 // on the host with the host libm and uploaded.  Tables only grow; a replaced
 // table stays allocated because queued kernels may still read it.
-int rope_table(size_t npos, size_t d, float theta, const RopeTable** out) {
+int rope_table(size_t npos, size_t d, float theta, RopeTable* out) {
     int dev = 0;
     CH_HIP(hipGetDevice(&dev));
     uint32_t tb;
@@ -107,7 +107,7 @@ int rope_table(size_t npos, size_t d, float theta, const RopeTable** out) {
         nt.npos = want;
         t = nt;  // previous buffers intentionally kept (see above)
     }
-    *out = &t;
+    *out = t;
     return CACTUS_HIP_OK;
 }
 
@@ -347,7 +347,7 @@ int cactus_hip_rms_norm_f16(const uint16_t* x, const uint16_t* w, uint16_t* y, s
 
 int cactus_hip_rope_reserve(size_t max_pos, size_t head_dim, float theta) {
     CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0, "rope: head_dim must be even");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     return rope_table(max_pos, head_dim, theta, &t);
 }
 
@@ -358,12 +358,12 @@ int cactus_hip_rope_f16(const uint16_t* x, uint16_t* y, size_t batch, size_t seq
     CH_REQUIRE(x && y, "rope: null pointer");
     CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim < (1u << 16),
                "rope: head_dim must be even");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     int rc = rope_table(seq_len + start_pos, head_dim, theta, &t);
     if (rc) return rc;
     const size_t pairs = batch * seq_len * num_heads * (head_dim / 2);
     hipLaunchKernelGGL(rope_kernel, dim3(grid_for(pairs, 256)), dim3(256), 0, as_stream(stream), x,
-                       y, t->cos_d, t->sin_d, pairs, (int)seq_len, (int)num_heads, (int)head_dim,
+                       y, t.cos_d, t.sin_d, pairs, (int)seq_len, (int)num_heads, (int)head_dim,
                        start_pos);
     return check_launch("rope");
 }
@@ -385,7 +385,7 @@ int cactus_hip_rms_norm_rope_qk_f16(const uint16_t* q, const uint16_t* q_weight,
                "rms_norm_rope: null pointer");
     CH_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, "rms_norm_rope: head_dim must be even, <= 256");
     CH_REQUIRE((rq + 3) / 4 + (rk + 3) / 4 < (1u << 31), "rms_norm_rope: too many rows");
-    const RopeTable* t = nullptr;
+    RopeTable t;
     int rc = rope_table(seq_len + start_pos, head_dim, theta, &t);
     if (rc) return rc;
     RopeRowsArgs a{};
@@ -396,7 +396,7 @@ int cactus_hip_rms_norm_rope_qk_f16(const uint16_t* q, const uint16_t* q_weight,
     a.X[1] = k;  a.W[1] = k_weight;  a.Y[1] = k_out;
     a.rows[1] = only_k ? 0 : rk;  a.H[1] = (int)(kv_heads ? kv_heads : 1);
     a.nblk0 = (int)((a.rows[0] + 3) / 4);
-    a.ct = t->cos_d;  a.stb = t->sin_d;
+    a.ct = t.cos_d;  a.stb = t.sin_d;
     a.S = (int)seq_len;  a.d = (int)head_dim;  a.start_pos = start_pos;  a.eps = eps;
     const size_t blocks = a.nblk0 + (a.rows[1] + 3) / 4;
     hipLaunchKernelGGL(rms_rope_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream), a);

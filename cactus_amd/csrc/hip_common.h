@@ -42,7 +42,9 @@ struct RopeTable {
     uint16_t* sin_d = nullptr;
     size_t npos = 0;
 };
-int rope_table(size_t npos, size_t head_dim, float theta, const RopeTable** out);
+// copies the table's pointers and length out under the lock (a concurrent grow
+// replaces the map entry)
+int rope_table(size_t npos, size_t head_dim, float theta, RopeTable* out);
 
 // fp32 -> fp16 bit pattern on the host: round to nearest even with one
 // rounding step (subnormals, overflow to inf, quiet NaN).  Used for tables
