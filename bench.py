@@ -301,24 +301,60 @@ def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: 
         tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
         return {"us_per_call": round(us, 2), "tops": round(tops, 1),
                 "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4), "timing": "direct launches"}
-    cm.call("cactus_hip_graph_capture_begin", st.handle)
-    for _ in range(reps):
-        fn()
-    ge = ctypes.c_void_p()
-    cm.call("cactus_hip_graph_capture_end", st.handle, ctypes.byref(ge))
-    cm.call("cactus_hip_graph_launch", ge, st.handle)
-    st.sync()
-    e0, e1 = cm.Event(), cm.Event()
-    e0.record(st)
-    for _ in range(rounds):
+    def graph_us(branches):
+        """us per call of a graph holding len(branches) chains of `reps`
+        calls, chain i on stream branches[i][0] (forked from and joined
+        back to `st`), replayed `rounds` times"""
+        fork, joins = cm.Event(), [cm.Event() for _ in branches]
+        cm.call("cactus_hip_graph_capture_begin", st.handle)
+        fork.record(st)
+        for bs, _ in branches:
+            if bs is not st:
+                cm.call("cactus_hip_stream_wait_event", bs.handle, fork.handle)
+        for _, bfn in branches:
+            for _ in range(reps):
+                bfn()
+        for (bs, _), j in zip(branches, joins):
+            if bs is not st:
+                j.record(bs)
+                cm.call("cactus_hip_stream_wait_event", st.handle, j.handle)
+        ge = ctypes.c_void_p()
+        cm.call("cactus_hip_graph_capture_end", st.handle, ctypes.byref(ge))
         cm.call("cactus_hip_graph_launch", ge, st.handle)
-    e1.record(st)
-    st.sync()
-    cm.call("cactus_hip_graph_destroy", ge)
-    us = e0.elapsed_ms(e1) * 1e3 / (reps * rounds)
-    tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
-    return {"us_per_call": round(us, 2), "tops": round(tops, 1),
-            "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+        st.sync()
+        e0, e1 = cm.Event(), cm.Event()
+        e0.record(st)
+        for _ in range(rounds):
+            cm.call("cactus_hip_graph_launch", ge, st.handle)
+        e1.record(st)
+        st.sync()
+        cm.call("cactus_hip_graph_destroy", ge)
+        return e0.elapsed_ms(e1) * 1e3 / (reps * rounds * len(branches))
+
+    def rate(us):
+        tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
+        return {"us_per_call": round(us, 2), "tops": round(tops, 1),
+                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+
+    out = rate(graph_us([(st, fn)]))
+    # three independent calls in flight, one per stream (each with its own
+    # output and activation scratch), the way the overlapped prefill runs its
+    # chunks' matmuls: aggregate rate with the launch latency overlapped
+    extra = []
+    for _ in range(2):
+        s2, C2 = cm.Stream(), cm.DeviceBuffer(M * N * 2)
+        if f16act:
+            def f2(s2=s2, C2=C2):
+                cm.call(name + "_f16act", A16.ptr, B.ptr, Bs.ptr, C2.ptr, M, K, N, gs, s2.handle)
+        else:
+            def f2(s2=s2, C2=C2):
+                cm.call(name, A8.ptr, As.ptr, B.ptr, Bs.ptr, C2.ptr, M, K, N, gs, s2.handle)
+        for _ in range(3):
+            f2()   # sizes this stream's activation scratch outside the capture
+        s2.sync()
+        extra.append((s2, f2, C2))
+    out["three_streams"] = rate(graph_us([(st, fn)] + [(e[0], e[1]) for e in extra]))
+    return out
 
 
 def bench_prefill_gemms(eager: bool = False):
