@@ -544,6 +544,63 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
     const float* pb = a.part + (size_t)bg * a.nsplit * GQ * PS;
     constexpr int NG = GQ * D / 4;                // float4 output groups
     constexpr int TPG = FA_THREADS / NG;          // threads (split lanes) per group
+    // Up to NR splits per thread (decode at a few thousand keys): the TPG
+    // consecutive lanes of one output group hold splits sj, sj + TPG, ...
+    // with their (M, sum) in registers; M*, the weights' sum and the
+    // weighted partial rows meet by DPP within the lane group, with no LDS
+    // and no barrier.
+    constexpr int NR = 4;
+    if constexpr (TPG >= 4 && TPG <= 16) {
+        if (nact <= TPG * NR) {
+            const int gi = tid / TPG, sj = tid % TPG;
+            const int gh = (gi * 4) / D, gd = (gi * 4) % D;
+            f32x4 cr[NR];
+            float mr[NR], lr[NR];
+#pragma unroll
+            for (int u = 0; u < NR; u++) {
+                const int t = sj + u * TPG;
+                cr[u] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+                mr[u] = -__builtin_inff();
+                lr[u] = 0.0f;
+                if (t < nact) {
+                    const float* pt = pb + ((size_t)t * GQ + gh) * PS;
+                    cr[u] = agent_load4(pt + gd);
+                    mr[u] = agent_load(pt + D);
+                    lr[u] = agent_load(pt + D + 1);
+                }
+            }
+            float mx = mr[0];
+#pragma unroll
+            for (int u = 1; u < NR; u++) mx = __builtin_fmaxf(mx, mr[u]);
+            mx = group_max<TPG>(mx);
+            float L = 0.0f;
+            f32x4 acc = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int u = 0; u < NR; u++) {
+                const float e = mr[u] > -__builtin_inff() ? fast_exp2((mr[u] - mx) * LOG2E) : 0.0f;
+                L = __builtin_fmaf(e, lr[u], L);
+                acc.x = __builtin_fmaf(e, cr[u].x, acc.x);
+                acc.y = __builtin_fmaf(e, cr[u].y, acc.y);
+                acc.z = __builtin_fmaf(e, cr[u].z, acc.z);
+                acc.w = __builtin_fmaf(e, cr[u].w, acc.w);
+            }
+            L = group_sum<TPG>(L);
+            acc.x = group_sum<TPG>(acc.x);
+            acc.y = group_sum<TPG>(acc.y);
+            acc.z = group_sum<TPG>(acc.z);
+            acc.w = group_sum<TPG>(acc.w);
+            if (sj == 0) {
+                uint16_t* out = a.o + ((size_t)b * a.Hq + g * GQ + gh) * D + gd;
+                const uint32_t lo = (uint32_t)f2h(L > 0.0f ? acc.x / L : 0.0f) |
+                                    ((uint32_t)f2h(L > 0.0f ? acc.y / L : 0.0f) << 16);
+                const uint32_t hi = (uint32_t)f2h(L > 0.0f ? acc.z / L : 0.0f) |
+                                    ((uint32_t)f2h(L > 0.0f ? acc.w / L : 0.0f) << 16);
+                *reinterpret_cast<uint2*>(out) = make_uint2(lo, hi);
+            }
+            if (tid == 0) __hip_atomic_store(a.cnt + bg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
     constexpr int NCH = 96 / TPG > 0 ? (96 / TPG < 24 ? 96 / TPG : 24) : 1;   // loads in flight per thread
     static_assert(FA_THREADS % NG == 0, "output groups");
     const int gi = tid % NG, sj = tid / NG;
