@@ -47,6 +47,9 @@ HIP_FILE_FLAGS = {
     "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     # the prefill attention scales its output accumulators every key tile
     "attention_fast.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # the decode value chains: the next block's scalar weight loads must stay
+    # ahead of this block's FMAs (machine sinking moves them behind)
+    "chain_stream.hip": ["-mllvm", "-disable-machine-sink"],
 }
 
 

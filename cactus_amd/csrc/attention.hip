@@ -21,6 +21,7 @@
 //     key, in increasing position, exactly as the reference.  The output is
 //     fp16(acc * (1/sum)) on the 8-aligned prefix of head_dim.
 #include "hip_common.h"
+#include "attention_args.h"
 #include "decode_device.h"
 
 #include <map>
@@ -28,94 +29,6 @@
 #include <mutex>
 
 namespace cactus_hip {
-
-constexpr int ATT_BLOCK = 32;
-constexpr int ATT_MAX_D = 256;
-constexpr int ATT_MAX_GQ = 8;      // query heads per KV head
-
-struct AttnArgs {
-    const uint16_t* q;
-    const uint16_t* k;        // FP16 keys [B][Skv][Hkv][d] or new keys [B][new][Hkv][d]
-    const uint16_t* v;
-    const int8_t* kc;         // INT8 cache [B][cache][Hkv][d]
-    const int8_t* vc;
-    const float* ks;          // [B][cache][Hkv][nqg]
-    const float* vs;
-    const uint16_t* mask;     // [B][S][Skv] or null
-    uint16_t* o;
-    float* w;                 // scratch: weights [B*S*Hq][wstride]
-    float* bmax;              // scratch: block max [B*S*Hq][nbstride]
-    float* bsum;              // scratch: block sums
-    size_t wstride;
-    int nbstride;
-    int B, S, Hq, Hkv, d, gq;
-    size_t Skv;               // FP16: kv_seq_len; hybrid: cache_len + new_len
-    size_t cache_len, new_len;
-    size_t pos_off, window;
-    int causal, qgs, nqg;
-    float scale;
-    // decode-step form: when set, cache_len = dyn[2] and position_offset =
-    // dyn[1] are read from device memory (the step state of the fused
-    // decode path), and the launch is sized for max_cache keys
-    const uint32_t* dyn;
-    size_t max_cache;
-    // fp32 value-product tiles of the INT8 cache (kv_shadow.hip), or null
-    const float* vsh;
-    size_t sh_ntile;
-    // decode step with the head preparation fused into the scores (null
-    // q_raw: q and the new key row come prepared in q and k): raw q / k / v
-    // rows of the step, head RMSNorm weights, RoPE tables, and the cache
-    // rows the new key and value are appended to
-    struct {
-        const uint16_t* q_raw; const uint16_t* k_raw; const uint16_t* v_raw;
-        const uint16_t* q_norm; const uint16_t* k_norm;
-        const uint16_t* cos_t; const uint16_t* sin_t;
-        float eps;
-        uint32_t table_pos;
-        int8_t* kc; int8_t* vc; float* ks; float* vs; float* vsh;
-    } prep;
-};
-
-__device__ __forceinline__ AttnArgs resolve(const AttnArgs& in) {
-    AttnArgs a = in;
-    if (a.dyn) {
-        a.cache_len = a.dyn[2];
-        a.pos_off = a.dyn[1];
-        a.Skv = a.cache_len + a.new_len;
-    }
-    return a;
-}
-
-// sign bit set on a non-negative float: a flag carried by a block sum
-__device__ __forceinline__ float set_sign(float x) {
-    return __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) | 0x80000000u);
-}
-
-__device__ __forceinline__ float lane_f(float v, int j) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), j));
-}
-
-// Key range and block limit of query position qp (kernel_attention.cpp:78-96
-// for FP16, :328-337 for the hybrid).
-template <bool HYBRID>
-__device__ __forceinline__ void kv_range(const AttnArgs& a, size_t qp, size_t& kv_start,
-                                         size_t& kv_end, size_t& blk_limit) {
-    const size_t aq = a.pos_off + qp;
-    kv_start = 0;
-    kv_end = a.Skv;
-    blk_limit = a.Skv;
-    if (!HYBRID) {
-        if (a.window > 0 && a.window < a.Skv) {
-            if (aq > a.window) kv_start = aq - a.window;
-            if (a.causal && aq + 1 < kv_end) kv_end = aq + 1;
-        } else if (a.causal && aq + 1 < kv_end) {
-            kv_end = aq + 1;
-        }
-    } else {
-        if (a.causal && aq + 1 < kv_end) kv_end = aq + 1;
-        blk_limit = kv_end;
-    }
-}
 
 // ----------------------------------------------------------------- kernel A
 // grid.x: 64-key chunks (4 per workgroup), grid.y: (b, qp, kv head).  A lane
@@ -354,6 +267,17 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     const int gq = a.gq, qr = NQ / gq;
     const int ngrp = (a.S + qr - 1) / qr;
     size_t gy = blockIdx.y;                            // (b, row group, kv head)
+    unsigned bx = blockIdx.x, nbx = gridDim.x;         // chunk, chunks (+ appender)
+    if (a.xcd_chunks) {
+        const int L = blockIdx.x;
+        int j = L >> 3;
+        nbx = (unsigned)a.xcd_chunks;
+        bx = (unsigned)(j % a.xcd_chunks);
+        j /= a.xcd_chunks;
+        const int kvx = (L & 7) + 8 * (j / a.xcd_rest);
+        if (kvx >= a.Hkv) return;                      // whole workgroup, before any barrier
+        gy = (size_t)(j % a.xcd_rest) * a.Hkv + kvx;
+    }
     const int kvh = (int)(gy % a.Hkv);
     gy /= a.Hkv;
     const int qp0 = (int)(gy % ngrp) * qr;
@@ -369,7 +293,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         kv_range<HYBRID>(a, (size_t)(qp0 + r), s0, e, bl);
         if (e > kv_end_max) kv_end_max = e;
     }
-    const size_t chunk = (size_t)blockIdx.x * NW + wid;
+    const size_t chunk = (size_t)bx * NW + wid;
     const size_t wbase = chunk * 64;                   // first key of the wave
     const int jl = lane & 31;
     const size_t bs0 = wbase + (lane & 32);
@@ -404,6 +328,31 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             pres = ssrc[0];
         }
     };
+    // decode form with value product tiles: the chain kernel that follows
+    // reads this chunk's tiles from the L2 of this XCD (its workgroups of kv
+    // head h run on XCD h % 8, as these do), so the chunk's 64 keys x D
+    // dims of products are read here, one dword per 128-byte line, and held
+    // until the end (the registers stay live until their wait)
+    uint32_t pfr[4] = {0u, 0u, 0u, 0u};
+    bool pf_on = false;
+    auto prefetch_tiles = [&]() {
+        if constexpr (HYBRID && PRE && NW == 1) {
+            if (a.vsh && wbase < a.cache_len) {
+                pf_on = true;
+                constexpr int NSL = D / 64;
+#pragma unroll
+                for (int sl = 0; sl < NSL && sl < 2; sl++) {
+                    const float* t = a.vsh + sh_index(kvh, NSL, sl, a.sh_ntile, wbase, 0);
+                    asm volatile("global_load_dword %0, %1, off" : "=&v"(pfr[2 * sl]) : "v"(t + lane * 32));
+                    asm volatile("global_load_dword %0, %1, off" : "=&v"(pfr[2 * sl + 1]) : "v"(t + (lane + 64) * 32));
+                }
+            }
+        }
+    };
+    auto prefetch_drain = [&]() {
+        if (pf_on)
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(pfr[0]), "+v"(pfr[1]), "+v"(pfr[2]), "+v"(pfr[3]));
+    };
     // decode form with the head preparation fused in (one wave, one row):
     // q of the group's heads and, in the chunk holding it, the new key row
     // get the reference's head RMSNorm and RoPE here (the step's attn_prep
@@ -414,7 +363,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     __shared__ uint16_t krot[PRE ? D : 1];
     if constexpr (PRE && NW == 1) {
         if (a.prep.q_raw) {
-            const bool appender = blockIdx.x == gridDim.x - 1;
+            const bool appender = bx == nbx - 1;
             if (!appender && wbase >= kv_end_max) return;   // one wave: no barrier waits for it
             const int end8 = (d / 8) * 8, half = d / 2, vh = (half / 8) * 8;
             const uint32_t pos = (uint32_t)a.pos_off;
@@ -437,6 +386,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             const uint16_t cv = lane < half ? a.prep.cos_t[trow + lane] : (uint16_t)0;
             const uint16_t sv = lane < half ? a.prep.sin_t[trow + lane] : (uint16_t)0;
             preload();   // (the appender too: no branch around loads)
+            if (!appender) prefetch_tiles();
             // rows r < nq: q heads h0 + r; row NQ: the new key
 #pragma unroll
             for (int r = 0; r <= NQ; r++)
@@ -500,6 +450,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     }
     if (!(PRE && NW == 1) || !a.prep.q_raw) {
         preload();
+        prefetch_tiles();
         for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
             const int v = i / D, dim = i % D;
             const int qp = qp0 + v / gq;
@@ -507,7 +458,10 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         }
     }
     __syncthreads();
-    if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
+    if (wbase >= kv_end_max) {                         // wave-uniform; no barrier follows
+        prefetch_drain();
+        return;
+    }
 
     // ---- dot products of this lane's key with every query vector
     float acc[NQ][8];
@@ -672,6 +626,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             }
         }
     }
+    prefetch_drain();
 }
 
 // ----------------------------------------------------------------- kernel B
@@ -1346,447 +1301,6 @@ __global__ void __launch_bounds__(64 * (ATT_MAX_GQ + CD_NP)) attn_chain_dma_kern
     }
 }
 
-// ------------------------------------------------ kernel B, product tiles
-// With the INT8 value cache mirrored as fp32 product tiles (every cached
-// (float)code * scale already rounded, kv_shadow.hip), the stage waves only
-// move memory: each step stages the 32-dim half of a product tile the
-// workgroup owns (8.5 KB) plus the weights, by LDS DMA D - 1 tiles ahead.
-// A chain wave runs its 32 dimensions on lanes 0-31, which halves the LDS
-// bytes it pulls per key: a chain step is then bound by the FMA latency, not
-// by the wave's LDS delivery.
-// Tile layout, per (batch, kv head, 64-dim slice, 64-key tile):
-// [64 dims][SH_PS keys].
-constexpr int SH_PS = CD_T + 4;                    // keys per dim row (4 of them padding)
-constexpr int SH_TILE_B = 64 * SH_PS * 4;          // 17408 bytes
-constexpr int SH_SW = 32;                          // dims per workgroup
-constexpr int SH_HALF_B = SH_SW * SH_PS * 4;       // 8704 bytes staged per step
-constexpr int SH_PCHUNKS = (SH_HALF_B + 1023) / 1024;   // 8 full 1 KB DMA + one half
-constexpr int SH_W_OFF = SH_HALF_B;
-constexpr int SH_SLOT = SH_HALF_B + ATT_MAX_GQ * CD_T * 4;
-static_assert(SH_HALF_B % 512 == 0 && SH_W_OFF % 16 == 0, "tile chunks");
-
-constexpr int SH_MAX_CHAINS = 4;   // chain waves per workgroup (register budget)
-
-template <int D>
-__global__ void __launch_bounds__(64 * (SH_MAX_CHAINS + CD_NP)) attn_chain_shadow_kernel(AttnArgs a_in, int qpg,
-                                                                                          int nbmax) {
-    constexpr int H = 1;
-    const AttnArgs a = resolve(a_in);
-    extern __shared__ __align__(16) unsigned char smem[];
-    const int gq = a.gq, nc = qpg * gq;          // chain rows
-    const int hw = gq / H;                       // chain waves per query position
-    const int ncw = qpg * hw;                    // chain waves
-    unsigned char* ring = smem;                                            // [D][SH_SLOT]
-    float* corr_s = reinterpret_cast<float*>(smem + D * SH_SLOT);          // [nc][nbmax]
-    float* bsum_s = corr_s + (size_t)nc * nbmax;
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
-
-    const int d = a.d, da = (d / 8) * 8;
-    const int nsl = (d + SH_SW - 1) / SH_SW;   // 32-dim slices (workgroups)
-    const int nsl64 = (d + 63) / 64;           // 64-dim slices (tile layout)
-    size_t g = blockIdx.x;
-    const int sl = (int)(g % nsl);
-    g /= nsl;
-    const int kvh = (int)(g % a.Hkv);
-    g /= a.Hkv;
-    const int ngrp = (a.S + qpg - 1) / qpg;
-    const int qp0 = (int)(g % ngrp) * qpg;
-    const size_t b = g / ngrp;
-    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int lane = threadIdx.x & 63;
-
-    size_t ks, ke_l, bl_l;
-    const int qlast = min(qp0 + qpg, a.S) - 1;
-    kv_range<true>(a, (size_t)qlast, ks, ke_l, bl_l);
-    size_t kneed = ks;
-    if (ke_l > ks) {
-        kneed = ks + ((ke_l - ks + ATT_BLOCK - 1) / ATT_BLOCK) * ATT_BLOCK;
-        if (kneed > bl_l) kneed = bl_l;
-    }
-    const size_t kt_end = kneed < a.cache_len ? kneed : (size_t)a.cache_len;
-    const int nst = kt_end > 0 ? (int)((kt_end + CD_T - 1) / CD_T) : 0;
-    const bool is_chain = wv < ncw;
-    const int pw = wv - ncw;
-
-    // stage wave pw: product chunks pw, pw + CD_NP, ...; the weights of
-    // rows 4k..4k+3 go to stage wave 1 + k
-    const int wn = (nc + 3) / 4;
-    const bool my_w = pw >= 1 && pw <= wn;
-    const int lpt = (SH_PCHUNKS - pw + CD_NP - 1) / CD_NP + (my_w ? 1 : 0);   // 2 or 3
-    const char* psrc = nullptr;
-    const float* wsrc = nullptr;
-    if (!is_chain) {
-        psrc = reinterpret_cast<const char*>(a.vsh) +
-               (((b * a.Hkv + kvh) * nsl64 + sl / 2) * a.sh_ntile) * (size_t)SH_TILE_B + (sl & 1) * SH_HALF_B +
-               lane * 16;
-        if (my_w) {
-            int r = (pw - 1) * 4 + lane / 16;
-            int qp = qp0 + r / gq;
-            if (r >= nc || qp >= a.S) {
-                r = 0;
-                qp = qp0;
-            }
-            const size_t row = (b * a.S + qp) * a.Hq + kvh * gq + r % gq;
-            wsrc = a.w + row * a.wstride + (lane % 16) * 4;
-        }
-    }
-    auto issue = [&](int t) {
-        const uint32_t slot = ring_lds + (uint32_t)((t % D) * SH_SLOT);
-        const char* src = psrc + (size_t)t * SH_TILE_B;
-        for (int c = pw; c < SH_PCHUNKS; c += CD_NP)
-            if (c * 1024 + lane * 16 < SH_HALF_B) lds_dma<16>(src + c * 1024, slot + c * 1024);
-        if (my_w) lds_dma<16>(wsrc + (size_t)t * CD_T, slot + SH_W_OFF + (pw - 1) * 1024);
-    };
-    auto wait_next = [&](bool all_issued) {
-        if (!all_issued) wait_dma<0>();
-        else if (lpt == 3) wait_dma<(D - 2) * 3>();
-        else wait_dma<(D - 2) * 2>();
-    };
-
-    // ---- chain wave: query position qp, heads hp*H .. hp*H + H-1, chain
-    // rows wv*H + j (position-major, the weight rows' order)
-    const int qp = qp0 + (is_chain ? wv / hw : 0);
-    const int hp = is_chain ? wv % hw : 0;
-    const bool row_ok = is_chain && qp < a.S;
-    const size_t row0 = (b * a.S + (size_t)(row_ok ? qp : 0)) * a.Hq + kvh * gq + hp * H;
-    const int c0 = (is_chain ? wv : 0) * H;
-    size_t rks = 0, rke = 0, rbl = 0;
-    int nb = 0, nb_tile = 0;
-    if (row_ok) {
-        kv_range<true>(a, (size_t)qp, rks, rke, rbl);
-        nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
-        nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
-    }
-    const int dim = sl * SH_SW + lane;
-    const bool dlane = lane < SH_SW;   // chain lanes
-    float pf_p = 0.0f, pf_w[H];
-    const bool pf = row_ok && a.cache_len < rke;
-#pragma unroll
-    for (int j = 0; j < H; j++) pf_w[j] = 0.0f;
-    if (pf) {
-#pragma unroll
-        for (int j = 0; j < H; j++) pf_w[j] = a.w[(row0 + j) * a.wstride + (a.cache_len - rks)];
-        if (dlane && dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
-    }
-    if (row_ok)
-        for (int j = 0; j < H; j++) chain_corr(a, row0 + j, nb, corr_s + (c0 + j) * nbmax, bsum_s + (c0 + j) * nbmax);
-
-    if (!is_chain && nst > 0) {
-        for (int t = 0; t < D - 1; t++)
-            if (t < nst) issue(t);
-        wait_next(nst >= D - 1);
-    }
-    const float* cw = corr_s + c0 * nbmax;
-    const float* cb = bsum_s + c0 * nbmax;
-    float acc[H], rs[H];
-#pragma unroll
-    for (int j = 0; j < H; j++) {
-        acc[j] = 0.0f;
-        rs[j] = 0.0f;
-    }
-    for (int t = 0; t < nst; t++) {
-        lds_barrier();
-        if (!is_chain) {
-            if (t + D - 1 < nst) issue(t + D - 1);
-            if (t + 1 < nst) wait_next(t + D - 1 < nst);
-            continue;
-        }
-        if (!row_ok) continue;
-        const unsigned char* slot = ring + (t % D) * SH_SLOT;
-        const float* pt = reinterpret_cast<const float*>(slot) + (lane & (SH_SW - 1)) * SH_PS;
-        const float* wt = reinterpret_cast<const float*>(slot + SH_W_OFF) + c0 * CD_T;
-        const int b0 = t * (CD_T / ATT_BLOCK);
-        const int b1 = min(nb_tile, b0 + CD_T / ATT_BLOCK);
-        if (dlane) chain_tile(pt, wt, b0, b1, rks, rbl, cw, cb, acc[0], rs[0]);
-    }
-    if (!row_ok || !dlane) return;
-    const int tl = nst > 0 ? nst - 1 : 0;
-    const unsigned char* slot = ring + (tl % D) * SH_SLOT;
-#pragma unroll
-    for (int j = 0; j < H; j++) {
-        chain_tail<true>(a, b, kvh, dim, row0 + j, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
-                         reinterpret_cast<const float*>(slot) + (lane & (SH_SW - 1)) * SH_PS,
-                         reinterpret_cast<const float*>(slot + SH_W_OFF) + (c0 + j) * CD_T, pf, pf_p, pf_w[j],
-                         cw + j * nbmax, cb + j * nbmax, acc[j], rs[j]);
-        if (dim < d) {
-            uint16_t* ov = a.o + (row0 + j) * (size_t)d;
-            if (!(rs[j] > 0.0f) || dim >= da) ov[dim] = 0;
-            else ov[dim] = f2h(acc[j] * (1.0f / rs[j]));
-        }
-    }
-}
-
-// ------------------------------------------------ kernel B, decode form
-// Decode form of the product-tile kernel: a workgroup is one chain wave and
-// NP stage waves.  The chain wave owns NH query heads of one KV head and DR
-// 16-dim sub-slices (16-lane row r -> head r % NH, sub-slice r / NH); the
-// heads share the product rows and each row reads its own head's weights.
-// Stage waves move the tiles (LDS DMA, D - 1 tiles ahead; one wave issues
-// LDS DMA at ~4.5 bytes per cycle, so six of them keep a chain fed) and
-// compute the rows' block corrections.  The chain wave holds half a tile in
-// registers and reads the next half while this one chains: between
-// barriers it only issues LDS reads and plain FMAs (a dependent FMA with a
-// DPP-broadcast operand costs about twice as much here).
-template <int NH, int DR, int NP>
-struct PairCfg {
-    static constexpr int SW = 16 * DR;                       // dims per workgroup
-    static constexpr int LANES = 16 * NH * DR;               // chain lanes
-    static constexpr int PB = SW * SH_PS * 4;                // product bytes per tile
-    static constexpr int NPC = (PB + 1023) / 1024;           // product DMA instructions per tile
-    static constexpr int W_OFF = PB;
-    static constexpr int SLOT = PB + NH * CD_T * 4;
-    static constexpr int NPT = NPC + 1;                      // DMA instructions per tile (+ weights)
-    static constexpr int PER = NPT / NP;                     // per stage wave and tile
-    static_assert(LANES <= 64 && PB % 16 == 0, "pair layout");
-    static_assert(NPT % NP == 0 && NH <= NP, "stage waves share the DMA evenly");
-};
-
-// s_waitcnt lgkmcnt(0) + s_barrier as compiler-visible instructions, so the
-// compiler's own wait tracking knows every LDS read before it has completed
-__device__ __forceinline__ void lds_sync() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7, lgkmcnt 0
-    __builtin_amdgcn_s_barrier();
-}
-
-// s_waitcnt vmcnt(min(y, N) * PER) for a wave-uniform y (y <= 0: vmcnt(0))
-template <int PER, int N>
-__device__ __forceinline__ void wait_younger(int y) {
-    if constexpr (N <= 0) {
-        wait_dma<0>();
-    } else {
-        if (y >= N) wait_dma<N * PER>();
-        else wait_younger<PER, N - 1>(y);
-    }
-}
-
-template <int D, int NH, int DR, int NP>
-__global__ void __launch_bounds__(64 * (NP + 1)) attn_chain_pair_kernel(AttnArgs a_in, int nbmax) {
-    using C = PairCfg<NH, DR, NP>;
-    const AttnArgs a = resolve(a_in);
-    extern __shared__ __align__(16) unsigned char smem[];
-    unsigned char* ring = smem;                                             // [D][SLOT]
-    float* corr_s = reinterpret_cast<float*>(smem + D * C::SLOT);           // [NH][nbmax]
-    float* bsum_s = corr_s + (size_t)NH * nbmax;
-    int* fast_s = reinterpret_cast<int*>(bsum_s + (size_t)NH * nbmax);     // [nbmax]: tile t on the fast path
-    const uint32_t ring_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)ring;
-    const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const bool is_chain = wv == 0;
-    const int pw = wv - 1;                                    // stage wave index
-    const int d = a.d, da = (d / 8) * 8;
-    const int nsl = (d + C::SW - 1) / C::SW;
-    const int nsl64 = (d + 63) / 64;
-    const int ngh = a.gq / NH;
-    size_t g = blockIdx.x;
-    const int sl = (int)(g % nsl);
-    g /= nsl;
-    const int hg = (int)(g % ngh);
-    g /= ngh;
-    const int kvh = (int)(g % a.Hkv);
-    g /= a.Hkv;
-    const int qp = (int)(g % a.S);
-    const size_t b = g / a.S;
-
-    const int r16 = lane >> 4, lr = lane & 15;
-    const int hj = r16 % NH;                                  // chain lane's head within the group
-    const bool dlane = is_chain && lane < C::LANES;
-    const int dim = sl * C::SW + (r16 / NH) * 16 + lr;
-    const size_t row0 = (b * a.S + qp) * a.Hq + (size_t)kvh * a.gq + hg * NH;
-    const size_t row = row0 + hj;
-
-    size_t rks, rke, rbl;
-    kv_range<true>(a, (size_t)qp, rks, rke, rbl);
-    const int nb = rke > rks ? (int)((rke - rks + ATT_BLOCK - 1) / ATT_BLOCK) : 0;
-    size_t kneed = rks;
-    if (rke > rks) {
-        kneed = rks + (size_t)nb * ATT_BLOCK;
-        if (kneed > rbl) kneed = rbl;
-    }
-    const size_t kt_end = kneed < a.cache_len ? kneed : (size_t)a.cache_len;
-    const int nst = kt_end > 0 ? (int)((kt_end + CD_T - 1) / CD_T) : 0;
-    const int nb_tile = rbl <= kt_end ? nb : min(nb, (int)((kt_end - rks) / ATT_BLOCK));
-
-    // stage wave pw moves DMA units u = pw + NP i of each tile: units below
-    // NPC are 1 KB product chunks, unit NPC the NH weight rows (16 lanes x
-    // 16 bytes each)
-    const char* psrc = reinterpret_cast<const char*>(a.vsh) +
-                       (((b * a.Hkv + kvh) * nsl64 + (sl * C::SW) / 64) * a.sh_ntile) * (size_t)SH_TILE_B +
-                       (size_t)((sl * C::SW) % 64) * SH_PS * 4 + lane * 16;
-    const float* wsrc = a.w + (row0 + min(lane >> 4, NH - 1)) * a.wstride + lr * 4;
-    auto issue = [&](int t) {
-        const uint32_t slot = ring_lds + (uint32_t)((t % D) * C::SLOT);
-#pragma unroll
-        for (int i = 0; i < C::PER; i++) {
-            const int u = pw + NP * i;
-            if (u < C::NPC) {
-                if (u * 1024 + lane * 16 < C::PB)
-                    lds_dma<16>(psrc + (size_t)t * SH_TILE_B + u * 1024, slot + u * 1024);
-            } else if (lane < 16 * NH) {
-                lds_dma<16>(wsrc + (size_t)t * CD_T, slot + C::W_OFF);
-            }
-        }
-    };
-    // this stage wave's DMA for tile t complete, younger tiles may fly:
-    // issued so far min(last, nst - 1) with last = t_issued
-    auto wait_landed = [&](int t, int last_issued) {
-        const int younger = min(last_issued, nst - 1) - t;
-        if (younger <= 0) wait_dma<0>();
-        else if (younger >= D - 2) wait_dma<(D - 2) * C::PER>();
-        else {
-            switch (younger) {
-                case 5: wait_dma<5 * C::PER>(); break;
-                case 4: wait_dma<4 * C::PER>(); break;
-                case 3: wait_dma<3 * C::PER>(); break;
-                case 2: wait_dma<2 * C::PER>(); break;
-                default: wait_dma<1 * C::PER>(); break;
-            }
-        }
-    };
-    static_assert(D <= 8, "wait counts above cover younger <= 6");
-
-    // ---- prologue: stage waves start the ring and compute the rows' block
-    // corrections and which tiles take the fast path; the chain wave fetches
-    // the first new row
-    float pf_p = 0.0f, pf_w = 0.0f;
-    const bool pf = a.cache_len < rke;
-    if (!is_chain) {
-        // the row's block maxima and sums come by LDS DMA ahead of the ring
-        // (exec-masked to the row's nb entries), so waiting for them -- an
-        // explicit vmcnt that leaves the ring's DMA in flight -- does not
-        // wait for the tiles
-        const bool corr_wave = pw < NH;
-        if (corr_wave) {
-            const float* bm = a.bmax + (row0 + pw) * a.nbstride;
-            const float* bsm = a.bsum + (row0 + pw) * a.nbstride;
-            const uint32_t cl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(corr_s + pw * nbmax);
-            const uint32_t sl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) float*)(bsum_s + pw * nbmax);
-            for (int c0 = 0; c0 < nb; c0 += 64) {
-                if (c0 + lane < nb) {
-                    lds_dma<4>(bm + c0 + lane, cl + 4 * c0);
-                    lds_dma<4>(bsm + c0 + lane, sl + 4 * c0);
-                }
-            }
-        }
-        for (int t = 0; t < D - 1; t++)
-            if (t < nst) issue(t);
-        if (corr_wave) {
-            wait_younger<C::PER, D - 1>(min(D - 1, nst));   // the corrections' DMA has landed
-            chain_corr_scan(nb, corr_s + pw * nbmax);
-        }
-    } else if (pf && dlane) {
-        pf_w = a.w[row * a.wstride + (a.cache_len - rks)];
-        if (dim < d) pf_p = h2f(a.v[((b * a.new_len) * a.Hkv + kvh) * (size_t)d + dim]);
-    }
-    lds_sync();
-    if (!is_chain) {
-        // tile t is fast when both its blocks lie inside the tile and no head
-        // has a zero weight in them (flag: sign of the block sum)
-        if (pw == 0) {
-            for (int t = lane; t < nst; t += 64) {
-                const int b0 = t * (CD_T / ATT_BLOCK);
-                bool f = b0 + 2 <= nb_tile && rks + (size_t)(b0 + 2) * ATT_BLOCK <= rbl;
-                for (int j = 0; j < NH && f; j++)
-                    f = !__builtin_signbit(bsum_s[j * nbmax + b0]) && !__builtin_signbit(bsum_s[j * nbmax + b0 + 1]);
-                fast_s[t] = f ? 1 : 0;
-            }
-        }
-        if (nst > 1) wait_landed(1, D - 2);
-        else if (nst > 0) wait_landed(0, D - 2);
-    }
-    lds_sync();
-    const float* cw = corr_s + hj * nbmax;
-    const float* cb = bsum_s + hj * nbmax;
-
-    float acc = 0.0f, rs = 0.0f;
-    // A fast tile chains as plain FMAs over two halves (one 32-key block
-    // each) held in registers: the block's 32 products of this lane's
-    // dimension, its head's 32 weights (a 16-lane row reads one head's
-    // weight row, so two heads share a wave) and the block's {corr, sum}.
-    // The next half is read while this one chains.  A tile whose blocks are
-    // partial or hold a zero weight runs key by key from LDS.
-    float pv[2][32], hw[2][32], mt[2][2];
-    const int prow = (r16 / NH) * 16 + lr;                    // product row within the slot
-    auto read_half = [&](int t, int h, float* p, float* w, float* m) {
-        const unsigned char* slot = ring + (t % D) * C::SLOT;
-        const float* pt = reinterpret_cast<const float*>(slot) + prow * SH_PS + 32 * h;
-        const float* wt = reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T + 32 * h;
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const float4 v = *reinterpret_cast<const float4*>(pt + 4 * q);
-            const float4 x = *reinterpret_cast<const float4*>(wt + 4 * q);
-            p[4 * q] = v.x;
-            p[4 * q + 1] = v.y;
-            p[4 * q + 2] = v.z;
-            p[4 * q + 3] = v.w;
-            w[4 * q] = x.x;
-            w[4 * q + 1] = x.y;
-            w[4 * q + 2] = x.z;
-            w[4 * q + 3] = x.w;
-        }
-        const int i = min(t * (CD_T / ATT_BLOCK) + h, nbmax - 1);
-        m[0] = cw[i];
-        m[1] = cb[i];
-    };
-    auto chain_half = [&](const float* p, const float* w, const float* m) {
-        const float NEG_INF = -__builtin_inff();
-        if (m[0] != NEG_INF) {
-            acc = acc * m[0];
-            rs = rs * m[0];
-        }
-#pragma unroll
-        for (int k = 0; k < ATT_BLOCK; k++) acc = __builtin_fmaf(p[k], w[k], acc);
-        rs = rs + m[1];
-    };
-
-    int fl = 0;
-    if (is_chain && nst > 0) {
-        read_half(0, 0, pv[0], hw[0], mt[0]);
-        fl = fast_s[0];
-    }
-    for (int tt = 0; tt < nst; tt++) {
-        if (is_chain) {
-            // tiles tt and tt + 1 have landed (the stage waves waited for
-            // tt + 1 before the previous barrier); the last tile re-reads
-            // itself, its slot stays intact
-            const int tn = min(tt + 1, nst - 1);
-            const int fn = fast_s[tn];
-            read_half(tt, 1, pv[1], hw[1], mt[1]);
-            if (__builtin_amdgcn_readfirstlane(fl)) {
-                chain_half(pv[0], hw[0], mt[0]);
-                read_half(tn, 0, pv[0], hw[0], mt[0]);
-                chain_half(pv[1], hw[1], mt[1]);
-            } else {
-                if (dlane) {
-                    const unsigned char* slot = ring + (tt % D) * C::SLOT;
-                    const int b0 = tt * (CD_T / ATT_BLOCK);
-                    chain_tile(reinterpret_cast<const float*>(slot) + prow * SH_PS,
-                               reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, b0,
-                               min(nb_tile, b0 + CD_T / ATT_BLOCK), rks, rbl, cw, cb, acc, rs);
-                }
-                read_half(tn, 0, pv[0], hw[0], mt[0]);
-            }
-            fl = fn;
-        } else {
-            // slot of tile tt - 1: its last reader finished before the
-            // previous barrier
-            if (tt + D - 1 < nst) issue(tt + D - 1);
-            if (tt + 2 < nst) wait_landed(tt + 2, tt + D - 1);
-        }
-        lds_sync();
-    }
-    if (!dlane) return;
-    const int tl = nst > 0 ? nst - 1 : 0;
-    const unsigned char* slot = ring + (tl % D) * C::SLOT;
-    chain_tail<true>(a, b, kvh, dim, row, nb_tile, nb, rks, rbl, kt_end, (size_t)tl * CD_T,
-                     reinterpret_cast<const float*>(slot) + prow * SH_PS,
-                     reinterpret_cast<const float*>(slot + C::W_OFF) + hj * CD_T, pf, pf_p, pf_w, cw, cb, acc, rs);
-    if (dim < d) {
-        uint16_t* ov = a.o + row * (size_t)d;
-        if (!(rs > 0.0f) || dim >= da) ov[dim] = 0;
-        else ov[dim] = f2h(acc * (1.0f / rs));
-    }
-}
-
 // ------------------------------------------------ kernel B, many query rows
 // Prefill form of the value chains.  A workgroup owns RW_CH chains -- RW_CH/gq
 // consecutive query rows times the gq heads of one kv head -- on one 64-dim
@@ -2072,28 +1586,8 @@ __global__ void __launch_bounds__(RW_THREADS) attn_rows_kernel(AttnArgs a_in, in
 static size_t rows_smem(int nbmax) { return (size_t)RW_PROD_B + RW_W_B + 2 * (size_t)RW_CH * nbmax * sizeof(float); }
 
 // ------------------------------------------------ per-(device, stream) scratch
-struct AttnScratch {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-static std::mutex g_att_mu;
-static std::map<std::pair<int, void*>, AttnScratch> g_att_scratch;
-
 static int attn_scratch(void* stream, size_t bytes, void** out) {
-    int dev = 0;
-    CH_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_att_mu);
-    AttnScratch& s = g_att_scratch[std::make_pair(dev, stream)];
-    if (s.bytes < bytes) {
-        // the previous buffer is kept: kernels queued on the stream may use it
-        size_t want = bytes + bytes / 4;
-        void* p = nullptr;
-        CH_HIP(hipMalloc(&p, want));
-        s.ptr = p;
-        s.bytes = want;
-    }
-    *out = s.ptr;
-    return CACTUS_HIP_OK;
+    return stream_scratch(SCR_ATTN, stream, bytes, false, out);
 }
 
 template <bool HYBRID>
@@ -2120,7 +1614,8 @@ static int launch_attention(AttnArgs a, void* stream) {
     const size_t rows = (size_t)a.B * a.S * a.Hq;
     const int nb = (int)((maxr + ATT_BLOCK - 1) / ATT_BLOCK);
     CH_REQUIRE(nb <= 1024, "attention: key range above 32768 is not supported");
-    a.wstride = (maxr + 63) & ~(size_t)63;
+    // (+64: the decode chain kernel reads one block past a row's last)
+    a.wstride = ((maxr + 63) & ~(size_t)63) + 64;
     a.nbstride = nb > 0 ? nb : 1;
     const size_t wbytes = rows * a.wstride * sizeof(float);
     const size_t bbytes = rows * (size_t)a.nbstride * sizeof(float);
@@ -2153,7 +1648,12 @@ static int launch_attention(AttnArgs a, void* stream) {
         // decode: one query row, its gq heads per wave, one wave per 64 keys
         // (with the fused head preparation, one more workgroup per kv head
         // appends the step's key and value)
-        dim3 ga((unsigned)(chunks + (a.prep.q_raw ? 1 : 0)), (unsigned)((size_t)a.B * a.S * a.Hkv));
+        // workgroups of kv head h on XCD h % 8, where the chain kernel's are
+        a.xcd_chunks = (int)(chunks + (a.prep.q_raw ? 1 : 0));
+        a.xcd_rest = a.B * a.S;                          // row groups of one row (NQ = gq)
+        const size_t nwg = 8 * (size_t)((a.Hkv + 7) / 8) * a.xcd_chunks * a.xcd_rest;
+        CH_REQUIRE(nwg < (1u << 31), "attention: decode key range too long");
+        dim3 ga((unsigned)nwg);
         auto go = [&](auto kern) { hipLaunchKernelGGL(kern, ga, dim3(64), 0, as_stream(stream), a); };
         if (a.d == 64) {
             if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 64, 1, 1>);
@@ -2182,24 +1682,7 @@ static int launch_attention(AttnArgs a, void* stream) {
     if (qpg < 1) qpg = 1;
     const int nbmax = a.nbstride;
     const size_t nsl = (size_t)(a.d + 63) / 64;
-    if (HYBRID && a.vsh && (size_t)a.B * a.S <= 2) {
-        // decode: one chain wave and six stage waves per workgroup, two heads
-        // per chain wave when the query-head group splits evenly
-        constexpr int SD = 8;
-        const bool two = a.gq % 2 == 0;
-        const size_t slot = two ? PairCfg<2, 1, 6>::SLOT : PairCfg<1, 1, 6>::SLOT;
-        const size_t smem = SD * slot + (2 * (size_t)(two ? 2 : 1) + 1) * nbmax * sizeof(float);
-        if (smem <= 64 * 1024) {
-            const size_t groups = (size_t)a.B * a.S * a.Hkv * (a.gq / (two ? 2 : 1)) * ((a.d + 15) / 16);
-            if (two)
-                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 2, 1, 6>), dim3((unsigned)groups), dim3(448), smem,
-                                   as_stream(stream), a, nbmax);
-            else
-                hipLaunchKernelGGL((attn_chain_pair_kernel<SD, 1, 1, 6>), dim3((unsigned)groups), dim3(448), smem,
-                                   as_stream(stream), a, nbmax);
-            return check_launch("attention values (decode)");
-        }
-    }
+    if (HYBRID && a.vsh) return launch_chain_stream(a, nbmax, stream);   // decode with value product tiles
     {
         // prefill: many query rows per workgroup, several chains per lane
         const bool aligned = (HYBRID ? (uintptr_t)a.vc % 4 == 0 && (uintptr_t)a.vs % 4 == 0 : true) &&
@@ -2220,34 +1703,6 @@ static int launch_attention(AttnArgs a, void* stream) {
             }
             (void)hipGetLastError();  // clear the sticky attribute error before the forms below
         }
-    }
-    if (HYBRID && a.vsh && a.gq <= SH_MAX_CHAINS) {
-        // product tiles: ring depth 8, or 5 where the rows' block data needs
-        // the room
-        auto sh_smem = [&](int q, int depth) {
-            return (size_t)depth * SH_SLOT + 2 * (size_t)q * a.gq * nbmax * sizeof(float);
-        };
-        int depth = 12;
-        while (qpg > 1 && qpg * a.gq > SH_MAX_CHAINS) qpg = (qpg + 1) / 2;
-        while (qpg > 1 && sh_smem(qpg, depth) > 160 * 1024) qpg = (qpg + 1) / 2;
-        if (sh_smem(qpg, depth) > 160 * 1024) depth = 5;
-        const size_t smem = sh_smem(qpg, depth);
-        CH_REQUIRE(smem <= 160 * 1024, "attention: key range too long for the product-tile kernel");
-        const size_t ngrp = ((size_t)a.S + qpg - 1) / qpg;
-        const size_t groups = (size_t)a.B * ngrp * a.Hkv * ((a.d + SH_SW - 1) / SH_SW);
-        const dim3 blk(64 * (qpg * a.gq + CD_NP));
-        static bool sh_attr[2] = {false, false};
-        auto launch = [&](auto kern, int di) -> int {
-            if (!sh_attr[di]) {
-                CH_HIP(hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024));
-                sh_attr[di] = true;
-            }
-            hipLaunchKernelGGL(kern, dim3((unsigned)groups), blk, smem, as_stream(stream), a, qpg, nbmax);
-            return CACTUS_HIP_OK;
-        };
-        const int lrc = depth == 12 ? launch(attn_chain_shadow_kernel<12>, 0) : launch(attn_chain_shadow_kernel<5>, 1);
-        if (lrc) return lrc;
-        return check_launch("attention values");
     }
     // LDS-DMA form: value rows in 16- or 4-byte chunks, one scale group per
     // 64-dim slice; otherwise the register-staged form

@@ -1120,34 +1120,24 @@ __global__ void __launch_bounds__(256) attn_prefill_combine_kernel(PrefillArgs a
 }
 
 // ------------------------------------------------ per-(device, stream) workspace
+// split partials, and the per-KV-head completion counters (zeroed when made;
+// the combining workgroup leaves its counter at zero)
 struct FastWs {
     float* part = nullptr;
     uint32_t* cnt = nullptr;
-    size_t part_floats = 0, ncnt = 0;
 };
-static std::mutex g_fast_mu;
-static std::map<std::pair<int, void*>, FastWs> g_fast_ws;
 
 static int fast_ws(void* stream, size_t part_floats, size_t ncnt, FastWs* out) {
-    int dev = 0;
-    CH_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_fast_mu);
-    FastWs& w = g_fast_ws[std::make_pair(dev, stream)];
-    if (w.part_floats < part_floats) {
-        // the previous buffers are kept: kernels queued on the stream may use them
-        void* p = nullptr;
-        CH_HIP(hipMalloc(&p, part_floats * sizeof(float)));
-        w.part = static_cast<float*>(p);
-        w.part_floats = part_floats;
+    void* p = nullptr;
+    int rc = stream_scratch(SCR_FAST_PART, stream, part_floats * sizeof(float), false, &p);
+    if (rc) return rc;
+    out->part = static_cast<float*>(p);
+    out->cnt = nullptr;
+    if (ncnt) {
+        rc = stream_scratch(SCR_FAST_CNT, stream, ncnt * sizeof(uint32_t), true, &p);
+        if (rc) return rc;
+        out->cnt = static_cast<uint32_t*>(p);
     }
-    if (w.ncnt < ncnt) {
-        void* p = nullptr;
-        CH_HIP(hipMalloc(&p, ncnt * sizeof(uint32_t)));
-        CH_HIP(hipMemsetAsync(p, 0, ncnt * sizeof(uint32_t), as_stream(stream)));
-        w.cnt = static_cast<uint32_t*>(p);
-        w.ncnt = ncnt;
-    }
-    *out = w;
     return CACTUS_HIP_OK;
 }
 
@@ -1351,7 +1341,7 @@ int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t*
                "decode_prep_attention_fast: bad head counts");
     CH_REQUIRE(fast_attention_supported(1, head_dim, num_q_heads / num_kv_heads, nullptr),
                "decode_prep_attention_fast: head_dim 64 or 128 with 1, 2 or 4 query heads per KV head");
-    CH_REQUIRE(max_cache + 1 <= FA_MAX_KEYS_HYBRID, "decode_prep_attention_fast: cache longer than 32767 tokens");
+    CH_REQUIRE(max_cache + 1 <= FA_MAX_KEYS_HYBRID, "decode_prep_attention_fast: cache longer than 131071 tokens");
     CH_REQUIRE(((uintptr_t)k_cache & 15) == 0 && ((uintptr_t)v_cache & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
                "decode_prep_attention_fast: misaligned cache or workspace");
     CH_REQUIRE(workspace_bytes >= cactus_hip_decode_attention_fast_workspace(num_q_heads, num_kv_heads, head_dim,

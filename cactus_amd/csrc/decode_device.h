@@ -137,7 +137,7 @@ __device__ __forceinline__ void rope_row(const uint16_t* ys, int d, const uint16
 
 // quantize_group_fp16_to_int8 per 128-dim group (kernel_quants.cpp:223-264);
 // with `sh`, also the row's fp32 products (float)code * scale into the
-// product tiles (kv_shadow.hip layout, key `key`, kv head `h`)
+// product tiles (sh_index layout, key `key`, kv head `h`)
 __device__ __forceinline__ void kv_append_row(const uint16_t* src, int8_t* dst, float* scales, int d,
                                               float* sh = nullptr, size_t ntile = 0, size_t key = 0, int h = 0) {
     const int lane = threadIdx.x & 63;
@@ -158,7 +158,7 @@ __device__ __forceinline__ void kv_append_row(const uint16_t* src, int8_t* dst, 
             if (sh) {
                 const int dim = g0 + i;
                 const float p = dim < da ? (float)code * s : 0.0f;
-                sh[(((size_t)h * nsl + dim / 64) * ntile + key / 64) * (64 * 68) + (dim % 64) * 68 + key % 64] = p;
+                sh[sh_index(h, nsl, dim / 64, ntile, key, dim % 64)] = p;
             }
         }
         if (lane == 0) scales[g] = s;

@@ -396,6 +396,13 @@ size_t QwenModel::build_block(size_t h, uint32_t l, size_t pos) {
     return fuse ? out : g.add(h1, out);
 }
 
+void QwenModel::check_token_ids(const std::vector<uint32_t>& tokens) const {
+    for (uint32_t t : tokens)
+        if (t >= cfg_.vocab)
+            throw std::runtime_error("Embedding index out of bounds: " + std::to_string(t) + " >= " +
+                                     std::to_string(cfg_.vocab));
+}
+
 // model_qwen.cpp:132-172 (use_cache = true)
 size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
     if (tokens.empty()) throw std::runtime_error("Token sequence cannot be empty");
@@ -405,10 +412,7 @@ size_t QwenModel::forward(const std::vector<uint32_t>& tokens) {
     const size_t pos = cache_.total_seq_len;
     // the reference's out-of-range check (graph_ops_tensor.cpp:256-263), on
     // the host ids before anything is launched
-    for (uint32_t t : tokens)
-        if (t >= cfg_.vocab)
-            throw std::runtime_error("Embedding index out of bounds: " + std::to_string(t) + " >= " +
-                                     std::to_string(cfg_.vocab));
+    check_token_ids(tokens);
     size_t ids = g.input({S}, Precision::FP32);
     size_t h = g.embedding_checked_ids(n_embedding_, ids);
     std::vector<float> idf(S);
@@ -437,6 +441,11 @@ void QwenModel::set_kv_window(size_t window, size_t sink) {
 // engine_model.cpp:170-219
 void QwenModel::prefill(const std::vector<uint32_t>& tokens) {
     if (tokens.empty()) return;
+    // every id is checked before the first chunk is queued: a bad id in a
+    // later chunk must not leave earlier chunks' KV appends in flight on the
+    // overlapped streams (the reference raises the same error from its
+    // embedding node, graph_ops_tensor.cpp:256-263)
+    check_token_ids(tokens);
     const size_t chunk = cfg_.prefill_chunk ? cfg_.prefill_chunk : 256;
     if (tokens.size() > chunk && cache_.fits(tokens.size())) {
         prefill_overlapped(tokens, chunk);
@@ -532,6 +541,15 @@ void QwenModel::prefill_overlapped(const std::vector<uint32_t>& tokens, size_t c
         }
     } catch (...) {
         cur_ = graph_.get();
+        // whatever the other streams queued (KV appends included) stays
+        // ordered before later work on stream_; errors of the join itself
+        // are dropped so the original exception propagates
+        for (int p = 1; p < NS; p++) {
+            if (cactus_hip_event_record(join_ev_[p], stream_of(p)) == 0)
+                (void)cactus_hip_stream_wait_event(stream_, join_ev_[p]);
+            else
+                (void)cactus_hip_stream_sync(stream_of(p));
+        }
         throw;
     }
     cur_ = graph_.get();

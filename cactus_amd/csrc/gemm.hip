@@ -590,28 +590,8 @@ static bool launch_lds_any(const GemmArgs& a, hipStream_t st) {
 }
 
 // ------------------------------------------------ activation scratch
-struct GemmScratch {
-    void* ptr = nullptr;
-    size_t bytes = 0;
-};
-static std::mutex g_gemm_mu;
-static std::map<std::pair<int, void*>, GemmScratch> g_gemm_scratch;
-
 static int gemm_scratch(hipStream_t st, size_t bytes, void** out) {
-    int dev = 0;
-    CH_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_gemm_mu);
-    GemmScratch& s = g_gemm_scratch[std::make_pair(dev, (void*)st)];
-    if (s.bytes < bytes) {
-        // the previous buffer is kept: kernels queued on the stream may use it
-        const size_t want = bytes + bytes / 4;
-        void* p = nullptr;
-        CH_HIP(hipMalloc(&p, want));
-        s.ptr = p;
-        s.bytes = want;
-    }
-    *out = s.ptr;
-    return CACTUS_HIP_OK;
+    return stream_scratch(SCR_GEMM_ACT, st, bytes, false, out);
 }
 
 // Rows from which the MFMA path pays off over the streaming GEMV.

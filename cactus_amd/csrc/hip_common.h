@@ -35,6 +35,39 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Value product tiles (kv_shadow.hip): an fp32 mirror of the INT8 value
+// cache, per (kv head, 64-dim slice) a run of 64-key tiles laid out
+// [key / 4][64 dims][4 keys], so one 16-byte load per lane (lane = dim)
+// brings four consecutive keys of a dimension and a wave's load of a key
+// quad is one contiguous kilobyte.  ntile = ceil(capacity / 64).
+constexpr int SH_TILE_KEYS = 64;
+constexpr size_t SH_TILE_FLOATS = (size_t)SH_TILE_KEYS * 64;     // 16 KB per tile
+__host__ __device__ inline size_t sh_region_floats(size_t ntile) { return ntile * SH_TILE_FLOATS; }
+__host__ __device__ inline size_t sh_index(int kvh, int nsl, int sl, size_t ntile, size_t key, int dl) {
+    return ((size_t)(kvh * nsl + sl) * ntile * SH_TILE_KEYS + (key & ~(size_t)3)) * 64 + (size_t)dl * 4 + (key & 3);
+}
+
+// Per-(device, stream, kind) scratch buffers of the library (runtime.hip).
+// A buffer grows to 1.25x the request when too small.  The buffer it
+// replaces is freed once the work queued on the stream before the growth has
+// finished (an event, polled on later calls), unless it was handed out
+// while the stream was being captured into a graph: a graph may replay it
+// at any time, so it is kept until the stream is destroyed
+// (cactus_hip_stream_destroy), which frees every buffer of the stream.
+// `zero`: a new buffer is zero-filled on the stream (a fill kernel, safe to
+// capture) before its first use.
+enum ScratchKind {
+    SCR_GEMM_ACT = 0,    // matmul activation codes + row scales
+    SCR_ATTN,            // exact attention weights, block maxima and sums
+    SCR_LM,              // LM head partial maxima + completion counter
+    SCR_FAST_PART,       // split-K attention partials
+    SCR_FAST_CNT,        // split-K attention completion counters
+    SCR_KINDS
+};
+int stream_scratch(int kind, void* stream, size_t bytes, bool zero, void** out);
+// frees every scratch buffer of `stream` (all devices) after synchronizing it
+int stream_scratch_release(void* stream);
+
 // Device RoPE tables (fp16 cos/sin [npos][head_dim/2]) built on the host,
 // cached per (device, head_dim, theta); grows to at least npos positions.
 struct RopeTable {

@@ -2,10 +2,10 @@
 //
 // The hybrid attention accumulates, per cached key, (float)code * scale
 // rounded to fp32 (kernel_attention.cpp:424-441).  The decode path keeps
-// those products precomputed in HBM, laid out as the value chains read them
-// from LDS, so that staging a tile is a plain memory copy (LDS DMA):
+// those products precomputed in HBM, laid out as the value chains load them
+// into registers (hip_common.h, sh_index):
 //
-//   [kv head][64-dim slice][64-key tile][64 dims][68 keys]   (4 keys padding)
+//   [kv head][64-dim slice][key / 4][64 dims][4 keys]
 //
 // The INT8 cache stays the reference state; the tiles are derived data,
 // rewritten whenever keys are appended (prefill chunks here, decode steps in
@@ -17,8 +17,7 @@
 
 namespace cactus_hip {
 
-constexpr int KS_T = 64;
-constexpr int KS_PS = 68;
+constexpr int KS_T = SH_TILE_KEYS;
 
 __global__ void kv_shadow_kernel(const int8_t* __restrict__ vc, const float* __restrict__ vs,
                                  float* __restrict__ sh, size_t start, int Hkv, int d, int qgs,
@@ -28,13 +27,10 @@ __global__ void kv_shadow_kernel(const int8_t* __restrict__ vc, const float* __r
     const int nqg = (d + 127) / 128;
     const int da = (d / 8) * 8, nsl = (d + 63) / 64;
     const size_t off = key * Hkv + kvh;
-    const size_t t = key / KS_T;
-    const int j = (int)(key % KS_T);
     for (int dim = threadIdx.x; dim < nsl * 64; dim += blockDim.x) {
         float p = 0.0f;
         if (dim < da) p = (float)vc[off * d + dim] * vs[off * nqg + ((dim / 8) * 8) / qgs];
-        const int sl = dim / 64, dl = dim % 64;
-        sh[(((size_t)kvh * nsl + sl) * ntile + t) * (KS_T * KS_PS) + dl * KS_PS + j] = p;
+        sh[sh_index(kvh, nsl, dim / 64, ntile, key, dim % 64)] = p;
     }
 }
 
@@ -95,15 +91,12 @@ __global__ void kv_shift_in_kernel(const KvLayer* __restrict__ layers, const uns
         // products from the moved codes and scales (same expression and
         // layout as kv_shadow_kernel)
         const int da = (d / 8) * 8, nsl = (d + 63) / 64;
-        const size_t tt = key / KS_T;
-        const int jj = (int)(key % KS_T);
         for (int x = threadIdx.x; x < Hkv * nsl * 64; x += blockDim.x) {
             const int kvh = x / (nsl * 64), dim = x % (nsl * 64);
             float p = 0.0f;
             if (dim < da)
                 p = (float)(int8_t)t[cb + (size_t)kvh * d + dim] * ts[sb + (size_t)kvh * nqg + ((dim / 8) * 8) / 128];
-            const int sl = dim / 64, dl = dim % 64;
-            L.sh[(((size_t)kvh * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = p;
+            L.sh[sh_index(kvh, nsl, dim / 64, ntile, key, dim % 64)] = p;
         }
     }
     if (state && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) state[2] = cache_len;
@@ -132,8 +125,6 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restric
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int ng = (d + 127) / 128, nsl = (d + 63) / 64;
     const int units = Hkv * ng;
-    const size_t tt = key / KS_T;
-    const int jj = (int)(key % KS_T);
     for (int w = wave + 4 * (int)blockIdx.z; w < 2 * units; w += 4 * (int)gridDim.z) {
         const bool isv = w >= units;
         const int hg = isv ? w - units : w, h = hg / ng, g = hg % ng;
@@ -152,8 +143,8 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restric
             const int8_t code = (int8_t)sat8(c);
             o[j] = code;
             if (isv && L.sh) {
-                const int dim = g0 + j, sl = dim / 64, dl = dim % 64;
-                L.sh[(((size_t)h * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = (float)code * sc;
+                const int dim = g0 + j;
+                L.sh[sh_index(h, nsl, dim / 64, ntile, key, dim % 64)] = (float)code * sc;
             }
         }
         if (lane == 0) (isv ? L.vs : L.ks)[(key * Hkv + h) * ng + g] = sc;
@@ -162,8 +153,8 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const KvLayer* __restric
     const int pad = nsl * 64 - d;
     if (L.sh && pad > 0 && blockIdx.z == 0)
         for (int x = threadIdx.x; x < Hkv * pad; x += blockDim.x) {
-            const int h = x / pad, dim = d + x % pad, sl = dim / 64, dl = dim % 64;
-            L.sh[(((size_t)h * nsl + sl) * ntile + tt) * (KS_T * KS_PS) + dl * KS_PS + jj] = 0.0f;
+            const int h = x / pad, dim = d + x % pad;
+            L.sh[sh_index(h, nsl, dim / 64, ntile, key, dim % 64)] = 0.0f;
         }
 }
 
@@ -180,7 +171,7 @@ extern "C" {
 int cactus_hip_kv_shadow_bytes(size_t max_seq, size_t kv_heads, size_t head_dim, size_t* bytes) {
     CH_REQUIRE(bytes, "kv_shadow_bytes: null");
     const size_t ntile = (max_seq + KS_T - 1) / KS_T;
-    *bytes = kv_heads * ((head_dim + 63) / 64) * ntile * (size_t)(KS_T * KS_PS) * sizeof(float);
+    *bytes = kv_heads * ((head_dim + 63) / 64) * sh_region_floats(ntile) * sizeof(float);
     return CACTUS_HIP_OK;
 }
 

@@ -215,31 +215,22 @@ __global__ void f16_matmul_scalar_kernel(const uint16_t* __restrict__ a,
 }
 
 // ------------------------------------------------ per-(device, stream) scratch
+// one buffer: the completion counter (zeroed when the buffer is made; the
+// last workgroup of every call leaves it at zero), then the per-workgroup
+// partial maxima and their indices
 struct LmScratch {
     float* val = nullptr;
     uint32_t* idx = nullptr;
     uint32_t* counter = nullptr;
-    size_t cap = 0;
 };
-static std::mutex g_lm_mu;
-static std::map<std::pair<int, void*>, LmScratch> g_lm_scratch;
 
 static int lm_scratch(void* stream, size_t blocks, LmScratch* out) {
-    int dev = 0;
-    CH_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_lm_mu);
-    LmScratch& s = g_lm_scratch[std::make_pair(dev, stream)];
-    if (s.cap < blocks) {
-        // earlier buffers are kept: kernels queued on the stream may still use them
-        LmScratch n;
-        CH_HIP(hipMalloc(&n.val, blocks * sizeof(float)));
-        CH_HIP(hipMalloc(&n.idx, blocks * sizeof(uint32_t)));
-        CH_HIP(hipMalloc(&n.counter, sizeof(uint32_t)));
-        CH_HIP(hipMemset(n.counter, 0, sizeof(uint32_t)));
-        n.cap = blocks;
-        s = n;
-    }
-    *out = s;
+    void* p = nullptr;
+    int rc = stream_scratch(SCR_LM, stream, 256 + 8 * blocks, true, &p);
+    if (rc) return rc;
+    out->counter = static_cast<uint32_t*>(p);
+    out->val = reinterpret_cast<float*>(static_cast<char*>(p) + 256);
+    out->idx = reinterpret_cast<uint32_t*>(out->val + blocks);
     return CACTUS_HIP_OK;
 }
 

@@ -1,7 +1,10 @@
 // runtime.hip -- error state, device memory, streams and events of the C ABI.
 #include "hip_common.h"
 
+#include <map>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 namespace cactus_hip {
 
@@ -33,6 +36,109 @@ __global__ void fill_bytes_kernel(uint8_t* dst, uint32_t word, size_t bytes) {
     } else {
         for (size_t i = tid; i < bytes; i += stride) dst[i] = (uint8_t)word;
     }
+}
+
+// ------------------------------------------------ per-stream scratch
+namespace {
+struct ScratchBuf {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    bool captured = false;   // handed out during a graph capture
+};
+struct Retired {
+    void* ptr;
+    hipEvent_t done;         // null: kept until the stream is destroyed
+};
+struct StreamScratch {
+    ScratchBuf cur[SCR_KINDS];
+    std::vector<Retired> retired;
+};
+std::mutex g_scr_mu;
+std::map<std::pair<int, void*>, StreamScratch> g_scr;
+
+// frees the retired buffers whose stream work has finished
+void reap(StreamScratch& S) {
+    size_t keep = 0;
+    for (size_t i = 0; i < S.retired.size(); i++) {
+        Retired& r = S.retired[i];
+        if (r.done && hipEventQuery(r.done) == hipSuccess) {
+            (void)hipFree(r.ptr);
+            (void)hipEventDestroy(r.done);
+        } else {
+            S.retired[keep++] = r;
+        }
+    }
+    S.retired.resize(keep);
+}
+}  // namespace
+
+int stream_scratch(int kind, void* stream, size_t bytes, bool zero, void** out) {
+    CH_REQUIRE(kind >= 0 && kind < SCR_KINDS && out, "scratch: bad request");
+    int dev = 0;
+    CH_HIP(hipGetDevice(&dev));
+    const hipStream_t st = as_stream(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (st) CH_HIP(hipStreamIsCapturing(st, &cs));
+    const bool capturing = cs == hipStreamCaptureStatusActive;
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    StreamScratch& S = g_scr[std::make_pair(dev, stream)];
+    reap(S);
+    ScratchBuf& b = S.cur[kind];
+    if (b.bytes < bytes || !b.ptr) {
+        const size_t want = (bytes + bytes / 4 + 255) & ~(size_t)255;
+        void* p = nullptr;
+        CH_HIP(hipMalloc(&p, want ? want : 256));
+        if (b.ptr) {
+            Retired r{b.ptr, nullptr};
+            if (!b.captured && !capturing) {
+                // work queued before this point may still read the old buffer
+                hipEvent_t e = nullptr;
+                if (hipEventCreateWithFlags(&e, hipEventDisableTiming) == hipSuccess) {
+                    if (hipEventRecord(e, st) == hipSuccess) r.done = e;
+                    else (void)hipEventDestroy(e);
+                }
+            }
+            S.retired.push_back(r);
+        }
+        b.ptr = p;
+        b.bytes = want ? want : 256;
+        b.captured = false;
+        if (zero) {
+            size_t blocks = (b.bytes / 4 + 255) / 256;
+            if (blocks > 4096) blocks = 4096;
+            hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (uint8_t*)p, 0u,
+                               b.bytes);
+            int rc = check_launch("scratch zero fill");
+            if (rc) return rc;
+        }
+    }
+    if (capturing) b.captured = true;
+    *out = b.ptr;
+    return CACTUS_HIP_OK;
+}
+
+int stream_scratch_release(void* stream) {
+    std::lock_guard<std::mutex> lk(g_scr_mu);
+    bool synced = false;
+    for (auto it = g_scr.begin(); it != g_scr.end();) {
+        if (it->first.second != stream) {
+            ++it;
+            continue;
+        }
+        if (!synced) {
+            CH_HIP(hipStreamSynchronize(as_stream(stream)));
+            synced = true;
+        }
+        StreamScratch& S = it->second;
+        for (ScratchBuf& b : S.cur)
+            if (b.ptr) (void)hipFree(b.ptr);
+        for (Retired& r : S.retired) {
+            (void)hipFree(r.ptr);
+            if (r.done) (void)hipEventDestroy(r.done);
+        }
+        it = g_scr.erase(it);
+    }
+    return CACTUS_HIP_OK;
 }
 
 }  // namespace cactus_hip
@@ -117,7 +223,11 @@ int cactus_hip_stream_create(void** stream) {
 }
 
 int cactus_hip_stream_destroy(void* stream) {
-    if (stream) CH_HIP(hipStreamDestroy(as_stream(stream)));
+    if (!stream) return CACTUS_HIP_OK;
+    // the library's scratch buffers of the stream go with it
+    int rc = stream_scratch_release(stream);
+    if (rc) return rc;
+    CH_HIP(hipStreamDestroy(as_stream(stream)));
     return CACTUS_HIP_OK;
 }
 

@@ -121,8 +121,12 @@ class Qwen:
         self._check(self.lib.cactus_qwen_set_decode_mode(self.h, mode))
 
     def set_attention_mode(self, mode: int):
-        """0: exact attention (bit-identical); 1: tolerance-mode split-K
-        attention for decode steps."""
+        """0: exact attention (bit-identical); 1: tolerance mode for every
+        attention node -- split-K kernels for decode steps and FP16-MFMA
+        flash attention for prefill chunks, each within 1e-3 + 1e-2 |ref| of
+        the reference per output (the softmax where the reference's block
+        rescale overflows); greedy tokens may then differ from the
+        reference's."""
         self._check(self.lib.cactus_qwen_set_attention_mode(self.h, mode))
 
     def reset(self):

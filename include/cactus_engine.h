@@ -85,11 +85,15 @@ int cactus_qwen_reset(void* model);
  * HIP graph per token.  Both are bit-identical. */
 int cactus_qwen_set_decode_mode(void* model, int mode);
 /* Selects the attention arithmetic: 0 = exact (the reference's operation
- * order, bit-identical; the default), 1 = tolerance mode: decode-shaped
- * attention (one query row) runs the split-K kernels of
+ * order, bit-identical; the default), 1 = tolerance mode: every attention
+ * node runs the _fast kernels -- decode steps the split-K kernels of
  * cactus_hip_attention_*_fast / cactus_hip_decode_prep_attention_fast,
- * within 1e-3 + 1e-2 |ref| of the reference per fp16 output; prefill chunks
- * stay exact.  Applies to both decode modes. */
+ * prefill chunks the FP16-MFMA flash attention of
+ * cactus_hip_attention_hybrid_int8_fp16_fast -- within 1e-3 + 1e-2 |ref| of
+ * the reference per fp16 output, and the softmax (not the reference's zero
+ * row) where the reference's block rescale overflows.  Greedy tokens are
+ * therefore not guaranteed to equal the reference's.  Applies to both
+ * decode modes. */
 int cactus_qwen_set_attention_mode(void* model, int mode);
 /* KVCache::set_window_size (engine/engine_cache.cpp:25-46): keep at most
  * `window` cached tokens -- the first `sink` of the sequence and the most

@@ -211,9 +211,15 @@ int cactus_hip_attention_hybrid_int8_fp16(const uint16_t* q, const int8_t* k_cac
  * heads per KV head; hybrid: quant_group_size >= head_dim) runs as a split-K
  * reduction over 256-key splits with one combine, so the launch is bound by
  * HBM bandwidth instead of the reference's sequential value accumulation.
- * The result is the same softmax attention with a different fp32 summation
- * order and exponential: within |gpu - ref| <= 1e-3 + 1e-2 |ref| of the
- * reference, not bit-identical.  Every other shape runs the exact kernels. */
+ * The hybrid variant also takes prefill rows (seq_len > 1, causal, 16-byte
+ * aligned rows, head_dim 64 or 128): they run as flash attention on FP16
+ * MFMA.  Both are the same softmax attention with a different fp32
+ * summation order and exponential: within |gpu - ref| <= 1e-3 + 1e-2 |ref|
+ * of the reference per output, not bit-identical.  Where the reference's
+ * block rescale overflows (a later block's max more than ~88 below an
+ * earlier one makes its running accumulators infinite and the row comes out
+ * zero, kernel_attention.cpp:395-403, 465-469) these variants return the
+ * softmax instead.  Every other shape runs the exact kernels. */
 int cactus_hip_attention_f16_fast(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                   uint16_t* o, size_t batch, size_t seq_len, size_t kv_seq_len,
                                   size_t num_q_heads, size_t num_kv_heads, size_t head_dim,
@@ -368,9 +374,11 @@ int cactus_hip_sample_history_reset(void* stream);
 /* ------------------------------------------------ value product tiles
  * No reference counterpart: an fp32 mirror of the INT8 value cache holding
  * each cached (float)code * scale, the operand the hybrid attention's value
- * accumulation rounds to (kernel_attention.cpp:424-441), tiled
- * [kv head][64-dim slice][64-key tile][64 dims][68 keys] for the decode
- * attention.  Batch 1, head_dim % 8 == 0, 128-dim scale groups. */
+ * accumulation rounds to (kernel_attention.cpp:424-441), laid out
+ * [kv head][64-dim slice][key / 4][64 dims][4 keys] (a slice's keys padded
+ * to whole 64-key tiles) for the decode attention: one 16-byte load per
+ * lane gives a dim's products of four consecutive keys.  Batch 1,
+ * head_dim % 8 == 0, 128-dim scale groups. */
 int cactus_hip_kv_shadow_bytes(size_t max_seq, size_t kv_heads, size_t head_dim, size_t* bytes);
 /* products of cached keys [start, start + count) from the INT8 values and
  * scales ([max_seq][kv_heads][head_dim], [max_seq][kv_heads][groups]) */

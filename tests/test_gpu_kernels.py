@@ -455,16 +455,17 @@ def test_attention_hybrid_batch2(dev, orc):
 
 
 def _shadow_ref(vc, vs, cap, d):
-    """Product tiles [kvh][slice][tile][64 dims][68 keys] of an INT8 cache
-    (numpy float32 products, the rounding the value chain consumes)."""
+    """Product tiles [kvh][slice][key / 4][64 dims][4 keys] (the key capacity
+    rounded up to 64) of an INT8 cache (numpy float32 products, the rounding
+    the value chain consumes)."""
     n, H = vc.shape[0], vc.shape[1]
     nsl, nt = (d + 63) // 64, (cap + 63) // 64
-    ref = np.zeros((H, nsl, nt, 64, 68), np.float32)
+    ref = np.zeros((H, nsl, nt * 16, 64, 4), np.float32)
     prod = vc.astype(np.float32) * np.repeat(vs, 128, axis=2)[:, :, :d]
     for key in range(n):
         for sl in range(nsl):
             w = min(64, d - sl * 64)
-            ref[:, sl, key // 64, :w, key % 64] = prod[key, :, sl * 64:sl * 64 + w]
+            ref[:, sl, key // 4, :w, key % 4] = prod[key, :, sl * 64:sl * 64 + w]
     return ref
 
 
@@ -497,10 +498,10 @@ def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, qmul, shadow):
         dev.cm.call("cactus_hip_kv_shadow_bytes", cap, Hkv, d, ctypes.byref(nbytes))
         sh = dev.empty(nbytes.value)
         dev.cm.call("cactus_hip_kv_shadow_update", vcp, vsp, sh.ptr, 0, cache, Hkv, d, 128, cap, None)
-        got = dev.get(sh, np.float32, (Hkv, (d + 63) // 64, (cap + 63) // 64, 64, 68))
+        got = dev.get(sh, np.float32, (Hkv, (d + 63) // 64, (cap + 63) // 64 * 16, 64, 4))
         want = _shadow_ref(vc[:cache], vs[:cache], cap, d)
         for key in (0, cache // 2, cache - 1):
-            t, j = key // 64, key % 64
+            t, j = key // 4, key % 4
             assert (got[:, :, t, :, j] == want[:, :, t, :, j]).all(), f"products of key {key}"
         shp = sh.ptr
     state = np.array([0, cache, cache, 0], np.uint32)
@@ -570,10 +571,10 @@ def test_decode_prep_attention_fused(dev, orc, cache, Hq, Hkv, d, shadow):
     if shadow:
         # written entries only: keys 0..cache (padding and later keys are
         # never written, so two fresh buffers differ there)
-        ts = (Hkv, (d + 63) // 64, (cap + 63) // 64, 64, 68)
+        ts = (Hkv, (d + 63) // 64, (cap + 63) // 64 * 16, 64, 4)
         keys = np.arange(cache + 1)
-        ta = dev.get(shA, np.float32, ts)[:, :, keys // 64, :, keys % 64]
-        tb = dev.get(shB, np.float32, ts)[:, :, keys // 64, :, keys % 64]
+        ta = dev.get(shA, np.float32, ts)[:, :, keys // 4, :, keys % 4]
+        tb = dev.get(shB, np.float32, ts)[:, :, keys // 4, :, keys % 4]
         assert (ta.view(np.uint32) == tb.view(np.uint32)).all(), "product tiles"
     qp = dev.get(q_out, np.uint16, (Hq, d)).reshape(1, 1, Hq, d)
     kp = dev.get(k_out, np.uint16, (Hkv, d)).reshape(1, 1, Hkv, d)

@@ -126,6 +126,44 @@ def test_qwen_prefill_rejects_out_of_range_token():
     assert list(toks) == list(ref)
 
 
+def test_qwen_overlapped_prefill_rejects_bad_id_in_last_chunk():
+    """A prompt long enough for the overlapped (three-stream) prefill whose
+    out-of-range id sits in its last chunk: refused before any chunk is
+    queued, the cache is left as it was, and a following prompt on the same
+    model -- prefill onto the first prompt's cache, then greedy decode --
+    matches the oracle bit for bit."""
+    say("qwen overlapped prefill, bad id in the last chunk")
+    cfg = qwen_small_config(prefill_chunk=32)
+    rng = np.random.default_rng(21)
+    w = qwen_weights(rng, cfg)
+    import cactus_amd
+    from cactus_amd.engine import Qwen
+    import oracle
+    cactus_amd.call("cactus_hip_init", 0)
+    gpu = Qwen(cfg, *w)
+    orc = oracle.OracleQwen(cfg, *w)
+    first = rng.integers(0, cfg["vocab"], 70).astype(np.uint32)
+    gpu.prefill(first)
+    orc.prefill(first, 32)
+    bad = rng.integers(0, cfg["vocab"], 100).astype(np.uint32)
+    bad[-3] = cfg["vocab"] + 2
+    with pytest.raises(Exception, match="Embedding index out of bounds"):
+        gpu.prefill(bad)
+    assert gpu.cache_len() == orc.cache_len() == 70
+    good = rng.integers(0, cfg["vocab"], 100).astype(np.uint32)
+    gpu.prefill(good)
+    orc.prefill(good, 32)
+    assert (gpu.last_hidden() == orc.last_hidden()).all(), "final hidden states"
+    for layer in range(cfg["num_layers"]):
+        for a, b in zip(gpu.read_kv(layer), orc.read_kv(layer)):
+            assert (a == b).all(), f"kv cache layer {layer}"
+    tok = int(rng.integers(0, cfg["vocab"]))
+    for _ in range(4):
+        t_gpu, t_orc = gpu.decode(tok), orc.decode(tok)
+        assert t_gpu == t_orc
+        tok = t_gpu
+
+
 @pytest.mark.parametrize("chunk,lens", [(64, (150,)), (64, (200,)), (32, (70, 130))])
 def test_qwen_overlapped_prefill_matches_oracle(chunk, lens):
     """Multi-chunk prompts run their chunks overlapped on three streams (chunk

@@ -222,10 +222,10 @@ def test_kv_window_shift_matches_memmove(hip_ready, dst, src, count):
         # value products of the moved tokens equal a fresh computation
         ref = cm.DeviceBuffer(nbytes.value)
         cm.call("cactus_hip_kv_shadow_update", d["v"].ptr, d["vs"].ptr, ref.ptr, 0, cap, kvh, hd, 128, cap, None)
-        # [kv head x 64-dim slice][64-key tile][64 dims][64 keys + 4 padding]:
-        # only keys below the capacity are ever written
+        # [kv head x 64-dim slice][key / 4][64 dims][4 keys]: only keys below
+        # the capacity are ever written
         def keys(buf):
-            a = buf.to_numpy(np.float32, (nbytes.value // 4,)).reshape(kvh * 2, -1, 64, 68)[..., :64]
+            a = buf.to_numpy(np.float32, (nbytes.value // 4,)).reshape(kvh * 2, -1, 64, 4)
             return a.transpose(0, 2, 1, 3).reshape(kvh * 2, 64, -1)[:, :, :cap]
         assert (keys(d["sh"]).view(np.uint32) == keys(ref).view(np.uint32)).all()
         ref.free()
