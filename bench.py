@@ -27,8 +27,11 @@ CPU model; and the other workloads the kernel layer is quoted on:
   qwen3_0p6b_decode_cpu_baseline   the oracle model's decode on the host
   qwen3_0p6b_prefill_cpu_baseline  the oracle model's prefill of 512 prompt
                                    tokens on the host
-  prefill_gemm_cpu_baseline        config 2 (INT8 M=512 matmul with row
-                                   quantization) by the oracle on the host
+
+Every other leg carries its own `cpu_baseline` beside its GPU figure, timed
+with the reference's thread policy: the INT8 M=512 matmul (whole pool), INT4
+M=1 (one thread: N < 5000) and M=256 (whole pool), and decode attention over
+both cache forms (one thread: 16 work items, below the ATTENTION threshold).
 """
 from __future__ import annotations
 
@@ -448,6 +451,129 @@ def cpu_gemm_baseline(seconds: float = 10.0, M: int = 512, K: int = 1024, N: int
                       f"quantized per row, {dt:.1f} s, x86 build of the CPU restatement, {threads} threads"}
 
 
+def cpu_int4_gemv_baseline(seconds: float = 5.0, nsets: int = 604):
+    """Config 3 at M=1 (INT4 K=3072 N=1024 g32) on one host core: the
+    reference runs the M=1 INT4 path through parallel_for over N columns
+    with the ELEMENT_WISE threshold (kernel_gemm.cpp:354-358,
+    kernel_utils.h:419-431), which keeps N=1024 on a single thread.  The
+    activation row is quantized per call, and `nsets` distinct packed weight
+    sets (about 1 GiB, as the GPU leg) are streamed in turn."""
+    import oracle
+    from _data import f16
+    L = oracle.lib()
+    L.orc_set_threads(1)
+    rng = np.random.default_rng(31)
+    per = N4 * K4 // 2
+    Bw = np.frombuffer(rng.bytes(nsets * per), np.uint8).reshape(nsets, per)
+    Bs = f16(np.abs(rng.normal(0, 0.02, size=(N4, K4 // GS))) / 7.0)
+    x = f16(rng.normal(0, 1, size=(1, K4)))
+    q = np.empty((1, K4), np.int8)
+    s = np.empty(1, np.float32)
+    C = np.empty((1, N4), np.uint16)
+    P = oracle.ptr
+    n = 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        L.orc_quantize_activations(P(x), P(q), P(s), 1, K4)
+        L.orc_matmul_int4(P(q), P(s), P(Bw[n % nsets]), P(Bs), P(C), 1, K4, N4, GS)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n * SET_BYTES_INT4 / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_call": round(dt / n * 1e6, 1),
+            "sample": f"{n} INT4 GEMVs M=1 K={K4} N={N4} g{GS} (activation row quantized per call) over "
+                      f"{nsets} distinct packed weight sets streamed in turn, {dt:.1f} s, x86 build of the "
+                      f"CPU restatement, 1 thread (the reference's M=1 policy at N < 5000)"}
+
+
+def cpu_int4_m256_baseline(seconds: float = 5.0, M: int = 256):
+    """Config 3 at M=256 on the host's pool (the reference tiles M > 1 over
+    every pool thread, kernel_gemm.cpp:380 with kernel_utils.h:439-456):
+    per-row activation quantization, then the INT4 grouped matmul."""
+    import oracle
+    from _data import f16
+    L = oracle.lib()
+    threads = min(16, os.cpu_count() or 1)
+    L.orc_set_threads(threads)
+    rng = np.random.default_rng(32)
+    Bp = rng.integers(0, 256, (N4, K4 // 2), dtype=np.uint8)
+    Bs = f16(np.abs(rng.normal(0, 0.02, size=(N4, K4 // GS))) / 7.0)
+    x = f16(rng.normal(0, 1, size=(M, K4)))
+    q = np.empty((M, K4), np.int8)
+    s = np.empty(M, np.float32)
+    C = np.empty((M, N4), np.uint16)
+    P = oracle.ptr
+    n = 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds:
+        L.orc_quantize_activations(P(x), P(q), P(s), M, K4)
+        L.orc_matmul_int4(P(q), P(s), P(Bp), P(Bs), P(C), M, K4, N4, GS)
+        n += 1
+    dt = time.perf_counter() - t0
+    L.orc_set_threads(1)
+    return {"value": round(2.0 * M * K4 * N4 * n / dt / 1e12, 5), "unit": "TOP/s", "cores": threads,
+            "kind": "port", "us_per_call": round(dt / n * 1e6, 1),
+            "sample": f"{n} calls of the INT4 M={M} K={K4} N={N4} g{GS} matmul with FP16 activations "
+                      f"quantized per row, {dt:.1f} s, x86 build of the CPU restatement, {threads} threads"}
+
+
+def cpu_attention_baselines(seconds: float = 5.0):
+    """Config 4 on one host core, both cache forms: one decode query (16
+    query / 8 KV heads, head_dim 128) over 4095 INT8 cached positions plus
+    one FP16 new row, and over 4096 FP16 positions.  The reference splits
+    the batch * heads * rows = 16 work items with the ATTENTION threshold
+    (kernel_attention.cpp:45 and :299, kernel_utils.h:419-431), so decode
+    attention runs on one thread.  Distinct caches are rotated so that the
+    host's caches do not hold them."""
+    import oracle
+    from _data import f16
+    L = oracle.lib()
+    L.orc_set_threads(1)
+    rng = np.random.default_rng(33)
+    Hq, Hkv, d, ctx = ATT_HQ, ATT_HKV, ATT_D, ATT_CTX
+    P = oracle.ptr
+    scale = d ** -0.5
+    out = {}
+    q = f16(rng.normal(0, 1, (1, Hq, d)))
+    o = np.empty((1, Hq, d), np.uint16)
+    # INT8 cache: 4095 cached positions + 1 new row
+    R8, cache = 32, ctx - 1
+    kc = rng.integers(-127, 128, (R8, cache, Hkv, d), dtype=np.int8)
+    vc = rng.integers(-127, 128, (R8, cache, Hkv, d), dtype=np.int8)
+    ks = np.abs(rng.normal(0, 0.02, (R8, cache, Hkv, 1))).astype(np.float32)
+    vs = np.abs(rng.normal(0, 0.02, (R8, cache, Hkv, 1))).astype(np.float32)
+    kn = f16(rng.normal(0, 1, (1, Hkv, d)))
+    vn = f16(rng.normal(0, 1, (1, Hkv, d)))
+    n = 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds / 2:
+        r = n % R8
+        L.orc_attention_hybrid_int8_fp16(P(q), P(kc[r]), P(vc[r]), P(ks[r]), P(vs[r]), P(kn), P(vn), P(o),
+                                         1, 1, cache, 1, Hq, Hkv, d, scale, cache, 1, 128)
+        n += 1
+    dt = time.perf_counter() - t0
+    us = dt / n * 1e6
+    out["int8_cache"] = {"us_per_call": round(us, 1), "gbs": round(ATT_BYTES_INT8 / us / 1e3, 3), "cores": 1,
+                         "kind": "port",
+                         "sample": f"{n} calls over {R8} distinct INT8 caches rotated, {dt:.1f} s, 1 thread"}
+    del kc, vc, ks, vs
+    # FP16 K/V: 4096 positions
+    R16 = 16
+    k16 = f16(rng.normal(0, 1, (R16, ctx, Hkv, d)))
+    v16 = f16(rng.normal(0, 1, (R16, ctx, Hkv, d)))
+    n = 0
+    t0 = time.perf_counter()
+    while n == 0 or time.perf_counter() - t0 < seconds / 2:
+        r = n % R16
+        L.orc_attention_f16(P(q), P(k16[r]), P(v16[r]), P(o), 1, 1, ctx, Hq, Hkv, d, scale, None, ctx - 1, 0, 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    us = dt / n * 1e6
+    out["fp16"] = {"us_per_call": round(us, 1), "gbs": round(ATT_BYTES_F16 / us / 1e3, 3), "cores": 1,
+                   "kind": "port", "sample": f"{n} calls over {R16} distinct FP16 caches rotated, {dt:.1f} s, 1 thread"}
+    out["unit"] = "us/call"
+    return out
+
+
 def cpu_prefill_baseline(tokens: int = 512):
     """The oracle's Qwen3-0.6B-shape model prefilling the first `tokens`
     tokens of the bench prompt on this host's cores (256-token chunks, 16 threads
@@ -632,6 +758,15 @@ def main():
     cpu_dec = None if args.skip_decode else cpu_decode_baseline(args.cpu_seconds)
     cpu_gemm = cpu_gemm_baseline(args.cpu_seconds)
     cpu_pf = None if args.skip_decode else cpu_prefill_baseline()
+    # each CPU baseline beside the GPU figure it is quoted with
+    g4["cpu_baseline"] = cpu_int4_gemv_baseline(args.cpu_seconds / 2)
+    gemms["int8_m512_k1024_n3072_g32"]["cpu_baseline"] = cpu_gemm
+    gemms["int4_k3072_n1024_g32"]["m256"]["cpu_baseline"] = cpu_int4_m256_baseline(args.cpu_seconds / 2)
+    gemms["int4_k3072_n1024_g32"]["m1"]["cpu_baseline"] = g4["cpu_baseline"]
+    cpu_att = cpu_attention_baselines(args.cpu_seconds)
+    for mode in ("exact", "tolerance"):
+        att[f"int8_cache_{mode}"]["cpu_baseline"] = cpu_att["int8_cache"]
+        att[f"fp16_{mode}"]["cpu_baseline"] = cpu_att["fp16"]
     out = {
         "metric": "INT8 GEMV GB/s (% HBM peak) + Qwen3-0.6B-shape decode tok/s, 1 MI355X",
         "value": round(g["gbs"], 2),
@@ -668,7 +803,6 @@ def main():
         "qwen3_0p6b_decode": dec,
         "qwen3_0p6b_decode_cpu_baseline": cpu_dec,
         "qwen3_0p6b_prefill_cpu_baseline": cpu_pf,
-        "prefill_gemm_cpu_baseline": cpu_gemm,
     }
     print(json.dumps(out), flush=True)
 

@@ -133,7 +133,13 @@ size_t CactusGraph::matmul(size_t a, size_t b, bool pretransposed_rhs) {
     return add_node(OpType::MATMUL, {a, b}, out, Precision::FP16, p);
 }
 
+// The node is typed INT8 (one byte per code, plus per-row scales).  The
+// reference's add_node re-types any node asked for INT8 to its first input's
+// precision (graph_builder.cpp:582-587), so there this node reports FP16 and
+// its codes sit in an FP16-sized buffer; consumers here read the INT8 type.
 size_t CactusGraph::quantize_activations(size_t input) {
+    if (node(input).out.precision != Precision::FP16)
+        throw std::invalid_argument("quantize_activations requires FP16 input");   // graph_builder.cpp:563-565
     return add_node(OpType::QUANTIZE_ACTIVATIONS, {input}, node(input).out.shape, Precision::INT8);
 }
 

@@ -164,6 +164,12 @@ int cactus_hip_device_count(int* count) {
     return CACTUS_HIP_OK;
 }
 
+int cactus_hip_device_memory(size_t* free_bytes, size_t* total_bytes) {
+    CH_REQUIRE(free_bytes && total_bytes, "cactus_hip_device_memory: null");
+    CH_HIP(hipMemGetInfo(free_bytes, total_bytes));
+    return CACTUS_HIP_OK;
+}
+
 int cactus_hip_malloc(void** ptr, size_t bytes) {
     CH_REQUIRE(ptr, "cactus_hip_malloc: null out pointer");
     *ptr = nullptr;

@@ -41,6 +41,10 @@ extern "C" {
 int         cactus_hip_init(int device);
 const char* cactus_hip_last_error(void);
 int         cactus_hip_device_count(int* count);
+/* free and total device memory of the current device (hipMemGetInfo); no
+ * reference counterpart: a diagnostic, e.g. to show that a call allocates
+ * nothing */
+int         cactus_hip_device_memory(size_t* free_bytes, size_t* total_bytes);
 int         cactus_hip_malloc(void** ptr, size_t bytes);
 int         cactus_hip_free(void* ptr);
 int         cactus_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
