@@ -20,7 +20,7 @@ namespace cactus_hip {
 // global_load_dwordx4 that every lane makes from the same address (a ring
 // of CS_R 32-key blocks, CS_R - 1 blocks in flight), and the block's
 // rescale factor by one v_readlane.  Wave 1 turns the row's block maxima
-// into the rescale factors, the per-block path masks and the running sum
+// into the rescale factors, the per-block fast-path mask and the running sum
 // (the reference's sequential order) while wave 0 chains.  The tiles and
 // weights stream from this XCD's L2: the score kernel before this one puts
 // kv head h's workgroups on XCD h % 8, as this kernel does, and reads the
@@ -57,6 +57,18 @@ __device__ __forceinline__ void wait_vm_tie2(V* p, V* w) {
                  : "n"(N));
 }
 
+// inclusive max-scan over the wave's lanes (identity -1): row_shr 1, 2, 4,
+// 8 within each 16-lane row, then row_bcast:15 and row_bcast:31 across rows
+__device__ __forceinline__ int wave_scan_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xA, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xC, 0xF, false));
+    return v;
+}
+
 struct CsMap {
     int row, kvh, hj, sl;
     bool valid;
@@ -78,8 +90,7 @@ static unsigned cs_grid(int S, int Hkv, int gq, int nsl) {
     return 8u * (unsigned)((Hkv + 7) / 8) * (unsigned)S * (unsigned)gq * (unsigned)nsl;
 }
 
-// wts: the weights a_in.w as a restrict-qualified argument, so that their
-// uniform loads become scalar loads
+// wts: the weights a_in.w (rows of wstride floats, padded by one block)
 __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs a_in, int nbmax,
                                                                       const float* __restrict__ wts) {
     typedef float f4v __attribute__((ext_vector_type(4)));
@@ -89,8 +100,7 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
     float* corr_s = reinterpret_cast<float*>(smem);                                   // [nch * 64]
     float* bsum_s = corr_s + (size_t)nch * 64;                                        // [nch * 64]
     uint64_t* fast_s = reinterpret_cast<uint64_t*>(bsum_s + (size_t)nch * 64);        // [nch]
-    uint64_t* fin_s = fast_s + nch;                                                   // [nch]
-    float* rs_s = reinterpret_cast<float*>(fin_s + nch);
+    float* rs_s = reinterpret_cast<float*>(fast_s + nch);
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int d = a.d, da = (d / 8) * 8, nsl = (d + 63) / 64;
@@ -108,7 +118,8 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
 
     if (wv == 1) {
         // ---- block data: rescale factors (the running max is the last
-        // finite block max), fast-path and finite-max masks; then the
+        // finite block max; a block without one keeps the factor 1, which
+        // leaves every value unchanged) and the fast-path mask; then the
         // running sum.  Barrier 1: chunk 0 ready; barrier 2: every chunk;
         // barrier 3: the running sum.
         const float* bm = a.bmax + row * a.nbstride;
@@ -120,14 +131,8 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
             const float mx = i < nb ? bm[i] : NEG_INF;
             const float bs = i < nb ? bsm[i] : 0.0f;
             const bool fin = mx > NEG_INF;
-            int idx = fin ? lane : -1;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const int o = __shfl_up(idx, off, 64);
-                if (lane >= off) idx = max(idx, o);
-            }
-            int ex = __shfl_up(idx, 1, 64);
-            if (lane == 0) ex = -1;
+            const int idx = wave_scan_max(fin ? lane : -1);        // last finite block at or before this one
+            const int ex = __builtin_amdgcn_update_dpp(-1, idx, 0x138, 0xF, 0xF, false);   // wave_shr:1
             const float pm = __shfl(mx, ex < 0 ? 0 : ex, 64);
             const float prev = ex >= 0 ? pm : carry;
             const float corr = fin ? cactus_expf(prev - mx) : 1.0f;
@@ -135,27 +140,30 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
             if (last >= 0) carry = lane_f(mx, last);
             const bool full = (size_t)(i + 1) * ATT_BLOCK <= kfull;
             const bool fast = i < nb && full && fin && !__builtin_signbit(bs);
-            const uint64_t fastm = __ballot(fast), finm = __ballot(i < nb && fin);
+            const uint64_t fastm = __ballot(fast);
             corr_s[i] = corr;
             bsum_s[i] = __builtin_fabsf(bs);
-            if (lane == 0) {
-                fast_s[c] = fastm;
-                fin_s[c] = finm;
-            }
+            if (lane == 0) fast_s[c] = fastm;
             if (c == 0) __syncthreads();                     // barrier 1
         }
         if (nchu == 0) __syncthreads();
         __syncthreads();                                     // barrier 2
-        // running sum in the reference's order, one block at a time
+        // running sum in the reference's order, one block at a time:
+        // rs = rs * corr, then rs = rs + block sum (two roundings)
         float rs = 0.0f;
         for (int c = 0; c < nchu; c++) {
             const float cj = corr_s[c * 64 + lane], bj = bsum_s[c * 64 + lane];
-            const uint64_t fw = fin_s[c];
-            const uint64_t fm = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(fw >> 32)) << 32) |
-                                (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)fw);
             const int nin = min(64, nb - c * 64);
-            for (int j = 0; j < nin; j++) {
-                if ((fm >> j) & 1) rs = rs * lane_f(cj, j);
+            int j = 0;
+            for (; j + 4 <= nin; j += 4) {
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    rs = rs * lane_f(cj, j + u);
+                    rs = rs + lane_f(bj, j + u);
+                }
+            }
+            for (; j < nin; j++) {
+                rs = rs * lane_f(cj, j);
                 rs = rs + lane_f(bj, j);
             }
         }
@@ -218,7 +226,7 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
     __syncthreads();                                         // barrier 1
     float acc = 0.0f;
     float cv = 0.0f;
-    uint64_t fastm = 0, finm = 0;
+    uint64_t fastm = 0;
     const uint32_t clen = (uint32_t)a.cache_len, kend = (uint32_t)rke;
 
     // block at ring position r: wait for its slot (all but the 16 loads of
@@ -252,7 +260,7 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
             for (int e = 0; e < 4; e++) af = __builtin_fmaf(pr[r % CS_R][q][e], wr[r % CS_R][q][e], af);
         acc = af;
         if (__builtin_expect(!fast, 0)) {
-            float as = ((finm >> bl) & 1) ? a0 * cb : a0;
+            float as = a0 * cb;
             const uint32_t bs0 = (uint32_t)blk * ATT_BLOCK;
             const uint32_t ncache = clen > bs0 ? clen - bs0 : 0u;     // keys of the block in the cache
             const uint32_t nlive = kend > bs0 ? kend - bs0 : 0u;      // keys of the block in the row
@@ -268,17 +276,15 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
     };
 
     // block data of the 64-block chunk c (its rescale factors in cv, one
-    // per lane; its path masks); wave 1 has written chunk 0 by barrier 1 and
+    // per lane; its fast-path mask); wave 1 has written chunk 0 by barrier 1 and
     // the others by barrier 2
     auto load_chunk = [&](int c) {
         if (c == 1) __syncthreads();                         // barrier 2
         cv = corr_s[c * 64 + lane];
-        const uint64_t fw = fast_s[c], iw = fin_s[c];
+        const uint64_t fw = fast_s[c];
         __builtin_amdgcn_s_waitcnt(waitcnt_imm<63, 0>());   // the chunk's block data is in registers
         fastm = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(fw >> 32)) << 32) |
                 (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)fw);
-        finm = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(iw >> 32)) << 32) |
-               (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)iw);
     };
     const int nchu = (nb + 63) / 64;
     if (nb > 0) load_chunk(0);
@@ -339,7 +345,7 @@ int launch_chain_stream(const AttnArgs& a, int nbmax, void* stream) {
                "attention: value product tiles serve one batch, at most two query rows and head_dim <= 256");
     const int nsl = (a.d + 63) / 64;
     const int nch = (nbmax + 63) / 64;
-    const size_t smem = 2 * (size_t)nch * 64 * sizeof(float) + 2 * (size_t)nch * sizeof(uint64_t) + 16;
+    const size_t smem = 2 * (size_t)nch * 64 * sizeof(float) + (size_t)nch * sizeof(uint64_t) + 16;
     hipLaunchKernelGGL(attn_chain_stream_kernel, dim3(cs_grid(a.S, a.Hkv, a.gq, nsl)), dim3(CS_THREADS), smem,
                        as_stream(stream), a, nbmax, (const float*)a.w);
     return check_launch("attention values (decode)");

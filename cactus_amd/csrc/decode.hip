@@ -64,6 +64,12 @@ struct DecGemvArgs {
     DecSeg seg[3];
 };
 
+// LDS row strides of the group sums (floats) and scales (halves): whole
+// 16-byte (8-byte) vectors per row, plus 16 bytes so that consecutive rows
+// start four banks apart
+__host__ __device__ inline int dec_acc_stride(int G) { return ((G + 3) & ~3) + 4; }
+__host__ __device__ inline int dec_scl_stride(int G) { return ((G + 3) & ~3) + 8; }
+
 // grid.x: row tiles, grid.y: segment (EPI_SILUMUL: one tile covers `rows`
 // gate rows of seg[0] and the same rows of the up projection seg[1])
 template <int PRO, int EPI, bool INT4, int CH>
@@ -81,9 +87,12 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 
     int8_t* actq = reinterpret_cast<int8_t*>(smem);                          // K
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem + ((K + 15) & ~15));     // K
-    int32_t* acc = reinterpret_cast<int32_t*>(xs + ((K + 7) & ~7) + 16 * RMS_T_PAD);   // vrows*G
-    uint16_t* scl = reinterpret_cast<uint16_t*>(acc + vrows * G);           // vrows*G
-    float* red = reinterpret_cast<float*>(scl + ((vrows * G + 1) & ~1));    // 8
+    // group sums (as float) and scales per virtual row, rows padded so that
+    // the rows' epilogue chains read distinct LDS banks
+    const int AP = dec_acc_stride(G), SP = dec_scl_stride(G);
+    float* accf = reinterpret_cast<float*>(xs + ((K + 7) & ~7) + 16 * RMS_T_PAD);   // vrows*AP
+    uint16_t* scl = reinterpret_cast<uint16_t*>(accf + vrows * AP);          // vrows*SP
+    float* red = reinterpret_cast<float*>(scl + vrows * SP);                  // 8
 
     const int cpr = INT4 ? K / 32 : K / 16;
     const int P = INT4 ? gs / 32 : gs / 16;
@@ -220,56 +229,65 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
             *reinterpret_cast<uint2*>(actq + 8 * c) = INT4 ? nib_pack8(lo, hi) : make_uint2(lo, hi);
         }
     }
-#pragma unroll
-    for (int u = 0; u < DEC_SCL; u++)
-        if (tid + u * GEMV_THREADS < vrows * G) scl[tid + u * GEMV_THREADS] = sval[u] ? sreg[u] : (uint16_t)0;
     __syncthreads();
 
-    // 3. dot products and exact group sums
+    // 3. dot products and exact group sums; then the group scales, the last
+    // loads issued, go to LDS for the epilogue (stored here rather than with
+    // the codes, so that the codes barrier does not wait for the weights)
 #pragma unroll
     for (int i = 0; i < CH; i++) {
         const bool valid = crow[i] < vrows && vrow_valid(crow[i]);
         int dot = valid ? chunk_dot<INT4>(actq, ccol[i], wreg[i]) : 0;
         dot = group_lane_sum(dot, P);
         if (valid && ((tid + i * GEMV_THREADS) & (P - 1)) == 0)
-            acc[crow[i] * G + (ccol[i] * (INT4 ? 32 : 16)) / gs] = dot;
+            accf[crow[i] * AP + (ccol[i] * (INT4 ? 32 : 16)) / gs] = (float)dot;   // the epilogue's conversion
     }
+#pragma unroll
+    for (int u = 0; u < DEC_SCL; u++)
+        if (tid + u * GEMV_THREADS < vrows * G) {
+            const int i = tid + u * GEMV_THREADS;
+            scl[(i / G) * SP + i % G] = sval[u] ? sreg[u] : (uint16_t)0;
+        }
     __syncthreads();
 
     // 4. reference epilogue
-    // one row's chain over its G groups; the next 16 groups' sums and scales
-    // are read from LDS while the current 16 FMAs run
+    // one row's chain over its G groups, 4 groups per LDS read (the fp16
+    // scales enter the FMAs unconverted, as mixed-precision operands); the
+    // next 16 groups are read while the current 16 FMAs run
     auto chain = [&](int vr) {
         float rs = 0.0f;
-        const int32_t* ar = acc + vr * G;
-        const uint16_t* sr = scl + vr * G;
+        const float* ar = accf + vr * AP;
+        const uint16_t* sr = scl + vr * SP;
         const int G16 = G & ~15;
-        int av[2][16];
-        uint16_t sv[2][16];
-        if (G16 > 0) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        f4v av[2][4];
+        uint2 sv[2][4];
+        auto load16 = [&](int h, int gb) {
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
-                av[0][j] = ar[j];
-                sv[0][j] = sr[j];
+            for (int j = 0; j < 4; j++) {
+                av[h][j] = *reinterpret_cast<const f4v*>(ar + gb + 4 * j);
+                sv[h][j] = *reinterpret_cast<const uint2*>(sr + gb + 4 * j);
             }
-        }
+        };
+        if (G16 > 0) load16(0, 0);
         for (int g = 0; g < G16; g += 32) {
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int gb = g + 16 * h;
                 if (gb < G16) {
-                    const int gn = min(gb + 16, G16 - 16);   // clamped prefetch: re-reads the last block
+                    load16(h ^ 1, min(gb + 16, G16 - 16));   // clamped prefetch: re-reads the last block
 #pragma unroll
-                    for (int j = 0; j < 16; j++) {
-                        av[h ^ 1][j] = ar[gn + j];
-                        sv[h ^ 1][j] = sr[gn + j];
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t s01 = sv[h][j].x, s23 = sv[h][j].y;
+                        rs = __builtin_fmaf(av[h][j][0], h2f((uint16_t)(s01 & 0xFFFFu)), rs);
+                        rs = __builtin_fmaf(av[h][j][1], h2f((uint16_t)(s01 >> 16)), rs);
+                        rs = __builtin_fmaf(av[h][j][2], h2f((uint16_t)(s23 & 0xFFFFu)), rs);
+                        rs = __builtin_fmaf(av[h][j][3], h2f((uint16_t)(s23 >> 16)), rs);
                     }
-#pragma unroll
-                    for (int j = 0; j < 16; j++) rs = __builtin_fmaf((float)av[h][j], h2f(sv[h][j]), rs);
                 }
             }
         }
-        for (int g = G16; g < G; g++) rs = __builtin_fmaf((float)ar[g], h2f(sr[g]), rs);
+        for (int g = G16; g < G; g++) rs = __builtin_fmaf(ar[g], h2f(sr[g]), rs);
         return f2h(rs * as);
     };
     for (int r = tid; r < nr; r += GEMV_THREADS) {
@@ -291,7 +309,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 
 static size_t dec_gemv_smem(int K, int vrows, int G) {
     size_t s = (size_t)((K + 15) & ~15) + ((size_t)((K + 7) & ~7) + 16 * RMS_T_PAD) * 2;
-    s += (size_t)vrows * G * 4 + (size_t)((vrows * G + 1) & ~1) * 2 + 8 * 4;
+    s += (size_t)vrows * dec_acc_stride(G) * 4 + (size_t)vrows * dec_scl_stride(G) * 2 + 8 * 4;
     return (s + 15) & ~(size_t)15;
 }
 
@@ -382,12 +400,70 @@ struct LmDecArgs {
     const uint16_t* h; const uint16_t* norm_w; const uint16_t* b;
     float eps;
     int K, N;
-    float* part_val; uint32_t* part_idx; uint32_t* counter;
+    uint32_t* counter;       // scratch: counter at byte 0, argmax key at byte 8
     uint32_t* st;            // token, pos, cache_len, step
     uint32_t* tokens_out;    // [max_steps] or null
     uint32_t max_steps;
     uint16_t* logits_out;    // fp16 [N] or null
 };
+
+// Greedy argmax over the rows of all workgroups and the step state's
+// advance by the last workgroup to finish; every thread passes its row's
+// (value, index) or index 0xFFFFFFFF for none.  The reference's argmax
+// (first index wins; a NaN logit at index 0 is never beaten, any other NaN
+// never wins) is a maximum over 64-bit keys: the value's bits in an
+// order-preserving form, then 0xFFFFFFFF - index.  Each workgroup posts its
+// best key with one atomic max, waits for that atomic to be performed, then
+// counts itself done; the last one reads the maximum back with an atomic.
+// Only atomics carry data between workgroups, so no cache writeback fence
+// is needed (an agent-scope release per workgroup -- an L2 writeback on
+// this GPU -- cost the 151936-row head ~20 us).  Scratch: the counter at
+// byte 0, the key at byte 8; both are left zero.
+__device__ __forceinline__ unsigned long long lm_argmax_key(float v, uint32_t idx) {
+    if (idx == 0xFFFFFFFFu) return 0ull;
+    if (v != v) return idx == 0 ? ~0ull : 0ull;
+    uint32_t u = __builtin_bit_cast(uint32_t, v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xFFFFFFFFu - idx);
+}
+
+template <int THREADS>
+__device__ __forceinline__ void lm_argmax_finish(const LmDecArgs& p, float best, uint32_t best_i) {
+    static_assert(THREADS % 64 == 0 && THREADS <= 1024, "whole waves");
+    __shared__ unsigned long long wk[THREADS / 64];
+    __shared__ unsigned long long old_s;
+    __shared__ bool last;
+    unsigned long long key = lm_argmax_key(best, best_i);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(key, off, 64);
+        key = o > key ? o : key;
+    }
+    if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = key;
+    __syncthreads();
+    unsigned long long* kp = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(p.counter) + 8);
+    if (threadIdx.x == 0) {
+        unsigned long long m = wk[0];
+        for (int w = 1; w < THREADS / 64; w++) m = wk[w] > m ? wk[w] : m;
+        // returning atomic (its old value is kept), then a wait for it, so
+        // that it is performed before this workgroup counts itself done
+        old_s = atomicMax(kp, m);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last || threadIdx.x != 0) return;
+    const unsigned long long m = atomicMax(kp, 0ull);     // every workgroup's key is in
+    const uint32_t tok = m == 0ull ? 0u : 0xFFFFFFFFu - (uint32_t)m;
+    const uint32_t step = p.st[3];
+    if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
+    p.st[0] = tok;
+    p.st[1] = p.st[1] + 1;
+    p.st[2] = p.st[2] + 1;
+    p.st[3] = step + 1;
+    atomicExch(kp, 0ull);
+    atomicExch(p.counter, 0u);
+}
 
 // LM head + greedy argmax, streamed: each wave owns 64 vocabulary rows (one
 // per lane) and moves them through its own ring of LMS_D slots by LDS DMA
@@ -407,8 +483,6 @@ constexpr int LMS_WAVES = 10, LMS_THREADS = 64 * LMS_WAVES;
 constexpr int LMS_KC = 32;                              // k-values per chunk
 constexpr int LMS_D = 3;                                // ring slots per wave
 constexpr int LMS_SLOT = 64 * LMS_KC * 2;               // 4 KB
-constexpr int LMS_P2 = 1024;                            // power of two >= LMS_THREADS (argmax tree)
-static_assert(LMS_P2 >= LMS_THREADS && LMS_P2 / 2 < LMS_THREADS, "argmax tree");
 constexpr int LMS_NI = LMS_SLOT / 1024;                 // DMA instructions per chunk
 static_assert(LMS_D >= 2 && LMS_D <= 4, "wait counts below");
 
@@ -491,56 +565,7 @@ __global__ void __launch_bounds__(LMS_THREADS) dec_lm_head_stream_kernel(LmDecAr
         best = h2f(logit);
         best_i = (uint32_t)my_row;
     }
-    __shared__ float bv_s[LMS_THREADS];
-    __shared__ uint32_t bi_s[LMS_THREADS];
-    __shared__ bool last;
-    auto reduce = [&]() {
-        for (int w = LMS_P2 / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w && (int)threadIdx.x + w < LMS_THREADS) {
-                const float ov = bv_s[threadIdx.x + w];
-                const uint32_t oi = bi_s[threadIdx.x + w];
-                const float mv = bv_s[threadIdx.x];
-                const uint32_t mi = bi_s[threadIdx.x];
-                const bool take = oi != 0xFFFFFFFFu && (mi == 0xFFFFFFFFu || ov > mv || (ov == mv && oi < mi));
-                if (take) { bv_s[threadIdx.x] = ov; bi_s[threadIdx.x] = oi; }
-            }
-            __syncthreads();
-        }
-    };
-    bv_s[threadIdx.x] = best;
-    bi_s[threadIdx.x] = best_i;
-    __syncthreads();
-    reduce();
-    if (threadIdx.x == 0) {
-        p.part_val[blockIdx.x] = bv_s[0];
-        p.part_idx[blockIdx.x] = bi_s[0];
-        __threadfence();
-        last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    float bv = -__builtin_inff();
-    uint32_t bi = 0xFFFFFFFFu;
-    for (unsigned i = threadIdx.x; i < gridDim.x; i += LMS_THREADS) {
-        const float v = p.part_val[i];
-        const uint32_t ix = p.part_idx[i];
-        if (ix != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && ix < bi))) { bv = v; bi = ix; }
-    }
-    bv_s[threadIdx.x] = bv;
-    bi_s[threadIdx.x] = bi;
-    __syncthreads();
-    reduce();
-    if (threadIdx.x == 0) {
-        const uint32_t tok = bi_s[0] == 0xFFFFFFFFu ? 0u : bi_s[0];
-        const uint32_t step = p.st[3];
-        if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
-        p.st[0] = tok;
-        p.st[1] = p.st[1] + 1;
-        p.st[2] = p.st[2] + 1;
-        p.st[3] = step + 1;
-        *p.counter = 0u;
-    }
+    lm_argmax_finish<LMS_THREADS>(p, best, best_i);
 }
 
 __global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
@@ -603,56 +628,131 @@ __global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
         best = h2f(logit);
         best_i = (uint32_t)my_row;
     }
-    __shared__ float bv_s[LM_THREADS];
-    __shared__ uint32_t bi_s[LM_THREADS];
-    __shared__ bool last;
-    auto reduce = [&]() {
-        for (int w = LM_THREADS / 2; w > 0; w >>= 1) {
-            if ((int)threadIdx.x < w) {
-                const float ov = bv_s[threadIdx.x + w];
-                const uint32_t oi = bi_s[threadIdx.x + w];
-                const float mv = bv_s[threadIdx.x];
-                const uint32_t mi = bi_s[threadIdx.x];
-                const bool take = oi != 0xFFFFFFFFu && (mi == 0xFFFFFFFFu || ov > mv || (ov == mv && oi < mi));
-                if (take) { bv_s[threadIdx.x] = ov; bi_s[threadIdx.x] = oi; }
-            }
-            __syncthreads();
-        }
+    lm_argmax_finish<LM_THREADS>(p, best, best_i);
+}
+
+// LM head over the tiled embedding (cactus_hip_lm_tiles_build), laid out
+// [K/8][N rounded up to 64][8 values]: wave w's 16-byte load of step q
+// (lane = row) reads the 1 KB at (q * Npad + 64 w) * 8 values -- one
+// contiguous read per wave instruction, straight into registers, no LDS
+// staging -- and the waves of a step read one contiguous band, so that the
+// whole grid sweeps memory in order (a row-block-major layout, where the
+// waves stream regions 128 KB apart, measured 87-91 us against 72 us for
+// this head).  Rows are step-major for that reason only.  LMT_D loads per lane in flight (issued before
+// the RMSNorm prologue, which they overlap); the normalized row is read
+// from LDS by broadcast.  Each lane's dot is the reference's 8-lane fp16
+// accumulation in k order (kernel_gemm.cpp:17-126).
+constexpr int LMT_WAVES = 4, LMT_THREADS = 64 * LMT_WAVES, LMT_D = 8;
+
+__global__ void __launch_bounds__(LMT_THREADS) dec_lm_head_tiled_kernel(LmDecArgs p) {
+    __shared__ __align__(16) uint16_t xs[4096 + 16 * RMS_T_PAD];
+    __shared__ __align__(16) uint16_t as[4096];
+    __shared__ float stats[2];
+    const int K = p.K, N = p.N, nq = K / 8;
+    const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
+    const int blk = (int)blockIdx.x * LMT_WAVES + wid;              // this wave's 64-row block
+    const bool live = blk * 64 < N;                                  // wave-uniform
+    // the row and the RMSNorm weights first: the prologue then waits for
+    // them alone, while the first LMT_D steps of weights are in flight
+    const int nch = K / 8;
+    uint4 hv[2], wv[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int c = min((int)threadIdx.x + j * LMT_THREADS, nch - 1);
+        hv[j] = reinterpret_cast<const uint4*>(p.h)[c];
+        wv[j] = reinterpret_cast<const uint4*>(p.norm_w)[c];
+    }
+    const size_t npad = ((size_t)N + 63) / 64 * 64;
+    const i32x4* tp = reinterpret_cast<const i32x4*>(p.b) + (size_t)(live ? blk : 0) * 64 + lane;
+    i32x4 ring[LMT_D];
+#pragma unroll
+    for (int u = 0; u < LMT_D; u++) ring[u] = __builtin_nontemporal_load(tp + (size_t)min(u, nq - 1) * npad);
+
+    // RMSNorm: the row chain-major in LDS when K % 128 == 0 (16 reads per
+    // chain of 64 values), as it is otherwise
+    auto elem = [](const uint4& v, int e) -> uint16_t {
+        const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+        return (uint16_t)(e & 1 ? w >> 16 : w & 0xFFFF);
     };
-    bv_s[threadIdx.x] = best;
-    bi_s[threadIdx.x] = best_i;
-    __syncthreads();
-    reduce();
-    if (threadIdx.x == 0) {
-        p.part_val[blockIdx.x] = bv_s[0];
-        p.part_idx[blockIdx.x] = bi_s[0];
-        __threadfence();
-        last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
+    const bool chain_major = (K & 127) == 0;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int c = (int)threadIdx.x + j * LMT_THREADS;
+        if (c < nch) {
+            if (chain_major) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) xs[rms_t_index(8 * c + e, K)] = elem(hv[j], e);
+            } else {
+                reinterpret_cast<uint4*>(xs)[c] = hv[j];
+            }
+        }
     }
     __syncthreads();
-    if (!last) return;
-    __threadfence();
-    float bv = -__builtin_inff();
-    uint32_t bi = 0xFFFFFFFFu;
-    for (unsigned i = threadIdx.x; i < gridDim.x; i += LM_THREADS) {
-        const float v = p.part_val[i];
-        const uint32_t ix = p.part_idx[i];
-        if (ix != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || v > bv || (v == bv && ix < bi))) { bv = v; bi = ix; }
+    if (wid == 0) {
+        float inv;
+        uint16_t hinv;
+        if (chain_major) rms_stats_wave_t(xs, K, p.eps, inv, hinv);
+        else rms_stats_wave(xs, K, p.eps, inv, hinv);
+        if (lane == 0) { stats[0] = inv; stats[1] = __builtin_bit_cast(float, (uint32_t)hinv); }
     }
-    bv_s[threadIdx.x] = bv;
-    bi_s[threadIdx.x] = bi;
     __syncthreads();
-    reduce();
-    if (threadIdx.x == 0) {
-        const uint32_t tok = bi_s[0] == 0xFFFFFFFFu ? 0u : bi_s[0];
-        const uint32_t step = p.st[3];
-        if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
-        p.st[0] = tok;
-        p.st[1] = p.st[1] + 1;
-        p.st[2] = p.st[2] + 1;
-        p.st[3] = step + 1;
-        *p.counter = 0u;
+    {
+        const float inv = stats[0];
+        const uint16_t hinv = (uint16_t)__builtin_bit_cast(uint32_t, stats[1]);
+        const int end8 = (K / 8) * 8;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int c = (int)threadIdx.x + j * LMT_THREADS;
+            if (c < nch) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) as[8 * c + e] = rms_apply(elem(hv[j], e), elem(wv[j], e), 8 * c + e, end8, inv, hinv);
+            }
+        }
     }
+    __syncthreads();
+
+    h2v acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = (h2v){(f16)0.0f, (f16)0.0f};
+    const uint4* av4 = reinterpret_cast<const uint4*>(as);
+    // whole groups of D steps (branch-free, so the compiler's wait before
+    // each step is for that step's load only), then the remaining steps
+    int q0 = 0;
+    for (; q0 + LMT_D <= nq; q0 += LMT_D) {
+#pragma unroll
+        for (int u = 0; u < LMT_D; u++) {
+            const int q = q0 + u;
+            const uint4 bv = __builtin_bit_cast(uint4, ring[u]);
+            // refill the slot with step q + D (clamped: the last steps re-read step nq - 1)
+            ring[u] = __builtin_nontemporal_load(tp + (size_t)min(q + LMT_D, nq - 1) * npad);
+            f16_step(acc, av4[q], bv);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < LMT_D; u++)
+        if (q0 + u < nq) f16_step(acc, av4[q0 + u], __builtin_bit_cast(uint4, ring[u]));
+    const int my_row = blk * 64 + lane;
+    float best = -__builtin_inff();
+    uint32_t best_i = 0xFFFFFFFFu;
+    if (live && my_row < N) {
+        const uint16_t logit = f16_hsum(acc);   // fp16 bits
+        if (p.logits_out) p.logits_out[my_row] = logit;
+        best = h2f(logit);
+        best_i = (uint32_t)my_row;
+    }
+    lm_argmax_finish<LMT_THREADS>(p, best, best_i);
+}
+
+// tiles[(q * Npad + row) * 8 + e] = embedding[row][8 q + e], 0 past N
+__global__ void lm_tiles_build_kernel(const uint16_t* __restrict__ emb, uint4* __restrict__ tiles, int K, int N,
+                                      size_t total) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;   // one 16-byte piece
+    if (i >= total) return;
+    const size_t npad = ((size_t)N + 63) / 64 * 64;
+    const size_t row = i % npad;
+    const int q = (int)(i / npad);
+    tiles[i] = row < (size_t)N ? *reinterpret_cast<const uint4*>(emb + row * K + 8 * (size_t)q)
+                               : make_uint4(0, 0, 0, 0);
 }
 
 }  // namespace cactus_hip
@@ -784,12 +884,10 @@ int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float e
     CH_REQUIRE(K % 8 == 0 && K <= 4096 && ((uintptr_t)embedding & 15) == 0, "decode_lm_head: bad K");
     const bool streamed = K % LMS_KC == 0;
     const unsigned blocks = streamed ? ceil_div(N, LMS_WAVES * 64) : ceil_div(N, (LM_THREADS / 64) * LM_ROWS_PER_WAVE);
-    CH_REQUIRE(scratch_bytes >= (size_t)blocks * 8 + 256, "decode_lm_head: scratch too small");
+    CH_REQUIRE(scratch_bytes >= 256, "decode_lm_head: scratch too small");
     LmDecArgs p{};
     p.h = h; p.norm_w = norm_w; p.b = embedding; p.eps = eps; p.K = (int)K; p.N = (int)N;
     p.counter = static_cast<uint32_t*>(scratch);
-    p.part_val = reinterpret_cast<float*>(static_cast<char*>(scratch) + 256);
-    p.part_idx = reinterpret_cast<uint32_t*>(p.part_val + blocks);
     p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps; p.logits_out = logits_out;
     if (streamed) {
         const size_t smem = 4 * K + (size_t)LMS_WAVES * LMS_D * LMS_SLOT;
@@ -808,6 +906,40 @@ int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float e
     const size_t smem = 4 * K + (size_t)(LM_THREADS / 64) * LM_ROWS_PER_WAVE * LM_ROW_STRIDE;
     hipLaunchKernelGGL(dec_lm_head_kernel, dim3(blocks), dim3(LM_THREADS), smem, as_stream(stream), p);
     return check_launch("decode_lm_head");
+}
+
+
+int cactus_hip_lm_tiles_bytes(size_t K, size_t N, size_t* bytes) {
+    CH_REQUIRE(bytes && K % 8 == 0 && K > 0 && K <= 4096 && N > 0 && N < (1u << 30), "lm_tiles_bytes: bad shape");
+    *bytes = (N + 63) / 64 * 64 * K * 2;
+    return CACTUS_HIP_OK;
+}
+
+int cactus_hip_lm_tiles_build(const uint16_t* embedding, size_t K, size_t N, uint16_t* tiles, void* stream) {
+    CH_REQUIRE(embedding && tiles, "lm_tiles_build: null pointer");
+    CH_REQUIRE(K % 8 == 0 && K > 0 && K <= 4096 && N > 0 && N < (1u << 30), "lm_tiles_build: bad shape");
+    CH_REQUIRE(((uintptr_t)embedding | (uintptr_t)tiles) % 16 == 0, "lm_tiles_build: pointers must be 16-byte aligned");
+    const size_t total = (N + 63) / 64 * 64 * (K / 8);
+    hipLaunchKernelGGL(lm_tiles_build_kernel, dim3((unsigned)ceil_div(total, (size_t)256)), dim3(256), 0,
+                       as_stream(stream), embedding, reinterpret_cast<uint4*>(tiles), (int)K, (int)N, total);
+    return check_launch("lm_tiles_build");
+}
+
+int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, float eps, const uint16_t* tiles,
+                                    size_t K, size_t N, uint32_t* state, uint32_t* tokens_out, size_t max_steps,
+                                    uint16_t* logits_out, void* scratch, size_t scratch_bytes, void* stream) {
+    CH_REQUIRE(h && norm_w && tiles && state && scratch, "decode_lm_head_tiled: null pointer");
+    CH_REQUIRE(K % 8 == 0 && K > 0 && K <= 4096 && N > 0 && N < (1u << 30), "decode_lm_head_tiled: bad K / N");
+    CH_REQUIRE(((uintptr_t)tiles | (uintptr_t)h | (uintptr_t)norm_w) % 16 == 0,
+               "decode_lm_head_tiled: tiles, h and norm_w must be 16-byte aligned");
+    const unsigned blocks = (unsigned)ceil_div(N, (size_t)LMT_WAVES * 64);
+    CH_REQUIRE(scratch_bytes >= 256, "decode_lm_head_tiled: scratch too small");
+    LmDecArgs p{};
+    p.h = h; p.norm_w = norm_w; p.b = tiles; p.eps = eps; p.K = (int)K; p.N = (int)N;
+    p.counter = static_cast<uint32_t*>(scratch);
+    p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps; p.logits_out = logits_out;
+    hipLaunchKernelGGL(dec_lm_head_tiled_kernel, dim3(blocks), dim3(LMT_THREADS), 0, as_stream(stream), p);
+    return check_launch("decode_lm_head_tiled");
 }
 
 }  // extern "C"

@@ -37,6 +37,13 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     lm_scratch_ = DevBuf(256 + 8 * blocks);
     logits_ = DevBuf((size_t)c.vocab * 2);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
+    // the LM head reads the embedding through its 64-row tiles (a second
+    // copy, built once: the weights do not change after loading)
+    size_t tile_bytes = 0;
+    check_hip(cactus_hip_lm_tiles_bytes(H, c.vocab, &tile_bytes), "lm_tiles_bytes");
+    lm_tiles_ = DevBuf(tile_bytes);
+    check_hip(cactus_hip_lm_tiles_build(m.embedding().as<uint16_t>(), H, c.vocab, lm_tiles_.as<uint16_t>(), m.stream()),
+              "lm_tiles_build");
     // split-K attention workspace (tolerance mode): counters zeroed once
     attn_ws_ = DevBuf(cactus_hip_decode_attention_fast_workspace(c.heads, c.kv_heads, hd, m.cache().slots));
     check_hip(cactus_hip_memset(attn_ws_.ptr, 0, attn_ws_.bytes, m.stream()), "memset");
@@ -143,9 +150,9 @@ void FusedDecoder::enqueue() {
                                                     h, st),
                   "decode_down");
     }
-    check_hip(cactus_hip_decode_lm_head(h, u16(m_.output_norm()), c.eps, u16(m_.embedding()), H, c.vocab, state,
-                                        tokens_.as<uint32_t>(), max_steps_, logits_.as<uint16_t>(), lm_scratch_.ptr,
-                                        lm_scratch_.bytes, st),
+    check_hip(cactus_hip_decode_lm_head_tiled(h, u16(m_.output_norm()), c.eps, lm_tiles_.as<uint16_t>(), H, c.vocab,
+                                              state, tokens_.as<uint32_t>(), max_steps_, logits_.as<uint16_t>(),
+                                              lm_scratch_.ptr, lm_scratch_.bytes, st),
               "decode_lm_head");
 }
 

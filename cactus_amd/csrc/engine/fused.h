@@ -31,6 +31,7 @@ private:
 
     QwenModel& m_;
     DevBuf state_, h_, q_raw_, k_raw_, v_raw_, q_rot_, k_rot_, attn_, mlp_, tokens_, lm_scratch_, logits_, attn_ws_;
+    DevBuf lm_tiles_;   // the tied embedding laid out for the streamed LM head
     size_t max_steps_ = 0;
     size_t rope_pos_ = 0;      // positions the RoPE tables hold
     void* graph_ = nullptr;

@@ -501,11 +501,25 @@ int cactus_hip_decode_prep_attention_fast(const uint16_t* q_raw, const uint16_t*
                                           size_t workspace_bytes, void* stream);
 /* token = argmax(matmul_f16(rms_norm(h), embedding)); writes tokens_out[step]
  * and advances state; logits_out (fp16 [N], or null) receives the logits
- * row.  scratch: >= 256 + 8 * ceil(N/128) bytes, zeroed once. */
+ * row.  scratch: >= 256 bytes, zeroed once (each call leaves it zeroed);
+ * calls sharing a scratch buffer must not overlap. */
 int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float eps,
                               const uint16_t* embedding, size_t K, size_t N, uint32_t* state,
                               uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,
                               void* scratch, size_t scratch_bytes, void* stream);
+/* No reference counterpart: the embedding [N][K] fp16 (the tied LM head)
+ * copied step-major, [K/8][N rounded up to 64][8 values], rows past N zero,
+ * so that one 16-byte load per lane of a wave (lane = row) reads 1 KB
+ * contiguous and the waves of one k-step read one contiguous band.
+ * K % 8 == 0, K <= 4096; pointers 16-byte aligned. */
+int cactus_hip_lm_tiles_bytes(size_t K, size_t N, size_t* bytes);
+int cactus_hip_lm_tiles_build(const uint16_t* embedding, size_t K, size_t N, uint16_t* tiles, void* stream);
+/* cactus_hip_decode_lm_head over the tiles of cactus_hip_lm_tiles_build:
+ * the same tokens, logits and state (h, norm_w and tiles 16-byte aligned). */
+int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, float eps,
+                                    const uint16_t* tiles, size_t K, size_t N, uint32_t* state,
+                                    uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,
+                                    void* scratch, size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -291,14 +291,16 @@ def test_lm_head_argmax_qwen_vocab(dev, orc):
         assert dev.get(tok, np.uint32, 1)[0] == orc.argmax(ref[0])
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("K,N", [(1024, 151936), (256, 1001), (200, 1000)])
-def test_decode_lm_head_state(dev, orc, K, N):
+def test_decode_lm_head_state(dev, orc, K, N, tiled):
     """The decode step's LM head: token = argmax(matmul_f16(rms_norm(h),
     embedding)) written to tokens_out[step], step state advanced.  K % 64 == 0
-    takes the streamed kernel (ragged N), K = 200 the staged one.  The
-    logits row is written on the second step only (logits_out null on the
-    first)."""
-    say("decode_lm_head", K, N)
+    takes the streamed kernel (ragged N), K = 200 the staged one; `tiled`
+    runs the entry over the embedding's step-major tiles (rows past N zero).
+    The logits row is written on the second step only (logits_out null on
+    the first)."""
+    say("decode_lm_head", K, N, "tiled" if tiled else "")
     rng = np.random.default_rng(K + N)
     h = f16(rng.normal(0, 1, (1, K)))
     w = f16(1 + rng.normal(0, 0.05, K))
@@ -314,8 +316,21 @@ def test_decode_lm_head_state(dev, orc, K, N):
     toks = dev.empty(16)
     hp, wp, ep = dev.put(h), dev.put(w), dev.put(emb)
     logits = dev.empty(2 * N)
+    name = "cactus_hip_decode_lm_head"
+    if tiled:
+        nb = ctypes.c_size_t()
+        dev.cm.call("cactus_hip_lm_tiles_bytes", K, N, ctypes.byref(nb))
+        assert nb.value == (N + 63) // 64 * 64 * K * 2
+        tiles = dev.empty(nb.value)
+        dev.cm.call("cactus_hip_lm_tiles_build", ep, K, N, tiles.ptr, None)
+        npad = (N + 63) // 64 * 64
+        t = dev.get(tiles, np.uint16, nb.value // 2).reshape(K // 8, npad, 8)
+        want = np.zeros((npad, K), np.uint16)
+        want[:N] = emb
+        assert (t.transpose(1, 0, 2).reshape(npad, K) == want).all()
+        ep, name = tiles.ptr, "cactus_hip_decode_lm_head_tiled"
     for i in range(2):   # steps 2 and 3; the argmax scratch resets itself
-        dev.cm.call("cactus_hip_decode_lm_head", hp, wp, ctypes.c_float(eps), ep, K, N, state.ptr, toks.ptr, 4,
+        dev.cm.call(name, hp, wp, ctypes.c_float(eps), ep, K, N, state.ptr, toks.ptr, 4,
                     logits.ptr if i else None, scratch.ptr, 256 + 8 * blocks, None)
     out = dev.get(toks, np.uint32, 4)
     assert out[2] == ref_tok and out[3] == ref_tok, (out, ref_tok)
