@@ -212,8 +212,8 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
     const float as = row_scale_from_max(mx);
     const float inv_s = 1.0f / as;
     const int body = (K / 8) * 8;
-    // the 8 codes of a chunk in its own 8 bytes (INT4: the nib_pack8
-    // layout): one 8-byte LDS store per chunk
+    // the 8 codes of a chunk in its own 8 bytes (INT4: its H and L dwords
+    // in the row's two planes, nib_store8)
 #pragma unroll
     for (int j = 0; j < CPT; j++) {
         const int c = tid + j * GEMV_THREADS;
@@ -226,7 +226,8 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
                 if (e < 4) lo |= code << (8 * e);
                 else hi |= code << (8 * (e - 4));
             }
-            *reinterpret_cast<uint2*>(actq + 8 * c) = INT4 ? nib_pack8(lo, hi) : make_uint2(lo, hi);
+            if (INT4) nib_store8(actq, K, c, nib_pack8(lo, hi));
+            else *reinterpret_cast<uint2*>(actq + 8 * c) = make_uint2(lo, hi);
         }
     }
     __syncthreads();
@@ -237,7 +238,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
 #pragma unroll
     for (int i = 0; i < CH; i++) {
         const bool valid = crow[i] < vrows && vrow_valid(crow[i]);
-        int dot = valid ? chunk_dot<INT4>(actq, ccol[i], wreg[i]) : 0;
+        int dot = valid ? chunk_dot<INT4>(actq, ccol[i], wreg[i], K / 2) : 0;
         dot = group_lane_sum(dot, P);
         if (valid && ((tid + i * GEMV_THREADS) & (P - 1)) == 0)
             accf[crow[i] * AP + (ccol[i] * (INT4 ? 32 : 16)) / gs] = (float)dot;   // the epilogue's conversion

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
                     for (int e = 0; e < 8; e++)
                         w2[e >> 2] |= (uint32_t)(uint8_t)quant_code(h2f(x[8 * r + e]), inv, 8 * r + e >= body)
                                       << (8 * (e & 3));
-                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                    nib_store8(actq + m * K, K, r, nib_pack8(w2[0], w2[1]));
                 }
             } else {
                 for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = quant_code(h2f(x[i]), inv, i >= body);
@@ -163,7 +163,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
                     uint32_t w2[2] = {0, 0};   // byte loads: the codes carry no alignment promise
 #pragma unroll
                     for (int e = 0; e < 8; e++) w2[e >> 2] |= (uint32_t)(uint8_t)x[8 * r + e] << (8 * (e & 3));
-                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                    nib_store8(actq + m * K, K, r, nib_pack8(w2[0], w2[1]));
                 }
             } else {
                 for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = x[i];
@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_grouped_kernel(GemvArgs a, 
             int dot[MR];
 #pragma unroll
             for (int m = 0; m < MR; m++) {
-                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], wcur[i]) : 0;
+                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], wcur[i], K / 2) : 0;
                 dot[m] = group_lane_sum(dot[m], P);
             }
             if (valid && ((tid + i * GEMV_THREADS) & (P - 1)) == 0) {
@@ -328,7 +328,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
                     for (int e = 0; e < 8; e++)
                         w2[e >> 2] |= (uint32_t)(uint8_t)quant_code(h2f(x[8 * r + e]), inv, 8 * r + e >= body)
                                       << (8 * (e & 3));
-                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                    nib_store8(actq + m * K, K, r, nib_pack8(w2[0], w2[1]));
                 }
             } else {
                 for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = quant_code(h2f(x[i]), inv, i >= body);
@@ -341,7 +341,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
                     uint32_t w2[2] = {0, 0};   // byte loads: the codes carry no alignment promise
 #pragma unroll
                     for (int e = 0; e < 8; e++) w2[e >> 2] |= (uint32_t)(uint8_t)x[8 * r + e] << (8 * (e & 3));
-                    *reinterpret_cast<uint2*>(actq + m * K + 8 * r) = nib_pack8(w2[0], w2[1]);
+                    nib_store8(actq + m * K, K, r, nib_pack8(w2[0], w2[1]));
                 }
             } else {
                 for (int i = tid; i < K; i += GEMV_THREADS) actq[m * K + i] = x[i];
@@ -373,7 +373,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             int dot[MR];
 #pragma unroll
             for (int m = 0; m < MR; m++) {
-                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], w[i]) : 0;
+                dot[m] = (valid && m < mr) ? chunk_dot<INT4>(actq + m * K, ccol[i], w[i], K / 2) : 0;
                 dot[m] = group_lane_sum(dot[m], P);
             }
             if (valid && (lane & (P - 1)) == 0) {
@@ -509,12 +509,16 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
     const bool fe = INT4 && a.gs == 32;
     if (pick_wave_tile(cpr, a.N, batch, &wch, &wrows) &&
         gemv_wave_smem(MR, a.K, wrows, G, fe) <= 60 * 1024) {
-        // wave tiles per workgroup: 4 (one per wave) up to 4*8, aiming at
-        // about three resident rounds of 2048 workgroups
+        // wave tiles per workgroup: 4 (one per wave) up to 4 * cap.  Every
+        // workgroup quantizes the activation row once, so INT4 rows (the
+        // K = 3072 MLP down shape) take more tiles per workgroup: swept on
+        // MI355X over 604 / 768 rotated weight sets, INT4 K=3072 streams at
+        // 0.706-0.710 of HBM with 8 per wave (0.68-0.69 with 6, 0.69-0.70
+        // with 12 or 16) and INT8 K=640 at 6.85 TB/s with 3-4 (6.72 with 8)
         const size_t nt = ceil_div(a.N, (size_t)wrows);
-        size_t per = nt * batch / (4 * 2048 * 3);
+        size_t per = nt * batch / (4 * 2048 * (INT4 ? 2 : 3));
         if (per < 1) per = 1;
-        if (per > 8) per = 8;
+        if (per > (INT4 ? 8u : 4u)) per = INT4 ? 8 : 4;
         size_t nb = ceil_div(nt, 4 * per);
         a.rows = wrows;
         a.tiles = (int)ceil_div(nt, nb);  // balanced: every workgroup but the last full
