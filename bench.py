@@ -261,6 +261,22 @@ def bench_attention():
     return out
 
 
+def exact_ceiling_us(M: int, K: int, N: int, gs: int) -> float:
+    """Lower bound on a grouped matmul that keeps the reference's exact
+    epilogue (kernel_gemm.cpp:311-324): per output and group one int32 ->
+    fp32 convert and one fp32 FMA (the fp16 scale enters a mixed-precision
+    FMA unconverted), i.e. 2 M N K/gs VALU lane operations; a wave64 VALU
+    instruction occupies a SIMD for 4 cycles, so on MI355X's 1024 SIMDs at
+    2.4 GHz they take 2 M N (K/gs) / 64 * 4 / 1024 / 2.4e9 s.  The integer
+    group sums (2 M N K ops on MFMA at the 5.0 POP/s dense INT8 peak) and the
+    operand traffic (A, B and C once at 8 TB/s) run beside it on other units;
+    the bound is the largest of the three."""
+    valu = 2.0 * M * N * (K // gs) / 64 * 4 / 1024 / 2.4e9
+    mfma = 2.0 * M * N * K / (INT8_MFMA_PEAK_TOPS * 1e12)
+    hbm = (M * K * 2 + N * K + 2 * N * (K // gs) + 2 * M * N) / (HBM_PEAK_GBS * 1e9)
+    return max(valu, mfma, hbm) * 1e6
+
+
 def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: int = 50, rounds: int = 5,
                eager: bool = False):
     """One grouped matmul (the reference's compute_matmul_node: FP16
@@ -268,6 +284,7 @@ def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: 
     matmul alone on pre-quantized activations), timed as a HIP graph of
     `reps` launches replayed `rounds` times, so host call overhead stays
     out of the per-call time."""
+    ceiling = exact_ceiling_us(M, K, N, gs)
     import cactus_amd as cm
     from _data import f16
     rng = np.random.default_rng(M + K + N)
@@ -303,7 +320,9 @@ def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: 
         us = e0.elapsed_ms(e1) * 1e3 / (reps * rounds)
         tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
         return {"us_per_call": round(us, 2), "tops": round(tops, 1),
-                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4), "timing": "direct launches"}
+                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                "exact_ceiling_us": round(ceiling, 3), "frac_of_exact_ceiling": round(ceiling / us, 4),
+                "timing": "direct launches"}
     def graph_us(branches):
         """us per call of a graph holding len(branches) chains of `reps`
         calls, chain i on stream branches[i][0] (forked from and joined
@@ -337,7 +356,8 @@ def bench_gemm(M: int, K: int, N: int, gs: int, int4: bool, f16act: bool, reps: 
     def rate(us):
         tops = 2.0 * M * K * N / (us * 1e-6) / 1e12
         return {"us_per_call": round(us, 2), "tops": round(tops, 1),
-                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+                "frac_int8_mfma_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                "exact_ceiling_us": round(ceiling, 3), "frac_of_exact_ceiling": round(ceiling / us, 4)}
 
     out = rate(graph_us([(st, fn)]))
     # three independent calls in flight, one per stream (each with its own
