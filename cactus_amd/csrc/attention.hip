@@ -256,6 +256,8 @@ __device__ __forceinline__ void sq_group16(float (&acc)[NQ][8], const float (&qv
 // prefill form is NQ = 8, NW = 4; the decode form (one query row) is
 // NQ = gq, NW = 1 with the lane's whole INT8 key row loaded before the
 // query, so the two memory round trips overlap.
+constexpr size_t SC_PF_KEYS = CS_PF_FROM * ATT_BLOCK;   // keys whose product tiles the scores prefetch
+
 template <bool HYBRID, int D, int NQ, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in) {
     constexpr bool PRE = NQ <= 2;                      // key row preloaded
@@ -329,29 +331,31 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         }
     };
     // decode form with value product tiles: the chain kernel that follows
-    // reads this chunk's tiles from the L2 of this XCD (its workgroups of kv
-    // head h run on XCD h % 8, as these do), so the chunk's 64 keys x D
-    // dims of products are read here, one dword per 128-byte line, and held
-    // until the end (the registers stay live until their wait)
-    uint32_t pfr[4] = {0u, 0u, 0u, 0u};
-    bool pf_on = false;
+    // reads the tiles from the L2 of this XCD (its workgroups of kv head h
+    // run on XCD h % 8, as these do).  The chunks of the first SC_PF_KEYS
+    // keys read their 64 keys x D dims of products here, one dword per
+    // 128-byte line, consumed by an empty asm at the end; the chain
+    // kernel's helper wave fetches the rest while the chains start.  (All
+    // of them here put 16 MB per layer in front of the key rows this kernel
+    // waits for.)  They are ordinary loads so that the compiler counts them:
+    // its waits for the query and key rows then leave them in flight
+    float pfr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     auto prefetch_tiles = [&]() {
         if constexpr (HYBRID && PRE && NW == 1) {
-            if (a.vsh && wbase < a.cache_len) {
-                pf_on = true;
+            if (a.vsh && wbase < SC_PF_KEYS) {
                 constexpr int NSL = D / 64;
+                const size_t k0 = wbase < a.cache_len ? wbase : 0;
 #pragma unroll
                 for (int sl = 0; sl < NSL && sl < 2; sl++) {
-                    const float* t = a.vsh + sh_index(kvh, NSL, sl, a.sh_ntile, wbase, 0);
-                    asm volatile("global_load_dword %0, %1, off" : "=&v"(pfr[2 * sl]) : "v"(t + lane * 32));
-                    asm volatile("global_load_dword %0, %1, off" : "=&v"(pfr[2 * sl + 1]) : "v"(t + (lane + 64) * 32));
+                    const float* t = a.vsh + sh_index(kvh, NSL, sl, a.sh_ntile, k0, 0);
+                    pfr[2 * sl] = t[lane * 32];
+                    pfr[2 * sl + 1] = t[(lane + 64) * 32];
                 }
             }
         }
     };
     auto prefetch_drain = [&]() {
-        if (pf_on)
-            asm volatile("s_waitcnt vmcnt(0)" : "+v"(pfr[0]), "+v"(pfr[1]), "+v"(pfr[2]), "+v"(pfr[3]));
+        asm volatile("" ::"v"(pfr[0]), "v"(pfr[1]), "v"(pfr[2]), "v"(pfr[3]));
     };
     // decode form with the head preparation fused in (one wave, one row):
     // q of the group's heads and, in the chunk holding it, the new key row
@@ -393,14 +397,11 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
 #pragma unroll
                 for (int e = 0; e < EPL; e++) prow[r][lane + 64 * e] = raw[r][e];
             wave_lds_order();
+            // the NQ + 1 rows' statistics at once, one 16-lane row each (a
+            // row that is not prepared gets values that are never used)
             float inv[NQ + 1];
             uint16_t hinv[NQ + 1];
-#pragma unroll
-            for (int r = 0; r <= NQ; r++) {
-                inv[r] = 0.0f;
-                hinv[r] = 0;
-                if ((r < nq) || (r == NQ && has_k)) rms_stats_wave(prow[r], d, a.prep.eps, inv[r], hinv[r]);
-            }
+            rms_stats_rows<D, NQ + 1>(&prow[0][0], D, a.prep.eps, inv, hinv);
 #pragma unroll
             for (int r = 0; r <= NQ; r++)
 #pragma unroll

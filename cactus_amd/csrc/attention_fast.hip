@@ -271,9 +271,11 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
 #pragma unroll
             for (int j = 0; j < EPL; j++) xs[lane + 64 * j] = xr[j];
             wave_lds_sync();
-            float inv;
-            uint16_t hinv;
-            rms_stats_wave(xs, D, a.eps, inv, hinv);
+            float inv1[1];
+            uint16_t hinv1[1];
+            rms_stats_rows<D, 1>(xs, D, a.eps, inv1, hinv1);
+            const float inv = inv1[0];
+            const uint16_t hinv = hinv1[0];
             uint16_t yv[EPL];
 #pragma unroll
             for (int j = 0; j < EPL; j++) yv[j] = rms_apply(xr[j], nr[j], lane + 64 * j, end8, inv, hinv);

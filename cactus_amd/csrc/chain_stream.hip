@@ -86,8 +86,36 @@ __device__ __forceinline__ CsMap cs_map(const AttnArgs& a, int nsl) {
     m.valid = m.kvh < a.Hkv;
     return m;
 }
-static unsigned cs_grid(int S, int Hkv, int gq, int nsl) {
+__host__ __device__ inline unsigned cs_grid(int S, int Hkv, int gq, int nsl) {
     return 8u * (unsigned)((Hkv + 7) / 8) * (unsigned)S * (unsigned)gq * (unsigned)nsl;
+}
+// Workgroups after the chain workgroups fetch the product tiles of blocks
+// CS_PF_FROM.. into the L2 of the chains' XCD while the chains start (the
+// score kernel fetched the first ones): the chains' own few CUs cannot do
+// it, each CU's outstanding misses cap its fetch rate near 50 GB/s and
+// would delay the chains' loads.  CS_PF_WGS per XCD, each on a CU of its
+// own beside the chains.
+constexpr int CS_PF_WGS = 16;
+__device__ void chain_tile_prefetch(const AttnArgs& a, int j, int nj, int nsl) {
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int x = j & 7;                                     // this workgroup's XCD = kv heads x, x + 8, ...
+    const int k = j >> 3, K = nj >> 3;
+    const int nkx = x < a.Hkv ? (a.Hkv - x + 7) / 8 : 0;
+    const int per = nkx * nsl;                               // tile slices of this XCD
+    const int nbc = (int)((a.cache_len + ATT_BLOCK - 1) / ATT_BLOCK);
+    const int total = nbc > CS_PF_FROM ? (nbc - CS_PF_FROM) * per : 0;
+    const unsigned off = (unsigned)lane * 128u;             // one dword per 128-byte line
+    int sink = 0;
+    // lowest blocks first; one 8 KB block slice per wave load, at most 32
+    // in flight; the register stays live until the last has landed
+    for (int it = __builtin_amdgcn_readfirstlane(2 * k + wv); it < total; it += 2 * K) {
+        const int b = CS_PF_FROM + it / per, r = it % per;
+        const char* p = reinterpret_cast<const char*>(
+            a.vsh + sh_index(x + 8 * (r / nsl), nsl, r % nsl, a.sh_ntile, (size_t)b * ATT_BLOCK, 0));
+        asm volatile("s_waitcnt vmcnt(31)\n\tglobal_load_dword %0, %1, %2" : "+v"(sink) : "v"(off), "s"(p));
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(sink));
 }
 
 // wts: the weights a_in.w (rows of wstride floats, padded by one block)
@@ -104,6 +132,11 @@ __global__ void __launch_bounds__(CS_THREADS) attn_chain_stream_kernel(AttnArgs 
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int d = a.d, da = (d / 8) * 8, nsl = (d + 63) / 64;
+    const unsigned nchain = cs_grid(a.S, a.Hkv, a.gq, nsl);
+    if (blockIdx.x >= nchain) {                              // whole workgroup, before any barrier
+        chain_tile_prefetch(a, (int)(blockIdx.x - nchain), (int)(gridDim.x - nchain), nsl);
+        return;
+    }
     const CsMap m = cs_map(a, nsl);
     if (!m.valid) return;                                    // whole workgroup, before any barrier
     const int qp = m.row;
@@ -346,7 +379,8 @@ int launch_chain_stream(const AttnArgs& a, int nbmax, void* stream) {
     const int nsl = (a.d + 63) / 64;
     const int nch = (nbmax + 63) / 64;
     const size_t smem = 2 * (size_t)nch * 64 * sizeof(float) + (size_t)nch * sizeof(uint64_t) + 16;
-    hipLaunchKernelGGL(attn_chain_stream_kernel, dim3(cs_grid(a.S, a.Hkv, a.gq, nsl)), dim3(CS_THREADS), smem,
+    const unsigned npf = a.cache_len > (size_t)CS_PF_FROM * ATT_BLOCK ? 8u * CS_PF_WGS : 0u;
+    hipLaunchKernelGGL(attn_chain_stream_kernel, dim3(cs_grid(a.S, a.Hkv, a.gq, nsl) + npf), dim3(CS_THREADS), smem,
                        as_stream(stream), a, nbmax, (const float*)a.w);
     return check_launch("attention values (decode)");
 }

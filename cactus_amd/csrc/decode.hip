@@ -432,7 +432,6 @@ template <int THREADS>
 __device__ __forceinline__ void lm_argmax_finish(const LmDecArgs& p, float best, uint32_t best_i) {
     static_assert(THREADS % 64 == 0 && THREADS <= 1024, "whole waves");
     __shared__ unsigned long long wk[THREADS / 64];
-    __shared__ unsigned long long old_s;
     __shared__ bool last;
     unsigned long long key = lm_argmax_key(best, best_i);
 #pragma unroll
@@ -446,10 +445,11 @@ __device__ __forceinline__ void lm_argmax_finish(const LmDecArgs& p, float best,
     if (threadIdx.x == 0) {
         unsigned long long m = wk[0];
         for (int w = 1; w < THREADS / 64; w++) m = wk[w] > m ? wk[w] : m;
-        // returning atomic (its old value is kept), then a wait for it, so
-        // that it is performed before this workgroup counts itself done
-        old_s = atomicMax(kp, m);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // returning atomic, then a wait that takes its result as an input:
+        // the atomic has been performed before this workgroup counts
+        // itself done
+        const unsigned long long old = atomicMax(kp, m);
+        asm volatile("s_waitcnt vmcnt(0)" ::"v"((uint32_t)old), "v"((uint32_t)(old >> 32)) : "memory");
         last = atomicAdd(p.counter, 1u) == gridDim.x - 1;
     }
     __syncthreads();

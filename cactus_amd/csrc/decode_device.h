@@ -58,6 +58,35 @@ __device__ __forceinline__ void rms_stats_wave(const uint16_t* xs, int n, float 
     hinv = f2h(inv);
 }
 
+// rms_stats_wave for R <= 4 rows of N values each (N % 16 == 0, a head
+// row), all at once: 16-lane row r of the wave runs row r's 16 chains, each
+// lane's N/16 reads issued before its FMAs, and the per-row combination by
+// the same DPP moves within that 16-lane row.  Row r starts at xs + r *
+// stride; every lane returns every row's inv and fp16(inv).
+template <int N, int R>
+__device__ __forceinline__ void rms_stats_rows(const uint16_t* xs, int stride, float eps, float (&inv)[R],
+                                               uint16_t (&hinv)[R]) {
+    static_assert(N % 16 == 0 && R >= 1 && R <= 4, "head rows");
+    const int lane = threadIdx.x & 63;
+    const int rr = lane >> 4, l = lane & 15;
+    const uint16_t* x = xs + min(rr, R - 1) * stride;
+    float v[N / 16];
+#pragma unroll
+    for (int i = 0; i < N / 16; i++) v[i] = h2f(x[i * 16 + l]);
+    float chain = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N / 16; i++) chain = __builtin_fmaf(v[i], v[i], chain);
+    const float t = rms_chain_combine4(chain);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float ss = (lane_value(t, 16 * r) + lane_value(t, 16 * r + 1)) +
+                         (lane_value(t, 16 * r + 2) + lane_value(t, 16 * r + 3));
+        const float rms = __builtin_sqrtf(ss / (float)N + eps);
+        inv[r] = 1.0f / rms;
+        hinv[r] = f2h(inv[r]);
+    }
+}
+
 // rms_stats_wave over a row stored chain-major in LDS: chain l's values
 // x[16 i + l] at xt[l * (n / 16 + 8) + i] (8 elements of padding per chain
 // keep the 16 chains' 16-byte reads on distinct banks).  n % 128 == 0.  Each
