@@ -256,8 +256,6 @@ __device__ __forceinline__ void sq_group16(float (&acc)[NQ][8], const float (&qv
 // prefill form is NQ = 8, NW = 4; the decode form (one query row) is
 // NQ = gq, NW = 1 with the lane's whole INT8 key row loaded before the
 // query, so the two memory round trips overlap.
-constexpr size_t SC_PF_KEYS = CS_PF_FROM * ATT_BLOCK;   // keys whose product tiles the scores prefetch
-
 template <bool HYBRID, int D, int NQ, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in) {
     constexpr bool PRE = NQ <= 2;                      // key row preloaded
@@ -330,33 +328,6 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             pres = ssrc[0];
         }
     };
-    // decode form with value product tiles: the chain kernel that follows
-    // reads the tiles from the L2 of this XCD (its workgroups of kv head h
-    // run on XCD h % 8, as these do).  The chunks of the first SC_PF_KEYS
-    // keys read their 64 keys x D dims of products here, one dword per
-    // 128-byte line, consumed by an empty asm at the end; the chain
-    // kernel's helper wave fetches the rest while the chains start.  (All
-    // of them here put 16 MB per layer in front of the key rows this kernel
-    // waits for.)  They are ordinary loads so that the compiler counts them:
-    // its waits for the query and key rows then leave them in flight
-    float pfr[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto prefetch_tiles = [&]() {
-        if constexpr (HYBRID && PRE && NW == 1) {
-            if (a.vsh && wbase < SC_PF_KEYS) {
-                constexpr int NSL = D / 64;
-                const size_t k0 = wbase < a.cache_len ? wbase : 0;
-#pragma unroll
-                for (int sl = 0; sl < NSL && sl < 2; sl++) {
-                    const float* t = a.vsh + sh_index(kvh, NSL, sl, a.sh_ntile, k0, 0);
-                    pfr[2 * sl] = t[lane * 32];
-                    pfr[2 * sl + 1] = t[(lane + 64) * 32];
-                }
-            }
-        }
-    };
-    auto prefetch_drain = [&]() {
-        asm volatile("" ::"v"(pfr[0]), "v"(pfr[1]), "v"(pfr[2]), "v"(pfr[3]));
-    };
     // decode form with the head preparation fused in (one wave, one row):
     // q of the group's heads and, in the chunk holding it, the new key row
     // get the reference's head RMSNorm and RoPE here (the step's attn_prep
@@ -390,7 +361,6 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             const uint16_t cv = lane < half ? a.prep.cos_t[trow + lane] : (uint16_t)0;
             const uint16_t sv = lane < half ? a.prep.sin_t[trow + lane] : (uint16_t)0;
             preload();   // (the appender too: no branch around loads)
-            if (!appender) prefetch_tiles();
             // rows r < nq: q heads h0 + r; row NQ: the new key
 #pragma unroll
             for (int r = 0; r <= NQ; r++)
@@ -451,7 +421,6 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     }
     if (!(PRE && NW == 1) || !a.prep.q_raw) {
         preload();
-        prefetch_tiles();
         for (int i = threadIdx.x; i < NQ * D; i += 64 * NW) {
             const int v = i / D, dim = i % D;
             const int qp = qp0 + v / gq;
@@ -459,10 +428,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         }
     }
     __syncthreads();
-    if (wbase >= kv_end_max) {                         // wave-uniform; no barrier follows
-        prefetch_drain();
-        return;
-    }
+    if (wbase >= kv_end_max) return;                   // wave-uniform; no barrier follows
 
     // ---- dot products of this lane's key with every query vector
     float acc[NQ][8];
@@ -627,7 +593,6 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             }
         }
     }
-    prefetch_drain();
 }
 
 // ----------------------------------------------------------------- kernel B

@@ -9,10 +9,6 @@ namespace cactus_hip {
 constexpr int ATT_BLOCK = 32;
 constexpr int ATT_MAX_D = 256;
 constexpr int ATT_MAX_GQ = 8;      // query heads per KV head
-// decode value chains: the score kernel prefetches the product tiles of
-// blocks [0, CS_PF_FROM) into the chains' L2, the chain kernel's helper wave
-// the rest
-constexpr int CS_PF_FROM = 16;
 
 struct AttnArgs {
     const uint16_t* q;

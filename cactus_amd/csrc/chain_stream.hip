@@ -22,10 +22,11 @@ namespace cactus_hip {
 // rescale factor by one v_readlane.  Wave 1 turns the row's block maxima
 // into the rescale factors, the per-block fast-path mask and the running sum
 // (the reference's sequential order) while wave 0 chains.  The tiles and
-// weights stream from this XCD's L2: the score kernel before this one puts
-// kv head h's workgroups on XCD h % 8, as this kernel does, and reads the
-// head's product tiles there (an L2 hit costs the chain ~7 cycles per key,
-// an Infinity Cache hit ~16, HBM ~25).
+// weights stream from this XCD's L2: kv head h's chain workgroups run on
+// XCD h % 8, where the score kernel before this one wrote the head's
+// weights and this kernel's prefetch workgroups fetch its product tiles
+// ahead of the chains (an L2 hit costs the chain ~7 cycles per key, an
+// Infinity Cache hit ~16, HBM ~25).
 constexpr int CS_R = 3;          // ring depth in 32-key blocks (CS_R - 1 blocks ahead)
 constexpr int CS_P = CS_R;       // blocks per unrolled step: the ring's period
 // s_waitcnt immediate (gfx9 encoding): vmcnt VM (6 bits, split), expcnt
@@ -89,13 +90,14 @@ __device__ __forceinline__ CsMap cs_map(const AttnArgs& a, int nsl) {
 __host__ __device__ inline unsigned cs_grid(int S, int Hkv, int gq, int nsl) {
     return 8u * (unsigned)((Hkv + 7) / 8) * (unsigned)S * (unsigned)gq * (unsigned)nsl;
 }
-// Workgroups after the chain workgroups fetch the product tiles of blocks
-// CS_PF_FROM.. into the L2 of the chains' XCD while the chains start (the
-// score kernel fetched the first ones): the chains' own few CUs cannot do
-// it, each CU's outstanding misses cap its fetch rate near 50 GB/s and
-// would delay the chains' loads.  CS_PF_WGS per XCD, each on a CU of its
-// own beside the chains.
-constexpr int CS_PF_WGS = 16;
+// Workgroups after the chain workgroups fetch the cached keys' product
+// tiles into the L2 of the chains' XCD, lowest blocks first, while the
+// chains start.  The chains' own few CUs cannot do it: each CU's
+// outstanding misses cap its fetch rate near 50 GB/s, and the fetch would
+// queue ahead of the chains' loads.  CS_PF_WGS per XCD, on CUs beside the
+// chains (8 per XCD fetch the 16 MB of a 4096-key layer ~3x faster than
+// the chains consume it).
+constexpr int CS_PF_WGS = 8;
 __device__ void chain_tile_prefetch(const AttnArgs& a, int j, int nj, int nsl) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -104,13 +106,13 @@ __device__ void chain_tile_prefetch(const AttnArgs& a, int j, int nj, int nsl) {
     const int nkx = x < a.Hkv ? (a.Hkv - x + 7) / 8 : 0;
     const int per = nkx * nsl;                               // tile slices of this XCD
     const int nbc = (int)((a.cache_len + ATT_BLOCK - 1) / ATT_BLOCK);
-    const int total = nbc > CS_PF_FROM ? (nbc - CS_PF_FROM) * per : 0;
+    const int total = nbc * per;
     const unsigned off = (unsigned)lane * 128u;             // one dword per 128-byte line
     int sink = 0;
     // lowest blocks first; one 8 KB block slice per wave load, at most 32
     // in flight; the register stays live until the last has landed
     for (int it = __builtin_amdgcn_readfirstlane(2 * k + wv); it < total; it += 2 * K) {
-        const int b = CS_PF_FROM + it / per, r = it % per;
+        const int b = it / per, r = it % per;
         const char* p = reinterpret_cast<const char*>(
             a.vsh + sh_index(x + 8 * (r / nsl), nsl, r % nsl, a.sh_ntile, (size_t)b * ATT_BLOCK, 0));
         asm volatile("s_waitcnt vmcnt(31)\n\tglobal_load_dword %0, %1, %2" : "+v"(sink) : "v"(off), "s"(p));
@@ -379,7 +381,7 @@ int launch_chain_stream(const AttnArgs& a, int nbmax, void* stream) {
     const int nsl = (a.d + 63) / 64;
     const int nch = (nbmax + 63) / 64;
     const size_t smem = 2 * (size_t)nch * 64 * sizeof(float) + (size_t)nch * sizeof(uint64_t) + 16;
-    const unsigned npf = a.cache_len > (size_t)CS_PF_FROM * ATT_BLOCK ? 8u * CS_PF_WGS : 0u;
+    const unsigned npf = a.cache_len > 0 ? 8u * CS_PF_WGS : 0u;
     hipLaunchKernelGGL(attn_chain_stream_kernel, dim3(cs_grid(a.S, a.Hkv, a.gq, nsl) + npf), dim3(CS_THREADS), smem,
                        as_stream(stream), a, nbmax, (const float*)a.w);
     return check_launch("attention values (decode)");
