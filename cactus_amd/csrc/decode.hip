@@ -639,11 +639,14 @@ __global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
 // staging -- and the waves of a step read one contiguous band, so that the
 // whole grid sweeps memory in order (a row-block-major layout, where the
 // waves stream regions 128 KB apart, measured 87-91 us against 72 us for
-// this head).  Rows are step-major for that reason only.  LMT_D loads per lane in flight (issued before
-// the RMSNorm prologue, which they overlap); the normalized row is read
-// from LDS by broadcast.  Each lane's dot is the reference's 8-lane fp16
-// accumulation in k order (kernel_gemm.cpp:17-126).
-constexpr int LMT_WAVES = 4, LMT_THREADS = 64 * LMT_WAVES, LMT_D = 8;
+// this head).  Rows are step-major for that reason only.  LMT_D loads per
+// lane in flight (issued before the RMSNorm prologue, which they overlap);
+// the normalized row is read from LDS by broadcast.  Each lane's dot is the
+// reference's 8-lane fp16 accumulation in k order (kernel_gemm.cpp:17-126).
+// Measured in the decode step (151936 x 1024 head, 594 workgroups): 62.2 us
+// with 8 loads in flight, 57.3-58.6 with 12, 58-59 with 14 or 16; 8 waves
+// per workgroup 65.0, 2 waves 67.5.
+constexpr int LMT_WAVES = 4, LMT_THREADS = 64 * LMT_WAVES, LMT_D = 12;
 
 __global__ void __launch_bounds__(LMT_THREADS) dec_lm_head_tiled_kernel(LmDecArgs p) {
     __shared__ __align__(16) uint16_t xs[4096 + 16 * RMS_T_PAD];
