@@ -103,17 +103,20 @@ def test_qwen3_full_shape_generate_fused(full):
 
 
 def test_qwen3_full_shape_tolerance_mode(full):
-    """Tolerance-mode attention (split-K decode attention, within 1e-3 +
-    1e-2 |ref| of the reference per fp16 output, tested kernel by kernel in
-    test_gpu_attention_fast.py) at model level.  The exact mode is first
-    checked against the fixture; then the tolerance mode is run teacher-forced
-    on the fixture's tokens and its logits compared step by step with the
-    exact mode's.  This random 28-layer model amplifies single-ulp attention
-    differences (measured: the first two steps bit-identical, later steps
-    2-13% relative L2 on the logits), so the bar is a loose relative L2 of
-    0.25 per step (garbage attention lands near 1) and the argmax agreeing on
-    at least half of the steps; the free-running token prefix that matches
-    the oracle is printed, not required."""
+    """Tolerance-mode attention (split-K decode attention and the MFMA
+    prefill attention, each within 1e-3 + 1e-2 |ref| of the reference per
+    fp16 output, tested kernel by kernel in test_gpu_attention_fast.py) at
+    model level.  The exact mode is first checked against the fixture; then
+    the tolerance mode is prefilled and run teacher-forced on the fixture's
+    tokens, and its logits compared step by step with the exact mode's.  This
+    random 28-layer model amplifies single-ulp attention differences.  Both
+    runs are deterministic; measured on MI355X: relative L2 of the logits
+    0.090-0.167 per step (mean 0.117; already 0.126 at step 0, from the
+    prefill) and the argmax equal on 89 of 128 steps.  The bounds sit ~20%
+    above the measured errors (every step <= 0.20, the mean <= 0.14) and ~10%
+    below the measured agreement (at least 80 of 128 argmax equal); garbage
+    attention lands near 1 and agrees on almost no step.  The free-running token prefix that matches the oracle
+    is printed, not required: it is 3 steps."""
     m, fx, cfg, prompt = full
     toks = fx["tokens"]
     say("qwen3-0.6b full shape, exact vs tolerance attention")
@@ -149,5 +152,7 @@ def test_qwen3_full_shape_tolerance_mode(full):
     prefix = int(np.argmax(free != toks)) if (free != toks).any() else len(toks)
     print(f"[tolerance mode] max relative L2 of logits {max(rel):.4f}, argmax agreement {agree}/{len(toks)}, "
           f"free-running tokens equal to the oracle's for the first {prefix} steps", flush=True)
-    assert max(rel) <= 0.25, rel
-    assert agree >= len(toks) // 2, agree
+    print(f"[tolerance mode] mean relative L2 {float(np.mean(rel)):.4f}", flush=True)
+    assert max(rel) <= 0.20, rel
+    assert float(np.mean(rel)) <= 0.14, rel
+    assert agree * 128 >= 80 * len(toks), agree
