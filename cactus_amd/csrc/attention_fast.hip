@@ -381,7 +381,10 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
         }
     }
 
-    // ---- 4. workgroup max and weights
+    // ---- 4. weights relative to this wave's max: no barrier, so a wave
+    // whose keys arrived goes on to its values while others still wait.
+    // The workgroup max M and each wave's factor e^(m_w - M) enter once, in
+    // the sum of the waves' rows below.
     constexpr float LOG2E = 1.4426950408889634f;
     float wm[GQ];
 #pragma unroll
@@ -392,33 +395,25 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
         wm[h] = wave_max_u(m);
         if (lane == 0) redm[h][wid] = wm[h];
     }
-    __syncthreads();
-    float M[GQ];
-#pragma unroll
-    for (int h = 0; h < GQ; h++) {
-        M[h] = redm[h][0];
-#pragma unroll
-        for (int w = 1; w < FA_WAVES; w++) M[h] = __builtin_fmaxf(M[h], redm[h][w]);
-    }
     float p[NI][GQ];
     if (HYBRID) {
 #pragma unroll
         for (int i = 0; i < NI; i++)
 #pragma unroll
             for (int h = 0; h < GQ; h++)
-                p[i][h] = sc[i][h] > -__builtin_inff() ? fast_exp2((sc[i][h] - M[h]) * LOG2E) : 0.0f;
+                p[i][h] = sc[i][h] > -__builtin_inff() ? fast_exp2((sc[i][h] - wm[h]) * LOG2E) : 0.0f;
     } else {
         // the reference weighs the first floor(n/4)*4 keys of each 32-key
         // block (blocks from kv_start, n = min(32, Skv - block start)) by its
         // second-order 2^x polynomial relative to the block max, the rest by
         // exp (kernel_attention.cpp:160-204).  A wave holds exactly one
-        // block here (32 keys from a block boundary).
+        // block here (32 keys from a block boundary), so the block max is the
+        // wave max and the block's factor is the wave's.
         static_assert(HYBRID || FA_KPW == 32, "one 32-key block per wave");
         const int bpoly = (int)(min((size_t)32, Skv > wk0 ? Skv - wk0 : (size_t)0) / 4) * 4;
 #pragma unroll
         for (int h = 0; h < GQ; h++) {
             const float bm = wm[h];
-            const float bscale = bm > -__builtin_inff() ? fast_exp2((bm - M[h]) * LOG2E) : 0.0f;
 #pragma unroll
             for (int i = 0; i < NI; i++) {
                 const int in_blk = i * R + rl;
@@ -426,7 +421,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
                 float w = 0.0f;
                 if (sv > -__builtin_inff())
                     w = in_blk < bpoly ? poly_exp_weight(sv, bm) : fast_exp2((sv - bm) * LOG2E);
-                p[i][h] = w * bscale;
+                p[i][h] = w;
             }
         }
     }
@@ -507,23 +502,42 @@ __global__ void __launch_bounds__(FA_THREADS) attn_splitk_kernel(FastArgs a) {
         }
     __syncthreads();
 
-    // ---- 6. this split's partial: (M, sum, acc[d]) per query head, written
-    // with agent-scope stores (visible to the combining workgroup on any XCD
-    // without a cache writeback)
+    // ---- 6. this split's partial: (M, sum, acc[d]) per query head, M the
+    // workgroup max, each wave's rows and weight sum scaled by e^(m_w - M);
+    // written with agent-scope stores (visible to the combining workgroup on
+    // any XCD without a cache writeback)
     constexpr int PS = D + 4;                     // floats per (split, head): acc[D], M, sum, 2 pad
     float* part = a.part + ((size_t)bg * a.nsplit + s) * GQ * PS;
+    auto wave_factors = [&](int h, float (&ew)[FA_WAVES]) -> float {
+        float mx = redm[h][0];
+#pragma unroll
+        for (int w = 1; w < FA_WAVES; w++) mx = __builtin_fmaxf(mx, redm[h][w]);
+#pragma unroll
+        for (int w = 0; w < FA_WAVES; w++) {
+            const float m = redm[h][w];
+            ew[w] = m > -__builtin_inff() ? fast_exp2((m - mx) * LOG2E) : 0.0f;
+        }
+        return mx;
+    };
     for (int i = tid; i < GQ * D; i += FA_THREADS) {
         const int h = i / D, dm = i % D;
+        float ew[FA_WAVES];
+        wave_factors(h, ew);
         float t = 0.0f;
 #pragma unroll
-        for (int r = 0; r < FA_WAVES * 4; r++) t += vsum[(r * GQ + h) * D + dm];
+        for (int w = 0; w < FA_WAVES; w++) {
+            const float* r = &vsum[(w * 4 * GQ + h) * D + dm];
+            t = __builtin_fmaf(ew[w], (r[0] + r[GQ * D]) + (r[2 * GQ * D] + r[3 * GQ * D]), t);
+        }
         agent_store(part + h * PS + dm, t);
     }
     if (tid < GQ) {
+        float ew[FA_WAVES];
+        const float mx = wave_factors(tid, ew);
         float l = 0.0f;
 #pragma unroll
-        for (int w = 0; w < FA_WAVES; w++) l += reds[tid][w];
-        agent_store(part + tid * PS + D, has_keys ? M[tid] : -__builtin_inff());
+        for (int w = 0; w < FA_WAVES; w++) l = __builtin_fmaf(ew[w], reds[tid][w], l);
+        agent_store(part + tid * PS + D, has_keys ? mx : -__builtin_inff());
         agent_store(part + tid * PS + D + 1, l);
     }
     // every store of the workgroup has completed before the count goes up

@@ -92,6 +92,7 @@ def _roped(orc, x, start):
     (1, 1000, 4, 2, 128, 600, 0, 1.0),     # causal cut: keys past the query position
     (1, 900, 4, 2, 128, 899, 300, 1.0),    # sliding window
     (1, 3000, 16, 8, 128, 2999, 0, 30.0),  # peaked scores
+    (1, 20000, 8, 2, 128, 19999, 0, 1.0),  # 79 splits of 4 query heads: the many-split combine
 ])
 def test_attention_f16_fast(dev, orc, B, Skv, Hq, Hkv, d, pos, window, qmul):
     say("attention_f16_fast", B, Skv, Hq, Hkv, d, pos, window, qmul)
@@ -115,6 +116,7 @@ def test_attention_f16_fast(dev, orc, B, Skv, Hq, Hkv, d, pos, window, qmul):
     (1, 511, 2, 8, 2, 128, 1.0),       # two new rows
     (2, 1000, 1, 8, 2, 64, 1.0),
     (1, 3000, 1, 16, 8, 128, 30.0),    # peaked scores
+    (1, 9000, 1, 16, 8, 128, 1.0),     # 36 splits: the many-split combine
 ])
 def test_attention_hybrid_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul):
     say("attention_hybrid_fast", B, cache, new, Hq, Hkv, d, qmul)
