@@ -761,6 +761,12 @@ def main():
         os.environ["CACTUS_DECODE_EAGER"] = "1"
     import cactus_amd as cm
     cm.call("cactus_hip_init", 0)
+    if args.copy_calibration:
+        n = 1 << 30
+        src, dst = cm.DeviceBuffer(n), cm.DeviceBuffer(n)
+        cm.call("cactus_hip_memcpy_d2d", dst.ptr, src.ptr, n, None)
+        cm.call("cactus_hip_stream_sync", None)
+        del src, dst
     if args.decode_only:
         print(json.dumps(bench_decode(new_tokens=args.new_tokens, mode=args.decode_mode)), flush=True)
         return
@@ -775,12 +781,6 @@ def main():
         g = bench_gemv(args.steps, args.warmup)
         print(json.dumps({"int8_gemv_gbs": round(g["gbs"], 1), "int4_gemv": g4}), flush=True)
         return
-    if args.copy_calibration:
-        n = 1 << 30
-        src, dst = cm.DeviceBuffer(n), cm.DeviceBuffer(n)
-        cm.call("cactus_hip_memcpy_d2d", dst.ptr, src.ptr, n, None)
-        cm.call("cactus_hip_stream_sync", None)
-        del src, dst
     # The streaming GEMVs run last.  When a GPU goes from idle (or from the
     # latency-bound decode) to streaming HBM at full rate, its launches slow
     # down by up to ~25% after the first ~10 and take ~100 launches (~20 ms)
