@@ -215,24 +215,28 @@ def test_decode_prep_attention_fast(dev, orc, cache, Hq, Hkv, d):
     assert (outs[1] == outs[2]).all(), "second launch on the same workspace"
 
 
-@pytest.mark.parametrize("B,cache,new,Hq,Hkv,d,qmul", [
-    (1, 3840, 256, 16, 8, 128, 1.0),   # the last 256-row chunk of a 4096-token prefill
-    (1, 0, 256, 16, 8, 128, 1.0),      # the first chunk: new rows only
-    (1, 700, 100, 8, 2, 128, 1.0),     # GQA 4, ragged row count
-    (2, 129, 37, 4, 4, 64, 1.0),       # batch 2, head_dim 64, GQA 1
-    (1, 1000, 256, 16, 8, 128, 6.0),   # peaked scores
-    (1, 3, 5, 4, 2, 128, 1.0),         # tiny
+@pytest.mark.parametrize("B,cache,new,Hq,Hkv,d,qmul,pos", [
+    (1, 3840, 256, 16, 8, 128, 1.0, None),   # the last 256-row chunk of a 4096-token prefill
+    (1, 0, 256, 16, 8, 128, 1.0, None),      # the first chunk: new rows only
+    (1, 700, 100, 8, 2, 128, 1.0, None),     # GQA 4, ragged row count
+    (2, 129, 37, 4, 4, 64, 1.0, None),       # batch 2, head_dim 64, GQA 1
+    (1, 1000, 256, 16, 8, 128, 6.0, None),   # peaked scores
+    (1, 3, 5, 4, 2, 128, 1.0, None),         # tiny
+    (1, 500, 64, 16, 8, 128, 1.0, 530),      # position past the cache length (a windowed cache)
+    (1, 0, 40, 4, 2, 128, 1.0, 17),          # no cache, rows from position 17
 ])
-def test_attention_hybrid_prefill_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul):
-    """Prefill rows (S = new rows at positions cache..cache+new-1, causal)
-    through the FP16-MFMA flash kernel, against the oracle's hybrid
+def test_attention_hybrid_prefill_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul, pos):
+    """Prefill rows (S = new rows at positions pos..pos+new-1, pos the
+    cache length unless given; the causal limit of row r is key index
+    pos + r) through the FP16-MFMA flash kernel, against the oracle's hybrid
     attention within 1e-3 + 1e-2 |ref|.  The peaked case keeps the score
     spread below ~88: the reference rescales by expf(previous block max -
     this block max) (kernel_attention.cpp:395-403), which overflows when a
     later block's maximum lies that far below an earlier one, and then
     writes a zero row (:465-469); the tolerance mode computes the softmax
     itself there."""
-    say("attention_hybrid_prefill_fast", B, cache, new, Hq, Hkv, d, qmul)
+    say("attention_hybrid_prefill_fast", B, cache, new, Hq, Hkv, d, qmul, pos)
+    pos = cache if pos is None else pos
     rng = np.random.default_rng(cache * 5 + new + d)
     kf = _roped(orc, f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d))), 0)
     vf = f16(rng.normal(0, 1, (B, max(cache, 1), Hkv, d)))
@@ -244,15 +248,15 @@ def test_attention_hybrid_prefill_fast(dev, orc, B, cache, new, Hq, Hkv, d, qmul
         kc[b], ks[b] = orc.quantize_kv(kf[b])
         vc[b], vs[b] = orc.quantize_kv(vf[b])
     kc, vc, ks, vs = (np.ascontiguousarray(x[:, :cache]) for x in (kc, vc, ks[:1], vs[:1]))
-    kn = _roped(orc, f16(rng.normal(0, 1, (B, new, Hkv, d))), cache)
+    kn = _roped(orc, f16(rng.normal(0, 1, (B, new, Hkv, d))), pos)
     vn = f16(rng.normal(0, 1, (B, new, Hkv, d)))
-    q = _roped(orc, f16(rng.normal(0, 1, (B, new, Hq, d)) * qmul), cache)
+    q = _roped(orc, f16(rng.normal(0, 1, (B, new, Hq, d)) * qmul), pos)
     scale = 1.0 / math.sqrt(d)
     ref = orc.attention_hybrid(q, kc if cache else None, vc if cache else None, ks if cache else None,
-                               vs if cache else None, kn, vn, scale, pos_off=cache)
+                               vs if cache else None, kn, vn, scale, pos_off=pos)
     o = dev.empty(q.nbytes)
     P = (lambda a: dev.put(a) if cache else None)
     dev.cm.call("cactus_hip_attention_hybrid_int8_fp16_fast", dev.put(q), P(kc), P(vc), P(ks), P(vs), dev.put(kn),
-                dev.put(vn), o.ptr, B, new, cache, new, Hq, Hkv, d, ctypes.c_float(scale), cache, 1, 128, None)
+                dev.put(vn), o.ptr, B, new, cache, new, Hq, Hkv, d, ctypes.c_float(scale), pos, 1, 128, None)
     err = close(dev.get(o, np.uint16, q.shape), ref, "attention_hybrid_prefill_fast")
     print(f"[prefill fast] max abs error {err:.2e}", flush=True)

@@ -196,3 +196,51 @@ def test_qwen_overlapped_prefill_matches_oracle(chunk, lens):
         t_gpu, t_orc = gpu.decode(tok), orc.decode(tok)
         assert t_gpu == t_orc
         tok = t_gpu
+
+
+def test_qwen_tolerance_prefill_close_to_oracle():
+    """Tolerance-mode prefill (the FP16-MFMA flash attention, 64-row chunks
+    overlapped on three streams) of a 230-token prompt against the oracle's
+    exact prefill, on a 4-layer model whose MLP down projection is small
+    (group scales |N(0, 0.001)|/7), so that a layer passes on its attention's
+    difference without the random MLP amplifying it.  Layer 0's KV cache,
+    computed before any attention, must be bit-identical.  Measured on
+    MI355X for the later layers: 69-85% of the INT8 codes equal, 97.5-99.9%
+    within one step, no code more than 5 steps off, final hidden state 0.69%
+    relative L2 from the oracle's.  Bounds with a margin: >= 60% equal,
+    >= 96% within one step, <= 8 steps, <= 1.5%.  A wrong stream order,
+    scale table or chunk offset moves whole rows and lands far outside."""
+    say("qwen tolerance prefill vs oracle")
+    cfg = qwen_small_config(prefill_chunk=64, num_layers=4)
+    rng = np.random.default_rng(91)
+    w = qwen_weights(rng, cfg, down_sd=0.001)
+    import cactus_amd
+    from cactus_amd.engine import Qwen
+    import oracle
+    cactus_amd.call("cactus_hip_init", 0)
+    gpu = Qwen(cfg, *w)
+    gpu.set_attention_mode(1)
+    orc = oracle.OracleQwen(cfg, *w)
+    p = rng.integers(0, cfg["vocab"], 230).astype(np.uint32)
+    try:
+        gpu.prefill(p)
+    finally:
+        gpu.set_attention_mode(0)
+    orc.prefill(p, 64)
+    assert gpu.cache_len() == orc.cache_len() == len(p)
+    for a, b in zip(gpu.read_kv(0), orc.read_kv(0)):
+        assert (a == b).all(), "kv cache layer 0"
+    for layer in range(1, cfg["num_layers"]):
+        kg, vg, _, _ = gpu.read_kv(layer)
+        ko, vo, _, _ = orc.read_kv(layer)
+        for nm, g_, o_ in (("k", kg, ko), ("v", vg, vo)):
+            d = np.abs(g_.astype(np.int16) - o_.astype(np.int16))
+            eq, one, step = float(np.mean(d == 0)), float(np.mean(d <= 1)), int(np.max(d))
+            print(f"[tolerance prefill] layer {layer} {nm}: codes equal {eq:.4f}, within one step {one:.4f}, "
+                  f"largest step {step}", flush=True)
+            assert eq >= 0.60 and one >= 0.96 and step <= 8, (layer, nm, eq, one, step)
+    hg = gpu.last_hidden().view(np.float16).astype(np.float64)
+    ho = orc.last_hidden().view(np.float16).astype(np.float64)
+    rel = float(np.linalg.norm(hg - ho) / np.linalg.norm(ho))
+    print(f"[tolerance prefill] final hidden relative L2 {rel:.2e}", flush=True)
+    assert rel <= 0.015, rel
