@@ -65,20 +65,24 @@ __device__ __forceinline__ float group_epilogue(const int32_t* ag, const uint16_
 
 // The same chain over group sums and scales that the lanes producing them
 // already converted to fp32 ((float)acc and the fp16 scale are exact): the
-// chain lane only reads and FMAs.
-template <int EPB = 8>
+// chain lane only reads and FMAs, eight groups per pair of 16-byte reads of
+// each row (rows 16-byte aligned: their stride is a multiple of 4 floats).
 __device__ __forceinline__ float group_epilogue_f(const float* ag, const float* sg, int G) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
     float rs = 0.0f;
     int g = 0;
-    for (; g + EPB <= G; g += EPB) {
-        float av[EPB], sv[EPB];
-#pragma unroll
-        for (int j = 0; j < EPB; j++) {
-            av[j] = ag[g + j];
-            sv[j] = sg[g + j];
-        }
-#pragma unroll
-        for (int j = 0; j < EPB; j++) rs = __builtin_fmaf(av[j], sv[j], rs);
+#pragma unroll 2
+    for (; g + 8 <= G; g += 8) {
+        const f4v a0 = *reinterpret_cast<const f4v*>(ag + g), a1 = *reinterpret_cast<const f4v*>(ag + g + 4);
+        const f4v s0 = *reinterpret_cast<const f4v*>(sg + g), s1 = *reinterpret_cast<const f4v*>(sg + g + 4);
+        rs = __builtin_fmaf(a0.x, s0.x, rs);
+        rs = __builtin_fmaf(a0.y, s0.y, rs);
+        rs = __builtin_fmaf(a0.z, s0.z, rs);
+        rs = __builtin_fmaf(a0.w, s0.w, rs);
+        rs = __builtin_fmaf(a1.x, s1.x, rs);
+        rs = __builtin_fmaf(a1.y, s1.y, rs);
+        rs = __builtin_fmaf(a1.z, s1.z, rs);
+        rs = __builtin_fmaf(a1.w, s1.w, rs);
     }
     for (; g < G; g++) rs = __builtin_fmaf(ag[g], sg[g], rs);
     return rs;
@@ -265,7 +269,9 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
     const int cpr = INT4 ? K / 32 : K / 16;  // 16-byte chunks per row
     const int P = INT4 ? gs / 32 : gs / 16;  // chunks per group (power of 2, <= 64)
     const size_t row_bytes = INT4 ? (size_t)K / 2 : (size_t)K;
-    const int Gs = FE ? G + 4 : G;   // row stride of the group sums and scales
+    // row stride of the group sums and scales (FE: whole 16-byte vectors,
+    // plus 16 bytes so that consecutive rows start four banks apart)
+    const int Gs = FE ? ((G + 3) & ~3) + 4 : G;
     const int acc_words = MR * rows * Gs;
     const int wave_bytes = ((acc_words * 4 + 15) & ~15) + ((rows * Gs * (FE ? 4 : 2) + 15) & ~15);
 
@@ -394,7 +400,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             const int m = o / nr, r = o - (o / nr) * nr;
             float rs;
             if constexpr (FE) {
-                rs = group_epilogue_f<4>(accf + (m * rows + r) * Gs, sclf + r * Gs, G);
+                rs = group_epilogue_f(accf + (m * rows + r) * Gs, sclf + r * Gs, G);
             } else {
                 const int32_t* ag = acc + (m * rows + r) * G;
                 const uint16_t* sg = scl + r * G;
@@ -411,7 +417,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
 }
 
 static size_t gemv_wave_smem(int MR, int K, int rows, int G, bool fe = false) {
-    const int Gs = fe ? G + 4 : G;
+    const int Gs = fe ? ((G + 3) & ~3) + 4 : G;
     const size_t wave = (size_t)((MR * rows * Gs * 4 + 15) & ~15) + (size_t)((rows * Gs * (fe ? 4 : 2) + 15) & ~15);
     return (size_t)((MR * K + 15) & ~15) + 4 * wave + (size_t)(MR + 4) * 4;
 }
@@ -513,8 +519,9 @@ static int launch_gemv(GemvArgs a, size_t batch, hipStream_t st) {
         // workgroup quantizes the activation row once, so INT4 rows (the
         // K = 3072 MLP down shape) take more tiles per workgroup: swept on
         // MI355X over 604 / 768 rotated weight sets, INT4 K=3072 streams at
-        // 0.706-0.710 of HBM with 8 per wave (0.68-0.69 with 6, 0.69-0.70
-        // with 12 or 16) and INT8 K=640 at 6.85 TB/s with 3-4 (6.72 with 8)
+        // 0.751-0.753 of HBM with 8 per wave (0.745-0.753 with 12 or 16;
+        // with the earlier scalar-read epilogue 0.706-0.710 with 8,
+        // 0.68-0.69 with 6) and INT8 K=640 at 6.85 TB/s with 3-4 (6.72 with 8)
         const size_t nt = ceil_div(a.N, (size_t)wrows);
         size_t per = nt * batch / (4 * 2048 * (INT4 ? 2 : 3));
         if (per < 1) per = 1;
