@@ -63,6 +63,22 @@ __device__ __forceinline__ float group_epilogue(const int32_t* ag, const uint16_
     return rs;
 }
 
+// group_epilogue for G % 4 == 0 over 16-byte aligned rows of sums and
+// 8-byte aligned rows of scales: four groups per pair of LDS reads
+__device__ __forceinline__ float group_epilogue_v4(const int32_t* ag, const uint16_t* sg, int G) {
+    float rs = 0.0f;
+#pragma unroll 4
+    for (int g = 0; g < G; g += 4) {
+        const i32x4 a4 = *reinterpret_cast<const i32x4*>(ag + g);
+        const uint2 s4 = *reinterpret_cast<const uint2*>(sg + g);
+        rs = __builtin_fmaf((float)a4.x, h2f((uint16_t)(s4.x & 0xFFFFu)), rs);
+        rs = __builtin_fmaf((float)a4.y, h2f((uint16_t)(s4.x >> 16)), rs);
+        rs = __builtin_fmaf((float)a4.z, h2f((uint16_t)(s4.y & 0xFFFFu)), rs);
+        rs = __builtin_fmaf((float)a4.w, h2f((uint16_t)(s4.y >> 16)), rs);
+    }
+    return rs;
+}
+
 // The same chain over group sums and scales that the lanes producing them
 // already converted to fp32 ((float)acc and the fp16 scale are exact): the
 // chain lane only reads and FMAs, eight groups per pair of 16-byte reads of
@@ -404,7 +420,8 @@ __global__ void __launch_bounds__(GEMV_THREADS) gemv_wave_kernel(GemvArgs a, int
             } else {
                 const int32_t* ag = acc + (m * rows + r) * G;
                 const uint16_t* sg = scl + r * G;
-                rs = group_epilogue(ag, sg, G);
+                // rows start 16-byte (sums) and 8-byte (scales) aligned when G % 4 == 0
+                rs = (G & 3) == 0 ? group_epilogue_v4(ag, sg, G) : group_epilogue(ag, sg, G);
             }
             float s = rsm[0];
 #pragma unroll
