@@ -291,6 +291,27 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         for (int g = G16; g < G; g++) rs = __builtin_fmaf(ar[g], h2f(sr[g]), rs);
         return f2h(rs * as);
     };
+    auto silu_mul = [&](int r, uint16_t val, uint16_t up) {
+        const float gx = h2f(val);
+        // silu's vector body uses fast_exp, its n % 8 tail expf (kernel_nn.cpp:12-44)
+        const float e = n0 + r < (sg.N / 8) * 8 ? fast_exp(-gx) : cactus_expf(-gx);
+        const float sig = 1.0f / (1.0f + e);
+        sg.out[n0 + r] = hmul(f2h(gx * sig), up);
+    };
+    if constexpr (EPI == EPI_SILUMUL) {
+        // gate rows on lanes 0..rows-1 of wave 0 and up rows on lanes
+        // rows..2 rows-1: both chains in one instruction stream, then the up
+        // value moves to its gate lane
+        if (2 * rows <= 64) {
+            if (tid < 64) {                                  // wave 0, uniform
+                uint16_t val = 0;
+                if (tid < 2 * rows && vrow_valid(tid)) val = chain(tid);
+                const uint16_t up = (uint16_t)__shfl((int)val, tid + rows, 64);
+                if (tid < nr) silu_mul(tid, val, up);
+            }
+            return;
+        }
+    }
     for (int r = tid; r < nr; r += GEMV_THREADS) {
         const uint16_t val = chain(r);
         if (EPI == EPI_STORE) {
@@ -298,12 +319,7 @@ __global__ void __launch_bounds__(GEMV_THREADS) dec_gemv_kernel(DecGemvArgs a) {
         } else if (EPI == EPI_RESID) {
             sg.out[n0 + r] = hadd(r == tid ? resv : a.res[n0 + r], val);
         } else {
-            const uint16_t up = chain(rows + r);
-            const float gx = h2f(val);
-            // silu's vector body uses fast_exp, its n % 8 tail expf (kernel_nn.cpp:12-44)
-            const float e = n0 + r < (sg.N / 8) * 8 ? fast_exp(-gx) : cactus_expf(-gx);
-            const float sig = 1.0f / (1.0f + e);
-            sg.out[n0 + r] = hmul(f2h(gx * sig), up);
+            silu_mul(r, val, chain(rows + r));
         }
     }
 }
