@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     constexpr bool PRE = NQ <= 2;                      // key row preloaded
     const AttnArgs a = resolve(a_in);
     __shared__ float qsh[NQ][D];
-    __shared__ float wsh[NW][NQ][64];
+    __shared__ __align__(16) float wsh[NW][NQ][64];
     __shared__ float msh[NW][NQ][2];
     const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
     const int gq = a.gq, qr = NQ / gq;
@@ -572,18 +572,30 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
                 const int bsz = (int)(be - bs);
                 const bool is_decode = (!HYBRID) && (qp == a.S - 1) && a.S > 1;
                 const bool block_skipped = !HYBRID && !is_decode && a.causal && bs > aq;
-                const float* x = &wsh[wid][q][32 * half];
+                // the block's 32 weights by eight 16-byte reads first (the slots
+                // past bsz hold other keys' weights or stale values; they are
+                // selected out), then the fold in the reference's order
+                typedef float f4v __attribute__((ext_vector_type(4)));
+                const f4v* x4 = reinterpret_cast<const f4v*>(&wsh[wid][q][32 * half]);
+                float x[32];
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const f4v v = x4[t];
+                    x[4 * t] = v.x; x[4 * t + 1] = v.y; x[4 * t + 2] = v.z; x[4 * t + 3] = v.w;
+                }
                 const int v4 = HYBRID ? 0 : (bsz / 4) * 4;
                 float sum = 0.0f;
                 bool has_zero = false;
-                int j = 0;
-                for (; j < v4; j += 4) {
-                    sum = sum + ((x[j] + x[j + 1]) + (x[j + 2] + x[j + 3]));
-                    has_zero |= !(x[j] != 0.0f) || !(x[j + 1] != 0.0f) || !(x[j + 2] != 0.0f) || !(x[j + 3] != 0.0f);
-                }
-                for (; j < bsz; j++) {
-                    sum = sum + x[j];
-                    has_zero |= !(x[j] != 0.0f);
+#pragma unroll
+                for (int j = 0; j < 32; j += 4) {
+                    if (!HYBRID && j < v4) {
+                        sum = sum + ((x[j] + x[j + 1]) + (x[j + 2] + x[j + 3]));
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; u++) sum = j + u < bsz ? sum + x[j + u] : sum;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++) has_zero |= j + u < bsz && !(x[j + u] != 0.0f);
                 }
                 const size_t row = (b * a.S + qp) * a.Hq + h0 + q % gq;
                 const int blk = (int)(bs / ATT_BLOCK);
