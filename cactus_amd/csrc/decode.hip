@@ -482,6 +482,68 @@ __device__ __forceinline__ void lm_argmax_finish(const LmDecArgs& p, float best,
     atomicExch(p.counter, 0u);
 }
 
+// The same argmax and state update for a grid whose workgroups finish
+// close together (one per CU): 238 returning atomics on one address then
+// queue behind each other (~14 us measured for the 151936-row head), so the
+// count is two-level.  Workgroup i stores its key in slot i and, once the
+// store has been performed, counts itself in group counter i % 8; the last
+// of a group counts the group in the top counter; the last overall reads
+// every slot, reduces them, advances the state and clears the counters.
+// Scratch: top counter at byte 0, group counters at bytes 64 + 64 g, slots
+// (8 bytes per workgroup) from byte 1024; counters are left zero.
+constexpr int LMG_GROUPS = 8;
+constexpr size_t LMG_SLOTS = 1024;
+template <int THREADS>
+__device__ __forceinline__ void lm_argmax_finish_groups(const LmDecArgs& p, float best, uint32_t best_i) {
+    static_assert(THREADS % 64 == 0 && THREADS <= 1024, "whole waves");
+    __shared__ unsigned long long wk[THREADS / 64];
+    __shared__ bool last;
+    auto block_max = [&](unsigned long long key) -> unsigned long long {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const unsigned long long o = __shfl_xor(key, off, 64);
+            key = o > key ? o : key;
+        }
+        if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = key;
+        __syncthreads();
+        unsigned long long m = wk[0];
+        for (int w = 1; w < THREADS / 64; w++) m = wk[w] > m ? wk[w] : m;
+        return m;
+    };
+    char* base = reinterpret_cast<char*>(p.counter);
+    unsigned long long* slots = reinterpret_cast<unsigned long long*>(base + LMG_SLOTS);
+    const unsigned long long m = block_max(lm_argmax_key(best, best_i));
+    if (threadIdx.x == 0) {
+        const unsigned g = blockIdx.x % LMG_GROUPS;
+        const unsigned ngroups = gridDim.x < LMG_GROUPS ? gridDim.x : LMG_GROUPS;
+        const unsigned in_group = (gridDim.x - g + LMG_GROUPS - 1) / LMG_GROUPS;
+        __hip_atomic_store(slots + blockIdx.x, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);              // the slot store is performed before the count
+        bool l = atomicAdd(reinterpret_cast<uint32_t*>(base + 64 + 64 * g), 1u) == in_group - 1;
+        if (l) l = atomicAdd(p.counter, 1u) == ngroups - 1;
+        last = l;
+    }
+    __syncthreads();
+    if (!last) return;
+    unsigned long long k = 0ull;
+    for (unsigned i = threadIdx.x; i < gridDim.x; i += THREADS) {
+        const unsigned long long v = __hip_atomic_load(slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        k = v > k ? v : k;
+    }
+    __syncthreads();                                 // wk reused
+    const unsigned long long mm = block_max(k);
+    if (threadIdx.x != 0) return;
+    const uint32_t tok = mm == 0ull ? 0u : 0xFFFFFFFFu - (uint32_t)mm;
+    const uint32_t step = p.st[3];
+    if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
+    p.st[0] = tok;
+    p.st[1] = p.st[1] + 1;
+    p.st[2] = p.st[2] + 1;
+    p.st[3] = step + 1;
+    for (int g = 0; g < LMG_GROUPS; g++) atomicExch(reinterpret_cast<uint32_t*>(base + 64 + 64 * g), 0u);
+    atomicExch(p.counter, 0u);
+}
+
 // LM head + greedy argmax, streamed: each wave owns 64 vocabulary rows (one
 // per lane) and moves them through its own ring of LMS_D slots by LDS DMA
 // (LMS_KC k-values of 64 rows per slot), LMS_D - 1 chunks ahead, with no
@@ -659,10 +721,14 @@ __global__ void __launch_bounds__(LM_THREADS) dec_lm_head_kernel(LmDecArgs p) {
 // lane in flight (issued before the RMSNorm prologue, which they overlap);
 // the normalized row is read from LDS by broadcast.  Each lane's dot is the
 // reference's 8-lane fp16 accumulation in k order (kernel_gemm.cpp:17-126).
-// Measured in the decode step (151936 x 1024 head, 594 workgroups): 62.2 us
-// with 8 loads in flight, 57.3-58.6 with 12, 58-59 with 14 or 16; 8 waves
-// per workgroup 65.0, 2 waves 67.5.
-constexpr int LMT_WAVES = 4, LMT_THREADS = 64 * LMT_WAVES, LMT_D = 12;
+// Ten waves per workgroup: the 151936 x 1024 head is 238 workgroups, at most
+// one per CU, so every CU streams the same ten 64-row blocks.  With four
+// waves (594 workgroups) CUs ran two or three workgroups and the CUs with
+// three finished ~1.5x later (per-workgroup timestamps: loop ends 26-54 us,
+// the head 57-58 us in the step); with ten it takes 50.9-51.4 us.  Measured
+// with four waves: 62.2 us with 8 loads in flight, 57.3-58.6 with 12, 58-59
+// with 14 or 16; 8 waves per workgroup 65.0, 2 waves 67.5.
+constexpr int LMT_WAVES = 10, LMT_THREADS = 64 * LMT_WAVES, LMT_D = 12;
 
 __global__ void __launch_bounds__(LMT_THREADS) dec_lm_head_tiled_kernel(LmDecArgs p) {
     __shared__ __align__(16) uint16_t xs[4096 + 16 * RMS_T_PAD];
@@ -742,10 +808,17 @@ __global__ void __launch_bounds__(LMT_THREADS) dec_lm_head_tiled_kernel(LmDecArg
 #pragma unroll
         for (int u = 0; u < LMT_D; u++) {
             const int q = q0 + u;
-            const uint4 bv = __builtin_bit_cast(uint4, ring[u]);
-            // refill the slot with step q + D (clamped: the last steps re-read step nq - 1)
+            // the slot is used before it is refilled (with step q + D, clamped:
+            // the last steps re-read step nq - 1), so each step waits for its
+            // own load only and the refill takes the slot's registers.  (The
+            // refill first kept the old value live past it: the compiler
+            // then copied all D slots, waiting for every load, before
+            // issuing any refill, and the ring drained every D steps.)
+            f16_step(acc, av4[q], __builtin_bit_cast(uint4, ring[u]));
             ring[u] = __builtin_nontemporal_load(tp + (size_t)min(q + LMT_D, nq - 1) * npad);
-            f16_step(acc, av4[q], bv);
+            // keep the refill here: the scheduler would otherwise gather the
+            // D refills at the end of the unrolled group
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
@@ -760,7 +833,7 @@ __global__ void __launch_bounds__(LMT_THREADS) dec_lm_head_tiled_kernel(LmDecArg
         best = h2f(logit);
         best_i = (uint32_t)my_row;
     }
-    lm_argmax_finish<LMT_THREADS>(p, best, best_i);
+    lm_argmax_finish_groups<LMT_THREADS>(p, best, best_i);
 }
 
 // tiles[(q * Npad + row) * 8 + e] = embedding[row][8 q + e], 0 past N
@@ -953,7 +1026,7 @@ int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, f
     CH_REQUIRE(((uintptr_t)tiles | (uintptr_t)h | (uintptr_t)norm_w) % 16 == 0,
                "decode_lm_head_tiled: tiles, h and norm_w must be 16-byte aligned");
     const unsigned blocks = (unsigned)ceil_div(N, (size_t)LMT_WAVES * 64);
-    CH_REQUIRE(scratch_bytes >= 256, "decode_lm_head_tiled: scratch too small");
+    CH_REQUIRE(scratch_bytes >= LMG_SLOTS + 8 * (size_t)blocks, "decode_lm_head_tiled: scratch too small");
     LmDecArgs p{};
     p.h = h; p.norm_w = norm_w; p.b = tiles; p.eps = eps; p.K = (int)K; p.N = (int)N;
     p.counter = static_cast<uint32_t*>(scratch);

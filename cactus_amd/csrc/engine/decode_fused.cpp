@@ -33,8 +33,10 @@ FusedDecoder::FusedDecoder(QwenModel& m) : m_(m) {
     mlp_ = DevBuf(F * 2);
     max_steps_ = c.max_seq + 1;
     tokens_ = DevBuf(max_steps_ * 4);
-    const size_t blocks = (c.vocab + 127) / 128;   // cactus_hip_decode_lm_head's scratch contract
-    lm_scratch_ = DevBuf(256 + 8 * blocks);
+    // covers the scratch contracts of cactus_hip_decode_lm_head (>= 256) and
+    // cactus_hip_decode_lm_head_tiled (>= 1024 + 8 * ceil(vocab / 640))
+    const size_t blocks = (c.vocab + 127) / 128;
+    lm_scratch_ = DevBuf(1024 + 8 * blocks);
     logits_ = DevBuf((size_t)c.vocab * 2);
     check_hip(cactus_hip_memset(lm_scratch_.ptr, 0, lm_scratch_.bytes, m.stream()), "memset");
     // the LM head reads the embedding through its 64-row tiles (a second

@@ -515,7 +515,9 @@ int cactus_hip_decode_lm_head(const uint16_t* h, const uint16_t* norm_w, float e
 int cactus_hip_lm_tiles_bytes(size_t K, size_t N, size_t* bytes);
 int cactus_hip_lm_tiles_build(const uint16_t* embedding, size_t K, size_t N, uint16_t* tiles, void* stream);
 /* cactus_hip_decode_lm_head over the tiles of cactus_hip_lm_tiles_build:
- * the same tokens, logits and state (h, norm_w and tiles 16-byte aligned). */
+ * the same tokens, logits and state (h, norm_w and tiles 16-byte aligned).
+ * scratch: >= 1024 + 8 * ceil(N / 640) bytes, zeroed once (each call leaves
+ * its counters zeroed; the rest is written before it is read). */
 int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, float eps,
                                     const uint16_t* tiles, size_t K, size_t N, uint32_t* state,
                                     uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,

@@ -309,8 +309,9 @@ def test_decode_lm_head_state(dev, orc, K, N, tiled):
     ref_logits = orc.matmul_f16(orc.rms_norm(h, w, eps), emb)[0]
     ref_tok = orc.argmax(ref_logits)
     blocks = (N + 127) // 128
-    scratch = dev.empty(256 + 8 * blocks)
-    dev.cm.call("cactus_hip_memset", scratch.ptr, 0, 256 + 8 * blocks, None)
+    scr_bytes = 1024 + 8 * blocks   # covers both entries' scratch contracts
+    scratch = dev.empty(scr_bytes)
+    dev.cm.call("cactus_hip_memset", scratch.ptr, 0, scr_bytes, None)
     state = dev.cm.DeviceBuffer.from_numpy(np.array([7, 100, 100, 2], np.uint32))
     dev.bufs.append(state)
     toks = dev.empty(16)
@@ -331,7 +332,7 @@ def test_decode_lm_head_state(dev, orc, K, N, tiled):
         ep, name = tiles.ptr, "cactus_hip_decode_lm_head_tiled"
     for i in range(2):   # steps 2 and 3; the argmax scratch resets itself
         dev.cm.call(name, hp, wp, ctypes.c_float(eps), ep, K, N, state.ptr, toks.ptr, 4,
-                    logits.ptr if i else None, scratch.ptr, 256 + 8 * blocks, None)
+                    logits.ptr if i else None, scratch.ptr, scr_bytes, None)
     out = dev.get(toks, np.uint32, 4)
     assert out[2] == ref_tok and out[3] == ref_tok, (out, ref_tok)
     assert (dev.get(logits, np.uint16, N) == ref_logits).all()
