@@ -337,10 +337,15 @@ static int launch_dec_gemv(DecGemvArgs a, int nseg, hipStream_t st) {
     const int vmul = EPI == EPI_SILUMUL ? 2 : 1;
     int maxN = 0, totalN = 0;
     for (int s = 0; s < nseg; s++) { maxN = max(maxN, a.seg[s].N); totalN += a.seg[s].N; }
-    // at most 2 chunks per thread; as few rows as keep >= 512 workgroups
+    // at most 2 chunks per thread; as few rows as keep >= 512 working
+    // workgroups (EPI_SILUMUL: one workgroup per tile of gate rows, its up
+    // rows included -- counting both had left the Qwen3 gate/up at 384
+    // workgroups, 1.5 per CU: 5.92-6.34 us per launch against 5.78-5.91
+    // with 768)
     int rows = (2 * GEMV_THREADS) / (cpr * vmul);
     if (rows < 1) rows = 1;
-    while (rows > 1 && (size_t)ceil_div(totalN, rows) < 512) rows = (rows + 1) / 2;
+    const int work_rows = EPI == EPI_SILUMUL ? maxN : totalN;
+    while (rows > 1 && (size_t)ceil_div(work_rows, rows) < 512) rows = (rows + 1) / 2;
     CH_REQUIRE(rows * cpr * vmul <= 2 * GEMV_THREADS, "decode matmul: K too large");
     CH_REQUIRE(rows * vmul * G <= DEC_SCL * GEMV_THREADS, "decode matmul: too many groups per tile");
     a.rows = rows;
