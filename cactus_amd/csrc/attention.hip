@@ -336,6 +336,8 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     __shared__ uint16_t prow[PRE ? NQ + 1 : 1][PRE ? D : 1];
     __shared__ uint16_t pys[PRE ? NQ + 1 : 1][PRE ? D : 1];
     __shared__ uint16_t krot[PRE ? D : 1];
+    __shared__ __align__(16) float nk_acc[PRE ? NQ : 1][8];
+    bool nk_lane = false;                               // the new key's accumulators come from nk_acc
     if constexpr (PRE && NW == 1) {
         if (a.prep.q_raw) {
             const bool appender = bx == nbx - 1;
@@ -416,7 +418,22 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
                 }
                 return;
             }
-            if (has_k && kp == a.cache_len) krow16 = krot;
+            // the new key's eight accumulators per query vector, lane
+            // 8 q + c running accumulator c of query q over dims 8 i + c in
+            // increasing i: the main loop's operands and order, one
+            // D/8-step chain per lane instead of the key lane's fp16 row read
+            // from LDS at every step of that loop
+            if (has_k) {
+                if (lane < 8 * NQ) {
+                    const int q = lane >> 3, c = lane & 7;
+                    float s = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < D / 8; i++) s = __builtin_fmaf(qsh[q][8 * i + c], h2f(krot[8 * i + c]), s);
+                    nk_acc[q][c] = s;
+                }
+                wave_lds_order();
+                nk_lane = kp == a.cache_len;
+            }
         }
     }
     if (!(PRE && NW == 1) || !a.prep.q_raw) {
@@ -499,7 +516,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         if constexpr (PRE) {
             if (kload && kint8) {
                 conv_i8(pre[m], (a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs]);
-            } else if (kload) {
+            } else if (kload && !nk_lane) {
                 conv_f16(*reinterpret_cast<const uint4*>(krow16 + 16 * m),
                          *reinterpret_cast<const uint4*>(krow16 + 16 * m + 8));
             } else {
@@ -516,6 +533,21 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
 #pragma unroll
         for (int q = 0; q < NQ; q++) qv[q] = qsh[q][16 * m + lr];
         sq_group16<NQ>(acc, qv, kk, std::make_integer_sequence<int, 16>{});
+    }
+    if constexpr (PRE && NW == 1) {
+        if (__builtin_amdgcn_readfirstlane(__ballot(nk_lane) != 0ull ? 1 : 0)) {   // the new key's chunk only
+            typedef float f4v __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                const f4v lo = *reinterpret_cast<const f4v*>(&nk_acc[q][0]);
+                const f4v hi = *reinterpret_cast<const f4v*>(&nk_acc[q][4]);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    acc[q][c] = nk_lane ? lo[c] : acc[q][c];
+                    acc[q][c + 4] = nk_lane ? hi[c] : acc[q][c + 4];
+                }
+            }
+        }
     }
 
     // ---- per query vector: mask, block max, weight, stores
