@@ -490,6 +490,16 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
             if (!one_scale) nxs[m & 1] = (kload && kint8) ? ksr[(16 * m) / a.qgs] : 0.0f;
         }
     };
+    // decode form: every step's query values in registers before the loop
+    // (a read from LDS right before its step's FMAs would wait out the LDS
+    // latency at each of the D/16 steps)
+    float qall[PRE ? D / 16 : 1][NQ];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int m = 0; m < D / 16; m++)
+#pragma unroll
+            for (int q = 0; q < NQ; q++) qall[m][q] = qsh[q][16 * m + lr];
+    }
     fetch(0);
 #pragma unroll
     for (int m = 0; m < D / 16; m++) {
@@ -531,7 +541,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
         }
         float qv[NQ];
 #pragma unroll
-        for (int q = 0; q < NQ; q++) qv[q] = qsh[q][16 * m + lr];
+        for (int q = 0; q < NQ; q++) qv[q] = PRE ? qall[m][q] : qsh[q][16 * m + lr];
         sq_group16<NQ>(acc, qv, kk, std::make_integer_sequence<int, 16>{});
     }
     if constexpr (PRE && NW == 1) {
