@@ -254,8 +254,9 @@ __device__ __forceinline__ void sq_group16(float (&acc)[NQ][8], const float (&qv
 
 // NQ query vectors per wave, NW waves (64-key chunks) per workgroup.  The
 // prefill form is NQ = 8, NW = 4; the decode form (one query row) is
-// NQ = gq, NW = 1 with the lane's whole INT8 key row loaded before the
-// query, so the two memory round trips overlap.
+// NQ = 1, NW = 1, the gq heads of a kv head in gq workgroups per chunk
+// (hsplit), with the lane's whole INT8 key row loaded before the query, so
+// the two memory round trips overlap.
 template <bool HYBRID, int D, int NQ, int NW>
 __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in) {
     constexpr bool PRE = NQ <= 2;                      // key row preloaded
@@ -264,15 +265,21 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     __shared__ __align__(16) float wsh[NW][NQ][64];
     __shared__ float msh[NW][NQ][2];
     const int wid = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)), lane = threadIdx.x & 63;
-    const int gq = a.gq, qr = NQ / gq;
+    // gq: the query heads of the kv head this workgroup takes (all of them,
+    // or 1 / hsplit of them in the decode form)
+    const int hsp = a.hsplit > 1 ? a.hsplit : 1;
+    const int gq = a.gq / hsp, qr = NQ / gq;
     const int ngrp = (a.S + qr - 1) / qr;
     size_t gy = blockIdx.y;                            // (b, row group, kv head)
     unsigned bx = blockIdx.x, nbx = gridDim.x;         // chunk, chunks (+ appender)
+    int hs = 0;                                        // head share of the split
     if (a.xcd_chunks) {
         const int L = blockIdx.x;
         int j = L >> 3;
-        nbx = (unsigned)a.xcd_chunks;
+        nbx = (unsigned)(a.xcd_chunks / hsp);
         bx = (unsigned)(j % a.xcd_chunks);
+        hs = (int)(bx % (unsigned)hsp);
+        bx /= (unsigned)hsp;
         j /= a.xcd_chunks;
         const int kvx = (L & 7) + 8 * (j / a.xcd_rest);
         if (kvx >= a.Hkv) return;                      // whole workgroup, before any barrier
@@ -283,7 +290,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     const int qp0 = (int)(gy % ngrp) * qr;
     const size_t b = gy / ngrp;
     const int d = a.d;
-    const int h0 = kvh * gq;
+    const int h0 = kvh * a.gq + hs * gq;
     // per query vector: its row's key range (kv_start is 0 on this path)
     const float NEG_INF = -__builtin_inff();
     size_t kv_end_max = 0;
@@ -341,6 +348,7 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
     if constexpr (PRE && NW == 1) {
         if (a.prep.q_raw) {
             const bool appender = bx == nbx - 1;
+            if (appender && hs != 0) return;               // one appender per kv head
             if (!appender && wbase >= kv_end_max) return;   // one wave: no barrier waits for it
             const int end8 = (d / 8) * 8, half = d / 2, vh = (half / 8) * 8;
             const uint32_t pos = (uint32_t)a.pos_off;
@@ -1668,20 +1676,19 @@ static int launch_attention(AttnArgs a, void* stream) {
         // decode: one query row, its gq heads per wave, one wave per 64 keys
         // (with the fused head preparation, one more workgroup per kv head
         // appends the step's key and value)
-        // workgroups of kv head h on XCD h % 8, where the chain kernel's are
-        a.xcd_chunks = (int)(chunks + (a.prep.q_raw ? 1 : 0));
-        a.xcd_rest = a.B * a.S;                          // row groups of one row (NQ = gq)
+        // workgroups of kv head h on XCD h % 8, where the chain kernel's are;
+        // two query heads per kv head split over two workgroups per chunk
+        // (consecutive, so on one XCD: the second reads the key rows from
+        // its L2), which halves each wave's dot and weight work
+        a.hsplit = a.gq;
+        a.xcd_chunks = (int)(chunks + (a.prep.q_raw ? 1 : 0)) * a.hsplit;
+        a.xcd_rest = a.B * a.S;                          // row groups of one row, one head
         const size_t nwg = 8 * (size_t)((a.Hkv + 7) / 8) * a.xcd_chunks * a.xcd_rest;
         CH_REQUIRE(nwg < (1u << 31), "attention: decode key range too long");
         dim3 ga((unsigned)nwg);
         auto go = [&](auto kern) { hipLaunchKernelGGL(kern, ga, dim3(64), 0, as_stream(stream), a); };
-        if (a.d == 64) {
-            if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 64, 1, 1>);
-            else go(attn_scores_rows_kernel<HYBRID, 64, 2, 1>);
-        } else {
-            if (a.gq == 1) go(attn_scores_rows_kernel<HYBRID, 128, 1, 1>);
-            else go(attn_scores_rows_kernel<HYBRID, 128, 2, 1>);
-        }
+        if (a.d == 64) go(attn_scores_rows_kernel<HYBRID, 64, 1, 1>);
+        else go(attn_scores_rows_kernel<HYBRID, 128, 1, 1>);
         rc = check_launch("attention scores (decode)");
         if (rc) return rc;
     } else if (chunks > 0) {

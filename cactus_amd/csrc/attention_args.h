@@ -43,6 +43,10 @@ struct AttnArgs {
     // i runs on XCD i % 8, kv head h's workgroups on XCD h % 8; xcd_chunks
     // workgroups per (row group, kv head), xcd_rest row groups
     int xcd_chunks, xcd_rest;
+    // decode scores: the query heads of a kv head split over this many
+    // workgroups per key chunk (0 or 1: one workgroup takes all gq heads);
+    // the workgroups of one chunk are consecutive within xcd_chunks
+    int hsplit;
     // decode step with the head preparation fused into the scores (null
     // q_raw: q and the new key row come prepared in q and k): raw q / k / v
     // rows of the step, head RMSNorm weights, RoPE tables, and the cache
