@@ -508,49 +508,61 @@ __global__ void __launch_bounds__(64 * NW) attn_scores_rows_kernel(AttnArgs a_in
 #pragma unroll
             for (int q = 0; q < NQ; q++) qall[m][q] = qsh[q][16 * m + lr];
     }
-    fetch(0);
+    auto conv_i8 = [](float (&kk)[16], const uint4 raw, const float s) {
+        const float ns = -128.0f * s;
+        const uint32_t w4[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
+                                raw.w ^ 0x80808080u};
 #pragma unroll
-    for (int m = 0; m < D / 16; m++) {
-        if (m + 1 < D / 16) fetch(m + 1);
-        const uint4 cur0 = nx0[m & 1], cur1 = nx1[m & 1];
-        const float cur_s = nxs[m & 1];
+        for (int e = 0; e < 16; e++)
+            kk[e] = __builtin_fmaf((float)((w4[e >> 2] >> (8 * (e & 3))) & 0xFFu), s, ns);
+    };
+    auto conv_f16 = [](float (&kk)[16], const uint4 r0, const uint4 r1) {
+        const uint32_t h[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            kk[2 * e] = h2f((uint16_t)(h[e] & 0xFFFF));
+            kk[2 * e + 1] = h2f((uint16_t)(h[e] >> 16));
+        }
+    };
+    // one 16-dim step; ALL_I8: the fused decode form with one scale per key
+    // row, where every lane converts its preloaded INT8 row without a branch
+    // (a lane past the last key converts its stand-in row and the new key's
+    // lane its own, unused: their scores are not computed, or replaced below)
+    auto step = [&](int m, auto all_i8) {
         float kk[16];
-        auto conv_i8 = [&](const uint4 raw, const float s) {
-            const float ns = -128.0f * s;
-            const uint32_t w4[4] = {raw.x ^ 0x80808080u, raw.y ^ 0x80808080u, raw.z ^ 0x80808080u,
-                                    raw.w ^ 0x80808080u};
-#pragma unroll
-            for (int e = 0; e < 16; e++)
-                kk[e] = __builtin_fmaf((float)((w4[e >> 2] >> (8 * (e & 3))) & 0xFFu), s, ns);
-        };
-        auto conv_f16 = [&](const uint4 r0, const uint4 r1) {
-            const uint32_t h[8] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                kk[2 * e] = h2f((uint16_t)(h[e] & 0xFFFF));
-                kk[2 * e + 1] = h2f((uint16_t)(h[e] >> 16));
-            }
-        };
-        if constexpr (PRE) {
+        if constexpr (PRE && decltype(all_i8)::value) {
+            conv_i8(kk, pre[m], pres);
+        } else if constexpr (PRE) {
             if (kload && kint8) {
-                conv_i8(pre[m], (a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs]);
+                conv_i8(kk, pre[m], (a.qgs >= D) ? pres : ksr[(16 * m) / a.qgs]);
             } else if (kload && !nk_lane) {
-                conv_f16(*reinterpret_cast<const uint4*>(krow16 + 16 * m),
+                conv_f16(kk, *reinterpret_cast<const uint4*>(krow16 + 16 * m),
                          *reinterpret_cast<const uint4*>(krow16 + 16 * m + 8));
             } else {
 #pragma unroll
                 for (int e = 0; e < 16; e++) kk[e] = 0.0f;
             }
         } else {
+            if (m + 1 < D / 16) fetch(m + 1);
             // a lane past the last key converts the row it loaded; its
             // scores are never used (not computed, or masked to -inf)
-            if (ldstep == 16) conv_i8(cur0, one_scale ? s_row : cur_s);
-            else conv_f16(cur0, cur1);
+            if (ldstep == 16) conv_i8(kk, nx0[m & 1], one_scale ? s_row : nxs[m & 1]);
+            else conv_f16(kk, nx0[m & 1], nx1[m & 1]);
         }
         float qv[NQ];
 #pragma unroll
         for (int q = 0; q < NQ; q++) qv[q] = PRE ? qall[m][q] : qsh[q][16 * m + lr];
         sq_group16<NQ>(acc, qv, kk, std::make_integer_sequence<int, 16>{});
+    };
+    fetch(0);
+    bool all_i8 = false;
+    if constexpr (PRE && NW == 1 && HYBRID) all_i8 = a.prep.q_raw != nullptr && a.qgs >= D;
+    if (all_i8) {
+#pragma unroll
+        for (int m = 0; m < D / 16; m++) step(m, std::true_type{});
+    } else {
+#pragma unroll
+        for (int m = 0; m < D / 16; m++) step(m, std::false_type{});
     }
     if constexpr (PRE && NW == 1) {
         if (__builtin_amdgcn_readfirstlane(__ballot(nk_lane) != 0ull ? 1 : 0)) {   // the new key's chunk only
