@@ -427,6 +427,10 @@ struct LmDecArgs {
     uint32_t* tokens_out;    // [max_steps] or null
     uint32_t max_steps;
     uint16_t* logits_out;    // fp16 [N] or null
+    // or null: the next step's input row, embed[token] ([N][K] fp16), is
+    // written to h_next by the last workgroup (zeros for a token >= N)
+    const uint16_t* embed;
+    uint16_t* h_next;
 };
 
 // Greedy argmax over the rows of all workgroups and the step state's
@@ -537,8 +541,15 @@ __device__ __forceinline__ void lm_argmax_finish_groups(const LmDecArgs& p, floa
     }
     __syncthreads();                                 // wk reused
     const unsigned long long mm = block_max(k);
-    if (threadIdx.x != 0) return;
     const uint32_t tok = mm == 0ull ? 0u : 0xFFFFFFFFu - (uint32_t)mm;
+    if (p.h_next) {
+        // the next step's embedding row (every workgroup has read h by now)
+        const bool ok = tok < (uint32_t)p.N;
+        const uint4* src = reinterpret_cast<const uint4*>(p.embed + (size_t)(ok ? tok : 0u) * p.K);
+        for (int c = threadIdx.x; c < p.K / 8; c += THREADS)
+            reinterpret_cast<uint4*>(p.h_next)[c] = ok ? src[c] : make_uint4(0, 0, 0, 0);
+    }
+    if (threadIdx.x != 0) return;
     const uint32_t step = p.st[3];
     if (p.tokens_out && step < p.max_steps) p.tokens_out[step] = tok;
     p.st[0] = tok;
@@ -1038,6 +1049,27 @@ int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, f
     p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps; p.logits_out = logits_out;
     hipLaunchKernelGGL(dec_lm_head_tiled_kernel, dim3(blocks), dim3(LMT_THREADS), 0, as_stream(stream), p);
     return check_launch("decode_lm_head_tiled");
+}
+
+int cactus_hip_decode_lm_head_tiled_embed(const uint16_t* h, const uint16_t* norm_w, float eps,
+                                          const uint16_t* tiles, const uint16_t* embedding, size_t K, size_t N,
+                                          uint32_t* state, uint32_t* tokens_out, size_t max_steps,
+                                          uint16_t* logits_out, uint16_t* h_next, void* scratch,
+                                          size_t scratch_bytes, void* stream) {
+    CH_REQUIRE(h && norm_w && tiles && embedding && h_next && state && scratch,
+               "decode_lm_head_tiled_embed: null pointer");
+    CH_REQUIRE(K % 8 == 0 && K > 0 && K <= 4096 && N > 0 && N < (1u << 30), "decode_lm_head_tiled_embed: bad K / N");
+    CH_REQUIRE(((uintptr_t)tiles | (uintptr_t)h | (uintptr_t)norm_w | (uintptr_t)embedding | (uintptr_t)h_next) % 16 == 0,
+               "decode_lm_head_tiled_embed: tiles, h, norm_w, embedding and h_next must be 16-byte aligned");
+    const unsigned blocks = (unsigned)ceil_div(N, (size_t)LMT_WAVES * 64);
+    CH_REQUIRE(scratch_bytes >= LMG_SLOTS + 8 * (size_t)blocks, "decode_lm_head_tiled_embed: scratch too small");
+    LmDecArgs p{};
+    p.h = h; p.norm_w = norm_w; p.b = tiles; p.eps = eps; p.K = (int)K; p.N = (int)N;
+    p.counter = static_cast<uint32_t*>(scratch);
+    p.st = state; p.tokens_out = tokens_out; p.max_steps = (uint32_t)max_steps; p.logits_out = logits_out;
+    p.embed = embedding; p.h_next = h_next;
+    hipLaunchKernelGGL(dec_lm_head_tiled_kernel, dim3(blocks), dim3(LMT_THREADS), 0, as_stream(stream), p);
+    return check_launch("decode_lm_head_tiled_embed");
 }
 
 }  // extern "C"

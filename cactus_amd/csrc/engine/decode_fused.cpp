@@ -103,7 +103,8 @@ void FusedDecoder::enqueue() {
     const size_t gqa = c.heads / c.kv_heads;
     const bool fused_prep = (hd == 64 || hd == 128) && (gqa == 1 || gqa == 2);
     const bool tolerance = m_.attention_mode() == 1 && (hd == 64 || hd == 128) && (gqa == 1 || gqa == 2 || gqa == 4);
-    check_hip(cactus_hip_decode_embed(u16(m_.embedding()), state, h, H, c.vocab, st), "decode_embed");
+    // h holds the step's input row: embedded by run() for the first step,
+    // then by the LM head of the step before
     for (uint32_t l = 0; l < c.num_layers; l++) {
         const QwenLayer& L = m_.layer(l);
         check_hip(cactus_hip_decode_qkv(h, u16(L.input_norm), c.eps, H, gs, L.q_w.as<int8_t>(), u16(L.q_s),
@@ -152,9 +153,11 @@ void FusedDecoder::enqueue() {
                                                     h, st),
                   "decode_down");
     }
-    check_hip(cactus_hip_decode_lm_head_tiled(h, u16(m_.output_norm()), c.eps, lm_tiles_.as<uint16_t>(), H, c.vocab,
-                                              state, tokens_.as<uint32_t>(), max_steps_, logits_.as<uint16_t>(),
-                                              lm_scratch_.ptr, lm_scratch_.bytes, st),
+    // the LM head's last workgroup also embeds the token it picks into h
+    check_hip(cactus_hip_decode_lm_head_tiled_embed(h, u16(m_.output_norm()), c.eps, lm_tiles_.as<uint16_t>(),
+                                                    u16(m_.embedding()), H, c.vocab, state, tokens_.as<uint32_t>(),
+                                                    max_steps_, logits_.as<uint16_t>(), h, lm_scratch_.ptr,
+                                                    lm_scratch_.bytes, st),
               "decode_lm_head");
 }
 
@@ -187,6 +190,9 @@ void FusedDecoder::run(uint32_t token, size_t n, uint32_t* out) {
                                  std::to_string(kv.max_seq_len) + " tokens; set a window or a larger context)");
     reserve(kv.total_seq_len + n, n);
     set_state(token);
+    check_hip(cactus_hip_decode_embed(m_.embedding().as<uint16_t>(), state_.as<uint32_t>(), h_.as<uint16_t>(),
+                                      m_.config().hidden, m_.config().vocab, m_.stream()),
+              "decode_embed");
     // the fused step keeps the last step's logits (in logits_), not the
     // final hidden state
     m_.last_hidden_ = SIZE_MAX;

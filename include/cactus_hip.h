@@ -522,6 +522,18 @@ int cactus_hip_decode_lm_head_tiled(const uint16_t* h, const uint16_t* norm_w, f
                                     const uint16_t* tiles, size_t K, size_t N, uint32_t* state,
                                     uint32_t* tokens_out, size_t max_steps, uint16_t* logits_out,
                                     void* scratch, size_t scratch_bytes, void* stream);
+/* cactus_hip_decode_lm_head_tiled that also writes the next step's input,
+ * h_next = embedding[token] (the greedy token just chosen; zeros for a token
+ * >= N, as cactus_hip_decode_embed), from the workgroup that finishes the
+ * argmax, so a step replayed back to back needs no embedding launch of its
+ * own (the first step of a run still takes cactus_hip_decode_embed).
+ * h_next may be h.  embedding [N][K] fp16, the table the tiles were built
+ * from; every pointer 16-byte aligned. */
+int cactus_hip_decode_lm_head_tiled_embed(const uint16_t* h, const uint16_t* norm_w, float eps,
+                                          const uint16_t* tiles, const uint16_t* embedding, size_t K, size_t N,
+                                          uint32_t* state, uint32_t* tokens_out, size_t max_steps,
+                                          uint16_t* logits_out, uint16_t* h_next, void* scratch,
+                                          size_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -339,6 +339,51 @@ def test_decode_lm_head_state(dev, orc, K, N, tiled):
     assert list(dev.get(state, np.uint32, 4)) == [ref_tok, 102, 102, 4]
 
 
+@pytest.mark.parametrize("K,N", [(1024, 151936), (256, 1001)])
+def test_decode_lm_head_tiled_embed(dev, orc, K, N):
+    """The tiled LM head that also embeds the token it picks: tokens and
+    state as the plain entry, h_next = embedding[token]; then two steps
+    with h_next = h (the fused step's use), each step's token the oracle's
+    argmax over the previous step's embedded row."""
+    say("decode_lm_head_tiled_embed", K, N)
+    rng = np.random.default_rng(K * 3 + N)
+    h = f16(rng.normal(0, 1, (1, K)))
+    w = f16(1 + rng.normal(0, 0.05, K))
+    emb = f16(rng.normal(0, 0.02, (N, K)))
+    eps = 1e-6
+    blocks = (N + 639) // 640
+    scr_bytes = 1024 + 8 * blocks
+    scratch = dev.empty(scr_bytes)
+    dev.cm.call("cactus_hip_memset", scratch.ptr, 0, scr_bytes, None)
+    state = dev.cm.DeviceBuffer.from_numpy(np.array([0, 50, 50, 0], np.uint32))
+    dev.bufs.append(state)
+    toks = dev.empty(16)
+    hp, wp, ep = dev.put(h), dev.put(w), dev.put(emb)
+    nb = ctypes.c_size_t()
+    dev.cm.call("cactus_hip_lm_tiles_bytes", K, N, ctypes.byref(nb))
+    tiles = dev.empty(nb.value)
+    dev.cm.call("cactus_hip_lm_tiles_build", ep, K, N, tiles.ptr, None)
+    name = "cactus_hip_decode_lm_head_tiled_embed"
+    # into a separate row
+    hn = dev.empty(2 * K)
+    dev.cm.call(name, hp, wp, ctypes.c_float(eps), tiles.ptr, ep, K, N, state.ptr, toks.ptr, 4, None, hn.ptr,
+                scratch.ptr, scr_bytes, None)
+    tok = orc.argmax(orc.matmul_f16(orc.rms_norm(h, w, eps), emb)[0])
+    assert dev.get(toks, np.uint32, 1)[0] == tok
+    assert (dev.get(hn, np.uint16, K) == emb[tok]).all()
+    # in place: each step reads the row the one before embedded
+    row = emb[tok][None, :]
+    dev.cm.call("cactus_hip_memcpy_d2d", hp, hn.ptr, 2 * K, None)
+    for step in (1, 2):
+        dev.cm.call(name, hp, wp, ctypes.c_float(eps), tiles.ptr, ep, K, N, state.ptr, toks.ptr, 4, None, hp,
+                    scratch.ptr, scr_bytes, None)
+        tok = orc.argmax(orc.matmul_f16(orc.rms_norm(row, w, eps), emb)[0])
+        assert dev.get(toks, np.uint32, step + 1)[step] == tok, step
+        row = emb[tok][None, :]
+        assert (dev.get_ptr(hp, np.uint16, K) == row[0]).all(), step
+    assert list(dev.get(state, np.uint32, 4)) == [tok, 53, 53, 3]
+
+
 # ------------------------------------------------------------------ a5/a6
 def _attn_inputs(rng, B, S, Skv, Hq, Hkv, d):
     q = f16(rng.normal(0, 1, (B, S, Hq, d)))
