@@ -572,7 +572,8 @@ def test_decode_attention_state(dev, orc, cache, Hq, Hkv, d, qmul, shadow):
     assert_bits(dev.get(o, np.uint16, q.shape), ref, "decode attention")
 
 
-@pytest.mark.parametrize("cache,Hq,Hkv,d", [(4095, 16, 8, 128), (700, 4, 4, 64), (127, 4, 2, 128)])
+@pytest.mark.parametrize("cache,Hq,Hkv,d", [(4095, 16, 8, 128), (700, 4, 4, 64), (127, 4, 2, 128),
+                                            (300, 8, 4, 64), (256, 16, 8, 128)])
 @pytest.mark.parametrize("shadow", [True, False])
 def test_decode_prep_attention_fused(dev, orc, cache, Hq, Hkv, d, shadow):
     """The head preparation fused into the attention's score kernel equals
